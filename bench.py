@@ -1,0 +1,322 @@
+#!/usr/bin/env python3
+"""bench.py -- quantized GEMV / MMQ throughput on one MI355X.
+
+Headline workload: one decode FFN step at batch 1,
+  Q8_K-quantize x[2560] -> gate/up GEMV (Q4_K [9728,2560] x2, one launch, the
+  two weights adjacent as matvecPair fuses them) -> Q8_K-quantize h[9728] ->
+  down GEMV (Q6_K [2560,9728]).
+`value` = algorithmic bytes of the step's GEMVs (packed weights + f32 x + f32 y
+per GEMV) / step time, inputs resident in HBM.  Weight sets rotate over enough
+device copies (> 512 MB per pass) that every step streams from HBM, not from
+the 256 MB Infinity Cache.
+
+Also reported: the other configurations' GEMV bandwidth, the dominant
+kernel's roofline fraction (HIP events around back-to-back launches of that
+kernel alone), and the reference's CPU path timed on this host's cores.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+       python bench.py --profile-kernel   (only the dominant kernel, for rocprofv3)
+       python bench.py --copy-calib       (a plain copy of known size, for counter scaling)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, vendor figure
+INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA (POP/s x 1e3)
+ROTATE_BYTES = 512 << 20  # per-pass footprint that defeats the MALL
+METRIC = "quant GEMV GB/s (% of HBM peak) at bs=1; MMQ prefill tokens/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(rows: int, cols: int, wbytes: int, tokens: int = 1) -> int:
+    """Algorithmic bytes of one GEMV: packed weights + f32 x + f32 y."""
+    return wbytes + 4 * cols * tokens + 4 * rows * tokens
+
+
+class Stream:
+    """Device copies of a weight set, rotated per launch."""
+
+    def __init__(self, torch, host_bytes, dev, min_bytes=ROTATE_BYTES, align=256):
+        import numpy as np
+        n = len(host_bytes)
+        stride = (n + align - 1) // align * align
+        self.copies = max(1, -(-min_bytes // stride)) if min_bytes else 1
+        self.buf = torch.empty(self.copies * stride, dtype=torch.uint8, device=dev)
+        src = torch.from_numpy(np.ascontiguousarray(host_bytes)).to(dev)
+        for c in range(self.copies):
+            self.buf[c * stride:c * stride + n].copy_(src)
+        self.stride = stride
+        self.n = n
+
+    def ptr(self, i: int) -> int:
+        return self.buf.data_ptr() + (i % self.copies) * self.stride
+
+
+def time_loop(torch, fn, iters: int, warmup: int) -> float:
+    """Average seconds per call of fn(i), HIP events on the current stream."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(iters):
+        fn(warmup + i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / iters
+
+
+def single_latency(torch, fn, reps: int = 20) -> float:
+    """Median seconds of one isolated launch (synchronized before and after)."""
+    ts = []
+    for i in range(reps):
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) * 1e-3)
+    return statistics.median(ts)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--profile-kernel", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the quantized matvec path has no "
+              "multi-GPU component; see DESIGN.md for how it would shard). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import qwen35_amd
+    from qwen35_amd import _lib, ops, synth
+
+    lib = _lib.load()
+    qwen35_amd.check("qhip_init", lib.qhip_init(0))
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    TQ4, TQ6, TQ8, TIQ = 12, 14, 8, 20
+
+    if args.copy_calib:
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n, "launches": 5}))
+        return 0
+
+    # ---- headline workload: cfg2 FFN step --------------------------------------
+    H, F = 2560, 9728
+    t0 = time.time()
+    wg = synth.make_weight(TQ4, F, H, seed=0, tag=1)
+    wu = synth.make_weight(TQ4, F, H, seed=0, tag=2)
+    wd = synth.make_weight(TQ6, H, F, seed=0, tag=3)
+    x = synth.make_act(H, 1, seed=0, tag=100)
+    hvec = synth.make_act(F, 1, seed=0, tag=101)
+    gu_bytes, d_bytes = wg.nbytes + wu.nbytes, wd.nbytes
+    host_set = np.concatenate([wg.reshape(-1), wu.reshape(-1), wd.reshape(-1)])
+    ws = Stream(torch, host_set, dev)
+    log(f"cfg2 weights {host_set.nbytes / 1e6:.1f} MB x {ws.copies} device copies "
+        f"(gen+upload {time.time() - t0:.1f}s), sha256 {synth.sha256(host_set)[:16]}")
+    xd = torch.from_numpy(x).to(dev)
+    hd = torch.from_numpy(hvec).to(dev)
+    xq = torch.empty(lib.qhip_act_row_bytes(TQ4, H), dtype=torch.uint8, device=dev)
+    hq = torch.empty(lib.qhip_act_row_bytes(TQ6, F), dtype=torch.uint8, device=dev)
+    y_gu = torch.empty(2 * F, device=dev)
+    y_d = torch.empty(H, device=dev)
+
+    def gate_up(i):
+        rc = lib.qhip_launch_mul_mat_vec(ws.ptr(i), xq.data_ptr(), y_gu.data_ptr(), 2 * F, H, 1, TQ4,
+                                         stream)
+        assert rc == 0, rc
+
+    def down(i):
+        rc = lib.qhip_launch_mul_mat_vec(ws.ptr(i) + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1,
+                                         TQ6, stream)
+        assert rc == 0, rc
+
+    def step(i):
+        assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
+        gate_up(i)
+        assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
+        down(i)
+
+    if args.profile_kernel:
+        for i in range(3):
+            step(i)
+        for i in range(200):
+            gate_up(i)
+        torch.cuda.synchronize()
+        print(json.dumps({"profiled": "gate_up Q4_K [19456,2560] x 200", "copies": ws.copies}))
+        return 0
+
+    step_bytes = gemv_bytes(2 * F, H, gu_bytes) + gemv_bytes(H, F, d_bytes)
+    sec = time_loop(torch, step, args.steps, args.warmup)
+    value = step_bytes / sec / 1e9
+    log(f"cfg2 step: {sec * 1e6:.2f} us, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% HBM)")
+
+    # dominant kernel alone (gate/up, the larger launch of the step)
+    n_k = max(200, args.steps)
+    gu_alg = gemv_bytes(2 * F, H, gu_bytes)
+    d_alg = gemv_bytes(H, F, d_bytes)
+    gu_sec = time_loop(torch, gate_up, n_k, 20)
+    d_sec = time_loop(torch, down, n_k, 20)
+    kernels = {
+        "gemv_q4_k_gate_up_19456x2560": {"alg_bytes": gu_alg, "avg_us": gu_sec * 1e6,
+                                         "gbs": gu_alg / gu_sec / 1e9},
+        "gemv_q6_k_down_2560x9728": {"alg_bytes": d_alg, "avg_us": d_sec * 1e6,
+                                     "gbs": d_alg / d_sec / 1e9},
+    }
+    dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
+    achieved = kernels[dom]["gbs"]
+    traffic = None
+    tpath = ROOT / "profiles" / "traffic.json"
+    if tpath.exists():
+        try:
+            traffic = json.loads(tpath.read_text()).get(dom, {}).get("hbm_bytes_per_launch")
+        except (ValueError, AttributeError):
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
+                "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
+                "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
+    latency = {"gate_up_single_launch_us": round(single_latency(torch, gate_up) * 1e6, 2),
+               "down_single_launch_us": round(single_latency(torch, down) * 1e6, 2)}
+
+    # ---- other configurations (GEMV bandwidth per launch, back-to-back) ------
+    extra = {}
+    if not args.no_extra:
+        for name, tt, rows, cols in (("cfg1_q8_0_6144x1024", TQ8, 6144, 1024),
+                                     ("cfg3_iq4_nl_248320x2560", TIQ, 248320, 2560),
+                                     ("cfg5_q4_k_17408x5120", TQ4, 17408, 5120),
+                                     ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408)):
+            t1 = time.time()
+            w = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
+            st = Stream(torch, w.reshape(-1), dev)
+            del w
+            xv = torch.from_numpy(synth.make_act(cols, 1, seed=0)).to(dev)
+            aq = ops.quantize_act(tt, xv)
+            yo = torch.empty(rows, device=dev)
+
+            def one(i, st=st, tt=tt, rows=rows, cols=cols, aq=aq, yo=yo):
+                rc = lib.qhip_launch_mul_mat_vec(st.ptr(i), aq.data_ptr(), yo.data_ptr(), rows, cols, 1,
+                                                 tt, stream)
+                assert rc == 0, rc
+
+            s = time_loop(torch, one, max(50, min(2000, int(2e9 // st.n))), 10)
+            alg = gemv_bytes(rows, cols, st.n)
+            extra[name] = {"gbs": round(alg / s / 1e9, 1), "hbm_frac": round(alg / s / 1e9 / HBM_PEAK_GBS, 4),
+                           "avg_us": round(s * 1e6, 3), "alg_bytes": alg, "copies": st.copies,
+                           "single_launch_us": round(single_latency(torch, one) * 1e6, 2)}
+            log(f"{name}: {extra[name]['gbs']} GB/s, {extra[name]['avg_us']} us/launch "
+                f"({st.copies} copies, {time.time() - t1:.1f}s)")
+            del st
+            torch.cuda.empty_cache()
+
+    # ---- CPU baseline: the reference's own kernels on this host ---------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(np, synth, wg, wu, wd, x, hvec, step_bytes, args.cpu_seconds)
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (SplitMix64 seed 0, BASELINE.json config rules)",
+        "config": {"workload": "cfg2 decode FFN step, batch 1: Q8_K quantize x[2560] + Q4_K gate/up "
+                               "[9728,2560]x2 (one launch) + Q8_K quantize h[9728] + Q6_K down "
+                               "[2560,9728]",
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": step_bytes,
+                   "weight_copies_rotated": ws.copies, "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "latency": latency,
+        "configs": extra,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def cpu_baseline(np, synth, wg, wu, wd, x, hvec, step_bytes, budget_s):
+    """The reference's x86 kernels (oracle/_ref, compiled from its sources) on
+    this host's cores: Q8_K quantize + row dots with the reference pool's chunk
+    rule, rotating weight copies (>512 MB) like the GPU does."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle
+    orc = pyoracle.Oracle()
+    ref = pyoracle.load_ref()
+    kind = "reference" if ref is not None else "port"
+    threads = pyoracle.host_threads()
+    H, F = x.shape[1], hvec.shape[1]
+    gu = np.concatenate([wg, wu])
+    one = gu.nbytes + wd.nbytes
+    copies = max(1, -(-ROTATE_BYTES // one))
+    gus = [gu.copy() for _ in range(copies)]
+    wds = [wd.copy() for _ in range(copies)]
+    quant = (ref or orc).quantize_act
+    dot4 = ref.dot_fn_addr(12) if ref else orc.dot_fn_addr(12)
+    dot6 = ref.dot_fn_addr(14) if ref else orc.dot_fn_addr(14)
+    y1 = np.empty((1, 2 * F), np.float32)
+    y2 = np.empty((1, H), np.float32)
+
+    def step(i, nt):
+        xq = quant(12, x)
+        orc.matvec_q_fn(dot4, 12, gus[i % copies], xq, H, y1, nt)
+        hq = quant(14, hvec)
+        orc.matvec_q_fn(dot6, 14, wds[i % copies], hq, F, y2, nt)
+
+    res = {}
+    for nt in (threads, 1):
+        for i in range(2):
+            step(i, nt)
+        ts, i = [], 0
+        deadline = time.time() + (budget_s if nt == threads else budget_s / 3)
+        while len(ts) < 200:
+            t = time.perf_counter()
+            step(i, nt)
+            ts.append(time.perf_counter() - t)
+            i += 1
+            if len(ts) >= 5 and time.time() > deadline:
+                break
+        res[nt] = (statistics.median(ts), len(ts))
+    med, n = res[threads]
+    tier = ref.tier() if ref else "scalar port"
+    log(f"cpu baseline ({kind}, {threads} threads, {tier}): {med * 1e3:.2f} ms/step, "
+        f"{step_bytes / med / 1e9:.2f} GB/s; 1 thread {res[1][0] * 1e3:.2f} ms")
+    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"cfg2 FFN step (Q8_K quantize + Q4_K 2x[9728,2560] + Q6_K [2560,9728] row dots), "
+                      f"median of {n} steps over {copies} rotating weight copies, tier {tier}",
+            "ms_per_step": round(med * 1e3, 3),
+            "one_thread_gbs": round(step_bytes / res[1][0] / 1e9, 3)}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,193 @@
+/*
+ * qwen35_hip.h -- C ABI of the MI355X (gfx950) quantized matvec / MMQ backend.
+ *
+ * This is the only surface a host engine sees.  It mirrors the reference's
+ * device-kernel ABI (src/kernels/cuda/api.h) and its backend vtable slots for
+ * the quantized-matvec path (src/backend.zig:110-178), so that a
+ * backend_hip.zig can sit beside src/backend_cpu.zig: plain C types, device
+ * pointers as `void *`, the stream as `void *` (a hipStream_t; NULL = the
+ * default stream), no HIP or torch types in any signature.
+ *
+ * Conventions (as the reference, src/kernels/cuda/api.h:1-13):
+ *   - launchers return the numeric hipError_t as int, 0 = success;
+ *   - QHIP_DECLINE (-1) means "this path does not serve the request, use
+ *     another one" (src/kernels/cuda/mmq.cu:2242-2245) -- never a silent CPU
+ *     fallback; nothing in this library runs arithmetic on the host;
+ *   - invalid type ids, shapes that are not a multiple of the block size, NULL
+ *     buffers and out-of-range counts return hipErrorInvalidValue (1) before
+ *     anything is launched (src/kernels/cuda/mmvq.cu:781-785 pattern).
+ *
+ * Type ids are the GGUF TensorType numbers (src/gguf.zig TensorType,
+ * src/kernels/cuda/api.h:52-75).  Supported: Q8_0, Q4_K, Q6_K, IQ4_NL.
+ *
+ * Layouts (all little-endian, GGUF block formats, src/gguf.zig:168-207):
+ *   weight rows   rows x (cols / block_elems) blocks, rows contiguous
+ *   Q8_0 act      34 B per 32 values: f16 d, int8 qs[32]
+ *   Q8_K act      292 B per 256 values: f32 d, int8 qs[256], int16 bsums[16]
+ *   output        float out[t * rows + r] = W[r] . x_t
+ * Fast paths need 4-byte aligned weight and activation pointers, a weight
+ * byte size that is a multiple of 4, and cols a multiple of 64 (32-value
+ * types); other inputs take the byte-granular generic kernel.
+ */
+#ifndef QWEN35_HIP_H
+#define QWEN35_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QHIP_TT_Q8_0 8
+#define QHIP_TT_Q4_K 12
+#define QHIP_TT_Q6_K 14
+#define QHIP_TT_IQ4_NL 20
+
+#define QHIP_DECLINE (-1)
+
+/* Kernel path selection for qhip_launch_mul_mat. */
+#define QHIP_PATH_AUTO 0    /* GEMV for small token counts, MMQ above the crossover */
+#define QHIP_PATH_GEMV 1    /* weight-streaming GEMV, tokens share each weight load */
+#define QHIP_PATH_MMQ 2     /* int8 MFMA tiles; declines (QHIP_DECLINE) if unsupported */
+#define QHIP_PATH_GENERIC 3 /* byte-granular reference kernel, any alignment */
+
+/* ---- device probe ---------------------------------------------------------
+ * Replaces q35_gpu_cc / q35_gpu_sm_count / q35_gpu_name
+ * (src/kernels/cuda/api.h:35-37) and the device check in CudaBackend.init
+ * (src/backend_cuda.zig:1601-1625).  qhip_init makes `device` current for
+ * the calling thread and fails with a HIP error if it is not a gfx950 GPU. */
+int qhip_init(int device);
+int qhip_gpu_arch(void);          /* e.g. 950 for gfx950; -1 without a device */
+int qhip_gpu_cu_count(void);      /* compute units; 0 without a device */
+const char *qhip_gpu_name(void);  /* marketing name, "" without a device */
+const char *qhip_error_string(int err);
+
+/* ---- geometry (pure host code) --------------------------------------------
+ * q35_quant_act_block_elems / q35_quant_geom (src/kernels/cuda/api.h:444-449). */
+int qhip_quant_act_block_elems(int ttype); /* 32 (Q8_0 act), 256 (Q8_K act), 0 unknown */
+int qhip_quant_geom(int ttype, int *block_elems, int *block_bytes); /* 1 ok, 0 unknown */
+/* Bytes of one quantized activation row / one packed weight row; -1 if invalid. */
+long qhip_act_row_bytes(int ttype, int cols);
+long qhip_weight_row_bytes(int ttype, int cols);
+
+/* ---- activation quantization ----------------------------------------------
+ * q35_launch_quantize_q8_0 / q35_launch_quantize_q8_K
+ * (src/kernels/cuda/api.h:77-84), bit-exact with the CPU quantize_q8_0 /
+ * quantize_q8_K (src/kernels/x86/kernels32.c:1064-1087,
+ * kernels256.c:865-896).  `nblocks` counts 32- resp. 256-value blocks. */
+int qhip_launch_quantize_q8_0(const float *d_x, void *d_out, int nblocks, void *stream);
+int qhip_launch_quantize_q8_K(const float *d_x, void *d_out, int nblocks, void *stream);
+/* `tokens` rows of `cols` floats -> the activation family of `ttype`
+ * (backend_cpu.zig:42-50 actFamily), one quantized row per token. */
+int qhip_launch_quantize_act(int ttype, const float *d_x, void *d_out, int cols, int tokens,
+                             void *stream);
+
+/* ---- matvec -----------------------------------------------------------------
+ * q35_launch_mul_mat_vec (src/kernels/cuda/api.h:104-112):
+ *   out[t*rows + r] = W[r] . xq[t] for t < tokens.
+ * d_xq holds `tokens` rows quantized with the weight's activation family. */
+int qhip_launch_mul_mat_vec(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
+                            int tokens, int ttype, void *stream);
+/* q35_launch_mul_mat_vec_q8_0 (src/kernels/cuda/api.h:116-117). */
+int qhip_launch_mul_mat_vec_q8_0(const void *d_w, const void *d_xq, float *d_out, int rows,
+                                 int cols, int tokens, void *stream);
+/* Same contract with an explicit kernel path (QHIP_PATH_*); replaces the
+ * reference's env switches (QWEN35_CUDA_MMQ, src/kernels/cuda/mmvq.cu:553-586)
+ * with an argument. */
+int qhip_launch_mul_mat(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
+                        int tokens, int ttype, int path, void *stream);
+
+/* The GEMV with explicit launch shape: `lanes_per_row` in {1,2,4,...,64}
+ * lanes cooperate on one weight row, `tokens_per_pass` in {1,2,4,8} tokens
+ * share each weight load; 0 picks the default for either.  Replaces the
+ * reference's launch-shape env knobs (QWEN35_CUDA_COOP_WARPS / _SPLIT / _RPB,
+ * src/kernels/cuda/mmvq.cu:685-772) with arguments.  Returns QHIP_DECLINE
+ * when the fast-path preconditions do not hold. */
+int qhip_launch_gemv_tuned(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
+                           int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
+                           void *stream);
+
+/* ---- ragged prefill (no reference counterpart: the reference prefills one
+ * sequence per chunk, src/engine.zig:1371) -------------------------------------
+ * Sequence i owns packed tokens [offsets[i], offsets[i+1]); offsets has
+ * nseq+1 entries, offsets[0] = 0, offsets[nseq] = total_tokens.
+ *
+ * Packer: quantizes each sequence's f32 rows (d_src[i] -> lengths from the
+ * offset table) into the packed activation buffer, in one launch.  d_src is a
+ * DEVICE array of nseq device pointers; d_offsets is a device array. */
+int qhip_launch_quantize_ragged(int ttype, const float *const *d_src, const int *d_offsets,
+                                int nseq, int total_tokens, int cols, void *d_xq_packed,
+                                void *stream);
+/* Host helper: offsets[0..nseq] = prefix sums of lengths; returns the total,
+ * or -1 for a negative length or overflow. */
+int qhip_ragged_offsets(const int *lengths, int nseq, int *offsets);
+/* One launch over all sequences: out[p*rows + r] = W[r] . xq[p] for every
+ * packed token p; token tiles never straddle a sequence boundary. */
+int qhip_launch_mul_mat_ragged(const void *d_w, const void *d_xq_packed, float *d_out, int rows,
+                               int cols, const int *d_offsets, int nseq, int total_tokens,
+                               int ttype, void *stream);
+
+/* ---- parity export -----------------------------------------------------------
+ * Exact per-block integers through the same unit decode as the GEMV kernels:
+ * ints[(t*rows + r)*nints + i], nints = cols/block_elems, except Q4_K which
+ * stores (isum, summs) per super-block (nints = 2*cols/256).  The integers
+ * of src/kernels/x86/kernels32.c:447-464 / :342-361 and
+ * kernels256.c:474-498 / :720-738. */
+int qhip_launch_block_ints(const void *d_w, const void *d_xq, int32_t *d_ints, int rows, int cols,
+                           int tokens, int ttype, void *stream);
+
+/* ---- backend (mirror of the Exec vtable's quantized-matvec slots) -----------
+ * src/backend.zig:110-178.  A backend owns device copies of weights
+ * (loadLinear, backend.zig:115-119; upload as in backend_cuda.zig:3458),
+ * activation scratch (allocScratch/allocScratchK/freeScratch, :133-139) and
+ * Buf regions (allocBuf, :141-146).  All matvec inputs/outputs are device
+ * pointers (Buf), so consecutive ops never cross PCIe. */
+typedef struct qhip_backend qhip_backend;
+
+/* LinearW.quant (backend.zig:47-50, gguf.zig QuantRow:312-365): a resident,
+ * packed 2-D weight. */
+typedef struct qhip_linear {
+  const void *dev;  /* device bytes, GGUF block layout */
+  int ttype;
+  int rows;
+  int cols;
+  long row_bytes;
+} qhip_linear;
+
+qhip_backend *qhip_backend_create(int device, int *err);
+void qhip_backend_destroy(qhip_backend *be);
+/* name()/describe() (backend.zig:493-498) */
+const char *qhip_backend_name(const qhip_backend *be);
+/* Upload `rows` packed rows from host memory.  Weights are placed back to back
+ * in a device arena, so two consecutive loads of the same shape are adjacent
+ * (the condition matvecPair fuses on, backend_cuda.zig:3743-3794). */
+int qhip_backend_load_linear(qhip_backend *be, int ttype, int rows, int cols,
+                             const void *host_data, qhip_linear *out);
+/* Adopt weights already resident on this device (no copy, not freed). */
+int qhip_backend_wrap_linear(qhip_backend *be, int ttype, int rows, int cols, const void *d_data,
+                             qhip_linear *out);
+void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
+int qhip_backend_alloc_scratch(qhip_backend *be, int max_cols);
+int qhip_backend_alloc_scratch_k(qhip_backend *be, int max_cols, int k);
+void qhip_backend_free_scratch(qhip_backend *be);
+/* allocBuf: `len` floats of device memory owned by the backend until
+ * free_scratch / destroy. */
+int qhip_backend_alloc_buf(qhip_backend *be, size_t len, float **d_out);
+/* matvec (backend.zig:153-158): d_out[rows] = W . d_x[cols] (f32 in, f32 out). */
+int qhip_backend_matvec(qhip_backend *be, float *d_out, const qhip_linear *w, const float *d_x);
+/* matvecPair (backend.zig:159-176): out[0..r) = A.x, out[r..2r) = B.x; one
+ * quantization and one launch when A and B are adjacent and alike, else two. */
+int qhip_backend_matvec_pair(qhip_backend *be, float *d_out, const qhip_linear *a,
+                             const qhip_linear *b, const float *d_x);
+/* matvecBatchK (backend.zig:177-178): out[j*rows + r] = W[r] . x_j, j < k. */
+int qhip_backend_matvec_batch_k(qhip_backend *be, float *d_out, const qhip_linear *w,
+                                const float *d_xK, int k);
+/* Stream for subsequent calls (NULL = default stream) and a host wait. */
+int qhip_backend_set_stream(qhip_backend *be, void *stream);
+int qhip_backend_sync(qhip_backend *be);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN35_HIP_H */

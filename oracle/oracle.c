@@ -1,0 +1,455 @@
+/*
+ * oracle.c -- CPU restatement of the reference's quantized matvec arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY: used by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py as the checker.  The shipped HIP library never
+ * links or calls it.  Each function cites the reference file:line it follows
+ * (paths relative to the reference repository).
+ *
+ * Built with -ffp-contract=off so every float expression rounds exactly as
+ * written (no fused multiply-add), matching the reference's one-operation-
+ * per-rounding statements.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* IQ4_NL codebook, reference src/iq_tables.zig:429-432 (ggml-common.h values). */
+static const int8_t orc_iq4nl_values[16] = {
+    -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113,
+};
+
+static uint16_t ld16(const uint8_t *p) { return (uint16_t)(p[0] | ((unsigned)p[1] << 8)); }
+static float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+/* IEEE binary16 -> binary32, exact; follows kernels32.c:45-66, including its
+ * choice to return +0.0 for both signed zeros. */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t ex = ((uint32_t)h >> 10) & 31u;
+    uint32_t mant = (uint32_t)h & 1023u;
+    if (ex == 0) {
+        if (mant == 0) return 0.0f;
+        /* subnormal: shift the leading one up to bit 10 */
+        int sh = 0;
+        while (!(mant & 1024u)) { mant <<= 1; ++sh; }
+        return bits_f32(sign | ((uint32_t)(113 - sh) << 23) | ((mant & 1023u) << 13));
+    }
+    if (ex == 31) return bits_f32(sign | 0x7F800000u | (mant << 13));
+    return bits_f32(sign | ((ex + 112u) << 23) | (mant << 13));
+}
+
+/* Same decode as kernels256.c:51-78, which keeps the sign of zero. */
+float orc_f16_to_f32_k256(uint16_t h) {
+    if ((h & 0x7FFFu) == 0) return (h & 0x8000u) ? -0.0f : 0.0f;
+    return orc_f16_to_f32(h);
+}
+
+/* binary32 -> binary16 bits, round to nearest even; follows kernels32.c:67-98.
+ * Quirks kept on purpose because they are the reference's behaviour:
+ *   NaN maps to infinity (sign kept);
+ *   a value that rounds up out of the subnormal range (to 2^-14) yields the
+ *   bit pattern 0x0380, not 0x0400 (kernels32.c:96). */
+uint16_t orc_f32_to_f16(float x) {
+    uint32_t u = f32_bits(x);
+    uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    uint32_t ex = (u >> 23) & 255u;
+    uint32_t mant = u & 0x7FFFFFu;
+    if (ex == 255u || ex >= 143u) return (uint16_t)(sign | 0x7C00u);
+    if (ex >= 113u) {
+        uint32_t m10 = mant >> 13, rest = mant & 0x1FFFu;
+        if (rest > 0x1000u || (rest == 0x1000u && (m10 & 1u))) ++m10;
+        uint32_t e16 = ex - 112u;
+        if (m10 == 1024u) { m10 = 0; ++e16; }
+        if (e16 >= 31u) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | (e16 << 10) | m10);
+    }
+    int shift = 126 - (int)ex; /* 14..126 */
+    if (shift >= 25) return sign;
+    uint32_t full = mant | 0x800000u;
+    uint32_t m10 = full >> shift;
+    uint32_t rest = full & ((1u << shift) - 1u), half = 1u << (shift - 1);
+    if (rest > half || (rest == half && (m10 & 1u))) ++m10;
+    if (m10 >= 1024u) return (uint16_t)(sign | 0x0380u);
+    return (uint16_t)(sign | m10);
+}
+
+/* x86 cvttss2si: truncation, and INT_MIN for NaN / out-of-range.  The
+ * reference's (int) casts run through it; stating it keeps non-finite inputs
+ * defined here. */
+static int32_t trunc_to_i32_x86(float v) {
+    if (!(v > -2147483904.0f && v < 2147483648.0f)) return INT32_MIN;
+    return (int32_t)v;
+}
+
+/* kernels32.c:1064-1087 */
+void orc_quantize_q8_0(int n, const float *x, uint8_t *out) {
+    for (int b = 0; b < n / 32; ++b) {
+        const float *xb = x + 32 * b;
+        uint8_t *ob = out + 34 * b;
+        float amax = 0.0f;
+        for (int i = 0; i < 32; ++i) {
+            float a = xb[i] < 0.0f ? -xb[i] : xb[i];
+            if (a > amax) amax = a;
+        }
+        float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        float inv = amax > 0.0f ? 1.0f / scale : 0.0f;
+        uint16_t hb = orc_f32_to_f16(scale);
+        ob[0] = (uint8_t)hb;
+        ob[1] = (uint8_t)(hb >> 8);
+        for (int i = 0; i < 32; ++i) {
+            float v = xb[i] * inv;
+            float r = v + (v >= 0.0f ? 0.5f : -0.5f);
+            int32_t q = trunc_to_i32_x86(r);
+            if (q > 127) q = 127;
+            if (q < -128) q = -128;
+            ob[2 + i] = (uint8_t)(int8_t)q;
+        }
+    }
+}
+
+/* kernels256.c:865-896 (clamp to [-127,127] per :886-888, NaN -> 127). */
+void orc_quantize_q8_K(int n, const float *x, uint8_t *out) {
+    for (int b = 0; b < n / 256; ++b) {
+        const float *xb = x + 256 * b;
+        uint8_t *ob = out + 292 * b;
+        float amax = 0.0f;
+        for (int i = 0; i < 256; ++i) {
+            float a = xb[i] < 0.0f ? -xb[i] : xb[i];
+            if (a > amax) amax = a;
+        }
+        float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        float inv = amax > 0.0f ? 1.0f / scale : 0.0f;
+        memcpy(ob, &scale, 4);
+        int16_t sums[16] = {0};
+        for (int i = 0; i < 256; ++i) {
+            float r = roundf(xb[i] * inv);
+            if (r < -127.0f) r = -127.0f;
+            if (r > 127.0f) r = 127.0f;
+            if (!(r >= -127.0f)) r = 127.0f;
+            int8_t q = (int8_t)(int32_t)r;
+            ob[4 + i] = (uint8_t)q;
+            sums[i / 16] = (int16_t)(sums[i / 16] + q);
+        }
+        memcpy(ob + 260, sums, 32);
+    }
+}
+
+/* ---- exact per-block integers ------------------------------------------ */
+
+/* kernels32.c:447-464: sum_j w[2+j]*a[2+j] over 32 int8 pairs. */
+int32_t orc_blk_q8_0(const uint8_t *w, const uint8_t *a) {
+    int32_t s = 0;
+    for (int j = 0; j < 32; ++j) s += (int32_t)(int8_t)w[2 + j] * (int8_t)a[2 + j];
+    return s;
+}
+
+/* kernels32.c:342-361: low nibble of qs[j] pairs with a[j], high with a[j+16]. */
+int32_t orc_blk_iq4_nl(const uint8_t *w, const uint8_t *a) {
+    int32_t s = 0;
+    for (int j = 0; j < 16; ++j) {
+        s += orc_iq4nl_values[w[2 + j] & 15] * (int32_t)(int8_t)a[2 + j];
+        s += orc_iq4nl_values[w[2 + j] >> 4] * (int32_t)(int8_t)a[18 + j];
+    }
+    return s;
+}
+
+/* 6-bit scale / min of sub-block sb (0..7) from the 12 packed bytes; the
+ * ggml get_scale_min_k4 rule, equal to kernels256.c:105-125 (sm[sb] / sm[8+sb]). */
+static void q4k_scale_min(const uint8_t *s12, int sb, int *sc, int *mn) {
+    if (sb < 4) {
+        *sc = s12[sb] & 63;
+        *mn = s12[sb + 4] & 63;
+    } else {
+        *sc = (s12[sb + 4] & 15) | ((s12[sb - 4] >> 6) << 4);
+        *mn = (s12[sb + 4] >> 4) | ((s12[sb] >> 6) << 4);
+    }
+}
+
+/* kernels256.c:474-498 with :179-186 (nibble layout) and :216-226 (dot256):
+ *   isum  = sum_g sc[g/2] * sum_{l<16} nib[16g+l] * q8[16g+l]
+ *   summs = sum_{j<16} bsum[j] * min[j/2]                                   */
+void orc_blk_q4_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs) {
+    const uint8_t *qs = w + 16;
+    const int8_t *q8 = (const int8_t *)(a + 4);
+    int32_t is = 0, sm = 0;
+    for (int sb = 0; sb < 8; ++sb) {
+        int sc, mn;
+        q4k_scale_min(w + 4, sb, &sc, &mn);
+        int c = sb / 2, hi = sb & 1;
+        int32_t sub = 0;
+        for (int l = 0; l < 32; ++l) {
+            int nib = hi ? (qs[32 * c + l] >> 4) : (qs[32 * c + l] & 15);
+            sub += nib * (int32_t)q8[32 * sb + l];
+        }
+        is += sc * sub;
+        for (int t = 0; t < 2; ++t) {
+            int16_t bs;
+            memcpy(&bs, a + 260 + 2 * (2 * sb + t), 2);
+            sm += (int32_t)bs * mn;
+        }
+    }
+    *isum = is;
+    *summs = sm;
+}
+
+/* kernels256.c:200-212 (value layout) and :720-738:
+ *   isum = sum_g sc[g] * sum_{l<16} (q6[16g+l] - 32) * q8[16g+l]              */
+int32_t orc_blk_q6_k(const uint8_t *w, const uint8_t *a) {
+    const uint8_t *ql = w, *qh = w + 128;
+    const int8_t *sc = (const int8_t *)(w + 192);
+    const int8_t *q8 = (const int8_t *)(a + 4);
+    int32_t isum = 0;
+    for (int g = 0; g < 16; ++g) {
+        int32_t sub = 0;
+        for (int l16 = 0; l16 < 16; ++l16) {
+            int e = 16 * g + l16;
+            int h = e / 128, q = (e % 128) / 32, l = e % 32;
+            int lowbits = (q & 1) ? ql[64 * h + 32 + l] : ql[64 * h + l];
+            lowbits = (q >= 2) ? (lowbits >> 4) : (lowbits & 15);
+            int highbits = (qh[32 * h + l] >> (2 * q)) & 3;
+            sub += ((lowbits | (highbits << 4)) - 32) * (int32_t)q8[e];
+        }
+        isum += sc[g] * sub;
+    }
+    return isum;
+}
+
+/* ---- geometry ------------------------------------------------------------ */
+
+int orc_geom(int ttype, int *be, int *bb) {
+    switch (ttype) {
+    case ORC_TT_Q8_0: *be = 32; *bb = 34; return 1;
+    case ORC_TT_IQ4_NL: *be = 32; *bb = 18; return 1;
+    case ORC_TT_Q4_K: *be = 256; *bb = 144; return 1;
+    case ORC_TT_Q6_K: *be = 256; *bb = 210; return 1;
+    default: return 0;
+    }
+}
+
+/* backend_cpu.zig:42-50 (actFamily): 32-element types take Q8_0, the rest Q8_K. */
+int orc_act_block_elems(int ttype) {
+    int be, bb;
+    if (!orc_geom(ttype, &be, &bb)) return 0;
+    return be == 32 ? 32 : 256;
+}
+
+long orc_act_bytes(int ttype, int cols) {
+    int ab = orc_act_block_elems(ttype);
+    if (!ab || cols <= 0 || cols % ab) return -1;
+    return ab == 32 ? (long)cols / 32 * 34 : (long)cols / 256 * 292;
+}
+
+long orc_row_bytes(int ttype, int cols) {
+    int be, bb;
+    if (!orc_geom(ttype, &be, &bb) || cols <= 0 || cols % be) return -1;
+    if (orc_act_bytes(ttype, cols) < 0) return -1;
+    return (long)cols / be * bb;
+}
+
+/* ---- row dots ------------------------------------------------------------ */
+
+static float dot_q8_0(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 32; ++b, w += 34, a += 34) {
+        float dx = orc_f16_to_f32(ld16(w)), dy = orc_f16_to_f32(ld16(a));
+        sumf += dx * dy * (float)orc_blk_q8_0(w, a);
+    }
+    return sumf;
+}
+
+static float dot_iq4_nl(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 32; ++b, w += 18, a += 34) {
+        float dx = orc_f16_to_f32(ld16(w)), dy = orc_f16_to_f32(ld16(a));
+        sumf += dx * dy * (float)orc_blk_iq4_nl(w, a);
+    }
+    return sumf;
+}
+
+static float dot_q4_k(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 144, a += 292) {
+        int32_t isum, summs;
+        orc_blk_q4_k(w, a, &isum, &summs);
+        float dy;
+        memcpy(&dy, a, 4);
+        float d = dy * orc_f16_to_f32_k256(ld16(w));
+        float dmin = dy * orc_f16_to_f32_k256(ld16(w + 2));
+        sumf += d * (float)isum - dmin * (float)summs;
+    }
+    return sumf;
+}
+
+static float dot_q6_k(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 210, a += 292) {
+        float dy;
+        memcpy(&dy, a, 4);
+        sumf += orc_f16_to_f32_k256(ld16(w + 208)) * dy * (float)orc_blk_q6_k(w, a);
+    }
+    return sumf;
+}
+
+orc_dot_fn orc_dot_fn_for(int ttype) {
+    switch (ttype) {
+    case ORC_TT_Q8_0: return dot_q8_0;
+    case ORC_TT_IQ4_NL: return dot_iq4_nl;
+    case ORC_TT_Q4_K: return dot_q4_k;
+    case ORC_TT_Q6_K: return dot_q6_k;
+    default: return 0;
+    }
+}
+
+orc_quant_fn orc_quant_fn_for(int ttype) {
+    int ab = orc_act_block_elems(ttype);
+    return ab == 32 ? orc_quantize_q8_0 : ab == 256 ? orc_quantize_q8_K : 0;
+}
+
+float orc_dot(int ttype, int n, const void *w, const void *a) {
+    orc_dot_fn f = orc_dot_fn_for(ttype);
+    return f ? f(n, w, a) : NAN;
+}
+
+int orc_row_block_ints(int ttype, int n, const void *vw, const void *va, int32_t *out) {
+    const uint8_t *w = vw, *a = va;
+    int be, bb;
+    if (!orc_geom(ttype, &be, &bb) || n % be) return -1;
+    int nb = n / be;
+    for (int b = 0; b < nb; ++b) {
+        switch (ttype) {
+        case ORC_TT_Q8_0: out[b] = orc_blk_q8_0(w + 34 * b, a + 34 * b); break;
+        case ORC_TT_IQ4_NL: out[b] = orc_blk_iq4_nl(w + 18 * b, a + 34 * b); break;
+        case ORC_TT_Q4_K: orc_blk_q4_k(w + 144 * b, a + 292 * b, &out[2 * b], &out[2 * b + 1]); break;
+        case ORC_TT_Q6_K: out[b] = orc_blk_q6_k(w + 210 * b, a + 292 * b); break;
+        }
+    }
+    return ttype == ORC_TT_Q4_K ? 2 * nb : nb;
+}
+
+int orc_quantize_act(int ttype, int cols, const float *x, uint8_t *out) {
+    orc_quant_fn q = orc_quant_fn_for(ttype);
+    if (!q || orc_act_bytes(ttype, cols) < 0) return -1;
+    q(cols, x, out);
+    return 0;
+}
+
+/* ---- matvec drivers ------------------------------------------------------ */
+
+/* pool.zig:468-550 chunk rule: ~4 chunks per thread, clamped to [16, 256];
+ * serial below 256 virtual rows (pool.zig:292-295). */
+static int chunk_rows(long vrows, int nthreads) {
+    long c = vrows / (4L * nthreads);
+    if (c < 16) c = 16;
+    if (c > 256) c = 256;
+    return (int)c;
+}
+
+int orc_matvec_q_fn(orc_dot_fn dot, int ttype, int rows, int cols, int k,
+                    const void *vw, const uint8_t *act, float *out, int nthreads) {
+    long rb = orc_row_bytes(ttype, cols), ab = orc_act_bytes(ttype, cols);
+    if (!dot || rb < 0 || ab < 0 || rows <= 0 || k <= 0) return -1;
+    const uint8_t *w = vw;
+    long vrows = (long)rows * k;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads == 1 || vrows < 256) {
+        for (long r = 0; r < vrows; ++r) {
+            long t = r / rows, rr = r % rows;
+            out[t * rows + rr] = dot(cols, w + rr * rb, act + t * ab);
+        }
+        return 0;
+    }
+    int chunk = chunk_rows(vrows, nthreads);
+#pragma omp parallel for num_threads(nthreads) schedule(dynamic, 1)
+    for (long c0 = 0; c0 < vrows; c0 += chunk) {
+        long c1 = c0 + chunk < vrows ? c0 + chunk : vrows;
+        for (long r = c0; r < c1; ++r) {
+            long t = r / rows, rr = r % rows;
+            out[t * rows + rr] = dot(cols, w + rr * rb, act + t * ab);
+        }
+    }
+    return 0;
+}
+
+int orc_matvec_batch_fn(orc_dot_fn dot, orc_quant_fn quant, int ttype, int rows,
+                        int cols, int k, const void *w, const float *x, float *out,
+                        uint8_t *act, int nthreads) {
+    long ab = orc_act_bytes(ttype, cols);
+    if (!quant || ab < 0 || k <= 0) return -1;
+    for (int t = 0; t < k; ++t) quant(cols, x + (long)t * cols, act + t * ab);
+    return orc_matvec_q_fn(dot, ttype, rows, cols, k, w, act, out, nthreads);
+}
+
+int orc_matvec_batch(int ttype, int rows, int cols, int k, const void *w,
+                     const float *x, float *out, int nthreads) {
+    long ab = orc_act_bytes(ttype, cols);
+    if (ab < 0 || k <= 0) return -1;
+    uint8_t *act = malloc((size_t)ab * k);
+    if (!act) return -1;
+    int rc = orc_matvec_batch_fn(orc_dot_fn_for(ttype), orc_quant_fn_for(ttype), ttype,
+                                 rows, cols, k, w, x, out, act, nthreads);
+    free(act);
+    return rc;
+}
+
+/* ---- dequantization (fixture semantics) --------------------------------- */
+
+/* quant_dequant.zig:1388-1402 (Q8_0), :347-360 (IQ4_NL), :54-77 (Q4_K),
+ * :222-251 (Q6_K). */
+int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
+    const uint8_t *w = vw;
+    if (orc_row_bytes(ttype, cols) < 0) return -1;
+    if (ttype == ORC_TT_Q8_0 || ttype == ORC_TT_IQ4_NL) {
+        int bb = ttype == ORC_TT_Q8_0 ? 34 : 18;
+        for (int b = 0; b < cols / 32; ++b) {
+            const uint8_t *blk = w + bb * b;
+            float d = orc_f16_to_f32(ld16(blk));
+            for (int j = 0; j < 32; ++j) {
+                int v;
+                if (ttype == ORC_TT_Q8_0) v = (int8_t)blk[2 + j];
+                else v = orc_iq4nl_values[j < 16 ? (blk[2 + j] & 15) : (blk[2 + j - 16] >> 4)];
+                out[32 * b + j] = d * (float)v;
+            }
+        }
+        return 0;
+    }
+    for (int b = 0; b < cols / 256; ++b) {
+        float *o = out + 256 * b;
+        if (ttype == ORC_TT_Q4_K) {
+            const uint8_t *blk = w + 144 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk)), mn = orc_f16_to_f32_k256(ld16(blk + 2));
+            for (int sb = 0; sb < 8; ++sb) {
+                int sc, m;
+                q4k_scale_min(blk + 4, sb, &sc, &m);
+                float d1 = d * (float)sc, m1 = mn * (float)m;
+                for (int l = 0; l < 32; ++l) {
+                    uint8_t q = blk[16 + 32 * (sb / 2) + l];
+                    int nib = (sb & 1) ? (q >> 4) : (q & 15);
+                    o[32 * sb + l] = d1 * (float)nib - m1;
+                }
+            }
+        } else {
+            const uint8_t *blk = w + 210 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk + 208));
+            const int8_t *sc = (const int8_t *)(blk + 192);
+            for (int e = 0; e < 256; ++e) {
+                int h = e / 128, q = (e % 128) / 32, l = e % 32;
+                int lo = (q & 1) ? blk[64 * h + 32 + l] : blk[64 * h + l];
+                lo = (q >= 2) ? (lo >> 4) : (lo & 15);
+                int hb = (blk[128 + 32 * h + l] >> (2 * q)) & 3;
+                o[e] = d * (float)sc[e / 16] * (float)((lo | (hb << 4)) - 32);
+            }
+        }
+    }
+    return 0;
+}

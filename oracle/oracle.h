@@ -1,0 +1,102 @@
+/*
+ * oracle.h -- CPU restatement of the reference's quantized matvec path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the shipped library links, loads or
+ * calls this code.  It exists so that tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py can check the HIP kernels against the
+ * reference's arithmetic, and time that arithmetic on the host.
+ *
+ * What it restates (paths relative to the reference repository):
+ *   f16 <-> f32            src/kernels/x86/kernels32.c:45-98, kernels256.c:51-78
+ *   quantize_q8_0          src/kernels/x86/kernels32.c:1064-1087
+ *   quantize_q8_K          src/kernels/x86/kernels256.c:865-896
+ *   Q8_0 x Q8_0            src/kernels/x86/kernels32.c:447-464, kernels512.c:53-81
+ *   IQ4_NL x Q8_0          src/kernels/x86/kernels32.c:342-361 (+ iq_tables.zig:429-432)
+ *   Q4_K x Q8_K            src/kernels/x86/kernels256.c:105-125, :179-186, :474-498
+ *   Q6_K x Q8_K            src/kernels/x86/kernels256.c:200-212, :720-738
+ *   matvec / batch driver  src/backend_cpu.zig:167-289, :328-446; src/pool.zig:300-336, :468-550
+ *   dequant (fixtures)     src/quant_dequant.zig:54-77, :222-251, :347-360, :1388-1402
+ *
+ * Float results follow the scalar / AVX-512-VNNI tier order (one sequential
+ * per-block fold).  The reference's AVX2 tier folds Q4_K/Q6_K with 8-lane
+ * FMA; integers are identical on every tier, floats are compared with a
+ * tolerance.
+ */
+#ifndef QWEN35_ORACLE_H
+#define QWEN35_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* gguf TensorType ids (reference src/gguf.zig TensorType, src/kernels/cuda/api.h:52-75) */
+#define ORC_TT_Q8_0   8
+#define ORC_TT_Q4_K  12
+#define ORC_TT_Q6_K  14
+#define ORC_TT_IQ4_NL 20
+
+float    orc_f16_to_f32(uint16_t h);        /* kernels32.c:45-66 (+0 for -0)  */
+float    orc_f16_to_f32_k256(uint16_t h);   /* kernels256.c:51-78 (keeps -0) */
+uint16_t orc_f32_to_f16(float x);           /* kernels32.c:67-98, RNE, NaN->inf */
+
+void orc_quantize_q8_0(int n, const float *x, uint8_t *out);
+void orc_quantize_q8_K(int n, const float *x, uint8_t *out);
+
+/* Exact per-block integers. */
+int32_t orc_blk_q8_0(const uint8_t *w, const uint8_t *a);
+int32_t orc_blk_iq4_nl(const uint8_t *w, const uint8_t *a);
+void    orc_blk_q4_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs);
+int32_t orc_blk_q6_k(const uint8_t *w, const uint8_t *a);
+
+/* Geometry: returns 1 and fills the outputs for a supported type, else 0. */
+int orc_geom(int ttype, int *block_elems, int *block_bytes);
+/* 32 (Q8_0 activation) or 256 (Q8_K activation); 0 for an unknown type. */
+int orc_act_block_elems(int ttype);
+/* Bytes of one quantized activation row of `cols` values; -1 on bad input. */
+long orc_act_bytes(int ttype, int cols);
+/* Bytes of one packed weight row; -1 on bad input. */
+long orc_row_bytes(int ttype, int cols);
+
+/* One weight row against one quantized activation row (n = cols). */
+float orc_dot(int ttype, int n, const void *w, const void *a);
+
+/* Per-block integers of one row.  Q8_0 / IQ4_NL / Q6_K write n/block ints;
+ * Q4_K writes 2 per super-block: isum then summs.  Returns ints written, or -1. */
+int orc_row_block_ints(int ttype, int n, const void *w, const void *a, int32_t *out);
+
+/* Quantize one f32 row with the type's activation family. 0 on success. */
+int orc_quantize_act(int ttype, int cols, const float *x, uint8_t *out);
+
+/* out[t*rows + r] = W[r] . x_t for k tokens (x is [k, cols] f32).
+ * Quantizes each token once, then row-parallel dots over `nthreads` threads
+ * with the reference pool's chunk rule.  Returns 0 on success. */
+int orc_matvec_batch(int ttype, int rows, int cols, int k, const void *w,
+                     const float *x, float *out, int nthreads);
+
+/* Same driver over caller-supplied C functions with the reference's own
+ * signatures: dot = float(int n, const void*, const void*),
+ * quant = void(int n, const float*, uint8_t*).  Used to time the compiled
+ * reference kernels with the same threading as the restatement. */
+typedef float (*orc_dot_fn)(int n, const void *w, const void *a);
+typedef void (*orc_quant_fn)(int n, const float *x, uint8_t *out);
+int orc_matvec_batch_fn(orc_dot_fn dot, orc_quant_fn quant, int ttype, int rows,
+                        int cols, int k, const void *w, const float *x, float *out,
+                        uint8_t *act_scratch, int nthreads);
+
+/* Dot phase only (activations already quantized, [k, act_bytes]). */
+int orc_matvec_q_fn(orc_dot_fn dot, int ttype, int rows, int cols, int k,
+                    const void *w, const uint8_t *act, float *out, int nthreads);
+
+/* Dequantize one packed row into cols floats (fixture semantics). */
+int orc_dequant_row(int ttype, int cols, const void *w, float *out);
+
+/* Function pointers of the restated dots/quantizers, for orc_matvec_batch_fn. */
+orc_dot_fn   orc_dot_fn_for(int ttype);
+orc_quant_fn orc_quant_fn_for(int ttype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,349 @@
+// api.hip -- extern "C" entry points of include/qwen35_hip.h: argument
+// validation, path dispatch and the ragged packer.  No arithmetic on the
+// host: every result comes from a kernel in this library.
+#include "../../include/qwen35_hip.h"
+#include "qhip_device.hpp"
+#include "qhip_internal.hpp"
+
+#include <climits>
+#include <cstdio>
+#include <cstring>
+
+namespace qhip {
+
+static bool geom(int ttype, int& be, int& bb) {
+  switch (ttype) {
+    case TT_Q8_0: be = 32; bb = 34; return true;
+    case TT_IQ4_NL: be = 32; bb = 18; return true;
+    case TT_Q4_K: be = 256; bb = 144; return true;
+    case TT_Q6_K: be = 256; bb = 210; return true;
+    default: return false;
+  }
+}
+
+static int act_elems(int ttype) {
+  int be, bb;
+  if (!geom(ttype, be, bb)) return 0;
+  return be == 32 ? 32 : 256;
+}
+
+static long act_row_bytes(int ttype, int cols) {
+  const int ab = act_elems(ttype);
+  if (!ab || cols <= 0 || cols % ab) return -1;
+  return ab == 32 ? (long)cols / 32 * 34 : (long)cols / 256 * 292;
+}
+
+static long weight_row_bytes(int ttype, int cols) {
+  int be, bb;
+  if (!geom(ttype, be, bb) || cols <= 0 || cols % be) return -1;
+  if (act_row_bytes(ttype, cols) < 0) return -1;
+  return (long)cols / be * bb;
+}
+
+static bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
+
+// Preconditions of the unit-decode kernels (see qhip_device.hpp): every load
+// is a dword-aligned access inside the unit's own bytes, which requires
+// 4-byte aligned bases, whole 64-value units, and (Q6_K, whose d is read as
+// an aligned dword) a total weight size that is a multiple of 4.
+static bool fast_ok(const GemvArgs& g) {
+  if (!aligned4(g.w) || !aligned4(g.xq)) return false;
+  if (g.cols % 64) return false;
+  if (((long)g.rows * g.row_bytes) % 4) return false;
+  return true;
+}
+
+static hipError_t make_args(const void* w, const void* xq, float* out, int rows, int cols,
+                            int tokens, int ttype, GemvArgs& g) {
+  if (!w || !xq || !out || rows < 0 || tokens < 0) return hipErrorInvalidValue;
+  const long rb = weight_row_bytes(ttype, cols);
+  const long ab = act_row_bytes(ttype, cols);
+  if (rb < 0 || ab < 0) return hipErrorInvalidValue;
+  if ((long)tokens > 65535L * 64) return hipErrorInvalidValue;
+  g = GemvArgs{ttype, w, xq, out, rows, cols, tokens, rb, ab};
+  return hipSuccess;
+}
+
+// Token count above which the MMQ tiles beat the weight-streaming GEMV
+// (measured crossover; the GEMV re-reads weights once per 8 tokens).
+static int mmq_min_tokens(int /*ttype*/) { return 1 << 30; }
+
+hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
+  if (g.rows == 0 || g.tokens == 0) return hipSuccess;
+  const bool fast = fast_ok(g);
+  switch (path) {
+    case QHIP_PATH_GENERIC: return launch_gemv_generic(g, s);
+    case QHIP_PATH_GEMV: return fast ? launch_gemv(g, 0, 0, s) : launch_gemv_generic(g, s);
+    case QHIP_PATH_MMQ: return (hipError_t)QHIP_DECLINE;
+    case QHIP_PATH_AUTO:
+      if (!fast) return launch_gemv_generic(g, s);
+      if (g.tokens >= mmq_min_tokens(g.ttype)) {
+        // MMQ path (declines fall through to the GEMV)
+      }
+      return launch_gemv(g, 0, 0, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// ---- ragged packer: one launch quantizes every sequence into the packed buffer
+// Grid: x = blocks of a token row, y = packed token.  The owning sequence of
+// packed token p is found by binary search over the offset table.
+__device__ __forceinline__ int find_seq(const int* __restrict__ off, int nseq, int p) {
+  int lo = 0, hi = nseq;  // off[lo] <= p < off[hi]
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (off[mid] <= p) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(256) void k_quantize_ragged_q8_0(const float* const* __restrict__ src,
+                                                              const int* __restrict__ off, int nseq,
+                                                              uint8_t* __restrict__ out, long nblocks,
+                                                              long cols, long out_stride) {
+  const long b = ((long)blockIdx.x * 256 + threadIdx.x) >> 5;
+  const int i = threadIdx.x & 31;
+  const int p = blockIdx.y;
+  const int sq = find_seq(off, nseq, p);
+  const float* x = src[sq] + (long)(p - off[sq]) * cols;
+  const bool ok = b < nblocks;
+  const float v = ok ? x[32 * b + i] : 0.0f;
+  float a = v < 0.0f ? -v : v;
+  a = a > 0.0f ? a : 0.0f;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+  const float scale = a > 0.0f ? a / 127.0f : 1.0f;
+  const float inv = a > 0.0f ? 1.0f / scale : 0.0f;
+  const float sv = v * inv;
+  const float r = sv + (sv >= 0.0f ? 0.5f : -0.5f);
+  int q = trunc_i32_x86(r);
+  q = q > 127 ? 127 : (q < -128 ? -128 : q);
+  if (ok) {
+    uint8_t* ob = out + (long)p * out_stride + 34 * b;
+    ob[2 + i] = (uint8_t)(int8_t)q;
+    if (i == 0) {
+      const uint32_t hb = f32_to_f16_bits(scale);
+      ob[0] = (uint8_t)hb;
+      ob[1] = (uint8_t)(hb >> 8);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_quantize_ragged_q8_K(const float* const* __restrict__ src,
+                                                              const int* __restrict__ off, int nseq,
+                                                              uint8_t* __restrict__ out, long nblocks,
+                                                              long cols, long out_stride) {
+  const long b = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
+  const int p = blockIdx.y;
+  const int sq = find_seq(off, nseq, p);
+  const float* x = src[sq] + (long)(p - off[sq]) * cols;
+  const bool ok = b < nblocks;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = ok ? x[256 * b + 4 * l + i] : 0.0f;
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float e = v[i] < 0.0f ? -v[i] : v[i];
+    a = fmaxf(a, e > 0.0f ? e : 0.0f);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+  const float scale = a > 0.0f ? a / 127.0f : 1.0f;
+  const float inv = a > 0.0f ? 1.0f / scale : 0.0f;
+  uint32_t packed = 0;
+  int gsum = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float r = roundf(v[i] * inv);
+    r = r < -127.0f ? -127.0f : r;
+    r = r > 127.0f ? 127.0f : r;
+    r = (r >= -127.0f) ? r : 127.0f;
+    const int q = (int)r;
+    packed |= ((uint32_t)q & 0xFFu) << (8 * i);
+    gsum += q;
+  }
+  gsum += __shfl_xor(gsum, 1, 64);
+  gsum += __shfl_xor(gsum, 2, 64);
+  if (ok) {
+    uint8_t* ob = out + (long)p * out_stride + 292 * b;
+    *(uint32_t*)(ob + 4 + 4 * l) = packed;
+    if ((l & 3) == 0) *(int16_t*)(ob + 260 + 2 * (l >> 2)) = (int16_t)gsum;
+    if (l == 0) *(float*)ob = scale;
+  }
+}
+
+}  // namespace qhip
+
+using namespace qhip;
+
+static hipStream_t S(void* s) { return (hipStream_t)s; }
+
+// ---- probe ----------------------------------------------------------------------
+
+static int g_arch = -2, g_cus = 0;
+static char g_name[256] = "";
+
+static void probe() {
+  if (g_arch != -2) return;
+  int dev = 0;
+  hipDeviceProp_t p;
+  if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&p, dev) != hipSuccess) {
+    g_arch = -1;
+    return;
+  }
+  int num = 0;
+  const char* a = p.gcnArchName;
+  if (a && !strncmp(a, "gfx", 3)) num = (int)strtol(a + 3, nullptr, 10);
+  g_arch = num;
+  g_cus = p.multiProcessorCount;
+  snprintf(g_name, sizeof g_name, "%s (%s)", p.name, a ? a : "?");
+}
+
+extern "C" {
+
+int qhip_init(int device) {
+  hipError_t e = hipSetDevice(device);
+  if (e != hipSuccess) return (int)e;
+  g_arch = -2;
+  probe();
+  if (g_arch != 950) {
+    fprintf(stderr, "qwen35_hip: device %d is %s, this library is built for gfx950 only\n",
+            device, g_name);
+    return (int)hipErrorInvalidDevice;
+  }
+  return 0;
+}
+
+int qhip_gpu_arch(void) { probe(); return g_arch; }
+int qhip_gpu_cu_count(void) { probe(); return g_cus; }
+const char* qhip_gpu_name(void) { probe(); return g_name; }
+
+const char* qhip_error_string(int err) {
+  if (err == QHIP_DECLINE) return "declined: this kernel path does not serve the request";
+  return hipGetErrorString((hipError_t)err);
+}
+
+int qhip_quant_act_block_elems(int ttype) { return act_elems(ttype); }
+
+int qhip_quant_geom(int ttype, int* block_elems, int* block_bytes) {
+  int be, bb;
+  if (!geom(ttype, be, bb)) return 0;
+  if (block_elems) *block_elems = be;
+  if (block_bytes) *block_bytes = bb;
+  return 1;
+}
+
+long qhip_act_row_bytes(int ttype, int cols) { return act_row_bytes(ttype, cols); }
+long qhip_weight_row_bytes(int ttype, int cols) { return weight_row_bytes(ttype, cols); }
+
+int qhip_launch_quantize_q8_0(const float* d_x, void* d_out, int nblocks, void* stream) {
+  if (nblocks < 0 || (nblocks > 0 && (!d_x || !d_out))) return (int)hipErrorInvalidValue;
+  return (int)launch_quantize_q8_0(d_x, d_out, nblocks, 1, 0, 0, S(stream));
+}
+
+int qhip_launch_quantize_q8_K(const float* d_x, void* d_out, int nblocks, void* stream) {
+  if (nblocks < 0 || (nblocks > 0 && (!d_x || !d_out))) return (int)hipErrorInvalidValue;
+  if (!aligned4(d_out)) return (int)hipErrorInvalidValue;
+  return (int)launch_quantize_q8_K(d_x, d_out, nblocks, 1, 0, 0, S(stream));
+}
+
+int qhip_launch_quantize_act(int ttype, const float* d_x, void* d_out, int cols, int tokens,
+                             void* stream) {
+  const long ab = act_row_bytes(ttype, cols);
+  if (ab < 0 || tokens < 0 || tokens > 65535) return (int)hipErrorInvalidValue;
+  if (tokens == 0) return 0;
+  if (!d_x || !d_out) return (int)hipErrorInvalidValue;
+  if (act_elems(ttype) == 32)
+    return (int)launch_quantize_q8_0(d_x, d_out, cols / 32, tokens, cols, ab, S(stream));
+  if (!aligned4(d_out)) return (int)hipErrorInvalidValue;
+  return (int)launch_quantize_q8_K(d_x, d_out, cols / 256, tokens, cols, ab, S(stream));
+}
+
+int qhip_launch_mul_mat(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
+                        int tokens, int ttype, int path, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  return (int)dispatch_mul_mat(g, path, S(stream));
+}
+
+int qhip_launch_mul_mat_vec(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
+                            int tokens, int ttype, void* stream) {
+  return qhip_launch_mul_mat(d_w, d_xq, d_out, rows, cols, tokens, ttype, QHIP_PATH_AUTO, stream);
+}
+
+int qhip_launch_mul_mat_vec_q8_0(const void* d_w, const void* d_xq, float* d_out, int rows,
+                                 int cols, int tokens, void* stream) {
+  return qhip_launch_mul_mat_vec(d_w, d_xq, d_out, rows, cols, tokens, QHIP_TT_Q8_0, stream);
+}
+
+int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
+                           int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
+                           void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  const int l = lanes_per_row, n = tokens_per_pass;
+  if (l < 0 || l > 64 || (l & (l - 1)) || n < 0 || n > 8 || (n & (n - 1)))
+    return (int)hipErrorInvalidValue;
+  if (!fast_ok(g)) return QHIP_DECLINE;
+  return (int)launch_gemv(g, l, n, S(stream));
+}
+
+int qhip_ragged_offsets(const int* lengths, int nseq, int* offsets) {
+  if (!lengths || !offsets || nseq < 0) return -1;
+  long acc = 0;
+  offsets[0] = 0;
+  for (int i = 0; i < nseq; ++i) {
+    if (lengths[i] < 0) return -1;
+    acc += lengths[i];
+    if (acc > INT_MAX) return -1;
+    offsets[i + 1] = (int)acc;
+  }
+  return (int)acc;
+}
+
+int qhip_launch_quantize_ragged(int ttype, const float* const* d_src, const int* d_offsets,
+                                int nseq, int total_tokens, int cols, void* d_xq_packed,
+                                void* stream) {
+  const long ab = act_row_bytes(ttype, cols);
+  if (ab < 0 || nseq < 0 || total_tokens < 0 || total_tokens > 65535) return (int)hipErrorInvalidValue;
+  if (total_tokens == 0) return 0;
+  if (nseq == 0 || !d_src || !d_offsets || !d_xq_packed) return (int)hipErrorInvalidValue;
+  if (act_elems(ttype) == 32) {
+    const long nb = cols / 32;
+    dim3 grid((unsigned)((nb * 32 + 255) / 256), (unsigned)total_tokens);
+    hipLaunchKernelGGL(k_quantize_ragged_q8_0, grid, dim3(256), 0, S(stream), d_src, d_offsets,
+                       nseq, (uint8_t*)d_xq_packed, nb, (long)cols, ab);
+  } else {
+    if (!aligned4(d_xq_packed)) return (int)hipErrorInvalidValue;
+    const long nb = cols / 256;
+    dim3 grid((unsigned)((nb + 3) / 4), (unsigned)total_tokens);
+    hipLaunchKernelGGL(k_quantize_ragged_q8_K, grid, dim3(256), 0, S(stream), d_src, d_offsets,
+                       nseq, (uint8_t*)d_xq_packed, nb, (long)cols, ab);
+  }
+  return (int)hipGetLastError();
+}
+
+int qhip_launch_mul_mat_ragged(const void* d_w, const void* d_xq_packed, float* d_out, int rows,
+                               int cols, const int* d_offsets, int nseq, int total_tokens,
+                               int ttype, void* stream) {
+  if (nseq < 0 || (nseq > 0 && !d_offsets)) return (int)hipErrorInvalidValue;
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_xq_packed, d_out, rows, cols, total_tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  return (int)dispatch_mul_mat(g, QHIP_PATH_AUTO, S(stream));
+}
+
+int qhip_launch_block_ints(const void* d_w, const void* d_xq, int32_t* d_ints, int rows, int cols,
+                           int tokens, int ttype, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_xq, reinterpret_cast<float*>(d_ints), rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (!fast_ok(g)) return (int)hipErrorInvalidValue;
+  return (int)launch_block_ints(g, d_ints, S(stream));
+}
+
+}  // extern "C"

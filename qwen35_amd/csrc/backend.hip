@@ -1,0 +1,221 @@
+// backend.hip -- the host side of the Exec vtable's quantized-matvec slots
+// (reference src/backend.zig:110-178), the part a backend_hip.zig would
+// forward to.  Behavioural spec: the reference device backend
+// (src/backend_cuda.zig:3458-4400): weights are uploaded once at load time and
+// stay resident; activations are quantized on the device into backend-owned
+// scratch; matvecPair runs as one launch when the two weights are adjacent and
+// alike (:3743-3794); a failed launch is reported, never replaced by a CPU
+// computation (:26-31).
+#include "../../include/qwen35_hip.h"
+#include "qhip_internal.hpp"
+
+#include <cstdio>
+#include <mutex>
+#include <new>
+#include <vector>
+
+namespace qhip {
+hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s);
+}
+
+using namespace qhip;
+
+struct qhip_backend {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  // Weight arena: large device chunks, bump-allocated with 256-byte alignment,
+  // so consecutive loads are contiguous on the device.
+  struct Chunk { uint8_t* base; size_t size, used; };
+  std::vector<Chunk> arena;
+  std::vector<void*> bufs;       // allocBuf regions (freed by free_scratch)
+  uint8_t* act = nullptr;        // quantized-activation scratch
+  size_t act_cap = 0;
+  char name[96] = "hip";
+};
+
+static constexpr size_t kArenaChunk = size_t(1) << 30;  // 1 GiB
+static constexpr size_t kAlign = 256;
+
+static hipError_t arena_alloc(qhip_backend* be, size_t bytes, uint8_t** out) {
+  bytes = (bytes + kAlign - 1) / kAlign * kAlign;
+  if (!be->arena.empty()) {
+    auto& c = be->arena.back();
+    if (c.size - c.used >= bytes) {
+      *out = c.base + c.used;
+      c.used += bytes;
+      return hipSuccess;
+    }
+  }
+  const size_t sz = bytes > kArenaChunk ? bytes : kArenaChunk;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, sz);
+  if (e != hipSuccess) return e;
+  be->arena.push_back({(uint8_t*)p, sz, bytes});
+  *out = (uint8_t*)p;
+  return hipSuccess;
+}
+
+static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
+  if (be->act_cap >= bytes) return hipSuccess;
+  if (be->act) (void)hipFree(be->act);
+  be->act = nullptr;
+  be->act_cap = 0;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return e;
+  be->act = (uint8_t*)p;
+  be->act_cap = bytes;
+  return hipSuccess;
+}
+
+// Bytes per value of the widest activation family (Q8_K: 292/256), so one
+// scratch serves every weight type.
+static size_t act_bytes_for(int cols, int k) {
+  const size_t c = (size_t)((cols + 255) / 256) * 256;
+  return c / 256 * 292 * (size_t)k + 256;
+}
+
+static int report(const char* what, hipError_t e) {
+  if (e != hipSuccess && (int)e != QHIP_DECLINE)
+    fprintf(stderr, "qwen35_hip: %s failed: %s\n", what, hipGetErrorString(e));
+  return (int)e;
+}
+
+static bool valid_linear(const qhip_linear* w) {
+  return w && w->dev && qhip_weight_row_bytes(w->ttype, w->cols) == w->row_bytes && w->rows >= 0;
+}
+
+// quantize `k` tokens of x into the scratch and run out = W . xq
+static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int rows, int cols,
+               long row_bytes, const float* x, int k) {
+  if (!out || !x || k < 0) return (int)hipErrorInvalidValue;
+  if (k == 0 || rows == 0) return 0;
+  hipError_t e = ensure_act(be, act_bytes_for(cols, k));
+  if (e != hipSuccess) return report("activation scratch", e);
+  int rc = qhip_launch_quantize_act(ttype, x, be->act, cols, k, be->stream);
+  if (rc) return report("quantize", (hipError_t)rc);
+  GemvArgs g{ttype, wdev, be->act, out, rows, cols, k, row_bytes, qhip_act_row_bytes(ttype, cols)};
+  return report("matvec", dispatch_mul_mat(g, QHIP_PATH_AUTO, be->stream));
+}
+
+extern "C" {
+
+qhip_backend* qhip_backend_create(int device, int* err) {
+  int rc = qhip_init(device);
+  if (err) *err = rc;
+  if (rc) return nullptr;
+  qhip_backend* be = new (std::nothrow) qhip_backend();
+  if (!be) {
+    if (err) *err = (int)hipErrorOutOfMemory;
+    return nullptr;
+  }
+  be->device = device;
+  snprintf(be->name, sizeof be->name, "hip:%d %s", device, qhip_gpu_name());
+  return be;
+}
+
+void qhip_backend_destroy(qhip_backend* be) {
+  if (!be) return;
+  (void)hipSetDevice(be->device);
+  (void)hipDeviceSynchronize();
+  qhip_backend_free_scratch(be);
+  for (auto& c : be->arena) (void)hipFree(c.base);
+  delete be;
+}
+
+const char* qhip_backend_name(const qhip_backend* be) { return be ? be->name : ""; }
+
+int qhip_backend_load_linear(qhip_backend* be, int ttype, int rows, int cols, const void* host,
+                             qhip_linear* out) {
+  const long rb = qhip_weight_row_bytes(ttype, cols);
+  if (!be || !out || !host || rows < 0 || rb < 0) return (int)hipErrorInvalidValue;
+  const size_t bytes = (size_t)rows * (size_t)rb;
+  uint8_t* dev = nullptr;
+  hipError_t e = arena_alloc(be, bytes ? bytes : 1, &dev);
+  if (e != hipSuccess) return report("weight upload", e);
+  e = hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return report("weight upload", e);
+  *out = qhip_linear{dev, ttype, rows, cols, rb};
+  return 0;
+}
+
+int qhip_backend_wrap_linear(qhip_backend* be, int ttype, int rows, int cols, const void* d_data,
+                             qhip_linear* out) {
+  const long rb = qhip_weight_row_bytes(ttype, cols);
+  if (!be || !out || !d_data || rows < 0 || rb < 0) return (int)hipErrorInvalidValue;
+  *out = qhip_linear{d_data, ttype, rows, cols, rb};
+  return 0;
+}
+
+void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
+  // Arena memory is returned at destroy; the handle is cleared so a stale use
+  // fails validation instead of reading freed memory.
+  (void)be;
+  if (w) *w = qhip_linear{nullptr, 0, 0, 0, 0};
+}
+
+int qhip_backend_alloc_scratch(qhip_backend* be, int max_cols) {
+  return qhip_backend_alloc_scratch_k(be, max_cols, 1);
+}
+
+int qhip_backend_alloc_scratch_k(qhip_backend* be, int max_cols, int k) {
+  if (!be || max_cols <= 0 || k <= 0) return (int)hipErrorInvalidValue;
+  return report("scratch", ensure_act(be, act_bytes_for(max_cols, k)));
+}
+
+void qhip_backend_free_scratch(qhip_backend* be) {
+  if (!be) return;
+  (void)hipDeviceSynchronize();
+  if (be->act) (void)hipFree(be->act);
+  be->act = nullptr;
+  be->act_cap = 0;
+  for (void* p : be->bufs) (void)hipFree(p);
+  be->bufs.clear();
+}
+
+int qhip_backend_alloc_buf(qhip_backend* be, size_t len, float** d_out) {
+  if (!be || !d_out) return (int)hipErrorInvalidValue;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, len ? len * sizeof(float) : sizeof(float));
+  if (e != hipSuccess) return report("allocBuf", e);
+  be->bufs.push_back(p);
+  *d_out = (float*)p;
+  return 0;
+}
+
+int qhip_backend_matvec(qhip_backend* be, float* d_out, const qhip_linear* w, const float* d_x) {
+  if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
+  return run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_x, 1);
+}
+
+int qhip_backend_matvec_pair(qhip_backend* be, float* d_out, const qhip_linear* a,
+                             const qhip_linear* b, const float* d_x) {
+  if (!be || !valid_linear(a) || !valid_linear(b) || !d_out) return (int)hipErrorInvalidValue;
+  const bool alike = a->ttype == b->ttype && a->rows == b->rows && a->cols == b->cols;
+  const bool adjacent =
+      alike && (const uint8_t*)a->dev + (size_t)a->rows * a->row_bytes == (const uint8_t*)b->dev;
+  if (adjacent)
+    return run(be, d_out, a->dev, a->ttype, 2 * a->rows, a->cols, a->row_bytes, d_x, 1);
+  int rc = run(be, d_out, a->dev, a->ttype, a->rows, a->cols, a->row_bytes, d_x, 1);
+  if (rc) return rc;
+  return run(be, d_out + a->rows, b->dev, b->ttype, b->rows, b->cols, b->row_bytes, d_x, 1);
+}
+
+int qhip_backend_matvec_batch_k(qhip_backend* be, float* d_out, const qhip_linear* w,
+                                const float* d_xK, int k) {
+  if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
+  return run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_xK, k);
+}
+
+int qhip_backend_set_stream(qhip_backend* be, void* stream) {
+  if (!be) return (int)hipErrorInvalidValue;
+  be->stream = (hipStream_t)stream;
+  return 0;
+}
+
+int qhip_backend_sync(qhip_backend* be) {
+  if (!be) return (int)hipErrorInvalidValue;
+  return report("sync", hipStreamSynchronize(be->stream));
+}
+
+}  // extern "C"

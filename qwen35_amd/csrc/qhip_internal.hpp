@@ -1,0 +1,30 @@
+// qhip_internal.hpp -- launch functions shared between the kernel files and
+// the C-ABI layer (api.hip).  Not part of the public interface.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qhip {
+
+struct GemvArgs {
+  int ttype;
+  const void* w;     // packed weight rows, GGUF block layout
+  const void* xq;    // quantized activations, reference layout, `tokens` rows
+  float* out;        // [tokens][rows]
+  int rows, cols, tokens;
+  long row_bytes;    // bytes of one weight row
+  long act_bytes;    // bytes of one quantized activation row
+};
+
+hipError_t launch_quantize_q8_0(const float* x, void* out, long nblocks, int tokens, long x_stride,
+                                long out_stride, hipStream_t s);
+hipError_t launch_quantize_q8_K(const float* x, void* out, long nblocks, int tokens, long x_stride,
+                                long out_stride, hipStream_t s);
+
+int gemv_pick_tpr(int rows, int cols);
+int gemv_pick_nt(int tokens);
+hipError_t launch_gemv(const GemvArgs& g, int tpr, int nt, hipStream_t s);
+hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s);
+hipError_t launch_block_ints(const GemvArgs& g, int* ints, hipStream_t s);
+
+}  // namespace qhip

@@ -1,0 +1,179 @@
+"""Thin torch-facing wrappers over the C ABI (device tensors in, device tensors out).
+
+Every call goes straight to a HIP kernel of libqwen35_hip.so on the current
+torch stream; nothing is computed on the host.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from ._lib import QhipLinear, check, load
+
+_GEOM = {8: (32, 34), 20: (32, 18), 12: (256, 144), 14: (256, 210)}
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _p(t: torch.Tensor) -> ctypes.c_void_p:
+    assert t.is_cuda and t.is_contiguous()
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def act_row_bytes(ttype: int, cols: int) -> int:
+    n = load().qhip_act_row_bytes(ttype, cols)
+    if n < 0:
+        raise ValueError(f"bad (ttype={ttype}, cols={cols})")
+    return n
+
+
+def weight_row_bytes(ttype: int, cols: int) -> int:
+    n = load().qhip_weight_row_bytes(ttype, cols)
+    if n < 0:
+        raise ValueError(f"bad (ttype={ttype}, cols={cols})")
+    return n
+
+
+def quantize_act(ttype: int, x: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [k, cols] f32 -> [k, act_row_bytes] uint8, the weight type's activation family."""
+    x2 = x.reshape(-1, x.shape[-1])
+    k, cols = x2.shape
+    if out is None:
+        out = torch.empty((k, act_row_bytes(ttype, cols)), dtype=torch.uint8, device=x.device)
+    check("quantize_act", load().qhip_launch_quantize_act(ttype, _p(x2), _p(out), cols, k, _stream()))
+    return out
+
+
+def quantize_q8_0(x: torch.Tensor) -> torch.Tensor:
+    n = x.numel()
+    out = torch.empty(n // 32 * 34, dtype=torch.uint8, device=x.device)
+    check("quantize_q8_0", load().qhip_launch_quantize_q8_0(_p(x), _p(out), n // 32, _stream()))
+    return out
+
+
+def quantize_q8_K(x: torch.Tensor) -> torch.Tensor:
+    n = x.numel()
+    out = torch.empty(n // 256 * 292, dtype=torch.uint8, device=x.device)
+    check("quantize_q8_K", load().qhip_launch_quantize_q8_K(_p(x), _p(out), n // 256, _stream()))
+    return out
+
+
+def mul_mat(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
+            path: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out [tokens, rows] = W . xq_t (xq already quantized)."""
+    if out is None:
+        out = torch.empty((tokens, rows), dtype=torch.float32, device=w.device)
+    check("mul_mat", load().qhip_launch_mul_mat(_p(w), _p(xq), _p(out), rows, cols, tokens, ttype,
+                                                path, _stream()))
+    return out
+
+
+def gemv_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
+               lanes_per_row: int, tokens_per_pass: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    if out is None:
+        out = torch.empty((tokens, rows), dtype=torch.float32, device=w.device)
+    check("gemv_tuned", load().qhip_launch_gemv_tuned(_p(w), _p(xq), _p(out), rows, cols, tokens,
+                                                      ttype, lanes_per_row, tokens_per_pass,
+                                                      _stream()))
+    return out
+
+
+def block_ints(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
+               tokens: int) -> torch.Tensor:
+    be = _GEOM[ttype][0]
+    nints = 2 * cols // 256 if ttype == 12 else cols // be
+    out = torch.empty((tokens, rows, nints), dtype=torch.int32, device=w.device)
+    check("block_ints", load().qhip_launch_block_ints(_p(w), _p(xq), _p(out), rows, cols, tokens,
+                                                      ttype, _stream()))
+    return out
+
+
+def ragged_offsets(lengths) -> tuple[list[int], int]:
+    n = len(lengths)
+    arr = (ctypes.c_int * n)(*lengths)
+    off = (ctypes.c_int * (n + 1))()
+    total = load().qhip_ragged_offsets(arr, n, off)
+    if total < 0:
+        raise ValueError("bad lengths")
+    return list(off), total
+
+
+def quantize_ragged(ttype: int, seqs: list[torch.Tensor], cols: int):
+    """Pack + quantize several [L_i, cols] f32 sequences in one launch.
+    Returns (xq_packed [total, act_row_bytes], offsets_dev [nseq+1] int32, total)."""
+    lengths = [int(s.shape[0]) for s in seqs]
+    off, total = ragged_offsets(lengths)
+    dev = seqs[0].device
+    ptrs = torch.tensor([s.data_ptr() for s in seqs], dtype=torch.int64, device=dev)
+    off_d = torch.tensor(off, dtype=torch.int32, device=dev)
+    xq = torch.empty((max(total, 1), act_row_bytes(ttype, cols)), dtype=torch.uint8, device=dev)
+    check("quantize_ragged", load().qhip_launch_quantize_ragged(
+        ttype, _p(ptrs), _p(off_d), len(seqs), total, cols, _p(xq), _stream()))
+    return xq, off_d, total
+
+
+def mul_mat_ragged(ttype: int, w: torch.Tensor, xq: torch.Tensor, off_d: torch.Tensor, nseq: int,
+                   total: int, rows: int, cols: int) -> torch.Tensor:
+    out = torch.empty((max(total, 1), rows), dtype=torch.float32, device=w.device)
+    check("mul_mat_ragged", load().qhip_launch_mul_mat_ragged(
+        _p(w), _p(xq), _p(out), rows, cols, _p(off_d), nseq, total, ttype, _stream()))
+    return out[:total]
+
+
+class Backend:
+    """Python handle on the C++ backend (the Exec-slot mirror)."""
+
+    def __init__(self, device: int = 0):
+        lib = load()
+        err = ctypes.c_int(0)
+        self._h = lib.qhip_backend_create(device, ctypes.byref(err))
+        if not self._h:
+            check("backend_create", err.value or -1)
+        self.lib = lib
+        check("set_stream", lib.qhip_backend_set_stream(self._h, _stream()))
+
+    def close(self):
+        if self._h:
+            self.lib.qhip_backend_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def name(self) -> str:
+        return self.lib.qhip_backend_name(self._h).decode()
+
+    def load_linear(self, ttype: int, rows: int, cols: int, host_bytes) -> QhipLinear:
+        import numpy as np
+        buf = np.ascontiguousarray(host_bytes, dtype=np.uint8)
+        lin = QhipLinear()
+        check("load_linear", self.lib.qhip_backend_load_linear(
+            self._h, ttype, rows, cols, ctypes.c_void_p(buf.ctypes.data), ctypes.byref(lin)))
+        return lin
+
+    def wrap_linear(self, ttype: int, rows: int, cols: int, dev: torch.Tensor) -> QhipLinear:
+        lin = QhipLinear()
+        check("wrap_linear", self.lib.qhip_backend_wrap_linear(self._h, ttype, rows, cols, _p(dev),
+                                                               ctypes.byref(lin)))
+        return lin
+
+    def matvec(self, out: torch.Tensor, w: QhipLinear, x: torch.Tensor) -> None:
+        check("matvec", self.lib.qhip_backend_matvec(self._h, _p(out), ctypes.byref(w), _p(x)))
+
+    def matvec_pair(self, out: torch.Tensor, a: QhipLinear, b: QhipLinear, x: torch.Tensor) -> None:
+        check("matvec_pair", self.lib.qhip_backend_matvec_pair(self._h, _p(out), ctypes.byref(a),
+                                                               ctypes.byref(b), _p(x)))
+
+    def matvec_batch_k(self, out: torch.Tensor, w: QhipLinear, xk: torch.Tensor, k: int) -> None:
+        check("matvec_batch_k", self.lib.qhip_backend_matvec_batch_k(self._h, _p(out),
+                                                                     ctypes.byref(w), _p(xk), k))
+
+    def sync(self) -> None:
+        check("sync", self.lib.qhip_backend_sync(self._h))

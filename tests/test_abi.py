@@ -1,0 +1,125 @@
+"""C-ABI structure tests that need no GPU: the library loads, exports exactly
+what include/qwen35_hip.h declares, and rejects bad arguments on the host
+before any launch (the reference's host-side validation pattern,
+src/kernels/cuda/mmvq.cu:781-785)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "qwen35_hip.h"
+INVALID = 1  # hipErrorInvalidValue
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(qhip_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import qwen35_amd
+    return qwen35_amd.load()
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "qhip_launch_mul_mat_vec" in names and "qhip_backend_matvec_pair" in names
+    assert len(names) >= 30
+
+
+def test_library_exports_every_declared_symbol(lib):
+    so = ROOT / "qwen35_amd" / "libqwen35_hip.so"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(so)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (qhip_\w+)", out))
+    missing = [n for n in declared() if n not in exported]
+    assert not missing, missing
+    extra = sorted(exported - set(declared()))
+    assert not extra, f"exported but undeclared: {extra}"
+
+
+def test_python_binding_covers_header(lib):
+    from qwen35_amd._lib import SIGNATURES
+    assert sorted(SIGNATURES) == declared()
+
+
+def test_geometry(lib):
+    be, bb = ctypes.c_int(), ctypes.c_int()
+    table = {8: (32, 34), 12: (256, 144), 14: (256, 210), 20: (32, 18)}
+    for tt, (e, b) in table.items():
+        assert lib.qhip_quant_geom(tt, ctypes.byref(be), ctypes.byref(bb)) == 1
+        assert (be.value, bb.value) == (e, b)
+        assert lib.qhip_quant_act_block_elems(tt) == (32 if e == 32 else 256)
+    assert lib.qhip_quant_geom(2, ctypes.byref(be), ctypes.byref(bb)) == 0  # Q4_0 unsupported
+    assert lib.qhip_quant_act_block_elems(99) == 0
+    assert lib.qhip_act_row_bytes(8, 1024) == 1088
+    assert lib.qhip_act_row_bytes(12, 2560) == 2920
+    assert lib.qhip_weight_row_bytes(14, 9728) == 7980
+    assert lib.qhip_weight_row_bytes(20, 2560) == 1440
+    assert lib.qhip_weight_row_bytes(12, 100) == -1  # not a multiple of 256
+    assert lib.qhip_act_row_bytes(8, 48) == -1
+
+
+def test_ragged_offsets(lib):
+    lens = (ctypes.c_int * 4)(5, 0, 7, 3)
+    off = (ctypes.c_int * 5)()
+    assert lib.qhip_ragged_offsets(lens, 4, off) == 15
+    assert list(off) == [0, 5, 5, 12, 15]
+    bad = (ctypes.c_int * 2)(3, -1)
+    assert lib.qhip_ragged_offsets(bad, 2, off) == -1
+
+
+def test_invalid_arguments_rejected_before_launch(lib):
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    # unknown type id
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 256, 1, 2, None) == INVALID
+    # cols not a multiple of the block size
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 100, 1, 12, None) == INVALID
+    # NULL buffers
+    assert lib.qhip_launch_mul_mat_vec(None, p, p, 16, 256, 1, 8, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec(p, None, p, 16, 256, 1, 8, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec(p, p, None, 16, 256, 1, 8, None) == INVALID
+    # negative counts
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, -1, 256, 1, 8, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 256, -2, 8, None) == INVALID
+    # bad path selector
+    assert lib.qhip_launch_mul_mat(p, p, p, 16, 256, 1, 8, 17, None) == INVALID
+    # quantizers
+    assert lib.qhip_launch_quantize_act(12, p, p, 100, 1, None) == INVALID
+    assert lib.qhip_launch_quantize_act(8, None, p, 64, 1, None) == INVALID
+    assert lib.qhip_launch_quantize_q8_0(None, p, 4, None) == INVALID
+    assert lib.qhip_launch_quantize_q8_K(p, ctypes.c_void_p(0x1002), 1, None) == INVALID
+    # ragged
+    assert lib.qhip_launch_mul_mat_ragged(p, p, p, 16, 256, None, 2, 10, 8, None) == INVALID
+    assert lib.qhip_launch_quantize_ragged(8, None, p, 2, 10, 256, p, None) == INVALID
+    # parity export
+    assert lib.qhip_launch_block_ints(p, p, p, 16, 96, 1, 8, None) == INVALID
+    # backend with bad handle
+    assert lib.qhip_backend_matvec(None, p, None, p) == INVALID
+    assert lib.qhip_backend_alloc_scratch(None, 1024) == INVALID
+
+
+def test_zero_sized_requests_are_no_ops(lib):
+    p = ctypes.c_void_p(0x1000)
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, 0, 256, 1, 8, None) == 0
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 256, 0, 8, None) == 0
+    assert lib.qhip_launch_quantize_act(8, p, p, 64, 0, None) == 0
+
+
+def test_error_strings(lib):
+    assert b"declined" in lib.qhip_error_string(-1)
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    from qwen35_amd import _lib
+    saved = _lib._lib
+    try:
+        _lib._lib = None
+        with pytest.raises(RuntimeError, match="no CPU fallback"):
+            _lib.load(tmp_path / "absent.so")
+    finally:
+        _lib._lib = saved

@@ -1,0 +1,158 @@
+"""GPU parity: HIP quantizers and GEMV against the CPU oracle, through the C ABI.
+
+Bar: quantized activations and per-block integers bit-exact; float outputs
+within 1e-5 relative L2 of the oracle (the tolerance BASELINE.json's
+north_star states for the float result after scale application).
+"""
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from qwen35_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5  # relative L2, float outputs
+TYPES = [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K]
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def to_dev(a: np.ndarray, dev) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def case_id(tt, rows, cols):
+    return f"{po.NAMES[tt]}-{rows}x{cols}"
+
+
+# ---- quantizers ------------------------------------------------------------------
+
+QUANT_INPUTS = {
+    "normal": lambda rng, k, n: rng.standard_normal((k, n)).astype(np.float32),
+    "wide": lambda rng, k, n: (rng.standard_normal((k, n)) * 10.0 ** rng.uniform(-30, 30, (k, 1))).astype(np.float32),
+    "ties": lambda rng, k, n: np.tile(np.float32([127, 63.5, -63.5, .5, -.5, 1.5, -2.5, 0]), (k, n // 8)),
+    "zeros": lambda rng, k, n: np.zeros((k, n), np.float32),
+}
+
+
+@pytest.mark.parametrize("kind", list(QUANT_INPUTS))
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K])
+def test_quantize_act_bit_exact(gpu, oracle, tt, kind):
+    rng = np.random.default_rng(17)
+    x = QUANT_INPUTS[kind](rng, 5, 4096)
+    if kind == "wide":
+        x[0, 3] = np.nan
+        x[1, :7] = -0.0
+        x[2, 9] = np.inf
+    want = oracle.quantize_act(tt, x)
+    got = ops.quantize_act(tt, to_dev(x, gpu)).cpu().numpy()
+    assert np.array_equal(got, want)
+
+
+def test_quantize_header_quirk(gpu, oracle):
+    # scale rounding out of the f16 subnormal range -> 0x0380 (kernels32.c:96)
+    x = np.random.default_rng(1).uniform(-1, 1, 64).astype(np.float32) * np.float32(0.0077)
+    x[0] = np.float32(0.0077491)
+    want = oracle.quantize_act(po.TT_Q8_0, x[None])
+    assert want[0, 0] | (want[0, 1] << 8) == 0x0380
+    got = ops.quantize_q8_0(to_dev(x, gpu)).cpu().numpy()
+    assert np.array_equal(got, want[0])
+
+
+def test_quantize_single_entry_points(gpu, oracle):
+    x = synth.make_act(2560, 1, seed=4)[0]
+    assert np.array_equal(ops.quantize_q8_0(to_dev(x, gpu)).cpu().numpy(),
+                          oracle.quantize_act(po.TT_Q8_0, x))
+    assert np.array_equal(ops.quantize_q8_K(to_dev(x, gpu)).cpu().numpy(),
+                          oracle.quantize_act(po.TT_Q4_K, x))
+
+
+# ---- GEMV ---------------------------------------------------------------------------
+
+SHAPES = {
+    po.TT_Q8_0: [(300, 1024), (64, 192), (1, 64)],
+    po.TT_IQ4_NL: [(200, 2560), (37, 256)],
+    po.TT_Q4_K: [(100, 2560), (33, 256)],
+    po.TT_Q6_K: [(50, 9728), (17, 256), (16, 2304)],
+}
+CASES = [(tt, r, c) for tt in TYPES for (r, c) in SHAPES[tt]]
+
+
+def setup(tt, rows, cols, k, dev, seed=0):
+    w = synth.make_weight(tt, rows, cols, seed=seed, tag=tt)
+    x = synth.make_act(cols, k, seed=seed)
+    return w, x, to_dev(w, dev), to_dev(x, dev)
+
+
+@pytest.mark.parametrize("tt,rows,cols", CASES, ids=[case_id(*c) for c in CASES])
+def test_block_ints_bit_exact(gpu, oracle, tt, rows, cols):
+    w, x, wd, xd = setup(tt, rows, cols, 2, gpu)
+    act = oracle.quantize_act(tt, x)
+    xq = ops.quantize_act(tt, xd)
+    assert np.array_equal(xq.cpu().numpy(), act)
+    got = ops.block_ints(tt, wd, xq, rows, cols, 2).cpu().numpy()
+    want = oracle.block_ints(tt, w, act, cols)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("tokens", [1, 3, 8, 9])
+@pytest.mark.parametrize("tt,rows,cols", CASES, ids=[case_id(*c) for c in CASES])
+def test_gemv_matches_oracle(gpu, oracle, tt, rows, cols, tokens):
+    w, x, wd, xd = setup(tt, rows, cols, tokens, gpu, seed=tokens)
+    want = oracle.matvec(tt, w, x)
+    xq = ops.quantize_act(tt, xd)
+    for path in (0, 1, 3):  # auto, gemv, generic
+        got = ops.mul_mat(tt, wd, xq, rows, cols, tokens, path=path).cpu().numpy()
+        assert rel_l2(got, want) < TOL, (path, rel_l2(got, want))
+
+
+@pytest.mark.parametrize("tt", TYPES)
+def test_every_launch_shape(gpu, oracle, tt):
+    rows, cols, tokens = 130, 2560 if tt != po.TT_Q6_K else 4096, 5
+    w, x, wd, xd = setup(tt, rows, cols, tokens, gpu, seed=3)
+    want = oracle.matvec(tt, w, x)
+    xq = ops.quantize_act(tt, xd)
+    for lpr in (1, 2, 4, 8, 16, 32, 64):
+        for tpp in (1, 2, 4, 8):
+            got = ops.gemv_tuned(tt, wd, xq, rows, cols, tokens, lpr, tpp).cpu().numpy()
+            assert rel_l2(got, want) < TOL, (lpr, tpp, rel_l2(got, want))
+
+
+@pytest.mark.parametrize("tt", TYPES)
+def test_unaligned_pointers_take_generic_path(gpu, oracle, tt):
+    rows, cols = 24, 512
+    w, x, _, xd = setup(tt, rows, cols, 2, gpu, seed=8)
+    want = oracle.matvec(tt, w, x)
+    xq = ops.quantize_act(tt, xd)
+    wbuf = torch.zeros(w.size + 2, dtype=torch.uint8, device=gpu)
+    wbuf[2:] = to_dev(w.reshape(-1), gpu)
+    xbuf = torch.zeros(xq.numel() + 2, dtype=torch.uint8, device=gpu)
+    xbuf[2:] = xq.reshape(-1)
+    got = ops.mul_mat(tt, wbuf[2:], xbuf[2:], rows, cols, 2).cpu().numpy()
+    assert rel_l2(got, want) < TOL
+
+
+def test_q6_k_odd_total_bytes_uses_generic(gpu, oracle):
+    # 9 super-blocks per row x 3 rows: total bytes % 4 == 2 -> generic kernel
+    tt, rows, cols = po.TT_Q6_K, 3, 2304
+    w, x, wd, xd = setup(tt, rows, cols, 1, gpu, seed=6)
+    want = oracle.matvec(tt, w, x)
+    xq = ops.quantize_act(tt, xd)
+    got = ops.mul_mat(tt, wd, xq, rows, cols, 1).cpu().numpy()
+    assert rel_l2(got, want) < TOL
+    from qwen35_amd import _lib
+    rc = _lib.load().qhip_launch_gemv_tuned(wd.data_ptr(), xq.data_ptr(), torch.empty(3, device=gpu).data_ptr(),
+                                           rows, cols, 1, tt, 4, 1, None)
+    assert rc == -1  # fast path declines
+
+
+def test_zero_weights_and_zero_activation(gpu, oracle):
+    tt, rows, cols = po.TT_Q4_K, 16, 512
+    w, x, wd, _ = setup(tt, rows, cols, 1, gpu)
+    xq = ops.quantize_act(tt, torch.zeros((1, cols), device=gpu))
+    assert torch.count_nonzero(ops.mul_mat(tt, wd, xq, rows, cols, 1)) == 0

@@ -1,0 +1,220 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the checker.
+
+Each check is chosen so a plausible restatement mistake (wrong nibble order,
+dropped min term, wrong sign, off-by-one group, wrong rounding) fails it:
+  * golden vectors written by the reference's own compiled kernels
+    (tests/golden/ref_vectors.npz, see gen_golden.py), including unit-scale
+    rows whose float result IS the exact block integer;
+  * the reference test fixtures testdata/udtest (dequant(row) . A_x);
+  * library routines / closed forms (numpy float16 conversion, exhaustive);
+  * an exact identity for IQ4_NL: an IQ4_NL block equals a Q8_0 block holding
+    the codebook values, so the reference's own q8_0_q8_0 pins it.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+GOLD = Path(__file__).resolve().parent / "golden"
+IQ4NL = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113],
+                 np.int8)  # reference src/iq_tables.zig:429-432
+
+
+@pytest.fixture(scope="module")
+def gv():
+    return dict(np.load(GOLD / "ref_vectors.npz"))
+
+
+# ---- f16 conversions ---------------------------------------------------------
+
+def test_f16_decode_exhaustive(oracle):
+    codes = np.arange(65536, dtype=np.uint16)
+    want = codes.view(np.float16).astype(np.float32)
+    got = np.array([oracle.f16_to_f32(int(c)) for c in codes], np.float32)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin].view(np.uint32) & 0x7FFFFFFF, want[fin].view(np.uint32) & 0x7FFFFFFF)
+    assert np.array_equal(np.signbit(got[fin & (want != 0)]), np.signbit(want[fin & (want != 0)]))
+    assert np.all(np.isinf(got[np.isinf(want)]))
+    assert np.all(np.isnan(got[np.isnan(want)]))
+
+
+def test_f16_encode_matches_round_to_nearest_even(oracle):
+    rng = np.random.default_rng(3)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.uniform(-9, 5, 20000).astype(np.float32),
+        (np.arange(-70000, 70000, 7, dtype=np.float32)),
+        np.float32([0.0, -0.0, 65504.0, 65519.0, 65520.0, 6e-8, 2.98e-8, 5.96e-8, 1e-40]),
+    ]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f32_to_f16(float(v)) for v in x], np.uint16)
+    # documented reference quirk: values rounding up out of the subnormal range
+    quirk = (np.abs(x) >= np.float32(1023.5 * 2.0 ** -24)) & (np.abs(x) < np.float32(2.0 ** -14))
+    assert np.array_equal(got[~quirk], want[~quirk])
+    assert np.all(got[quirk] & 0x7FFF == 0x0380)
+
+
+def test_f16_encode_nan_maps_to_inf(oracle):
+    assert oracle.f32_to_f16(float("nan")) & 0x7FFF == 0x7C00
+    assert oracle.f32_to_f16(float("inf")) == 0x7C00
+    assert oracle.f32_to_f16(float("-inf")) == 0xFC00
+
+
+# ---- quantizers against the reference's compiled output ----------------------
+
+@pytest.mark.parametrize("name,tt", [("q8_0", po.TT_Q8_0), ("q8_k", po.TT_Q4_K)])
+def test_quantizer_golden(oracle, gv, name, tt):
+    got = oracle.quantize_act(tt, gv[f"quant_{name}_x"])
+    assert np.array_equal(got, gv[f"quant_{name}_act"])
+
+
+def test_quantizer_q8_0_quirk_row_present(gv):
+    # the golden set really exercises the 0x0380 header (kernels32.c:96)
+    q = gv["quant_q8_0_act"]
+    act = q.reshape(q.shape[0], -1, 34)
+    heads = act[:, :, 0].astype(np.uint16) | (act[:, :, 1].astype(np.uint16) << 8)
+    assert np.any(heads == 0x0380)
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K])
+def test_quantizer_vs_ref_random(oracle, ref, tt):
+    rng = np.random.default_rng(99)
+    x = (rng.standard_normal((64, 1024)) * 10.0 ** rng.uniform(-6, 4, (64, 1))).astype(np.float32)
+    x[3, 5] = np.nan
+    x[4, 7] = np.inf
+    x[5, :] = -0.0
+    assert np.array_equal(oracle.quantize_act(tt, x), ref.quantize_act(tt, x))
+
+
+def test_q8_k_bsums_and_clamp(oracle):
+    x = np.linspace(-3, 3, 512).astype(np.float32)
+    a = oracle.quantize_act(po.TT_Q4_K, x).reshape(2, 292)
+    for b in range(2):
+        qs = a[b, 4:260].view(np.int8).astype(np.int32)
+        bs = a[b, 260:292].view(np.int16)
+        assert np.array_equal(bs, qs.reshape(16, 16).sum(1))
+        assert qs.min() >= -127 and qs.max() <= 127
+
+
+# ---- block integers pinned bit for bit by unit-scale reference rows ---------
+
+@pytest.mark.parametrize("name,tt,key", [("q8_0", po.TT_Q8_0, "isum"), ("q4_k", po.TT_Q4_K, "isum"),
+                                         ("q4_k", po.TT_Q4_K, "summs"), ("q6_k", po.TT_Q6_K, "isum")])
+def test_block_ints_unit_scale(oracle, gv, name, tt, key):
+    w, a, val = gv[f"{name}_unit_{key}_w"], gv[f"{name}_unit_{key}_a"], gv[f"{name}_unit_{key}_val"]
+    be = po.GEOM[tt][0]
+    got = np.array([oracle.block_ints(tt, w[i:i + 1], a[i:i + 1], be)[0, 0] for i in range(len(w))])
+    if tt == po.TT_Q4_K:
+        got = got[:, 0] if key == "isum" else -got[:, 1]
+    else:
+        got = got[:, 0]
+    assert np.all(np.abs(val) < 2 ** 24)  # exactly representable
+    assert np.array_equal(got.astype(np.float32), val)
+
+
+@pytest.mark.parametrize("name,tt", [("q8_0", po.TT_Q8_0), ("q4_k", po.TT_Q4_K), ("q6_k", po.TT_Q6_K)])
+def test_row_dot_golden(oracle, gv, name, tt):
+    w, x, want = gv[f"{name}_w"], gv[f"{name}_x"], gv[f"{name}_dot"]
+    cols = x.shape[1]
+    got = oracle.matvec(tt, w, x)
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    assert rel < 1e-6, rel
+    if tt == po.TT_Q8_0:  # same sequential fold as the VNNI tier
+        assert np.array_equal(got, want)
+    assert cols % 256 == 0
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K])
+def test_row_dot_vs_ref_random(oracle, ref, tt):
+    from qwen35_amd import synth
+    cols = 2560 if tt != po.TT_Q6_K else 2816
+    w = synth.make_weight(tt, 64, cols, seed=5, tag=tt)
+    x = synth.make_act(cols, 2, seed=5)
+    act = ref.quantize_act(tt, x)
+    want = np.array([[ref.dot(tt, w[r], act[t], cols) for r in range(64)] for t in range(2)])
+    got = oracle.matvec(tt, w, x)
+    assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-6
+
+
+def _iq4nl_as_q8_0(wrow: np.ndarray, cols: int) -> np.ndarray:
+    blk = wrow.reshape(cols // 32, 18)
+    out = np.zeros((cols // 32, 34), np.uint8)
+    out[:, 0:2] = blk[:, 0:2]
+    lo, hi = blk[:, 2:] & 15, blk[:, 2:] >> 4
+    out[:, 2:18] = IQ4NL[lo].view(np.uint8)
+    out[:, 18:34] = IQ4NL[hi].view(np.uint8)
+    return out.reshape(-1)
+
+
+def test_iq4_nl_equals_q8_0_of_codebook(oracle, ref):
+    from qwen35_amd import synth
+    cols = 2560
+    w = synth.make_weight(po.TT_IQ4_NL, 48, cols, seed=9, tag=20)
+    x = synth.make_act(cols, 2, seed=9)
+    act = ref.quantize_act(po.TT_Q8_0, x)
+    got = oracle.matvec(po.TT_IQ4_NL, w, x)
+    for t in range(2):
+        want = np.array([ref.dot(po.TT_Q8_0, _iq4nl_as_q8_0(w[r], cols), act[t], cols)
+                         for r in range(48)], np.float32)
+        assert np.array_equal(got[t], want)  # same integers, same sequential fold
+    ints = oracle.block_ints(po.TT_IQ4_NL, w, act, cols)
+    w8 = np.stack([_iq4nl_as_q8_0(w[r], cols) for r in range(48)])
+    ints8 = oracle.block_ints(po.TT_Q8_0, w8, act, cols)
+    assert np.array_equal(ints, ints8)
+
+
+# ---- the reference's own fixtures (testdata/udtest) ------------------------------
+
+UD = {po.TT_Q8_0: ("Q8_0", 320), po.TT_Q4_K: ("Q4_K", 144), po.TT_Q6_K: ("Q6_K", 210),
+      po.TT_IQ4_NL: ("IQ4_NL", 144)}
+
+
+@pytest.mark.parametrize("tt", list(UD))
+def test_udtest_dequant_fixture(oracle, tt):
+    name, stride = UD[tt]
+    raw = np.fromfile(GOLD / "udtest" / f"{name}.bin", np.uint8).reshape(-1, stride)
+    exp = np.fromfile(GOLD / "udtest" / f"{name}_expected.f32", np.float32)
+    ax = np.fromfile(GOLD / "udtest" / "A_x.f32", np.float32)
+    rb = po.row_bytes(tt, 256)
+    rows = raw[:, :rb]  # Q8_0 rows carry 48 bytes of padding after 8 blocks
+    deq = np.stack([oracle.dequant_row(tt, rows[r], 256) for r in range(len(rows))])
+    err = np.abs(deq.astype(np.float64) @ ax - exp)
+    assert err.max() < 1e-3, err.max()  # quant_dequant.zig:1175-1205 bound
+    # quantized-activation row dot vs the same expectation (simd_tests256.zig:120-159 bound)
+    got = oracle.matvec(tt, np.ascontiguousarray(rows), ax[None, :])[0]
+    rel = np.abs(got - exp) / np.maximum(np.abs(exp), 1.0)
+    assert rel.max() < 5e-2, rel.max()
+    assert np.linalg.norm(got - exp) / np.linalg.norm(exp) < 5e-3
+
+
+def test_hand_computed_q8_0_block(oracle):
+    # backend_cpu.zig:1366-1379: d = 1.5, q = {0, 1, -1, 32, -128}
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.5).tobytes(), np.uint8)
+    blk[2:7] = np.array([0, 1, -1, 32, -128], np.int8).view(np.uint8)
+    deq = oracle.dequant_row(po.TT_Q8_0, blk, 32)
+    assert list(deq[:5]) == [0.0, 1.5, -1.5, 48.0, -192.0]
+
+
+# ---- driver semantics ---------------------------------------------------------------
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K, po.TT_IQ4_NL])
+def test_threads_and_batch_bit_identical(oracle, tt):
+    from qwen35_amd import synth
+    cols = 1024
+    w = synth.make_weight(tt, 300, cols, seed=2, tag=tt)
+    x = synth.make_act(cols, 3, seed=2)
+    one = oracle.matvec(tt, w, x, nthreads=1)
+    many = oracle.matvec(tt, w, x, nthreads=4)
+    assert np.array_equal(one, many)
+    for t in range(3):
+        assert np.array_equal(oracle.matvec(tt, w, x[t:t + 1], nthreads=1)[0], one[t])
+
+
+def test_zero_activation_gives_zero(oracle):
+    from qwen35_amd import synth
+    w = synth.make_weight(po.TT_Q4_K, 8, 512, seed=1)
+    out = oracle.matvec(po.TT_Q4_K, w, np.zeros((1, 512), np.float32))
+    assert np.all(out == 0)
