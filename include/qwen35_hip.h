@@ -26,8 +26,9 @@
  *   Q8_K act      292 B per 256 values: f32 d, int8 qs[256], int16 bsums[16]
  *   output        float out[t * rows + r] = W[r] . x_t
  * Fast paths need 4-byte aligned weight and activation pointers, a weight
- * byte size that is a multiple of 4, and cols a multiple of 64 (32-value
- * types); other inputs take the byte-granular generic kernel.
+ * byte size that is a multiple of 4, and cols a multiple of 64; other inputs
+ * take the byte-granular generic kernel.
+
  */
 #ifndef QWEN35_HIP_H
 #define QWEN35_HIP_H
@@ -98,15 +99,17 @@ int qhip_launch_mul_mat_vec_q8_0(const void *d_w, const void *d_xq, float *d_out
 int qhip_launch_mul_mat(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
                         int tokens, int ttype, int path, void *stream);
 
-/* The GEMV with explicit launch shape: `lanes_per_row` in {1,2,4,...,64}
- * lanes cooperate on one weight row, `tokens_per_pass` in {1,2,4,8} tokens
- * share each weight load; 0 picks the default for either.  Replaces the
- * reference's launch-shape env knobs (QWEN35_CUDA_COOP_WARPS / _SPLIT / _RPB,
- * src/kernels/cuda/mmvq.cu:685-772) with arguments.  Returns QHIP_DECLINE
- * when the fast-path preconditions do not hold. */
+/* The GEMV with explicit launch shape: `lanes_per_row` (1..64) lanes share
+ * one weight row, walking its 64-value units in turn, and fold their partial
+ * sums,
+ * and `tokens_per_pass` in {1,2,4,8} tokens share each weight load; 0 picks
+ * the default for either.  Replaces the reference's launch-shape env knobs
+ * (QWEN35_CUDA_SPLIT / _COOP_WARPS / _RPB, src/kernels/cuda/mmvq.cu:685-772)
+ * with arguments.  Returns QHIP_DECLINE when the fast-path preconditions do
+ * not hold. */
 int qhip_launch_gemv_tuned(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
                            int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
-                           void *stream);
+                           int rows_per_lane, void *stream);
 
 /* ---- ragged prefill (no reference counterpart: the reference prefills one
  * sequence per chunk, src/engine.zig:1371) -------------------------------------

@@ -41,7 +41,7 @@ SIGNATURES = {
     "qhip_launch_mul_mat": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                     c_void_p]),
     "qhip_launch_gemv_tuned": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
-                                       c_int, c_int, c_void_p]),
+                                       c_int, c_int, c_int, c_void_p]),
     "qhip_launch_quantize_ragged": (c_int, [c_int, c_void_p, c_void_p, c_int, c_int, c_int,
                                             c_void_p, c_void_p]),
     "qhip_ragged_offsets": (c_int, [c_int_p, c_int, c_int_p]),

@@ -43,9 +43,10 @@ static long weight_row_bytes(int ttype, int cols) {
 static bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 
 // Preconditions of the unit-decode kernels (see qhip_device.hpp): every load
-// is a dword-aligned access inside the unit's own bytes, which requires
-// 4-byte aligned bases, whole 64-value units, and (Q6_K, whose d is read as
-// an aligned dword) a total weight size that is a multiple of 4.
+// is a dword-aligned access inside the weight or activation buffer, which
+// requires 4-byte aligned bases, whole 64-value units, and a total weight
+// size that is a multiple of 4 (Q6_K pieces are read from the dword at or
+// below their 2-byte aligned start).
 static bool fast_ok(const GemvArgs& g) {
   if (!aligned4(g.w) || !aligned4(g.xq)) return false;
   if (g.cols % 64) return false;
@@ -73,14 +74,14 @@ hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
   const bool fast = fast_ok(g);
   switch (path) {
     case QHIP_PATH_GENERIC: return launch_gemv_generic(g, s);
-    case QHIP_PATH_GEMV: return fast ? launch_gemv(g, 0, 0, s) : launch_gemv_generic(g, s);
+    case QHIP_PATH_GEMV: return fast ? launch_gemv(g, 0, 0, 0, s) : launch_gemv_generic(g, s);
     case QHIP_PATH_MMQ: return (hipError_t)QHIP_DECLINE;
     case QHIP_PATH_AUTO:
       if (!fast) return launch_gemv_generic(g, s);
       if (g.tokens >= mmq_min_tokens(g.ttype)) {
         // MMQ path (declines fall through to the GEMV)
       }
-      return launch_gemv(g, 0, 0, s);
+      return launch_gemv(g, 0, 0, 0, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -281,15 +282,17 @@ int qhip_launch_mul_mat_vec_q8_0(const void* d_w, const void* d_xq, float* d_out
 
 int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
                            int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
-                           void* stream) {
+                           int rows_per_lane, void* stream) {
   GemvArgs g;
   hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
-  const int l = lanes_per_row, n = tokens_per_pass;
-  if (l < 0 || l > 64 || (l & (l - 1)) || n < 0 || n > 8 || (n & (n - 1)))
+  const int n = tokens_per_pass, nr = rows_per_lane;
+  if (lanes_per_row < 0 || lanes_per_row > 64 || n < 0 || n > 8 || (n & (n - 1)))
+    return (int)hipErrorInvalidValue;
+  if (nr < 0 || nr > 4 || nr == 3 || (nr > 2 && n > 1) || (nr > 1 && n > 2))
     return (int)hipErrorInvalidValue;
   if (!fast_ok(g)) return QHIP_DECLINE;
-  return (int)launch_gemv(g, l, n, S(stream));
+  return (int)launch_gemv(g, lanes_per_row, n, nr, S(stream));
 }
 
 int qhip_ragged_offsets(const int* lengths, int nseq, int* offsets) {

@@ -1,17 +1,11 @@
 // qhip_device.hpp -- device-side building blocks shared by the quantizer,
 // GEMV and MMQ kernels: GGUF block geometry, exact f16 handling, int8 dot
-// primitives and the per-format decode of one 64-value work unit.
+// primitives, the IQ4_NL codebook lookup and the per-format decode of one
+// 64-value work unit.
 //
-// Work unit.  Every kernel walks a weight row in units of 64 values:
-//   Q8_0    two 34-byte blocks          (68 B, blocks 2u and 2u+1)
-//   IQ4_NL  two 18-byte blocks          (36 B)
-//   Q4_K    one quarter of a 144-byte super-block: 32 B of nibbles (sub-blocks
-//           2c and 2c+1) plus the shared 16-byte header
-//   Q6_K    one quarter of a 210-byte super-block: (h, l-half) of the
-//           ql/qh planes, four 16-value groups
-// Q8_0 and IQ4_NL pair with a Q8_0 activation (34 B / 32 values), Q4_K and
-// Q6_K with a Q8_K activation (292 B / 256 values), as the reference's
-// actFamily (src/backend_cpu.zig:42-50) prescribes.
+// Q8_0 and IQ4_NL weights pair with a Q8_0 activation (34 B / 32 values),
+// Q4_K and Q6_K with a Q8_K activation (292 B / 256 values), as the
+// reference's actFamily (src/backend_cpu.zig:42-50) prescribes.
 //
 // Integer arithmetic inside a block is exact and equals the reference's
 // per-block integers (src/kernels/x86/kernels32.c:342-361, :447-464;
@@ -86,115 +80,158 @@ __device__ __forceinline__ int trunc_i32_x86(float v) {
 // ---- IQ4_NL codebook lookup on 4 packed indices --------------------------------
 // Codebook (reference src/iq_tables.zig:429-432):
 //   -127 -104 -83 -65 -49 -35 -22 -10 1 13 25 38 53 69 89 113
-// v_perm_b32 selects bytes 0..7 of {src0:src1}; entries 0..7 and 8..15 are two
-// 8-byte tables indexed by the low 3 bits, merged by bit 3 of each index.
+// v_perm_b32 selects bytes 0..7 of {src0:src1}.  Entries 0..7 and 8..15 are two
+// 8-byte tables looked up with the low 3 index bits; a third perm then picks,
+// per byte, the entry of the table that bit 3 names (selector byte i or 4+i).
 constexpr uint32_t IQ4_T0 = 0xBFAD9881u;  // -127 -104  -83  -65
 constexpr uint32_t IQ4_T1 = 0xF6EADDCFu;  //  -49  -35  -22  -10
 constexpr uint32_t IQ4_T2 = 0x26190D01u;  //    1   13   25   38
 constexpr uint32_t IQ4_T3 = 0x71594535u;  //   53   69   89  113
 
-// sel: four indices in 0..7 (one per byte); bit3: per-byte 0x80 when the
-// index is >= 8 (other bits ignored).
-__device__ __forceinline__ uint32_t iq4_lut(uint32_t sel, uint32_t bit3) {
-  const uint32_t lo = __builtin_amdgcn_perm(IQ4_T1, IQ4_T0, sel);
-  const uint32_t hi = __builtin_amdgcn_perm(IQ4_T3, IQ4_T2, sel);
-  // replicate bit 7 of every byte of bit3 across its byte
-  const uint32_t m = (bit3 >> 7) & 0x01010101u;
-  const uint32_t mask = (m << 8) - m;
-  return (hi & mask) | (lo & ~mask);
+__device__ __forceinline__ uint32_t iq4_lookup(uint32_t s7, uint32_t pick) {
+  const uint32_t lo = __builtin_amdgcn_perm(IQ4_T1, IQ4_T0, s7);
+  const uint32_t hi = __builtin_amdgcn_perm(IQ4_T3, IQ4_T2, s7);
+  return __builtin_amdgcn_perm(hi, lo, pick);
 }
 // Low / high nibbles of 4 packed bytes -> 4 int8 codebook values.
-__device__ __forceinline__ uint32_t iq4_lo(uint32_t q) { return iq4_lut(q & 0x07070707u, q << 4); }
-__device__ __forceinline__ uint32_t iq4_hi(uint32_t q) { return iq4_lut((q >> 4) & 0x07070707u, q); }
-
-// ---- Q4_K 6-bit scale / min of sub-block j (0..7) -------------------------------
-// s0,s1,s2 are the 12 packed bytes (header bytes 4..15).  ggml's
-// get_scale_min_k4 rule, equal to the reference unpack at
-// src/kernels/x86/kernels256.c:105-125.
-__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
-                                              int& sc, int& mn) {
-  const uint32_t sh = 8u * (uint32_t)(j & 3);
-  const uint32_t b0 = (s0 >> sh) & 0xFFu, b1 = (s1 >> sh) & 0xFFu, b2 = (s2 >> sh) & 0xFFu;
-  if (j < 4) {
-    sc = (int)(b0 & 63u);
-    mn = (int)(b1 & 63u);
-  } else {
-    sc = (int)((b2 & 15u) | ((b0 >> 6) << 4));
-    mn = (int)((b2 >> 4) | ((b1 >> 6) << 4));
-  }
+__device__ __forceinline__ uint32_t iq4_lo(uint32_t q) {
+  return iq4_lookup(q & 0x07070707u, ((q >> 1) & 0x04040404u) | 0x03020100u);
+}
+__device__ __forceinline__ uint32_t iq4_hi(uint32_t q) {
+  return iq4_lookup((q >> 4) & 0x07070707u, ((q >> 5) & 0x04040404u) | 0x03020100u);
 }
 
 // ---- per-format unit decode ------------------------------------------------------
-// Each format provides
-//   W             weight registers of one unit
-//   load_w        (row base, unit) -> W
-//   A             activation registers of one unit
-//   load_a        (activation row base, unit) -> A
-//   dot           W x A -> float contribution (scaled, for GEMV)
-//   ints          W x A -> exact integer partials of the unit (for parity)
+// Every GEMV lane walks a weight row in units of 64 values:
+//   Q8_0    two 34-byte blocks (68 B, blocks 2u and 2u+1)
+//   IQ4_NL  two 18-byte blocks (36 B)
+//   Q4_K    one quarter of a 144-byte super-block: 32 B of nibbles (sub-blocks
+//           2c and 2c+1) plus the shared 16-byte header
+//   Q6_K    one quarter of a 210-byte super-block: the (h, l-half) slice of the
+//           ql/qh planes, four 16-value groups
+// Consecutive units of a row are adjacent in memory.
+//
+// Each format gives
+//   W, load_w(row, u)      weight registers of unit u, canonical (quants
+//                          dword-aligned); `row` may point to global memory or
+//                          to a copy of the row bytes in LDS
+//   A, load_a(act, u)      activation registers of unit u from a quantized
+//                          activation row in the reference layout (global)
+//      load_a_split(sp, u) the same from the split layout in LDS (ActSplit)
+//   ints(w, a, out)        the unit's exact integer partials
+//   dot(w, a)              the unit's float contribution, built on ints()
+// so the GEMV paths and the parity export share one integer core.
 template <int TT>
 struct Unit;
 
+// Activation in LDS, split into planes (all 16-byte aligned):
+//   qs  int8 values, `cols` bytes
+//   d   per-block f32 scale (32-value blocks for Q8_0, 256 for Q8_K)
+//   bs  Q8_K only: int16 sums of each 16 values
+struct ActSplit {
+  const uint8_t* qs;
+  const float* d;
+  const int16_t* bs;
+};
+
+// 68-byte Q8_0 block pair (d0 q0[32] d1 q1[32]) at a 4-byte aligned address,
+// canonicalised: q[0..7] block 0 quants, q[8..15] block 1 quants.
+__device__ __forceinline__ void load_q8_pair(const uint8_t* p, uint32_t* q, uint32_t& d0, uint32_t& d1) {
+  uint32_t v[17];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 x = ld128(p + 16 * i);
+    v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
+  }
+  v[16] = ld32(p + 64);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[i] = funnel(v[i + 1], v[i], 2);  // bytes 2..33
+#pragma unroll
+  for (int i = 0; i < 8; ++i) q[8 + i] = v[9 + i];                 // bytes 36..67
+  d0 = v[0] & 0xFFFFu;
+  d1 = v[8] >> 16;
+}
+
+// activation of a 32-value-block weight: two Q8_0 blocks (64 values)
+struct ActPair {
+  uint32_t q[16];
+  float d0, d1;
+};
+__device__ __forceinline__ ActPair act_pair_ref(const uint8_t* act, int u) {
+  ActPair a;
+  uint32_t d0, d1;
+  load_q8_pair(act + 68 * u, a.q, d0, d1);
+  a.d0 = h2f(d0);
+  a.d1 = h2f(d1);
+  return a;
+}
+__device__ __forceinline__ ActPair act_pair_split(const ActSplit& sp, int u) {
+  ActPair a;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 x = *(const u32x4*)(sp.qs + 64 * u + 16 * i);
+    a.q[4 * i] = x.x; a.q[4 * i + 1] = x.y; a.q[4 * i + 2] = x.z; a.q[4 * i + 3] = x.w;
+  }
+  a.d0 = sp.d[2 * u];
+  a.d1 = sp.d[2 * u + 1];
+  return a;
+}
+
 template <>
 struct Unit<TT_Q8_0> {
-  static constexpr int kVals = 64, kWBytes = 68, kABytes = 68, kInts = 2;
-  struct W { uint32_t v[17]; };
-  struct A { uint32_t v[17]; };
-  static __device__ __forceinline__ void load17(const uint8_t* p, uint32_t* v) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 x = ld128(p + 16 * i);
-      v[4 * i] = x.x; v[4 * i + 1] = x.y; v[4 * i + 2] = x.z; v[4 * i + 3] = x.w;
-    }
-    v[16] = ld32(p + 64);
-  }
+  static constexpr int kWBytes = 68, kInts = 2;
+  struct W { uint32_t q[16]; uint32_t d0, d1; };
+  using A = ActPair;
   static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
-    W w; load17(row + 68 * u, w.v); return w;
+    W w;
+    load_q8_pair(row + 68 * u, w.q, w.d0, w.d1);
+    return w;
   }
-  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) {
-    A a; load17(act + 68 * u, a.v); return a;
-  }
-  // Both sides share the 34-byte block layout, so byte k of the weight dword
-  // pairs with byte k of the activation dword; the two scale bytes inside
-  // dwords 0 and 8 are masked off on the weight side.
-  static __device__ __forceinline__ void sums(const W& w, const A& a, int& s0, int& s1) {
-    s0 = dot4(w.v[0] & 0xFFFF0000u, a.v[0], 0);
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return act_pair_ref(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) { return act_pair_split(sp, u); }
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* s) {
+    int s0 = 0, s1 = 0;
 #pragma unroll
-    for (int i = 1; i < 8; ++i) s0 = dot4(w.v[i], a.v[i], s0);
-    s0 = dot4(w.v[8] & 0x0000FFFFu, a.v[8], s0);
-    s1 = 0;
-#pragma unroll
-    for (int i = 9; i < 17; ++i) s1 = dot4(w.v[i], a.v[i], s1);
+    for (int i = 0; i < 8; ++i) {
+      s0 = dot4(w.q[i], a.q[i], s0);
+      s1 = dot4(w.q[8 + i], a.q[8 + i], s1);
+    }
+    s[0] = s0;
+    s[1] = s1;
   }
   static __device__ __forceinline__ float dot(const W& w, const A& a) {
-    int s0, s1;
-    sums(w, a, s0, s1);
-    const float d0 = h2f(w.v[0]) * h2f(a.v[0]);
-    const float d1 = h2f(w.v[8] >> 16) * h2f(a.v[8] >> 16);
-    return d0 * (float)s0 + d1 * (float)s1;
+    int s[2];
+    ints(w, a, s);
+    return (h2f(w.d0) * a.d0) * (float)s[0] + (h2f(w.d1) * a.d1) * (float)s[1];
   }
-  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) { sums(w, a, out[0], out[1]); }
 };
 
 template <>
 struct Unit<TT_IQ4_NL> {
-  static constexpr int kVals = 64, kWBytes = 36, kABytes = 68, kInts = 2;
-  struct W { uint32_t v[9]; };
-  using A = Unit<TT_Q8_0>::A;
+  static constexpr int kWBytes = 36, kInts = 2;
+  struct W { uint32_t q[8]; uint32_t d0, d1; };  // q[0..3] block 0 indices, q[4..7] block 1
+  using A = ActPair;
   static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
     const uint8_t* p = row + 36 * u;
-    W w;
+    uint32_t v[9];
     const u32x4 x0 = ld128(p), x1 = ld128(p + 16);
-    w.v[0] = x0.x; w.v[1] = x0.y; w.v[2] = x0.z; w.v[3] = x0.w;
-    w.v[4] = x1.x; w.v[5] = x1.y; w.v[6] = x1.z; w.v[7] = x1.w;
-    w.v[8] = ld32(p + 32);
+    v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+    v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    v[8] = ld32(p + 32);
+    W w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      w.q[i] = funnel(v[i + 1], v[i], 2);  // block 0 indices: bytes 2..17
+      w.q[4 + i] = v[5 + i];               // block 1 indices: bytes 20..35
+    }
+    w.d0 = v[0] & 0xFFFFu;
+    w.d1 = v[4] >> 16;
     return w;
   }
-  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) {
-    return Unit<TT_Q8_0>::load_a(act, u);
-  }
-  // One block: q[4] packed index bytes (byte j: low nibble -> value j, high
-  // nibble -> value j+16), y[8] activation qs dwords (values 0..31).
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return act_pair_ref(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) { return act_pair_split(sp, u); }
+  // one block: 4 index dwords (byte j: low nibble -> value j, high nibble ->
+  // value j+16) against 8 activation dwords (values 0..31)
   static __device__ __forceinline__ int block(const uint32_t* q, const uint32_t* y) {
     int s = 0;
 #pragma unroll
@@ -204,37 +241,31 @@ struct Unit<TT_IQ4_NL> {
     }
     return s;
   }
-  static __device__ __forceinline__ void sums(const W& w, const A& a, int& s0, int& s1) {
-    uint32_t q0[4], q1[4], y0[8], y1[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      q0[i] = funnel(w.v[i + 1], w.v[i], 2);  // block 0 indices: bytes 2..17
-      q1[i] = w.v[5 + i];                      // block 1 indices: bytes 20..35
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      y0[i] = funnel(a.v[i + 1], a.v[i], 2);  // activation block 0 qs: bytes 2..33
-      y1[i] = a.v[9 + i];                      // activation block 1 qs: bytes 36..67
-    }
-    s0 = block(q0, y0);
-    s1 = block(q1, y1);
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* s) {
+    s[0] = block(w.q, a.q);
+    s[1] = block(w.q + 4, a.q + 8);
   }
   static __device__ __forceinline__ float dot(const W& w, const A& a) {
-    int s0, s1;
-    sums(w, a, s0, s1);
-    const float d0 = h2f(w.v[0]) * h2f(a.v[0]);
-    const float d1 = h2f(w.v[4] >> 16) * h2f(a.v[8] >> 16);
-    return d0 * (float)s0 + d1 * (float)s1;
+    int s[2];
+    ints(w, a, s);
+    return (h2f(w.d0) * a.d0) * (float)s[0] + (h2f(w.d1) * a.d1) * (float)s[1];
   }
-  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) { sums(w, a, out[0], out[1]); }
+};
+
+// activation of a K-quant quarter unit: 64 Q8_K values, the block scale and
+// the four 16-value sums the unit needs
+struct ActQ8K {
+  uint32_t y[16];
+  float d;
+  int bs[4];
 };
 
 template <>
 struct Unit<TT_Q4_K> {
   // unit u: super-block u>>2, quarter c = u&3 (values 64c..64c+63)
-  static constexpr int kVals = 64, kWBytes = 48, kABytes = 64, kInts = 2;
+  static constexpr int kWBytes = 48, kInts = 2;
   struct W { uint32_t hdr[4]; uint32_t q[8]; int c; };
-  struct A { uint32_t y[16]; float d; uint32_t bs01, bs23; };
+  using A = ActQ8K;
   static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
     const uint8_t* blk = row + 144 * (u >> 2);
     W w;
@@ -246,6 +277,7 @@ struct Unit<TT_Q4_K> {
     w.q[4] = b.x; w.q[5] = b.y; w.q[6] = b.z; w.q[7] = b.w;
     return w;
   }
+  // bsums of this quarter: groups 4c..4c+3
   static __device__ __forceinline__ A load_a(const uint8_t* act, int u) {
     const uint8_t* blk = act + 292 * (u >> 2);
     const int c = u & 3;
@@ -256,42 +288,65 @@ struct Unit<TT_Q4_K> {
       a.y[4 * i] = x.x; a.y[4 * i + 1] = x.y; a.y[4 * i + 2] = x.z; a.y[4 * i + 3] = x.w;
     }
     a.d = __builtin_bit_cast(float, ld32(blk));
-    a.bs01 = ld32(blk + 260 + 8 * c);
-    a.bs23 = ld32(blk + 264 + 8 * c);
+    const uint32_t b01 = ld32(blk + 260 + 8 * c), b23 = ld32(blk + 264 + 8 * c);
+    a.bs[0] = sext16(b01); a.bs[1] = sext16(b01 >> 16);
+    a.bs[2] = sext16(b23); a.bs[3] = sext16(b23 >> 16);
+    return a;
+  }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    const int sb = u >> 2, c = u & 3;
+    A a;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 x = *(const u32x4*)(sp.qs + 256 * sb + 64 * c + 16 * i);
+      a.y[4 * i] = x.x; a.y[4 * i + 1] = x.y; a.y[4 * i + 2] = x.z; a.y[4 * i + 3] = x.w;
+    }
+    a.d = sp.d[sb];
+    const u32x2 b = *(const u32x2*)(sp.bs + 16 * sb + 4 * c);
+    a.bs[0] = sext16(b.x); a.bs[1] = sext16(b.x >> 16);
+    a.bs[2] = sext16(b.y); a.bs[3] = sext16(b.y >> 16);
     return a;
   }
   // isum over sub-blocks 2c (low nibbles) and 2c+1 (high nibbles); summs over
-  // the bsums of those two sub-blocks.
-  static __device__ __forceinline__ void sums(const W& w, const A& a, int& isum, int& summs) {
+  // the bsums of those two sub-blocks.  The 6-bit scales and mins are unpacked
+  // four at a time with the rule of src/kernels/x86/kernels256.c:105-125
+  // applied bytewise, then the pair of this quarter is shifted out.
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
     int lo = 0, hi = 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       lo = dot4(w.q[i] & 0x0F0F0F0Fu, a.y[i], lo);
       hi = dot4((w.q[i] >> 4) & 0x0F0F0F0Fu, a.y[8 + i], hi);
     }
-    int sc0, m0, sc1, m1;
-    q4k_scale_min(w.hdr[1], w.hdr[2], w.hdr[3], 2 * w.c, sc0, m0);
-    q4k_scale_min(w.hdr[1], w.hdr[2], w.hdr[3], 2 * w.c + 1, sc1, m1);
-    isum = sc0 * lo + sc1 * hi;
-    summs = m0 * (sext16(a.bs01) + sext16(a.bs01 >> 16)) + m1 * (sext16(a.bs23) + sext16(a.bs23 >> 16));
+    const uint32_t S0 = w.hdr[1], S1 = w.hdr[2], S2 = w.hdr[3];
+    const bool upper = w.c >= 2;  // sub-blocks 4..7
+    const uint32_t scw = upper ? ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u)) : (S0 & 0x3F3F3F3Fu);
+    const uint32_t mnw = upper ? (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) : (S1 & 0x3F3F3F3Fu);
+    const uint32_t sh = 16u * (uint32_t)(w.c & 1);
+    const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+    const int m0 = (int)((mnw >> sh) & 0xFFu), m1 = (int)((mnw >> (sh + 8)) & 0xFFu);
+    out[0] = sc0 * lo + sc1 * hi;
+    out[1] = m0 * (a.bs[0] + a.bs[1]) + m1 * (a.bs[2] + a.bs[3]);
   }
   static __device__ __forceinline__ float dot(const W& w, const A& a) {
-    int isum, summs;
-    sums(w, a, isum, summs);
+    int s[2];
+    ints(w, a, s);
     const float d = a.d * h2f(w.hdr[0]);
     const float dmin = a.d * h2f(w.hdr[0] >> 16);
-    return d * (float)isum - dmin * (float)summs;
+    return d * (float)s[0] - dmin * (float)s[1];
   }
-  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) { sums(w, a, out[0], out[1]); }
 };
 
 template <>
 struct Unit<TT_Q6_K> {
-  // unit u: super-block u>>2, h = (u>>1)&1, lh = u&1; values 128h + 32q + 16lh + (0..15), q=0..3
-  static constexpr int kVals = 64, kWBytes = 52, kABytes = 64, kInts = 1;
+  // unit u: super-block u>>2, h = (u>>1)&1, lh = u&1; values
+  // 128h + 32q + 16lh + (0..15) for q = 0..3, in 16-value groups 8h + lh + 2q
+  static constexpr int kWBytes = 52, kInts = 1;
   struct W { uint32_t la[4], lb[4], qh[4]; uint32_t sc01, sc23; uint32_t d; };
-  struct A { uint32_t y[16]; float d; uint32_t bs[4]; int lh; };
-  // 16 bytes at a 2-byte aligned address: 5 aligned dwords, funnel-shifted.
+  using A = ActQ8K;
+  // 16 bytes at a 2-byte aligned address: 5 aligned dwords, funnel-shifted
+  // (the reads stay inside the super-block, or the weight buffer, whose size
+  // is a multiple of 4).
   static __device__ __forceinline__ void load16(const uint8_t* p, uint32_t* out) {
     const uint32_t sh = (uint32_t)(uintptr_t)p & 3u;
     const uint8_t* b = p - sh;
@@ -331,14 +386,30 @@ struct Unit<TT_Q6_K> {
       a.y[4 * q] = x.x; a.y[4 * q + 1] = x.y; a.y[4 * q + 2] = x.z; a.y[4 * q + 3] = x.w;
     }
     const u32x4 b = ld128(blk + 260 + 16 * h);  // bsums of groups 8h..8h+7
-    a.bs[0] = b.x; a.bs[1] = b.y; a.bs[2] = b.z; a.bs[3] = b.w;
+    const int sh = 16 * lh;
+    a.bs[0] = sext16(b.x >> sh); a.bs[1] = sext16(b.y >> sh);
+    a.bs[2] = sext16(b.z >> sh); a.bs[3] = sext16(b.w >> sh);
     a.d = __builtin_bit_cast(float, ld32(blk));
-    a.lh = lh;
     return a;
   }
-  // isum of the unit's four 16-value groups g = 8h + lh + 2q:
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    const int sb = u >> 2, h = (u >> 1) & 1, lh = u & 1;
+    A a;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 x = *(const u32x4*)(sp.qs + 256 * sb + 128 * h + 32 * q + 16 * lh);
+      a.y[4 * q] = x.x; a.y[4 * q + 1] = x.y; a.y[4 * q + 2] = x.z; a.y[4 * q + 3] = x.w;
+    }
+    const u32x4 b = *(const u32x4*)(sp.bs + 16 * sb + 8 * h);
+    const int sh = 16 * lh;
+    a.bs[0] = sext16(b.x >> sh); a.bs[1] = sext16(b.y >> sh);
+    a.bs[2] = sext16(b.z >> sh); a.bs[3] = sext16(b.w >> sh);
+    a.d = sp.d[sb];
+    return a;
+  }
+  // isum of the unit's four 16-value groups:
   //   sum_q sc[g] * sum_l (q6 - 32) * q8  =  sum_q sc[g] * (sum_l q6*q8 - 32*bsum[g])
-  static __device__ __forceinline__ int isum(const W& w, const A& a) {
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
     int s[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -352,16 +423,15 @@ struct Unit<TT_Q6_K> {
       s[2] = dot4(v2, a.y[8 + i], s[2]);
       s[3] = dot4(v3, a.y[12 + i], s[3]);
     }
-    const int sh = 16 * a.lh;
     const int sc0 = sext8(w.sc01), sc1 = sext8(w.sc01 >> 16), sc2 = sext8(w.sc23), sc3 = sext8(w.sc23 >> 16);
-    const int b0 = sext16(a.bs[0] >> sh), b1 = sext16(a.bs[1] >> sh);
-    const int b2 = sext16(a.bs[2] >> sh), b3 = sext16(a.bs[3] >> sh);
-    return sc0 * (s[0] - 32 * b0) + sc1 * (s[1] - 32 * b1) + sc2 * (s[2] - 32 * b2) + sc3 * (s[3] - 32 * b3);
+    out[0] = sc0 * (s[0] - 32 * a.bs[0]) + sc1 * (s[1] - 32 * a.bs[1]) + sc2 * (s[2] - 32 * a.bs[2]) +
+             sc3 * (s[3] - 32 * a.bs[3]);
   }
   static __device__ __forceinline__ float dot(const W& w, const A& a) {
-    return (h2f(w.d) * a.d) * (float)isum(w, a);
+    int s[1];
+    ints(w, a, s);
+    return (h2f(w.d) * a.d) * (float)s[0];
   }
-  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) { out[0] = isum(w, a); }
 };
 
 }  // namespace qhip

@@ -21,9 +21,13 @@ hipError_t launch_quantize_q8_0(const float* x, void* out, long nblocks, int tok
 hipError_t launch_quantize_q8_K(const float* x, void* out, long nblocks, int tokens, long x_stride,
                                 long out_stride, hipStream_t s);
 
-int gemv_pick_tpr(int rows, int cols);
+// Waves a GEMV launch aims for (8 per CU on 256 CUs) when choosing lanes per row.
+constexpr int kGemvTargetWaves = 2048;
+int gemv_pick_team(int rows, int cols, int target_waves);
 int gemv_pick_nt(int tokens);
-hipError_t launch_gemv(const GemvArgs& g, int tpr, int nt, hipStream_t s);
+// team: lanes per row group (0 = pick), nt: tokens per pass (0 = pick),
+// nr: rows per lane (1, 2 or 4; 0 = 1)
+hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t s);
 hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s);
 hipError_t launch_block_ints(const GemvArgs& g, int* ints, hipStream_t s);
 

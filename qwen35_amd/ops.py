@@ -72,12 +72,13 @@ def mul_mat(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
 
 
 def gemv_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
-               lanes_per_row: int, tokens_per_pass: int, out: torch.Tensor | None = None) -> torch.Tensor:
+               lanes_per_row: int, tokens_per_pass: int, rows_per_lane: int = 1,
+               out: torch.Tensor | None = None) -> torch.Tensor:
     if out is None:
         out = torch.empty((tokens, rows), dtype=torch.float32, device=w.device)
     check("gemv_tuned", load().qhip_launch_gemv_tuned(_p(w), _p(xq), _p(out), rows, cols, tokens,
                                                       ttype, lanes_per_row, tokens_per_pass,
-                                                      _stream()))
+                                                      rows_per_lane, _stream()))
     return out
 
 
