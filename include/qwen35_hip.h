@@ -111,6 +111,22 @@ int qhip_launch_gemv_tuned(const void *d_w, const void *d_xq, float *d_out, int 
                            int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
                            int rows_per_lane, void *stream);
 
+/* ---- batched prefill on int8 MFMA tiles (MMQ) -----------------------------------
+ * q35_launch_mul_mat_vec_tile (src/kernels/cuda/mmq.cu:2232-2336): the same
+ * product as qhip_launch_mul_mat_vec for a batch of tokens, on 32x32 int8 MFMA
+ * tiles.  Returns QHIP_DECLINE when the fast-path preconditions above do not
+ * hold (the caller then uses qhip_launch_mul_mat_vec, as mmvq.cu:789-800 does).
+ * Unlike the reference it serves every type here (Q8_0 included) and any
+ * token count. */
+int qhip_launch_mul_mat_vec_tile(const void *d_w, const void *d_xq, float *d_out, int rows,
+                                 int cols, int tokens, int ttype, void *stream);
+/* The MMQ with an explicit workgroup tile: `tile_tokens` x `tile_rows`
+ * outputs, each 64 or 128 (0 picks).  Replaces the reference's compile-time
+ * tile constants (mmq.cu, 128 rows x 8 tokens per CTA) with arguments.
+ * Returns QHIP_DECLINE when the fast-path preconditions do not hold. */
+int qhip_launch_mmq_tuned(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
+                          int tokens, int ttype, int tile_tokens, int tile_rows, void *stream);
+
 /* ---- ragged prefill (no reference counterpart: the reference prefills one
  * sequence per chunk, src/engine.zig:1371) -------------------------------------
  * Sequence i owns packed tokens [offsets[i], offsets[i+1]); offsets has
@@ -126,7 +142,8 @@ int qhip_launch_quantize_ragged(int ttype, const float *const *d_src, const int 
  * or -1 for a negative length or overflow. */
 int qhip_ragged_offsets(const int *lengths, int nseq, int *offsets);
 /* One launch over all sequences: out[p*rows + r] = W[r] . xq[p] for every
- * packed token p; token tiles never straddle a sequence boundary. */
+ * packed token p (GEMV or MMQ by the total token count).  Every packed token
+ * row is an independent product, so MMQ token tiles may span sequences. */
 int qhip_launch_mul_mat_ragged(const void *d_w, const void *d_xq_packed, float *d_out, int rows,
                                int cols, const int *d_offsets, int nseq, int total_tokens,
                                int ttype, void *stream);

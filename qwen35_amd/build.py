@@ -28,9 +28,14 @@ FLAGS = [
 ]
 
 
+# Per-file additions.  mmq.hip: keep MFMA accumulators in ordinary VGPRs, so
+# the per-element scaling reads them without v_accvgpr_read copies.
+FILE_FLAGS = {"mmq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

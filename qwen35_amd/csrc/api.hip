@@ -65,9 +65,9 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
   return hipSuccess;
 }
 
-// Token count above which the MMQ tiles beat the weight-streaming GEMV
-// (measured crossover; the GEMV re-reads weights once per 8 tokens).
-static int mmq_min_tokens(int /*ttype*/) { return 1 << 30; }
+// Token count from which the MMQ tiles beat the weight-streaming GEMV (the
+// GEMV re-reads the weights once per 8 tokens; the MMQ once per 64 or 128).
+static int mmq_min_tokens(int /*ttype*/) { return 16; }
 
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
   if (g.rows == 0 || g.tokens == 0) return hipSuccess;
@@ -75,12 +75,10 @@ hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
   switch (path) {
     case QHIP_PATH_GENERIC: return launch_gemv_generic(g, s);
     case QHIP_PATH_GEMV: return fast ? launch_gemv(g, 0, 0, 0, s) : launch_gemv_generic(g, s);
-    case QHIP_PATH_MMQ: return (hipError_t)QHIP_DECLINE;
+    case QHIP_PATH_MMQ: return fast ? launch_mmq(g, 0, 0, s) : (hipError_t)QHIP_DECLINE;
     case QHIP_PATH_AUTO:
       if (!fast) return launch_gemv_generic(g, s);
-      if (g.tokens >= mmq_min_tokens(g.ttype)) {
-        // MMQ path (declines fall through to the GEMV)
-      }
+      if (g.tokens >= mmq_min_tokens(g.ttype)) return launch_mmq(g, 0, 0, s);
       return launch_gemv(g, 0, 0, 0, s);
     default: return hipErrorInvalidValue;
   }
@@ -293,6 +291,23 @@ int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int 
     return (int)hipErrorInvalidValue;
   if (!fast_ok(g)) return QHIP_DECLINE;
   return (int)launch_gemv(g, lanes_per_row, n, nr, S(stream));
+}
+
+int qhip_launch_mmq_tuned(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
+                          int tokens, int ttype, int tile_tokens, int tile_rows, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  const bool bt_ok = tile_tokens == 0 || tile_tokens == 64 || tile_tokens == 128;
+  const bool br_ok = tile_rows == 0 || tile_rows == 64 || tile_rows == 128;
+  if (!bt_ok || !br_ok) return (int)hipErrorInvalidValue;
+  if (!fast_ok(g)) return QHIP_DECLINE;
+  return (int)launch_mmq(g, tile_tokens, tile_rows, S(stream));
+}
+
+int qhip_launch_mul_mat_vec_tile(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
+                                 int tokens, int ttype, void* stream) {
+  return qhip_launch_mul_mat(d_w, d_xq, d_out, rows, cols, tokens, ttype, QHIP_PATH_MMQ, stream);
 }
 
 int qhip_ragged_offsets(const int* lengths, int nseq, int* offsets) {

@@ -1,0 +1,489 @@
+// mmq.hip -- batched / ragged quantized matrix product (prefill) on int8 MFMA.
+//
+// out[t*rows + r] = W[r] . xq[t] for many tokens at once (reference contract:
+// src/kernels/cuda/mmq.cu:2232-2336, reached from mmvq.cu:789 when tokens > 1).
+//
+// Tiling.  A workgroup of four waves owns a BT-token x BR-row output tile; the
+// waves split it 2 x 2 and each wave covers its quarter with 32x32 MFMA
+// tiles.  The K dimension is walked in chunks of 256 values: the chunk's
+// weight bytes (BR rows) and activation bytes (BT tokens) are decoded into
+// plain int8 rows in LDS (IQ4_NL codebook lookup, Q4_K nibbles, Q6_K 6-bit
+// values minus 32), plus each format's scales, then the MFMAs read aligned
+// 16-byte fragments from there.
+//
+// Operand roles.  MFMA operand A carries the activations (tile rows = tokens),
+// operand B the weights (tile columns = rows), so in the accumulator layout
+// every lane holds ONE weight row and 16 tokens: weight-side scales are lane
+// scalars, token-side scales are read per element.
+//
+// Exactness.  Each MFMA covers exactly one scale group of the format, so its
+// int32 result is the reference's per-block integer:
+//   Q8_0, IQ4_NL  v_mfma_i32_32x32x32_i8 per 32-value block
+//                 (src/kernels/x86/kernels32.c:447-464, :342-361)
+//   Q4_K          v_mfma_i32_32x32x32_i8 per 32-value sub-block, times its
+//                 6-bit scale in integer arithmetic; the mins term
+//                 sum_j bsum[j]*min[j/2] as an exact f16 MFMA (K = 16
+//                 bsums, all partial sums < 2^24)  (kernels256.c:474-498)
+//   Q6_K          v_mfma_i32_32x32x16_i8 per 16-value group, times its int8
+//                 scale in integer arithmetic  (kernels256.c:720-738)
+// and the float scaling follows per block / super-block.  For the 32-value
+// formats the accumulator input is the bit pattern of 1.5*2^23, so the MFMA
+// result read as a float is 1.5*2^23 + sumi exactly (|sumi| <= 2^19); one
+// fma removes the offset while applying the weight scale:
+//   dw*sumi = fma(F, dw, -1.5*2^23*dw)      (the product -1.5*2^23*dw is exact)
+// which saves the int->float conversion per element.
+#include "qhip_device.hpp"
+#include "qhip_internal.hpp"
+
+#include <type_traits>
+
+namespace qhip {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef long i64x1_a8 __attribute__((aligned(8)));
+
+constexpr int kChunk = 256;         // values per staged K-chunk
+constexpr int kQS = kChunk + 16;    // LDS bytes per int8 row (pad: rows 4 banks apart)
+constexpr float kBias = 12582912.0f;  // 1.5 * 2^23
+constexpr int kBiasBits = 0x4B400000;
+
+// ---- LDS images ---------------------------------------------------------------------
+template <int TT, int BT, int BR, bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL)>
+struct MmqSmem;
+
+template <int TT, int BT, int BR>
+struct alignas(16) MmqSmem<TT, BT, BR, true> {
+  uint8_t aq[BT * kQS];
+  uint8_t bq[BR * kQS];
+  float ad[8][BT];  // activation block scales of the chunk
+  float wd[8][BR];  // weight block scales
+};
+
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_Q4_K, BT, BR, false> {
+  uint8_t aq[BT * kQS];
+  uint8_t bq[BR * kQS];
+  _Float16 abs[BT][16];  // activation 16-value sums (exact in f16: |bsum| <= 2032)
+  _Float16 wmn[BR][16];  // min of the sub-block of each 16-value group
+  float ady[BT];
+  float wd[BR], wdmin[BR];
+  uint32_t wsc[BR][2];  // eight 6-bit sub-block scales, one per byte
+};
+
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_Q6_K, BT, BR, false> {
+  uint8_t aq[BT * kQS];
+  uint8_t bq[BR * kQS];
+  float ady[BT];
+  float wd[BR];
+  uint32_t wsc[BR][4];  // sixteen int8 group scales
+};
+
+__device__ __forceinline__ void st16(uint8_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  *(uint4*)p = make_uint4(a, b, c, d);
+}
+
+// q6 - 32 on four packed 6-bit values: flip bit 5, then sign-extend from it
+__device__ __forceinline__ uint32_t q6_minus32(uint32_t v) {
+  const uint32_t x = v ^ 0x20202020u;
+  const uint32_t s = x & 0x20202020u;
+  return x | (s << 1) | (s << 2);
+}
+
+__device__ __forceinline__ uint32_t f16_pair(uint32_t n) {
+  const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)(float)n);
+  return h | (h << 16);
+}
+
+__device__ __forceinline__ int sext24(int v) { return (v << 8) >> 8; }
+
+// ---- staging: weights ---------------------------------------------------------------
+// Staging is split in two so that the global loads of chunk c+1 are in flight
+// while chunk c is multiplied: the Unit<> loaders fill registers, emit_w /
+// emit_a decode those registers into the LDS image after the barrier.
+//
+// emit_w: weight unit u4 (0..3) of the chunk, local row `row`
+template <int TT, int BT, int BR>
+__device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename Unit<TT>::W& w, int row,
+                                       int u4) {
+  uint8_t* dst = sm.bq + row * kQS + 64 * u4;
+  if constexpr (TT == TT_Q8_0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16(dst + 16 * i, w.q[4 * i], w.q[4 * i + 1], w.q[4 * i + 2], w.q[4 * i + 3]);
+    sm.wd[2 * u4][row] = h2f(w.d0);
+    sm.wd[2 * u4 + 1][row] = h2f(w.d1);
+  } else if constexpr (TT == TT_IQ4_NL) {
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t* q = w.q + 4 * b;
+      st16(dst + 32 * b, iq4_lo(q[0]), iq4_lo(q[1]), iq4_lo(q[2]), iq4_lo(q[3]));
+      st16(dst + 32 * b + 16, iq4_hi(q[0]), iq4_hi(q[1]), iq4_hi(q[2]), iq4_hi(q[3]));
+    }
+    sm.wd[2 * u4][row] = h2f(w.d0);
+    sm.wd[2 * u4 + 1][row] = h2f(w.d1);
+  } else if constexpr (TT == TT_Q4_K) {
+    const uint32_t m = 0x0F0F0F0Fu;
+    st16(dst, w.q[0] & m, w.q[1] & m, w.q[2] & m, w.q[3] & m);
+    st16(dst + 16, w.q[4] & m, w.q[5] & m, w.q[6] & m, w.q[7] & m);
+    st16(dst + 32, (w.q[0] >> 4) & m, (w.q[1] >> 4) & m, (w.q[2] >> 4) & m, (w.q[3] >> 4) & m);
+    st16(dst + 48, (w.q[4] >> 4) & m, (w.q[5] >> 4) & m, (w.q[6] >> 4) & m, (w.q[7] >> 4) & m);
+    if (u4 == 0) {
+      // 6-bit scales and mins, unpacked bytewise by the rule of
+      // src/kernels/x86/kernels256.c:105-125
+      const uint32_t S0 = w.hdr[1], S1 = w.hdr[2], S2 = w.hdr[3];
+      const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
+      const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+      const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+      sm.wsc[row][0] = sc_lo;
+      sm.wsc[row][1] = sc_hi;
+      uint8_t* mp = (uint8_t*)&sm.wmn[row][0];
+      st16(mp, f16_pair(mn_lo & 255u), f16_pair((mn_lo >> 8) & 255u), f16_pair((mn_lo >> 16) & 255u),
+           f16_pair(mn_lo >> 24));
+      st16(mp + 16, f16_pair(mn_hi & 255u), f16_pair((mn_hi >> 8) & 255u), f16_pair((mn_hi >> 16) & 255u),
+           f16_pair(mn_hi >> 24));
+      sm.wd[row] = h2f(w.hdr[0]);
+      sm.wdmin[row] = h2f(w.hdr[0] >> 16);
+    }
+  } else {  // Q6_K: unit (h, lh) holds values 128h + 32q + 16lh + (0..15), q = 0..3
+    const int h = (u4 >> 1) & 1, lh = u4 & 1;
+    uint32_t v[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t la = w.la[i], lb = w.lb[i], qh = w.qh[i];
+      v[0][i] = q6_minus32((la & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4));
+      v[1][i] = q6_minus32((lb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u));
+      v[2][i] = q6_minus32(((la >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u));
+      v[3][i] = q6_minus32(((lb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u));
+    }
+    uint8_t* rowp = sm.bq + row * kQS;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) st16(rowp + 128 * h + 32 * q + 16 * lh, v[q][0], v[q][1], v[q][2], v[q][3]);
+    // scales sc[8h + lh + 2q]: bytes 0 and 2 of sc01 and sc23
+    uint8_t* sp = (uint8_t*)&sm.wsc[row][0] + 8 * h + lh;
+    sp[0] = (uint8_t)w.sc01;
+    sp[2] = (uint8_t)(w.sc01 >> 16);
+    sp[4] = (uint8_t)w.sc23;
+    sp[6] = (uint8_t)(w.sc23 >> 16);
+    if (u4 == 0) sm.wd[row] = h2f(w.d);
+  }
+}
+
+// ---- staging: activations --------------------------------------------------------------
+// The 32-value formats take Q8_0 activations (two blocks per unit); the
+// K-quants take a Q8_K quarter in plain value order: values 64*u4 .. 64*u4+63.
+template <int TT>
+using MmqAct = typename std::conditional<(TT == TT_Q8_0 || TT == TT_IQ4_NL), ActPair, ActQ8K>::type;
+
+template <int TT>
+__device__ __forceinline__ MmqAct<TT> load_act(const uint8_t* arow, int u) {
+  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) return act_pair_ref(arow, u);
+  else return Unit<TT_Q4_K>::load_a(arow, u);
+}
+
+template <int TT, int BT, int BR>
+__device__ __forceinline__ void emit_a(MmqSmem<TT, BT, BR>& sm, const MmqAct<TT>& a, int tok, int u4) {
+  uint8_t* dst = sm.aq + tok * kQS + 64 * u4;
+  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16(dst + 16 * i, a.q[4 * i], a.q[4 * i + 1], a.q[4 * i + 2], a.q[4 * i + 3]);
+    sm.ad[2 * u4][tok] = a.d0;
+    sm.ad[2 * u4 + 1][tok] = a.d1;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16(dst + 16 * i, a.y[4 * i], a.y[4 * i + 1], a.y[4 * i + 2], a.y[4 * i + 3]);
+    if constexpr (TT == TT_Q4_K) {
+      _Float16* bp = &sm.abs[tok][4 * u4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bp[i] = (_Float16)(float)a.bs[i];
+    }
+    if (u4 == 0) sm.ady[tok] = a.d;
+  }
+}
+
+// ---- the kernel -------------------------------------------------------------------------
+template <int TT, int BT, int BR>
+__global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                              float* __restrict__ Y, int rows, int tokens, long row_bytes,
+                                              long act_bytes, int upr, int ntile_t) {
+  constexpr bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL);
+  constexpr int NA = BT / 64, NB = BR / 64;
+  __shared__ MmqSmem<TT, BT, BR> sm;
+
+  // Tile order: the hardware deals workgroups round-robin to the 8 XCDs;
+  // give each XCD a contiguous run of row tiles (all their token tiles), so
+  // a weight chunk is fetched into one XCD's L2 and reused there.
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);
+  const int r0 = (g / ntile_t) * BR, t0 = (g % ntile_t) * BT;
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  const int tb0 = (wv & 1) * (BT / 2), rb0 = (wv >> 1) * (BR / 2);
+
+  f32x16 acc[NA][NB];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+
+  // Thread tid stages weight units tid + 256*i (row q>>2, unit q&3) and the
+  // activation units likewise; rows / tokens past the end re-read the last one.
+  constexpr int UW = BR / 64, UA = BT / 64;
+  typename Unit<TT>::W wreg[UW];
+  MmqAct<TT> areg[UA];
+  const uint8_t* wrow[UW];
+  const uint8_t* arow[UA];
+#pragma unroll
+  for (int i = 0; i < UW; ++i) {
+    const int row = (tid + 256 * i) >> 2;
+    wrow[i] = W + (long)(r0 + row < rows ? r0 + row : rows - 1) * row_bytes;
+  }
+#pragma unroll
+  for (int i = 0; i < UA; ++i) {
+    const int tok = (tid + 256 * i) >> 2;
+    arow[i] = XQ + (long)(t0 + tok < tokens ? t0 + tok : tokens - 1) * act_bytes;
+  }
+  const int u4 = tid & 3;
+  const int nchunks = (upr + 3) >> 2;
+  auto load_chunk = [&](int ch) {
+    if (4 * ch + u4 < upr) {
+#pragma unroll
+      for (int i = 0; i < UW; ++i) wreg[i] = Unit<TT>::load_w(wrow[i], 4 * ch + u4);
+#pragma unroll
+      for (int i = 0; i < UA; ++i) areg[i] = load_act<TT>(arow[i], 4 * ch + u4);
+    }
+  };
+  load_chunk(0);
+  for (int ch = 0; ch < nchunks; ++ch) {
+    const int nu = upr - 4 * ch < 4 ? upr - 4 * ch : 4;  // units in this chunk
+    __syncthreads();  // the previous chunk's fragments have been read
+    if (u4 < nu) {
+#pragma unroll
+      for (int i = 0; i < UW; ++i) emit_w<TT, BT, BR>(sm, wreg[i], (tid + 256 * i) >> 2, u4);
+#pragma unroll
+      for (int i = 0; i < UA; ++i) emit_a<TT, BT, BR>(sm, areg[i], (tid + 256 * i) >> 2, u4);
+    }
+    __syncthreads();
+    if (ch + 1 < nchunks) load_chunk(ch + 1);  // in flight during this chunk's MFMAs
+
+    if constexpr (K32) {
+      i32x16 bias;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) bias[e] = kBiasBits;
+      // opaque to the optimizer: the bias stays in 16 registers as every
+      // MFMA's accumulator input (instead of being re-created per MFMA)
+      asm volatile("" : "+v"(bias));
+      const int nsteps = 2 * nu;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if (s < nsteps) {
+          i32x4 af[NA], bf[NB];
+          f32x4 da[NA][4];
+          float dw[NB], cw[NB];
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) da[a][q] = *(const f32x4*)&sm.ad[s][tb0 + 32 * a + 8 * q + 4 * lh];
+          }
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            bf[b] = *(const i32x4*)(sm.bq + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
+            dw[b] = sm.wd[s][rb0 + 32 * b + li];
+            cw[b] = -kBias * dw[b];
+          }
+#pragma unroll
+          for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], bias, 0, 0, 0);
+#pragma unroll
+              for (int e = 0; e < 16; ++e) {
+                // (a scalar copy first: bit-casting the vector element
+                // expression c[e] directly reads element 0 for every e)
+                const int ce = c[e];
+                const float t = __builtin_fmaf(__int_as_float(ce), dw[b], cw[b]);
+                acc[a][b][e] = __builtin_fmaf(t, da[a][e >> 2][e & 3], acc[a][b][e]);
+              }
+            }
+        }
+      }
+    } else if constexpr (TT == TT_Q4_K) {
+      i32x16 isum[NA][NB];
+      const i32x16 zero = {};
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) isum[a][b] = zero;
+      uint32_t scw[NB][2];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        scw[b][0] = sm.wsc[rb0 + 32 * b + li][0];
+        scw[b][1] = sm.wsc[rb0 + 32 * b + li][1];
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        i32x4 af[NA], bf[NB];
+#pragma unroll
+        for (int a = 0; a < NA; ++a) af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) bf[b] = *(const i32x4*)(sm.bq + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int sc = (int)((scw[b][s >> 2] >> (8 * (s & 3))) & 0xFFu);
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], zero, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) isum[a][b][e] += sc * sext24(c[e]);
+          }
+        }
+      }
+      // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
+      f16x8 am[NA], bm[NB];
+      f32x4 dy[NA][4];
+      float d[NB], ndm[NB];
+#pragma unroll
+      for (int a = 0; a < NA; ++a) {
+        am[a] = *(const f16x8*)&sm.abs[tb0 + 32 * a + li][8 * lh];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dy[a][q] = *(const f32x4*)&sm.ady[tb0 + 32 * a + 8 * q + 4 * lh];
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        bm[b] = *(const f16x8*)&sm.wmn[rb0 + 32 * b + li][8 * lh];
+        d[b] = sm.wd[rb0 + 32 * b + li];
+        ndm[b] = -sm.wdmin[rb0 + 32 * b + li];
+      }
+      const f32x16 fz = {};
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[a], bm[b], fz, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const float inner = __builtin_fmaf(d[b], (float)isum[a][b][e], ndm[b] * cm[e]);
+            acc[a][b][e] = __builtin_fmaf(dy[a][e >> 2][e & 3], inner, acc[a][b][e]);
+          }
+        }
+    } else {  // Q6_K
+      i32x16 isum[NA][NB];
+      const i32x16 zero = {};
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) isum[a][b] = zero;
+      uint32_t scw[NB][4];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint4 v = *(const uint4*)&sm.wsc[rb0 + 32 * b + li][0];
+        scw[b][0] = v.x; scw[b][1] = v.y; scw[b][2] = v.z; scw[b][3] = v.w;
+      }
+#pragma unroll
+      for (int gq = 0; gq < 16; ++gq) {
+        long af[NA], bf[NB];
+#pragma unroll
+        for (int a = 0; a < NA; ++a) af[a] = *(const i64x1_a8*)(sm.aq + (tb0 + 32 * a + li) * kQS + 16 * gq + 8 * lh);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) bf[b] = *(const i64x1_a8*)(sm.bq + (rb0 + 32 * b + li) * kQS + 16 * gq + 8 * lh);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int sc = sext8(scw[b][gq >> 2] >> (8 * (gq & 3)));
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x16_i8(af[a], bf[b], zero, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) isum[a][b][e] += sc * sext24(c[e]);
+          }
+        }
+      }
+      f32x4 dy[NA][4];
+      float d[NB];
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dy[a][q] = *(const f32x4*)&sm.ady[tb0 + 32 * a + 8 * q + 4 * lh];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) d[b] = sm.wd[rb0 + 32 * b + li];
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            acc[a][b][e] = __builtin_fmaf(d[b] * dy[a][e >> 2][e & 3], (float)isum[a][b][e], acc[a][b][e]);
+    }
+  }
+
+  // lanes 0..31 of a wave write 32 consecutive rows of one token per element
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int row = r0 + rb0 + 32 * b + li;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
+        if (row < rows && tok < tokens) Y[(long)tok * rows + row] = acc[a][b][e];
+      }
+    }
+}
+
+// ---- launchers --------------------------------------------------------------------------
+template <int TT, int BT, int BR>
+static hipError_t launch_mmq_t(const GemvArgs& g, hipStream_t s) {
+  const int upr = g.cols / 64;
+  const long ntr = (g.rows + BR - 1) / BR, ntt = (g.tokens + BT - 1) / BT;
+  const long G = ntr * ntt;
+  if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_mmq<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt);
+  return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, hipStream_t s) {
+  if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, s);
+  if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, s);
+  if (bt == 128 && br == 64) return launch_mmq_t<TT, 128, 64>(g, s);
+  if (bt == 128 && br == 128) return launch_mmq_t<TT, 128, 128>(g, s);
+  return hipErrorInvalidValue;
+}
+
+// Default tile: the largest that still gives every CU two workgroups.
+static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
+  const long target = 512;
+  const int cand[4][2] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}};
+  for (const auto& c : cand) {
+    const long n = (long)((g.rows + c[1] - 1) / c[1]) * ((g.tokens + c[0] - 1) / c[0]);
+    if (n >= target) {
+      bt = c[0];
+      br = c[1];
+      return;
+    }
+  }
+  bt = 64;
+  br = 64;
+}
+
+hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
+  if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  if (bt <= 0 || br <= 0) mmq_default_tile(g, bt, br);
+  switch (g.ttype) {
+    case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, s);
+    case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, s);
+    case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, s);
+    case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qhip

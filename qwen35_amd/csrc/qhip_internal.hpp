@@ -30,5 +30,7 @@ int gemv_pick_nt(int tokens);
 hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t s);
 hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s);
 hipError_t launch_block_ints(const GemvArgs& g, int* ints, hipStream_t s);
+// MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)
+hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s);
 
 }  // namespace qhip

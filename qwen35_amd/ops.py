@@ -82,6 +82,16 @@ def gemv_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: i
     return out
 
 
+def mmq_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
+              tile_tokens: int = 0, tile_rows: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The int8-MFMA tile path with an explicit workgroup tile (64 or 128 each, 0 = pick)."""
+    if out is None:
+        out = torch.empty((tokens, rows), dtype=torch.float32, device=w.device)
+    check("mmq_tuned", load().qhip_launch_mmq_tuned(_p(w), _p(xq), _p(out), rows, cols, tokens, ttype,
+                                                    tile_tokens, tile_rows, _stream()))
+    return out
+
+
 def block_ints(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
                tokens: int) -> torch.Tensor:
     be = _GEOM[ttype][0]

@@ -1,0 +1,171 @@
+"""GPU parity: the int8-MFMA tile path (MMQ) against the CPU oracle, through
+the C ABI.
+
+Bar: float outputs within 1e-5 relative L2 of the oracle; with every scale
+set to 1.0 the float result is the plain sum of the per-block integers, so
+those cases pin the MMQ's block integers bit-exactly against the oracle's.
+"""
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+import qwen35_amd
+from qwen35_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+TILES = [(64, 64), (64, 128), (128, 64), (128, 128)]
+F16_ONE = np.array([0x00, 0x3C], np.uint8)  # 1.0 as little-endian binary16
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+# rows / tokens not multiples of any tile, partial 256-value chunks for the
+# 32-value formats (cols % 256 != 0), K-quants at several super-block counts
+CASES = [
+    (po.TT_Q8_0, 200, 320, 37),
+    (po.TT_Q8_0, 130, 1024, 130),
+    (po.TT_IQ4_NL, 96, 576, 70),
+    (po.TT_IQ4_NL, 33, 2560, 20),
+    (po.TT_Q4_K, 150, 512, 65),
+    (po.TT_Q4_K, 64, 2560, 16),
+    (po.TT_Q6_K, 100, 768, 40),
+    (po.TT_Q6_K, 72, 2304, 129),
+]
+IDS = [f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in CASES]
+
+
+@pytest.mark.parametrize("tt,rows,cols,tokens", CASES, ids=IDS)
+def test_mmq_matches_oracle_every_tile(gpu, oracle, tt, rows, cols, tokens):
+    w = synth.make_weight(tt, rows, cols, seed=tokens, tag=tt)
+    x = synth.make_act(cols, tokens, seed=tokens)
+    want = oracle.matvec(tt, w, x)
+    wd = to_dev(w, gpu)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    for bt, br in TILES + [(0, 0)]:
+        got = ops.mmq_tuned(tt, wd, xq, rows, cols, tokens, bt, br).cpu().numpy()
+        assert rel_l2(got, want) < TOL, (bt, br, rel_l2(got, want))
+    # the reference-named entry point and the automatic path agree
+    out = torch.empty((tokens, rows), device=gpu)
+    rc = _lib.load().qhip_launch_mul_mat_vec_tile(wd.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols,
+                                                 tokens, tt, None)
+    assert rc == 0
+    assert rel_l2(out.cpu().numpy(), want) < TOL
+    assert rel_l2(ops.mul_mat(tt, wd, xq, rows, cols, tokens).cpu().numpy(), want) < TOL
+
+
+def unit_scale_weight(tt, rows, cols, seed):
+    w = synth.make_weight(tt, rows, cols, seed=seed, tag=tt).copy()
+    be, bb = po.GEOM[tt]
+    blk = w.reshape(rows, cols // be, bb)
+    if tt in (po.TT_Q8_0, po.TT_IQ4_NL):
+        blk[:, :, 0:2] = F16_ONE
+    elif tt == po.TT_Q4_K:
+        blk[:, :, 0:2] = F16_ONE
+        blk[:, :, 2:4] = F16_ONE
+    else:
+        blk[:, :, 208:210] = F16_ONE
+    return w
+
+
+def unit_scale_act(cols, tokens, seed):
+    # integers in [-127, 127] with +-127 in every 32-value block: the Q8_0 and
+    # Q8_K scales are both exactly 1.0 and the quantized values equal x
+    rng = np.random.default_rng(seed)
+    x = rng.integers(-127, 128, (tokens, cols)).astype(np.float32)
+    x[:, ::32] = np.where(rng.random((tokens, cols // 32)) < 0.5, -127.0, 127.0)
+    return x
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K])
+def test_mmq_block_integers_exact(gpu, oracle, tt):
+    rows, cols, tokens = 96, 1024, 72
+    w = unit_scale_weight(tt, rows, cols, seed=5)
+    x = unit_scale_act(cols, tokens, seed=5)
+    act = oracle.quantize_act(tt, x)
+    ints = oracle.block_ints(tt, w, act, cols).astype(np.int64)  # [tokens][rows][nints]
+    if tt == po.TT_Q4_K:
+        want = ints[:, :, 0::2].sum(-1) - ints[:, :, 1::2].sum(-1)  # isum - summs
+    else:
+        want = ints.sum(-1)
+    assert np.abs(want).max() < 2 ** 24  # every partial float sum is exact
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    assert np.array_equal(xq.cpu().numpy(), act)
+    wd = to_dev(w, gpu)
+    for bt, br in TILES:
+        got = ops.mmq_tuned(tt, wd, xq, rows, cols, tokens, bt, br).cpu().numpy()
+        assert np.array_equal(got.astype(np.int64), want), (bt, br)
+        assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q6_K])
+def test_mmq_declines_unaligned(gpu, tt):
+    rows, cols, tokens = 16, 512, 20
+    w = synth.make_weight(tt, rows, cols, seed=1, tag=tt)
+    x = synth.make_act(cols, tokens, seed=1)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    wbuf = torch.zeros(w.size + 2, dtype=torch.uint8, device=gpu)
+    wbuf[2:] = to_dev(w.reshape(-1), gpu)
+    out = torch.empty((tokens, rows), device=gpu)
+    L = _lib.load()
+    rc = L.qhip_launch_mmq_tuned(wbuf[2:].data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt,
+                                 64, 64, None)
+    assert rc == qwen35_amd.DECLINE
+    rc = L.qhip_launch_mul_mat_vec_tile(wbuf[2:].data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols,
+                                        tokens, tt, None)
+    assert rc == qwen35_amd.DECLINE
+    # the automatic path still serves it (generic kernel)
+    got = ops.mul_mat(tt, wbuf[2:], xq, rows, cols, tokens).cpu().numpy()
+    assert rel_l2(got, po.Oracle().matvec(tt, w, x)) < TOL
+
+
+def test_mmq_rejects_bad_tiles(gpu):
+    tt, rows, cols, tokens = po.TT_Q4_K, 16, 256, 8
+    w = torch.zeros(rows * 144, dtype=torch.uint8, device=gpu)
+    xq = torch.zeros(tokens * 292, dtype=torch.uint8, device=gpu)
+    out = torch.empty((tokens, rows), device=gpu)
+    L = _lib.load()
+    for bt, br in [(32, 64), (64, 256), (-1, 64)]:
+        rc = L.qhip_launch_mmq_tuned(w.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt, bt,
+                                     br, None)
+        assert rc not in (0, qwen35_amd.DECLINE), (bt, br)
+
+
+def test_mmq_zero_tokens_and_rows_are_noops(gpu):
+    tt = po.TT_Q8_0
+    w = torch.zeros(34 * 2, dtype=torch.uint8, device=gpu)
+    xq = torch.zeros(34 * 2, dtype=torch.uint8, device=gpu)
+    out = torch.full((1,), 7.0, device=gpu)
+    L = _lib.load()
+    assert L.qhip_launch_mmq_tuned(w.data_ptr(), xq.data_ptr(), out.data_ptr(), 1, 64, 0, tt, 0, 0, None) == 0
+    assert L.qhip_launch_mmq_tuned(w.data_ptr(), xq.data_ptr(), out.data_ptr(), 0, 64, 1, tt, 0, 0, None) == 0
+    assert out.item() == 7.0
+
+
+def test_cfg4_ragged_batch_through_mmq(gpu, oracle):
+    """BASELINE config 4 shape: eight sequences, lengths uniform on [16,256],
+    packed with the offset table and multiplied in one launch."""
+    tt, rows, cols = po.TT_Q8_0, 3584, 1024
+    lens = [int(v) for v in synth.ragged_lengths(8, 16, 256, seed=0)]
+    w = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
+    seqs = [synth.make_act(cols, n, seed=300 + i) for i, n in enumerate(lens)]
+    dseqs = [to_dev(s, gpu) for s in seqs]
+    xq, off_d, total = ops.quantize_ragged(tt, dseqs, cols)
+    assert total == sum(lens)
+    packed = np.concatenate(seqs)
+    wd = to_dev(w, gpu)
+    out = ops.mul_mat_ragged(tt, wd, xq, off_d, len(lens), total, rows, cols).cpu().numpy()
+    # sampled rows of every token against the oracle (the full product is 1.1G MACs on the CPU)
+    idx = np.unique(np.concatenate([[0, rows - 1], np.random.default_rng(4).integers(0, rows, 200)]))
+    want = oracle.matvec(tt, np.ascontiguousarray(w[idx]), packed)
+    assert rel_l2(out[:, idx], want) < TOL
+    assert np.all(np.isfinite(out))
