@@ -15,7 +15,7 @@ kernel's roofline fraction (HIP events around back-to-back launches of that
 kernel alone), and the reference's CPU path timed on this host's cores.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --profile-kernel   (only the dominant kernel, for rocprofv3)
+       python bench.py --profile-kernel down --steps 200   (one kernel only, for rocprofv3)
        python bench.py --copy-calib       (a plain copy of known size, for counter scaling)
 """
 from __future__ import annotations
@@ -101,7 +101,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--profile-kernel", action="store_true")
+    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "step", "mmq_cfg5_q4k", "mmq_cfg4"],
+                    help="run only this kernel (for rocprofv3) and exit")
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -168,13 +169,17 @@ def main() -> int:
         assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
         down(i)
 
-    if args.profile_kernel:
+    if args.profile_kernel in ("down", "gate_up", "step"):
         for i in range(3):
             step(i)
-        for i in range(200):
-            gate_up(i)
+        fn = {"down": down, "gate_up": gate_up, "step": step}[args.profile_kernel]
+        for i in range(args.steps):
+            fn(i)
         torch.cuda.synchronize()
-        print(json.dumps({"profiled": "gate_up Q4_K [19456,2560] x 200", "copies": ws.copies}))
+        print(json.dumps({"profiled": args.profile_kernel, "launches": args.steps, "copies": ws.copies}))
+        return 0
+    if args.profile_kernel:
+        profile_mmq(torch, lib, ops, synth, dev, stream, args.profile_kernel, args.steps)
         return 0
 
     step_bytes = gemv_bytes(2 * F, H, gu_bytes) + gemv_bytes(H, F, d_bytes)
@@ -240,6 +245,11 @@ def main() -> int:
             del st
             torch.cuda.empty_cache()
 
+    # ---- MMQ prefill: config 4 (ragged + dense 512) and config 5 crossover ------
+    mmq = None
+    if not args.no_extra:
+        mmq = bench_mmq(torch, np, lib, ops, synth, dev, stream)
+
     # ---- CPU baseline: the reference's own kernels on this host ---------------
     cpu = None
     if not args.no_cpu:
@@ -260,9 +270,108 @@ def main() -> int:
         "kernels": kernels,
         "latency": latency,
         "configs": extra,
+        "mmq": mmq,
     }
     print(json.dumps(out), flush=True)
     return 0
+
+
+def profile_mmq(torch, lib, ops, synth, dev, stream, which, launches):
+    """Only the MMQ kernel of one configuration, for rocprofv3."""
+    tt, rows, cols, T = (12, 17408, 5120, 512) if which == "mmq_cfg5_q4k" else (8, 3584, 1024, 512)
+    w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
+    aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
+    y = torch.empty((T, rows), device=dev)
+    for _ in range(launches):
+        assert lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt, 2, stream) == 0
+    torch.cuda.synchronize()
+    print(json.dumps({"profiled": which, "launches": launches}))
+
+
+def bench_mmq(torch, np, lib, ops, synth, dev, stream):
+    """Config 4: Q8_0 [3584,1024] with eight ragged sequences (lengths uniform on
+    [16,256], packed by the ragged quantizer, one launch) and a dense 512-token
+    sequence.  Config 5: Q4_K gate [17408,5120] and Q6_K down [5120,17408] at
+    T = 1, 4, 16, 64, 512 on the GEMV and on the MMQ, and the crossover.
+    Throughput: tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak."""
+    PATH_GEMV, PATH_MMQ = 1, 2
+    res = {}
+
+    def timed(fn, iters):
+        return time_loop(torch, lambda i: fn(), iters, 3)
+
+    def frac(rows, cols, T, sec):
+        tops = 2.0 * rows * cols * T / sec / 1e12
+        return round(tops, 1), round(tops / INT8_PEAK_TOPS, 4)
+
+    # config 4
+    tt, rows, cols = 8, 3584, 1024
+    w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
+    lens = [int(v) for v in synth.ragged_lengths(8, 16, 256, seed=0)]
+    seqs = [torch.from_numpy(synth.make_act(cols, n, seed=0, tag=300 + i)).to(dev) for i, n in enumerate(lens)]
+    total = sum(lens)
+    xq, off_d, _ = ops.quantize_ragged(tt, seqs, cols)
+    ptrs = torch.tensor([q.data_ptr() for q in seqs], dtype=torch.int64, device=dev)
+    yo = torch.empty((total, rows), device=dev)
+
+    def ragged_step():
+        assert lib.qhip_launch_quantize_ragged(tt, ptrs.data_ptr(), off_d.data_ptr(), len(lens), total, cols,
+                                               xq.data_ptr(), stream) == 0
+        assert lib.qhip_launch_mul_mat_ragged(w.data_ptr(), xq.data_ptr(), yo.data_ptr(), rows, cols,
+                                              off_d.data_ptr(), len(lens), total, tt, stream) == 0
+
+    def ragged_mmq_only():
+        assert lib.qhip_launch_mul_mat_ragged(w.data_ptr(), xq.data_ptr(), yo.data_ptr(), rows, cols,
+                                              off_d.data_ptr(), len(lens), total, tt, stream) == 0
+
+    s_step = timed(ragged_step, 200)
+    s_mm = timed(ragged_mmq_only, 200)
+    tops, fr = frac(rows, cols, total, s_mm)
+    res["cfg4_ragged_q8_0_3584x1024"] = {
+        "lengths": lens, "tokens": total, "tokens_per_s": round(total / s_step, 1),
+        "us_pack_quantize_and_mmq": round(s_step * 1e6, 2), "us_mmq": round(s_mm * 1e6, 2),
+        "int8_tops": tops, "int8_mfma_frac": fr}
+    T = 512
+    xd = torch.from_numpy(synth.make_act(cols, T, seed=0, tag=400)).to(dev)
+    xq5 = ops.quantize_act(tt, xd)
+    y5 = torch.empty((T, rows), device=dev)
+    s_d = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), xq5.data_ptr(), y5.data_ptr(), rows, cols, T, tt,
+                                                PATH_MMQ, stream), 200)
+    tops, fr = frac(rows, cols, T, s_d)
+    res["cfg4_dense512_q8_0_3584x1024"] = {"tokens": T, "tokens_per_s": round(T / s_d, 1),
+                                           "us_mmq": round(s_d * 1e6, 2), "int8_tops": tops, "int8_mfma_frac": fr}
+    log(f"mmq cfg4: ragged {total} tokens {s_mm * 1e6:.1f} us ({res['cfg4_ragged_q8_0_3584x1024']['int8_mfma_frac']:.3f} "
+        f"of int8 peak); dense 512 {s_d * 1e6:.1f} us")
+    del w, xq, yo, seqs
+
+    # config 5 sweep
+    sweep = {}
+    for name, tt, rows, cols in (("q4_k_17408x5120", 12, 17408, 5120), ("q6_k_5120x17408", 14, 5120, 17408)):
+        w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
+        rows_out = []
+        cross = None
+        for T in (1, 4, 16, 64, 512):
+            x = torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev)
+            aq = ops.quantize_act(tt, x)
+            y = torch.empty((T, rows), device=dev)
+            it = 100 if T <= 64 else 30
+            s_g = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+                                                        PATH_GEMV, stream), it)
+            s_m = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+                                                        PATH_MMQ, stream), it)
+            tops, fr = frac(rows, cols, T, s_m)
+            rows_out.append({"T": T, "gemv_us": round(s_g * 1e6, 2), "mmq_us": round(s_m * 1e6, 2),
+                             "gemv_tokens_per_s": round(T / s_g, 1), "mmq_tokens_per_s": round(T / s_m, 1),
+                             "mmq_int8_tops": tops, "mmq_int8_mfma_frac": fr})
+            if cross is None and s_m < s_g:
+                cross = T
+        sweep[name] = {"points": rows_out, "crossover_T": cross}
+        log(f"mmq cfg5 {name}: " + ", ".join(f"T={p['T']} gemv {p['gemv_us']} / mmq {p['mmq_us']} us"
+                                              for p in rows_out) + f"; crossover T={cross}")
+        del w
+        torch.cuda.empty_cache()
+    res["cfg5_sweep"] = sweep
+    return res
 
 
 def cpu_baseline(np, synth, wg, wu, wd, x, hvec, step_bytes, budget_s):

@@ -66,8 +66,17 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
 }
 
 // Token count from which the MMQ tiles beat the weight-streaming GEMV (the
-// GEMV re-reads the weights once per 8 tokens; the MMQ once per 64 or 128).
-static int mmq_min_tokens(int /*ttype*/) { return 16; }
+// GEMV re-reads the weights once per 8 tokens; the MMQ once per 64 tokens),
+// from the GEMV-vs-MMQ sweep at the BASELINE shapes on MI355X: Q4_K and
+// IQ4_NL cross between 4 and 16 tokens, Q8_0 between 16 and 64, Q6_K (the
+// MMQ's most VALU-heavy format) between 16 and 64.
+static int mmq_min_tokens(int ttype) {
+  switch (ttype) {
+    case TT_Q4_K: case TT_IQ4_NL: return 16;
+    case TT_Q8_0: return 32;
+    default: return 48;
+  }
+}
 
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
   if (g.rows == 0 || g.tokens == 0) return hipSuccess;
