@@ -1,10 +1,11 @@
 #!/usr/bin/env python3
 """bench.py -- quantized GEMV / MMQ throughput on one MI355X.
 
-Headline workload: one decode FFN step at batch 1,
-  Q8_K-quantize x[2560] -> gate/up GEMV (Q4_K [9728,2560] x2, one launch, the
-  two weights adjacent as matvecPair fuses them) -> Q8_K-quantize h[9728] ->
-  down GEMV (Q6_K [2560,9728]).
+Headline workload: one decode FFN step at batch 1
+through the Exec mirror (the slots the engine calls): matvecPair over the Q4_K
+gate/up weights [9728,2560] x2 (adjacent in the weight arena: one launch) from
+f32 x[2560], then matvec over the Q6_K down weight [2560,9728] from f32
+h[9728]; each launch quantizes its activation (Q8_K) inside the GEMV.
 `value` = algorithmic bytes of the step's GEMVs (packed weights + f32 x + f32 y
 per GEMV) / step time, inputs resident in HBM.  Weight sets rotate over enough
 device copies (> 512 MB per pass) that every step streams from HBM, not from
@@ -101,7 +102,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "step", "mmq_cfg5_q4k", "mmq_cfg4"],
+    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "step", "step_unfused", "mmq_cfg5_q4k",
+                                                 "mmq_cfg4"],
                     help="run only this kernel (for rocprofv3) and exit")
     ap.add_argument("--copy-calib", action="store_true")
     args = ap.parse_args()
@@ -133,7 +135,10 @@ def main() -> int:
         print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n, "launches": 5}))
         return 0
 
-    # ---- headline workload: cfg2 FFN step --------------------------------------
+    # ---- headline workload: cfg2 FFN step through the Exec mirror --------------
+    # matvecPair(gate, up, x) + matvec(down, h): one launch each, the activation
+    # quantized inside the GEMV (src/backend.zig:153-176 slots).
+    import ctypes
     H, F = 2560, 9728
     t0 = time.time()
     wg = synth.make_weight(TQ4, F, H, seed=0, tag=1)
@@ -142,41 +147,74 @@ def main() -> int:
     x = synth.make_act(H, 1, seed=0, tag=100)
     hvec = synth.make_act(F, 1, seed=0, tag=101)
     gu_bytes, d_bytes = wg.nbytes + wu.nbytes, wd.nbytes
-    host_set = np.concatenate([wg.reshape(-1), wu.reshape(-1), wd.reshape(-1)])
-    ws = Stream(torch, host_set, dev)
-    log(f"cfg2 weights {host_set.nbytes / 1e6:.1f} MB x {ws.copies} device copies "
-        f"(gen+upload {time.time() - t0:.1f}s), sha256 {synth.sha256(host_set)[:16]}")
-    xd = torch.from_numpy(x).to(dev)
-    hd = torch.from_numpy(hvec).to(dev)
-    xq = torch.empty(lib.qhip_act_row_bytes(TQ4, H), dtype=torch.uint8, device=dev)
-    hq = torch.empty(lib.qhip_act_row_bytes(TQ6, F), dtype=torch.uint8, device=dev)
+    set_bytes = gu_bytes + d_bytes
+    copies = max(1, -(-ROTATE_BYTES // set_bytes))
+    be = ops.Backend(0)
+    lins = []
+    for _ in range(copies):
+        lg = be.load_linear(TQ4, F, H, wg)
+        lu = be.load_linear(TQ4, F, H, wu)
+        ld = be.load_linear(TQ6, H, F, wd)
+        assert lu.dev == lg.dev + F * lg.row_bytes  # adjacent: matvecPair is one launch
+        lins.append((ctypes.byref(lg), ctypes.byref(lu), ctypes.byref(ld), lg))
+    sha = synth.sha256(np.concatenate([wg.reshape(-1), wu.reshape(-1), wd.reshape(-1)]))
+    log(f"cfg2 weights {set_bytes / 1e6:.1f} MB x {copies} copies in the backend arena "
+        f"(gen+upload {time.time() - t0:.1f}s), sha256 {sha[:16]}")
+    xd = torch.from_numpy(x[0]).to(dev)
+    hd = torch.from_numpy(hvec[0]).to(dev)
     y_gu = torch.empty(2 * F, device=dev)
     y_d = torch.empty(H, device=dev)
+    bh = be._h
+    p_x, p_h, p_ygu, p_yd = (ctypes.c_void_p(t.data_ptr()) for t in (xd, hd, y_gu, y_d))
 
     def gate_up(i):
-        rc = lib.qhip_launch_mul_mat_vec(ws.ptr(i), xq.data_ptr(), y_gu.data_ptr(), 2 * F, H, 1, TQ4,
-                                         stream)
+        g_, u_, _, _ = lins[i % copies]
+        rc = lib.qhip_backend_matvec_pair(bh, p_ygu, g_, u_, p_x)
         assert rc == 0, rc
 
     def down(i):
-        rc = lib.qhip_launch_mul_mat_vec(ws.ptr(i) + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1,
-                                         TQ6, stream)
+        rc = lib.qhip_backend_matvec(bh, p_yd, lins[i % copies][2], p_h)
         assert rc == 0, rc
 
     def step(i):
-        assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
         gate_up(i)
-        assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
         down(i)
 
-    if args.profile_kernel in ("down", "gate_up", "step"):
+    # the same step on the C ABI's separate quantize + matvec launches (4 launches)
+    xq = torch.empty(lib.qhip_act_row_bytes(TQ4, H), dtype=torch.uint8, device=dev)
+    hq = torch.empty(lib.qhip_act_row_bytes(TQ6, F), dtype=torch.uint8, device=dev)
+
+    # the step's two GEMV kernels alone, on activations quantized beforehand
+    assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
+    assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
+
+    def gemv_gate_up(i):
+        rc = lib.qhip_launch_mul_mat_vec(lins[i % copies][3].dev, xq.data_ptr(), y_gu.data_ptr(), 2 * F, H, 1, TQ4,
+                                         stream)
+        assert rc == 0, rc
+
+    def gemv_down(i):
+        rc = lib.qhip_launch_mul_mat_vec(lins[i % copies][3].dev + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1,
+                                         TQ6, stream)
+        assert rc == 0, rc
+
+    def step_unfused(i):
+        lg = lins[i % copies][3]
+        assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
+        assert lib.qhip_launch_mul_mat_vec(lg.dev, xq.data_ptr(), y_gu.data_ptr(), 2 * F, H, 1, TQ4, stream) == 0
+        assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
+        assert lib.qhip_launch_mul_mat_vec(lg.dev + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1, TQ6,
+                                           stream) == 0
+
+    if args.profile_kernel in ("down", "gate_up", "step", "step_unfused"):
         for i in range(3):
             step(i)
-        fn = {"down": down, "gate_up": gate_up, "step": step}[args.profile_kernel]
+        fn = {"down": gemv_down, "gate_up": gemv_gate_up, "step": step,
+              "step_unfused": step_unfused}[args.profile_kernel]
         for i in range(args.steps):
             fn(i)
         torch.cuda.synchronize()
-        print(json.dumps({"profiled": args.profile_kernel, "launches": args.steps, "copies": ws.copies}))
+        print(json.dumps({"profiled": args.profile_kernel, "launches": args.steps, "copies": copies}))
         return 0
     if args.profile_kernel:
         profile_mmq(torch, lib, ops, synth, dev, stream, args.profile_kernel, args.steps)
@@ -186,13 +224,15 @@ def main() -> int:
     sec = time_loop(torch, step, args.steps, args.warmup)
     value = step_bytes / sec / 1e9
     log(f"cfg2 step: {sec * 1e6:.2f} us, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% HBM)")
+    sec_unfused = time_loop(torch, step_unfused, args.steps, args.warmup)
+    log(f"cfg2 step, separate quantize launches: {sec_unfused * 1e6:.2f} us")
 
-    # dominant kernel alone (gate/up, the larger launch of the step)
+    # each GEMV kernel of the step alone, back to back (the roofline's kernel)
     n_k = max(200, args.steps)
     gu_alg = gemv_bytes(2 * F, H, gu_bytes)
     d_alg = gemv_bytes(H, F, d_bytes)
-    gu_sec = time_loop(torch, gate_up, n_k, 20)
-    d_sec = time_loop(torch, down, n_k, 20)
+    gu_sec = time_loop(torch, gemv_gate_up, n_k, 20)
+    d_sec = time_loop(torch, gemv_down, n_k, 20)
     kernels = {
         "gemv_q4_k_gate_up_19456x2560": {"alg_bytes": gu_alg, "avg_us": gu_sec * 1e6,
                                          "gbs": gu_alg / gu_sec / 1e9},
@@ -212,8 +252,9 @@ def main() -> int:
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
                 "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
-    latency = {"gate_up_single_launch_us": round(single_latency(torch, gate_up) * 1e6, 2),
-               "down_single_launch_us": round(single_latency(torch, down) * 1e6, 2)}
+    latency = {"gate_up_single_launch_us": round(single_latency(torch, gemv_gate_up) * 1e6, 2),
+               "down_single_launch_us": round(single_latency(torch, gemv_down) * 1e6, 2),
+               "step_single_us": round(single_latency(torch, step) * 1e6, 2)}
 
     # ---- other configurations (GEMV bandwidth per launch, back-to-back) ------
     extra = {}
@@ -260,11 +301,12 @@ def main() -> int:
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
         "data": "synthetic (SplitMix64 seed 0, BASELINE.json config rules)",
-        "config": {"workload": "cfg2 decode FFN step, batch 1: Q8_K quantize x[2560] + Q4_K gate/up "
-                               "[9728,2560]x2 (one launch) + Q8_K quantize h[9728] + Q6_K down "
-                               "[2560,9728]",
+        "config": {"workload": "cfg2 decode FFN step, batch 1, through the Exec mirror: matvecPair "
+                               "Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down [2560,9728] "
+                               "from f32 h[9728] (Q8_K quantization inside each GEMV launch)",
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": step_bytes,
-                   "weight_copies_rotated": ws.copies, "parallelism": "single GPU"},
+                   "weight_copies_rotated": copies, "parallelism": "single GPU",
+                   "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,

@@ -99,11 +99,24 @@ int qhip_launch_mul_mat_vec_q8_0(const void *d_w, const void *d_xq, float *d_out
 int qhip_launch_mul_mat(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
                         int tokens, int ttype, int path, void *stream);
 
-/* The GEMV with explicit launch shape: `lanes_per_row` (1..64) lanes share
- * one weight row, walking its 64-value units in turn, and fold their partial
- * sums,
- * and `tokens_per_pass` in {1,2,4,8} tokens share each weight load; 0 picks
- * the default for either.  Replaces the reference's launch-shape env knobs
+/* Quantize-and-multiply for one token in ONE launch: d_x is the f32
+ * activation (16-byte aligned); every workgroup quantizes it with the
+ * reference quantizer of the weight's activation family (bit-exact with
+ * qhip_launch_quantize_act) into LDS and runs the GEMV on it.  d_xq_out
+ * (nullable) receives the quantized activation in the reference layout.
+ * Replaces the reference's quantize launch + matvec launch pair
+ * (src/backend_cuda.zig matvec path: q35_launch_quantize_q8_0/_q8_K then
+ * q35_launch_mul_mat_vec, src/kernels/cuda/api.h:79-112); no reference kernel
+ * fuses them.  Returns QHIP_DECLINE when the fast-path preconditions do not
+ * hold or cols is too wide for the LDS image (about 57000 values). */
+int qhip_launch_quantize_mul_mat_vec(const void *d_w, const float *d_x, void *d_xq_out, float *d_out,
+                                     int rows, int cols, int ttype, void *stream);
+
+/* The GEMV with explicit launch shape: `lanes_per_row` (1..64, or 128 / 256
+ * = two / four whole waves, one token only) lanes share `rows_per_lane` (1, 2
+ * or 4) weight rows, walking their 64-value units in turn, and fold their
+ * partial sums; `tokens_per_pass` in {1,2,4,8} tokens share each weight load;
+ * 0 picks the default for any of them.  Replaces the reference's launch-shape env knobs
  * (QWEN35_CUDA_SPLIT / _COOP_WARPS / _RPB, src/kernels/cuda/mmvq.cu:685-772)
  * with arguments.  Returns QHIP_DECLINE when the fast-path preconditions do
  * not hold. */

@@ -44,6 +44,8 @@ SIGNATURES = {
                                              c_void_p]),
     "qhip_launch_mmq_tuned": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                       c_int, c_void_p]),
+    "qhip_launch_quantize_mul_mat_vec": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
+                                                 c_void_p]),
     "qhip_launch_gemv_tuned": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                        c_int, c_int, c_int, c_void_p]),
     "qhip_launch_quantize_ragged": (c_int, [c_int, c_void_p, c_void_p, c_int, c_int, c_int,

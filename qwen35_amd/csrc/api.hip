@@ -116,21 +116,12 @@ __global__ __launch_bounds__(256) void k_quantize_ragged_q8_0(const float* const
   const float* x = src[sq] + (long)(p - off[sq]) * cols;
   const bool ok = b < nblocks;
   const float v = ok ? x[32 * b + i] : 0.0f;
-  float a = v < 0.0f ? -v : v;
-  a = a > 0.0f ? a : 0.0f;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
-  const float scale = a > 0.0f ? a / 127.0f : 1.0f;
-  const float inv = a > 0.0f ? 1.0f / scale : 0.0f;
-  const float sv = v * inv;
-  const float r = sv + (sv >= 0.0f ? 0.5f : -0.5f);
-  int q = trunc_i32_x86(r);
-  q = q > 127 ? 127 : (q < -128 ? -128 : q);
+  uint32_t hb;
+  const int q = quant_q8_0_lane(v, hb);
   if (ok) {
     uint8_t* ob = out + (long)p * out_stride + 34 * b;
     ob[2 + i] = (uint8_t)(int8_t)q;
     if (i == 0) {
-      const uint32_t hb = f32_to_f16_bits(scale);
       ob[0] = (uint8_t)hb;
       ob[1] = (uint8_t)(hb >> 8);
     }
@@ -150,30 +141,9 @@ __global__ __launch_bounds__(256) void k_quantize_ragged_q8_K(const float* const
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = ok ? x[256 * b + 4 * l + i] : 0.0f;
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float e = v[i] < 0.0f ? -v[i] : v[i];
-    a = fmaxf(a, e > 0.0f ? e : 0.0f);
-  }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
-  const float scale = a > 0.0f ? a / 127.0f : 1.0f;
-  const float inv = a > 0.0f ? 1.0f / scale : 0.0f;
-  uint32_t packed = 0;
-  int gsum = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float r = roundf(v[i] * inv);
-    r = r < -127.0f ? -127.0f : r;
-    r = r > 127.0f ? 127.0f : r;
-    r = (r >= -127.0f) ? r : 127.0f;
-    const int q = (int)r;
-    packed |= ((uint32_t)q & 0xFFu) << (8 * i);
-    gsum += q;
-  }
-  gsum += __shfl_xor(gsum, 1, 64);
-  gsum += __shfl_xor(gsum, 2, 64);
+  int gsum;
+  float scale;
+  const uint32_t packed = quant_q8_K_lane(v, gsum, scale);
   if (ok) {
     uint8_t* ob = out + (long)p * out_stride + 292 * b;
     *(uint32_t*)(ob + 4 + 4 * l) = packed;
@@ -287,6 +257,18 @@ int qhip_launch_mul_mat_vec_q8_0(const void* d_w, const void* d_xq, float* d_out
   return qhip_launch_mul_mat_vec(d_w, d_xq, d_out, rows, cols, tokens, QHIP_TT_Q8_0, stream);
 }
 
+int qhip_launch_quantize_mul_mat_vec(const void* d_w, const float* d_x, void* d_xq_out, float* d_out,
+                                     int rows, int cols, int ttype, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_x, d_out, rows, cols, 1, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (d_xq_out && !aligned4(d_xq_out)) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  // float4 activation reads: x 16-byte aligned
+  if (!fast_ok(g) || ((uintptr_t)d_x & 15u) || !gemv_fused_fits(ttype, cols)) return QHIP_DECLINE;
+  return (int)launch_gemv_fused(g, d_x, d_xq_out, 0, 0, S(stream));
+}
+
 int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
                            int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
                            int rows_per_lane, void* stream) {
@@ -294,10 +276,12 @@ int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int 
   hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
   const int n = tokens_per_pass, nr = rows_per_lane;
-  if (lanes_per_row < 0 || lanes_per_row > 64 || n < 0 || n > 8 || (n & (n - 1)))
+  const bool multiwave = lanes_per_row == 128 || lanes_per_row == 256;
+  if (lanes_per_row < 0 || (lanes_per_row > 64 && !multiwave) || n < 0 || n > 8 || (n & (n - 1)))
     return (int)hipErrorInvalidValue;
   if (nr < 0 || nr > 4 || nr == 3 || (nr > 2 && n > 1) || (nr > 1 && n > 2))
     return (int)hipErrorInvalidValue;
+  if (multiwave && (tokens != 1 || n > 1)) return (int)hipErrorInvalidValue;
   if (!fast_ok(g)) return QHIP_DECLINE;
   return (int)launch_gemv(g, lanes_per_row, n, nr, S(stream));
 }

@@ -90,6 +90,15 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
                long row_bytes, const float* x, int k) {
   if (!out || !x || k < 0) return (int)hipErrorInvalidValue;
   if (k == 0 || rows == 0) return 0;
+  if (k == 1) {
+    // one launch, the activation quantized inside the GEMV, where that is
+    // faster than a separate quantize launch (narrow matrices)
+    const GemvArgs g1{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
+    if (gemv_fused_preferred(g1)) {
+      const int rc = qhip_launch_quantize_mul_mat_vec(wdev, x, nullptr, out, rows, cols, ttype, be->stream);
+      if (rc != QHIP_DECLINE) return report("matvec", (hipError_t)rc);
+    }
+  }
   hipError_t e = ensure_act(be, act_bytes_for(cols, k));
   if (e != hipSuccess) return report("activation scratch", e);
   int rc = qhip_launch_quantize_act(ttype, x, be->act, cols, k, be->stream);

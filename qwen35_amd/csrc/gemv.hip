@@ -48,7 +48,6 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int k = 0; k < NR; ++k) acc[t][k] = 0.0f;
-#pragma unroll 2
     for (int u = j; u < u_end; u += team) {
       typename U::W w[NR];
 #pragma unroll
@@ -83,6 +82,196 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
           if ((NT == 1 || t0 + t < tokens) && row0 + k < rows)
             Y[(long)(t0 + t) * rows + row0 + k] = acc[t][k];
     }
+  }
+}
+
+// Teams of WV whole waves (128 or 256 lanes per row group), one token.  For
+// matrices with few long rows (the FFN down projection): the rows' units are
+// split over the team's waves, so NR rows can share each activation load
+// without cutting the number of waves in flight.  Wave s of a team walks
+// units lane + 64s, stepping 64*WV; each wave folds its lanes with the
+// shuffle tree, then the team's waves are added in wave order through LDS
+// (deterministic).
+template <int TT, int NR, int WV>
+__global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
+                                                  const uint8_t* __restrict__ XQ,
+                                                  float* __restrict__ Y, int rows, long row_bytes,
+                                                  int upr) {
+  using U = Unit<TT>;
+  constexpr int TPB = 4 / WV;  // teams per workgroup
+  __shared__ float part[4][NR];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tm = wv / WV, sl = wv % WV;
+  const long row0 = ((long)blockIdx.x * TPB + tm) * NR;
+  const bool active = row0 < rows;
+  const uint8_t* wrow[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const long rk = row0 + k < rows ? row0 + k : rows - 1;
+    wrow[k] = W + (active ? rk : 0) * row_bytes;
+  }
+  const int u_end = active ? upr : 0;
+  float acc[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) acc[k] = 0.0f;
+  for (int u = lane + 64 * sl; u < u_end; u += 64 * WV) {
+    typename U::W w[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) w[k] = U::load_w(wrow[k], u);
+    const typename U::A a = U::load_a(XQ, u);
+#pragma unroll
+    for (int k = 0; k < NR; ++k) acc[k] += U::dot(w[k], a);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+    for (int k = 0; k < NR; ++k) acc[k] += __shfl_down(acc[k], off, 64);
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k) part[wv][k] = acc[k];
+  }
+  __syncthreads();
+  if (sl == 0 && lane < NR && active && row0 + lane < rows) {
+    float v = part[tm * WV][lane];
+#pragma unroll
+    for (int q = 1; q < WV; ++q) v += part[tm * WV + q][lane];
+    Y[row0 + lane] = v;
+  }
+}
+
+// ---- quantize + GEMV in one launch (batch 1) ---------------------------------------
+// Every workgroup quantizes the f32 activation itself, bit-exactly as the
+// standalone quantizers do, into an LDS image split into planes (ActSplit:
+// int8 values, per-block f32 scales, Q8_K 16-value sums), then runs the same
+// team-of-lanes GEMV as k_gemv with the activation read from LDS instead of
+// through the texture path.  Before quantizing, each lane issues the loads of
+// its first weight unit, so the quantize prologue runs while those bytes are
+// on their way from HBM; later units are prefetched one ahead.  This removes
+// the separate quantize launch (about 2-3 us each on this GPU) from every
+// decode matvec.  Workgroup 0 also writes the quantized activation in the
+// reference layout when `XQ` is not null.
+__host__ __device__ constexpr long fused_lds_qs(int cols) { return cols; }
+__host__ __device__ constexpr long fused_lds_bytes(int ttype, int cols) {
+  // qs[cols] | d[nblk] f32 (16-aligned) | Q8_K: bs[cols/16] int16
+  return ttype == TT_Q8_0 || ttype == TT_IQ4_NL
+             ? (long)cols + (((long)cols / 32 * 4 + 15) & ~15L)
+             : (long)cols + (((long)cols / 256 * 4 + 15) & ~15L) + (long)cols / 16 * 2;
+}
+
+template <int TT, int NR>
+__global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, const float* __restrict__ X,
+                                                 uint8_t* __restrict__ XQ, float* __restrict__ Y, int rows,
+                                                 int cols, long row_bytes, int upr, int team) {
+  using U = Unit<TT>;
+  constexpr bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL);
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  const int nblk = K32 ? cols / 32 : cols / 256;
+  uint8_t* qs = lds;
+  float* dsc = (float*)(lds + cols);
+  int16_t* bs = (int16_t*)(lds + cols + ((nblk * 4 + 15) & ~15));
+  const ActSplit sp{qs, dsc, bs};
+
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tpw = 64 / team;
+  const int r = lane / team, j = lane - r * team;
+  const long row0 = (((long)blockIdx.x * 4 + wv) * tpw + r) * NR;
+  const bool active = r < tpw && row0 < rows;
+  const uint8_t* wrow[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const long rk = row0 + k < rows ? row0 + k : rows - 1;
+    wrow[k] = W + (active ? rk : 0) * row_bytes;
+  }
+  const int u_end = active ? upr : 0;
+
+  // first weight unit in flight before the prologue
+  typename U::W wcur[NR];
+  if (j < u_end) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k) wcur[k] = U::load_w(wrow[k], j);
+  }
+
+  const bool out_q = XQ != nullptr && blockIdx.x == 0;
+  if constexpr (K32) {
+    // one value per thread, a 32-lane group per block
+    for (int b0 = 0; b0 < nblk; b0 += 8) {
+      const int b = b0 + (threadIdx.x >> 5), i = threadIdx.x & 31;
+      const bool ok = b < nblk;
+      uint32_t hb;
+      const int q = quant_q8_0_lane(ok ? X[32 * b + i] : 0.0f, hb);
+      if (ok) {
+        qs[32 * b + i] = (uint8_t)(int8_t)q;
+        if (i == 0) dsc[b] = h2f(hb);
+        if (out_q) {
+          uint8_t* ob = XQ + 34L * b;
+          ob[2 + i] = (uint8_t)(int8_t)q;
+          if (i == 0) {
+            ob[0] = (uint8_t)hb;
+            ob[1] = (uint8_t)(hb >> 8);
+          }
+        }
+      }
+    }
+  } else {
+    // a wave per 256-value block, four values per lane
+    for (int b0 = 0; b0 < nblk; b0 += 4) {
+      const int b = b0 + wv;
+      const bool ok = b < nblk;
+      float v[4];
+      if (ok) {
+        const float4 f = *(const float4*)(X + 256L * b + 4 * lane);
+        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+      } else {
+        v[0] = v[1] = v[2] = v[3] = 0.0f;
+      }
+      int gsum;
+      float scale;
+      const uint32_t packed = quant_q8_K_lane(v, gsum, scale);
+      if (ok) {
+        *(uint32_t*)(qs + 256 * b + 4 * lane) = packed;
+        if ((lane & 3) == 0) bs[16 * b + (lane >> 2)] = (int16_t)gsum;
+        if (lane == 0) dsc[b] = scale;
+        if (out_q) {
+          uint8_t* ob = XQ + 292L * b;
+          *(uint32_t*)(ob + 4 + 4 * lane) = packed;
+          if ((lane & 3) == 0) *(int16_t*)(ob + 260 + 2 * (lane >> 2)) = (int16_t)gsum;
+          if (lane == 0) *(float*)ob = scale;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  float acc[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) acc[k] = 0.0f;
+  for (int u = j; u < u_end; u += team) {
+    const int un = u + team;
+    typename U::W wnext[NR];
+    if (un < u_end) {
+#pragma unroll
+      for (int k = 0; k < NR; ++k) wnext[k] = U::load_w(wrow[k], un);
+    }
+    const typename U::A a = U::load_a_split(sp, u);
+#pragma unroll
+    for (int k = 0; k < NR; ++k) acc[k] += U::dot(wcur[k], a);
+#pragma unroll
+    for (int k = 0; k < NR; ++k) wcur[k] = wnext[k];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    if (off < team) {
+#pragma unroll
+      for (int k = 0; k < NR; ++k) {
+        const float v = __shfl_down(acc[k], off, 64);
+        if (j + off < team) acc[k] += v;
+      }
+    }
+  }
+  if (active && j == 0) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k)
+      if (row0 + k < rows) Y[row0 + k] = acc[k];
   }
 }
 
@@ -269,16 +458,30 @@ static hipError_t launch_gemv_type(const GemvArgs& g, int team, int nt, int nr, 
 }
 
 // Default launch shape for batch-1, from sweeps on MI355X at the benchmark
-// shapes: Q6_K decode issues the most loads per byte and wants the most
-// parallelism (one row per lane group of up to 64 lanes); Q4_K and IQ4_NL
-// want the activation reused over two rows per lane; Q8_0 over two rows
-// when the matrix is large enough to fill the GPU anyway.
+// shapes.  Long Q6_K / Q4_K rows (>= 8192 / 4096 values) take teams of four /
+// two whole waves with two or four rows per team: the activation is shared
+// by the rows while the waves in flight stay many (Q6_K [2560, 9728]: 7.6 us
+// vs 9.0 us with 64-lane teams; [5120, 17408]: 18.2 vs 21.9 us; Q4_K
+// [17408, 5120]: 11.4 vs 12.9 us).  Otherwise Q6_K uses 64 lanes per row,
+// Q4_K and IQ4_NL reuse the activation over two or four rows per lane, and
+// Q8_0 over two rows when the matrix is large enough to fill the GPU anyway.
 static void default_shape(const GemvArgs& g, int& team, int& nr) {
   const int upr = g.cols / 64;
+  // long rows: teams of whole waves (k_gemv_mw), several rows per team
+  if (g.ttype == TT_Q6_K && upr >= 128) {
+    team = 256;
+    nr = g.rows >= 4096 ? 4 : 2;
+    return;
+  }
+  if (g.ttype == TT_Q4_K && upr >= 64) {
+    team = 128;
+    nr = 4;
+    return;
+  }
   switch (g.ttype) {
-    case TT_Q6_K: nr = 1; team = 64; break;
+    case TT_Q6_K: nr = g.rows >= 4096 ? 2 : 1; team = 64; break;
     case TT_Q4_K: nr = g.rows >= 16384 && upr <= 40 ? 4 : 2; team = upr <= 40 ? 40 : 20; break;
-    case TT_IQ4_NL: nr = 2; team = 20; break;
+    case TT_IQ4_NL: nr = 4; team = 20; break;
     default: nr = g.rows >= 4096 ? 2 : 1; team = 16; break;
   }
   if (team > upr) team = upr;
@@ -290,6 +493,8 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
   }
 }
 
+static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipStream_t s);
+
 hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   if (team <= 0 && nr <= 0 && g.tokens == 1) {
@@ -298,12 +503,116 @@ hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t 
     if (nr <= 0) nr = 1;
     if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);
   }
+  if (team > 64) return launch_gemv_multiwave(g, nr, team / 64, s);
   if (nt <= 0) nt = gemv_pick_nt(g.tokens);
   switch (g.ttype) {
     case TT_Q8_0: return launch_gemv_type<TT_Q8_0>(g, team, nt, nr, s);
     case TT_IQ4_NL: return launch_gemv_type<TT_IQ4_NL>(g, team, nt, nr, s);
     case TT_Q4_K: return launch_gemv_type<TT_Q4_K>(g, team, nt, nr, s);
     case TT_Q6_K: return launch_gemv_type<TT_Q6_K>(g, team, nt, nr, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int TT, int NR, int WV>
+static hipError_t launch_gemv_mw_t(const GemvArgs& g, hipStream_t s) {
+  constexpr int TPB = 4 / WV;
+  const long teams = (g.rows + NR - 1) / NR;
+  const unsigned grid = (unsigned)((teams + TPB - 1) / TPB);
+  hipLaunchKernelGGL((k_gemv_mw<TT, NR, WV>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
+                     (const uint8_t*)g.xq, g.out, g.rows, g.row_bytes, g.cols / 64);
+  return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t launch_gemv_mw_type(const GemvArgs& g, int nr, int wv, hipStream_t s) {
+  if (wv == 2) {
+    switch (nr) {
+      case 1: return launch_gemv_mw_t<TT, 1, 2>(g, s);
+      case 2: return launch_gemv_mw_t<TT, 2, 2>(g, s);
+      case 4: return launch_gemv_mw_t<TT, 4, 2>(g, s);
+    }
+  } else if (wv == 4) {
+    switch (nr) {
+      case 1: return launch_gemv_mw_t<TT, 1, 4>(g, s);
+      case 2: return launch_gemv_mw_t<TT, 2, 4>(g, s);
+      case 4: return launch_gemv_mw_t<TT, 4, 4>(g, s);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+// one token, teams of wv = 2 or 4 waves
+static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipStream_t s) {
+  if (g.tokens != 1) return hipErrorInvalidValue;
+  switch (g.ttype) {
+    case TT_Q8_0: return launch_gemv_mw_type<TT_Q8_0>(g, nr, wv, s);
+    case TT_IQ4_NL: return launch_gemv_mw_type<TT_IQ4_NL>(g, nr, wv, s);
+    case TT_Q4_K: return launch_gemv_mw_type<TT_Q4_K>(g, nr, wv, s);
+    case TT_Q6_K: return launch_gemv_mw_type<TT_Q6_K>(g, nr, wv, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int TT, int NR>
+static hipError_t launch_gemv_q_t(const GemvArgs& g, const float* x, void* xq_out, int team, hipStream_t s) {
+  const int upr = g.cols / 64;
+  if (team > upr) team = upr;
+  if (team > 64) team = 64;
+  const int tpw = 64 / team;
+  const long teams = (g.rows + NR - 1) / NR;
+  const long waves = (teams + tpw - 1) / tpw;
+  const unsigned grid = (unsigned)((waves + 3) / 4);
+  const size_t lds = (size_t)fused_lds_bytes(TT, g.cols);
+  hipLaunchKernelGGL((k_gemv_q<TT, NR>), dim3(grid), dim3(256), lds, s, (const uint8_t*)g.w, x,
+                     (uint8_t*)xq_out, g.out, g.rows, g.cols, g.row_bytes, upr, team);
+  return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t launch_gemv_q_type(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
+                                     hipStream_t s) {
+  switch (nr) {
+    case 1: return launch_gemv_q_t<TT, 1>(g, x, xq_out, team, s);
+    case 2: return launch_gemv_q_t<TT, 2>(g, x, xq_out, team, s);
+    case 4: return launch_gemv_q_t<TT, 4>(g, x, xq_out, team, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool gemv_fused_fits(int ttype, int cols) { return fused_lds_bytes(ttype, cols) <= kFusedMaxLds; }
+
+// Every workgroup of the fused kernel quantizes the whole activation, so its
+// extra work grows with workgroups x cols.  Measured on MI355X against the
+// separate quantize + GEMV launches: the fused launch wins below about 4e5
+// quantized values in total (Q8_0 [1024..6144, 1024]: 5.5-6.2 us vs 7.2-7.8
+// us), ties around 7e5 (Q4_K [4096, 4096]) and loses above (IQ4_NL
+// [248320, 2560]: 148 us vs 76 us).
+bool gemv_fused_preferred(const GemvArgs& g) {
+  if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols)) return false;
+  int team = 0, nr = 0;
+  default_shape(g, team, nr);
+  if (team > 64) return false;  // long rows: the prologue would dominate
+  const long tpw = 64 / team;
+  const long waves = ((g.rows + nr - 1) / nr + tpw - 1) / tpw;
+  return (waves + 3) / 4 * (long)g.cols <= 400000L;
+}
+
+hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
+                             hipStream_t s) {
+  if (g.rows <= 0) return hipSuccess;
+  if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols)) return hipErrorInvalidValue;
+  if (team <= 0 && nr <= 0) {
+    default_shape(g, team, nr);
+  } else {
+    if (nr <= 0) nr = 1;
+    if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);
+  }
+  switch (g.ttype) {
+    case TT_Q8_0: return launch_gemv_q_type<TT_Q8_0>(g, x, xq_out, team, nr, s);
+    case TT_IQ4_NL: return launch_gemv_q_type<TT_IQ4_NL>(g, x, xq_out, team, nr, s);
+    case TT_Q4_K: return launch_gemv_q_type<TT_Q4_K>(g, x, xq_out, team, nr, s);
+    case TT_Q6_K: return launch_gemv_q_type<TT_Q6_K>(g, x, xq_out, team, nr, s);
     default: return hipErrorInvalidValue;
   }
 }

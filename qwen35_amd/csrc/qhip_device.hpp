@@ -21,6 +21,9 @@ enum : int { TT_Q8_0 = 8, TT_Q4_K = 12, TT_Q6_K = 14, TT_IQ4_NL = 20 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
+// unaligned views (byte-aligned addresses; global memory only)
+typedef uint32_t u32x4_u __attribute__((ext_vector_type(4), aligned(1)));
+typedef uint32_t u32x2_u __attribute__((ext_vector_type(2), aligned(1)));
 
 // ---- loads (addresses are 4-byte aligned; see each caller) -----------------
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
@@ -75,6 +78,61 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float x) {
 // is what the reference's (int) cast compiles to on its CPU path.
 __device__ __forceinline__ int trunc_i32_x86(float v) {
   return (v > -2147483904.0f && v < 2147483648.0f) ? (int)v : (int)0x80000000u;
+}
+
+// ---- activation quantizers, one block per lane group -------------------------------
+// Q8_0 (src/kernels/x86/kernels32.c:1064-1087): lane i of a 32-lane group holds
+// value i of the block.  Returns the lane's quantized value; `hbits` gets the
+// block's f16 scale bits.  Every lane of the group must call it (shuffles).
+__device__ __forceinline__ int quant_q8_0_lane(float v, uint32_t& hbits) {
+  // |v| with the reference's "if (a > amax)" NaN handling: NaN never wins.
+  float a = v < 0.0f ? -v : v;
+  a = a > 0.0f ? a : 0.0f;
+#pragma unroll
+  for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+  const float scale = a > 0.0f ? a / 127.0f : 1.0f;
+  const float inv = a > 0.0f ? 1.0f / scale : 0.0f;
+  const float sv = v * inv;
+  const float r = sv + (sv >= 0.0f ? 0.5f : -0.5f);
+  int q = trunc_i32_x86(r);
+  q = q > 127 ? 127 : q;
+  q = q < -128 ? -128 : q;
+  hbits = f32_to_f16_bits(scale);
+  return q;
+}
+
+// Q8_K (src/kernels/x86/kernels256.c:865-896): lane l of a wave holds values
+// 4l..4l+3 of the 256-value block.  Returns them quantized and packed (byte i
+// = value 4l+i); `gsum` gets the sum of the lane's 16-value group (lanes 4g..4g+3
+// agree), `scale` the block's f32 scale.  Every lane of the wave must call it.
+__device__ __forceinline__ uint32_t quant_q8_K_lane(const float* v, int& gsum, float& scale) {
+  float a = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float e = v[i] < 0.0f ? -v[i] : v[i];
+    e = e > 0.0f ? e : 0.0f;
+    a = fmaxf(a, e);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
+  scale = a > 0.0f ? a / 127.0f : 1.0f;
+  const float inv = a > 0.0f ? 1.0f / scale : 0.0f;
+  uint32_t packed = 0;
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float r = roundf(v[i] * inv);
+    r = r < -127.0f ? -127.0f : r;
+    r = r > 127.0f ? 127.0f : r;
+    r = (r >= -127.0f) ? r : 127.0f;  // NaN
+    const int q = (int)r;
+    packed |= ((uint32_t)q & 0xFFu) << (8 * i);
+    s += q;
+  }
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  gsum = s;
+  return packed;
 }
 
 // ---- IQ4_NL codebook lookup on 4 packed indices --------------------------------
@@ -344,18 +402,14 @@ struct Unit<TT_Q6_K> {
   static constexpr int kWBytes = 52, kInts = 1;
   struct W { uint32_t la[4], lb[4], qh[4]; uint32_t sc01, sc23; uint32_t d; };
   using A = ActQ8K;
-  // 16 bytes at a 2-byte aligned address: 5 aligned dwords, funnel-shifted
-  // (the reads stay inside the super-block, or the weight buffer, whose size
-  // is a multiple of 4).
+  // Q6_K super-blocks are 210 bytes, so every other one starts 2-byte
+  // aligned.  gfx950 global loads take unaligned addresses (the target has
+  // unaligned buffer access; the compiler emits one global_load_dwordx4 for
+  // them), so each 16-byte piece is one load and every read stays inside the
+  // super-block.
   static __device__ __forceinline__ void load16(const uint8_t* p, uint32_t* out) {
-    const uint32_t sh = (uint32_t)(uintptr_t)p & 3u;
-    const uint8_t* b = p - sh;
-    const u32x4 x = ld128(b);
-    const uint32_t e = ld32(b + 16);
-    out[0] = funnel(x.y, x.x, sh);
-    out[1] = funnel(x.z, x.y, sh);
-    out[2] = funnel(x.w, x.z, sh);
-    out[3] = funnel(e, x.w, sh);
+    const u32x4_u v = *(const u32x4_u*)p;
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
   }
   static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
     const uint8_t* blk = row + 210 * (u >> 2);
@@ -364,16 +418,11 @@ struct Unit<TT_Q6_K> {
     load16(blk + 64 * h + 16 * lh, w.la);
     load16(blk + 64 * h + 32 + 16 * lh, w.lb);
     load16(blk + 128 + 32 * h + 16 * lh, w.qh);
-    // scales sc[8h + lh + 2q], q = 0..3: bytes 0,2,4,6 of the window at ws
-    const uint8_t* ws = blk + 192 + 8 * h + lh;
-    const uint32_t ssh = (uint32_t)(uintptr_t)ws & 3u;
-    const uint8_t* wb = ws - ssh;
-    const uint32_t s0 = ld32(wb), s1 = ld32(wb + 4), s2 = ld32(wb + 8);
-    w.sc01 = funnel(s1, s0, ssh);
-    w.sc23 = funnel(s2, s1, ssh);
-    const uint8_t* dp = blk + 208;
-    const uint32_t dsh = (uint32_t)(uintptr_t)dp & 3u;
-    w.d = ld32(dp - dsh) >> (8 * dsh);
+    // scales sc[8h + lh + 2q], q = 0..3: bytes 0, 2, 4, 6 of the 8 at ws
+    const u32x2_u sc = *(const u32x2_u*)(blk + 192 + 8 * h + lh);
+    w.sc01 = sc.x;
+    w.sc23 = sc.y;
+    w.d = *(const uint16_t*)(blk + 208);
     return w;
   }
   static __device__ __forceinline__ A load_a(const uint8_t* act, int u) {

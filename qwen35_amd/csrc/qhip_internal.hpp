@@ -30,6 +30,15 @@ int gemv_pick_nt(int tokens);
 hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t s);
 hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s);
 hipError_t launch_block_ints(const GemvArgs& g, int* ints, hipStream_t s);
+// Quantize + GEMV in one launch for one token: x is f32, the activation is
+// quantized inside every workgroup (bit-exact with the quantizers) into LDS;
+// xq_out (nullable) receives it in the reference layout.
+constexpr long kFusedMaxLds = 64 * 1024;
+bool gemv_fused_fits(int ttype, int cols);
+// whether the fused launch beats quantize + GEMV for this shape (measured rule)
+bool gemv_fused_preferred(const GemvArgs& g);
+hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
+                             hipStream_t s);
 // MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)
 hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s);
 

@@ -22,24 +22,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
   const long t = blockIdx.y;                                  // token
   const bool ok = b < nblocks;
   const float v = ok ? x[t * x_stride + 32 * b + i] : 0.0f;
-  // |v| with the reference's "if (a > amax)" NaN handling: NaN never wins.
-  float a = v < 0.0f ? -v : v;
-  a = a > 0.0f ? a : 0.0f;
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
-  const float amax = a;
-  const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-  const float inv = amax > 0.0f ? 1.0f / scale : 0.0f;
-  const float s = v * inv;
-  const float r = s + (s >= 0.0f ? 0.5f : -0.5f);
-  int q = trunc_i32_x86(r);
-  q = q > 127 ? 127 : q;
-  q = q < -128 ? -128 : q;
+  uint32_t hb;
+  const int q = quant_q8_0_lane(v, hb);
   if (ok) {
     uint8_t* ob = out + t * out_stride + 34 * b;
     ob[2 + i] = (uint8_t)(int8_t)q;
     if (i == 0) {
-      const uint32_t hb = f32_to_f16_bits(scale);
       ob[0] = (uint8_t)hb;
       ob[1] = (uint8_t)(hb >> 8);
     }
@@ -57,33 +45,9 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float* __restrict__
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = ok ? x[t * x_stride + 256 * b + 4 * l + i] : 0.0f;
-  float a = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float e = v[i] < 0.0f ? -v[i] : v[i];
-    e = e > 0.0f ? e : 0.0f;
-    a = fmaxf(a, e);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 64));
-  const float amax = a;
-  const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
-  const float inv = amax > 0.0f ? 1.0f / scale : 0.0f;
-  uint32_t packed = 0;
-  int gsum = 0;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float r = roundf(v[i] * inv);
-    r = r < -127.0f ? -127.0f : r;
-    r = r > 127.0f ? 127.0f : r;
-    r = (r >= -127.0f) ? r : 127.0f;  // NaN
-    const int q = (int)r;
-    packed |= ((uint32_t)q & 0xFFu) << (8 * i);
-    gsum += q;
-  }
-  // 16-value group = 4 consecutive lanes
-  gsum += __shfl_xor(gsum, 1, 64);
-  gsum += __shfl_xor(gsum, 2, 64);
+  int gsum;
+  float scale;
+  const uint32_t packed = quant_q8_K_lane(v, gsum, scale);
   if (ok) {
     uint8_t* ob = out + t * out_stride + 292 * b;
     *(uint32_t*)(ob + 4 + 4 * l) = packed;

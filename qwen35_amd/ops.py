@@ -71,6 +71,16 @@ def mul_mat(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
     return out
 
 
+def quantize_mul_mat_vec(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
+                         xq_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One launch: quantize f32 x (one token) inside the GEMV and multiply."""
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=w.device)
+    check("quantize_mul_mat_vec", load().qhip_launch_quantize_mul_mat_vec(
+        _p(w), _p(x), _p(xq_out) if xq_out is not None else None, _p(out), rows, cols, ttype, _stream()))
+    return out
+
+
 def gemv_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
                lanes_per_row: int, tokens_per_pass: int, rows_per_lane: int = 1,
                out: torch.Tensor | None = None) -> torch.Tensor:

@@ -171,3 +171,80 @@ def test_zero_weights_and_zero_activation(gpu, oracle):
     xq = ops.quantize_act(tt, torch.zeros((1, cols), device=gpu))
     assert torch.count_nonzero(ops.mul_mat(tt, wd, xq, rows, cols, 1)) == 0
 
+
+
+# ---- quantize + GEMV in one launch -----------------------------------------------------
+
+FUSED = [(po.TT_Q8_0, 300, 1024), (po.TT_Q8_0, 6144, 1024), (po.TT_IQ4_NL, 200, 2560),
+         (po.TT_Q4_K, 100, 2560), (po.TT_Q4_K, 19456, 2560), (po.TT_Q6_K, 50, 9728),
+         (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 16, 2304)]
+
+
+@pytest.mark.parametrize("tt,rows,cols", FUSED, ids=[case_id(*c) for c in FUSED])
+def test_fused_quantize_gemv(gpu, oracle, tt, rows, cols):
+    w = synth.make_weight(tt, rows, cols, seed=11, tag=tt)
+    x = synth.make_act(cols, 1, seed=11)
+    want = oracle.matvec(tt, w, x)[0]
+    wd = to_dev(w, gpu)
+    xq = torch.empty(oracle.quantize_act(tt, x).shape[-1], dtype=torch.uint8, device=gpu)
+    got = ops.quantize_mul_mat_vec(tt, wd, to_dev(x[0], gpu), rows, cols, xq_out=xq).cpu().numpy()
+    assert np.array_equal(xq.cpu().numpy(), oracle.quantize_act(tt, x)[0])
+    assert rel_l2(got, want) < TOL
+    # same numbers as the two-launch path
+    two = ops.mul_mat(tt, wd, ops.quantize_act(tt, to_dev(x, gpu)), rows, cols, 1).cpu().numpy()[0]
+    assert rel_l2(got, two) < 1e-6
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K])
+def test_fused_quantize_special_values(gpu, oracle, tt):
+    rows, cols = 40, 2048
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal(cols) * 10.0 ** rng.uniform(-20, 20, cols // 256).repeat(256)).astype(np.float32)
+    x[5] = np.inf
+    x[300] = -0.0
+    x[700:740] = 0.0
+    x[1024:1030] = np.float32([127, 63.5, -63.5, .5, -.5, 1.5])
+    w = synth.make_weight(tt, rows, cols, seed=2, tag=tt)
+    xq = torch.empty(oracle.quantize_act(tt, x[None]).shape[-1], dtype=torch.uint8, device=gpu)
+    ops.quantize_mul_mat_vec(tt, to_dev(w, gpu), to_dev(x, gpu), rows, cols, xq_out=xq)
+    assert np.array_equal(xq.cpu().numpy(), oracle.quantize_act(tt, x[None])[0])
+
+
+def test_fused_declines(gpu):
+    from qwen35_amd import _lib
+    L = _lib.load()
+    tt, rows, cols = po.TT_Q4_K, 8, 512
+    w = torch.zeros(rows * 288, dtype=torch.uint8, device=gpu)
+    xbuf = torch.zeros(cols + 4, device=gpu)
+    out = torch.empty(rows, device=gpu)
+    # activation not 16-byte aligned
+    assert L.qhip_launch_quantize_mul_mat_vec(w.data_ptr(), xbuf[1:].data_ptr(), None, out.data_ptr(), rows,
+                                              cols, tt, None) == qwen35_amd.DECLINE
+    # too wide for the LDS image
+    wide = 65536
+    w2 = torch.zeros(2 * wide // 32 * 34, dtype=torch.uint8, device=gpu)
+    x2 = torch.zeros(wide, device=gpu)
+    assert L.qhip_launch_quantize_mul_mat_vec(w2.data_ptr(), x2.data_ptr(), None, out.data_ptr(), 2, wide,
+                                              po.TT_Q8_0, None) == qwen35_amd.DECLINE
+    # invalid type is an error, not a decline
+    rc = L.qhip_launch_quantize_mul_mat_vec(w.data_ptr(), xbuf.data_ptr(), None, out.data_ptr(), rows, cols, 99,
+                                            None)
+    assert rc not in (0, qwen35_amd.DECLINE)
+
+
+@pytest.mark.parametrize("tt", TYPES)
+def test_multiwave_team_shapes(gpu, oracle, tt):
+    """Teams of two / four whole waves (one token), rows not a multiple of the
+    rows per team, and uneven splits of the units over the waves."""
+    rows, cols = 37, (9728 if tt == po.TT_Q6_K else 5120)
+    w, x, wd, xd = setup(tt, rows, cols, 1, gpu, seed=9)
+    want = oracle.matvec(tt, w, x)
+    xq = ops.quantize_act(tt, xd)
+    for lpr in (128, 256):
+        for nr in (1, 2, 4):
+            got = ops.gemv_tuned(tt, wd, xq, rows, cols, 1, lpr, 1, nr).cpu().numpy()
+            assert rel_l2(got, want) < TOL, (lpr, nr, rel_l2(got, want))
+    # multi-wave teams serve one token only
+    xq2 = ops.quantize_act(tt, to_dev(synth.make_act(cols, 2, seed=9), gpu))
+    with pytest.raises(qwen35_amd.QhipError):
+        ops.gemv_tuned(tt, wd, xq2, rows, cols, 2, 128, 1, 1)
