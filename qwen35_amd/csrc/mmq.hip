@@ -280,39 +280,59 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
       // opaque to the optimizer: the bias stays in 16 registers as every
       // MFMA's accumulator input (instead of being re-created per MFMA)
       asm volatile("" : "+v"(bias));
-      const int nsteps = 2 * nu;
+      // issue: fragments of block s and its MFMAs; finish: scale and
+      // accumulate block s.  Software-pipelined: block s+1's MFMAs are issued
+      // before block s is scaled, so the matrix core and the VALU overlap.
+      auto issue = [&](int s, i32x16 (&c)[NA][NB], float (&dw)[NB]) {
+        i32x4 af[NA], bf[NB];
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (s < nsteps) {
-          i32x4 af[NA], bf[NB];
-          f32x4 da[NA][4];
-          float dw[NB], cw[NB];
+        for (int a = 0; a < NA; ++a)
+          af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
 #pragma unroll
-          for (int a = 0; a < NA; ++a) {
-            af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
+        for (int b = 0; b < NB; ++b) {
+          bf[b] = *(const i32x4*)(sm.bq + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
+          dw[b] = sm.wd[s][rb0 + 32 * b + li];
+        }
 #pragma unroll
-            for (int q = 0; q < 4; ++q) da[a][q] = *(const f32x4*)&sm.ad[s][tb0 + 32 * a + 8 * q + 4 * lh];
-          }
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) c[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], bias, 0, 0, 0);
+      };
+      auto finish = [&](int s, const i32x16 (&c)[NA][NB], const float (&dw)[NB]) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          f32x4 da[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) da[q] = *(const f32x4*)&sm.ad[s][tb0 + 32 * a + 8 * q + 4 * lh];
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
-            bf[b] = *(const i32x4*)(sm.bq + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
-            dw[b] = sm.wd[s][rb0 + 32 * b + li];
-            cw[b] = -kBias * dw[b];
-          }
+            const float cw = -kBias * dw[b];
 #pragma unroll
-          for (int a = 0; a < NA; ++a)
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-              const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], bias, 0, 0, 0);
-#pragma unroll
-              for (int e = 0; e < 16; ++e) {
-                // (a scalar copy first: bit-casting the vector element
-                // expression c[e] directly reads element 0 for every e)
-                const int ce = c[e];
-                const float t = __builtin_fmaf(__int_as_float(ce), dw[b], cw[b]);
-                acc[a][b][e] = __builtin_fmaf(t, da[a][e >> 2][e & 3], acc[a][b][e]);
-              }
+            for (int e = 0; e < 16; ++e) {
+              // (a scalar copy first: bit-casting the vector element
+              // expression c[e] directly reads element 0 for every e)
+              const int ce = c[a][b][e];
+              const float t = __builtin_fmaf(__int_as_float(ce), dw[b], cw);
+              acc[a][b][e] = __builtin_fmaf(t, da[e >> 2][e & 3], acc[a][b][e]);
             }
+          }
+        }
+      };
+      i32x16 c0[NA][NB], c1[NA][NB];
+      float dw0[NB], dw1[NB];
+      if (nu == 4) {
+        issue(0, c0, dw0);
+#pragma unroll
+        for (int s2 = 0; s2 < 8; s2 += 2) {
+          issue(s2 + 1, c1, dw1);
+          finish(s2, c0, dw0);
+          if (s2 + 2 < 8) issue(s2 + 2, c0, dw0);
+          finish(s2 + 1, c1, dw1);
+        }
+      } else {
+        for (int s2 = 0; s2 < 2 * nu; ++s2) {
+          issue(s2, c0, dw0);
+          finish(s2, c0, dw0);
         }
       }
     } else if constexpr (TT == TT_Q4_K) {
@@ -328,23 +348,37 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         scw[b][0] = sm.wsc[rb0 + 32 * b + li][0];
         scw[b][1] = sm.wsc[rb0 + 32 * b + li][1];
       }
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      // pipelined as in the 32-value path: sub-block s+1's MFMAs are issued
+      // before sub-block s's integer scaling
+      auto issue = [&](int s, i32x16 (&c)[NA][NB]) {
         i32x4 af[NA], bf[NB];
 #pragma unroll
         for (int a = 0; a < NA; ++a) af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
 #pragma unroll
         for (int b = 0; b < NB; ++b) bf[b] = *(const i32x4*)(sm.bq + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
 #pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) c[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], zero, 0, 0, 0);
+      };
+      auto finish = [&](int s, const i32x16 (&c)[NA][NB]) {
+#pragma unroll
         for (int b = 0; b < NB; ++b) {
           const int sc = (int)((scw[b][s >> 2] >> (8 * (s & 3))) & 0xFFu);
 #pragma unroll
-          for (int a = 0; a < NA; ++a) {
-            const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bf[b], zero, 0, 0, 0);
+          for (int a = 0; a < NA; ++a)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) isum[a][b][e] += sc * sext24(c[e]);
-          }
+            for (int e = 0; e < 16; ++e) isum[a][b][e] += sc * sext24(c[a][b][e]);
         }
+      };
+      i32x16 c0[NA][NB], c1[NA][NB];
+      issue(0, c0);
+#pragma unroll
+      for (int s = 0; s < 8; s += 2) {
+        issue(s + 1, c1);
+        finish(s, c0);
+        if (s + 2 < 8) issue(s + 2, c0);
+        finish(s + 1, c1);
       }
       // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
       f16x8 am[NA], bm[NB];
@@ -387,23 +421,36 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         const uint4 v = *(const uint4*)&sm.wsc[rb0 + 32 * b + li][0];
         scw[b][0] = v.x; scw[b][1] = v.y; scw[b][2] = v.z; scw[b][3] = v.w;
       }
-#pragma unroll
-      for (int gq = 0; gq < 16; ++gq) {
+      // pipelined: group g+1's MFMAs are issued before group g is scaled
+      auto issue = [&](int gq, i32x16 (&c)[NA][NB]) {
         long af[NA], bf[NB];
 #pragma unroll
         for (int a = 0; a < NA; ++a) af[a] = *(const i64x1_a8*)(sm.aq + (tb0 + 32 * a + li) * kQS + 16 * gq + 8 * lh);
 #pragma unroll
         for (int b = 0; b < NB; ++b) bf[b] = *(const i64x1_a8*)(sm.bq + (rb0 + 32 * b + li) * kQS + 16 * gq + 8 * lh);
 #pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) c[a][b] = __builtin_amdgcn_mfma_i32_32x32x16_i8(af[a], bf[b], zero, 0, 0, 0);
+      };
+      auto finish = [&](int gq, const i32x16 (&c)[NA][NB]) {
+#pragma unroll
         for (int b = 0; b < NB; ++b) {
           const int sc = sext8(scw[b][gq >> 2] >> (8 * (gq & 3)));
 #pragma unroll
-          for (int a = 0; a < NA; ++a) {
-            const i32x16 c = __builtin_amdgcn_mfma_i32_32x32x16_i8(af[a], bf[b], zero, 0, 0, 0);
+          for (int a = 0; a < NA; ++a)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) isum[a][b][e] += sc * sext24(c[e]);
-          }
+            for (int e = 0; e < 16; ++e) isum[a][b][e] += sc * sext24(c[a][b][e]);
         }
+      };
+      i32x16 c0[NA][NB], c1[NA][NB];
+      issue(0, c0);
+#pragma unroll
+      for (int gq = 0; gq < 16; gq += 2) {
+        issue(gq + 1, c1);
+        finish(gq, c0);
+        if (gq + 2 < 16) issue(gq + 2, c0);
+        finish(gq + 1, c1);
       }
       f32x4 dy[NA][4];
       float d[NB];
