@@ -84,6 +84,15 @@ int qhip_launch_quantize_q8_K(const float *d_x, void *d_out, int nblocks, void *
 int qhip_launch_quantize_act(int ttype, const float *d_x, void *d_out, int cols, int tokens,
                              void *stream);
 
+/* ---- dequantization ---------------------------------------------------------
+ * q35_launch_dequantize (src/kernels/cuda/api.h:95-96): `nblocks` NATIVE blocks
+ * (32 values for Q8_0 / IQ4_NL, 256 for Q4_K / Q6_K) of packed bytes to f32.
+ * q35_launch_dequantize_row (api.h:101-102): one row of `cols` values.
+ * Bit-exact with src/quant_dequant.zig (the CPU dequantRowInto,
+ * src/backend_cpu.zig:661-679). */
+int qhip_launch_dequantize(int ttype, const void *d_src, float *d_dst, int nblocks, void *stream);
+int qhip_launch_dequantize_row(int ttype, const void *d_src_row, float *d_dst, int cols, void *stream);
+
 /* ---- matvec -----------------------------------------------------------------
  * q35_launch_mul_mat_vec (src/kernels/cuda/api.h:104-112):
  *   out[t*rows + r] = W[r] . xq[t] for t < tokens.
@@ -216,6 +225,9 @@ int qhip_backend_matvec_pair(qhip_backend *be, float *d_out, const qhip_linear *
 /* matvecBatchK (backend.zig:177-178): out[j*rows + r] = W[r] . x_j, j < k. */
 int qhip_backend_matvec_batch_k(qhip_backend *be, float *d_out, const qhip_linear *w,
                                 const float *d_xK, int k);
+/* dequantRow (backend.zig:148-151): d_dst[cols] = f32 values of weight row `row`
+ * (the embedding lookup). */
+int qhip_backend_dequant_row(qhip_backend *be, float *d_dst, const qhip_linear *w, int row);
 /* Stream for subsequent calls (NULL = default stream) and a host wait. */
 int qhip_backend_set_stream(qhip_backend *be, void *stream);
 int qhip_backend_sync(qhip_backend *be);

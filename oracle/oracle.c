@@ -413,7 +413,9 @@ int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
         int bb = ttype == ORC_TT_Q8_0 ? 34 : 18;
         for (int b = 0; b < cols / 32; ++b) {
             const uint8_t *blk = w + bb * b;
-            float d = orc_f16_to_f32(ld16(blk));
+            /* quant_dequant.zig:34-37 converts with @floatCast, which keeps
+             * the sign of a zero scale (unlike the dot path's k32 decode) */
+            float d = orc_f16_to_f32_k256(ld16(blk));
             for (int j = 0; j < 32; ++j) {
                 int v;
                 if (ttype == ORC_TT_Q8_0) v = (int8_t)blk[2 + j];

@@ -34,6 +34,8 @@ SIGNATURES = {
     "qhip_launch_quantize_q8_0": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "qhip_launch_quantize_q8_K": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
     "qhip_launch_quantize_act": (c_int, [c_int, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "qhip_launch_dequantize": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p]),
+    "qhip_launch_dequantize_row": (c_int, [c_int, c_void_p, c_void_p, c_int, c_void_p]),
     "qhip_launch_mul_mat_vec": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,
                                         c_void_p]),
     "qhip_launch_mul_mat_vec_q8_0": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
@@ -72,6 +74,7 @@ SIGNATURES = {
                                          ctypes.POINTER(QhipLinear), c_void_p]),
     "qhip_backend_matvec_batch_k": (c_int, [c_void_p, c_void_p, ctypes.POINTER(QhipLinear),
                                             c_void_p, c_int]),
+    "qhip_backend_dequant_row": (c_int, [c_void_p, c_void_p, ctypes.POINTER(QhipLinear), c_int]),
     "qhip_backend_set_stream": (c_int, [c_void_p, c_void_p]),
     "qhip_backend_sync": (c_int, [c_void_p]),
 }

@@ -239,6 +239,22 @@ int qhip_launch_quantize_act(int ttype, const float* d_x, void* d_out, int cols,
   return (int)launch_quantize_q8_K(d_x, d_out, cols / 256, tokens, cols, ab, S(stream));
 }
 
+int qhip_launch_dequantize(int ttype, const void* d_src, float* d_dst, int nblocks, void* stream) {
+  int be, bb;
+  if (!geom(ttype, be, bb) || nblocks < 0) return (int)hipErrorInvalidValue;
+  if (nblocks == 0) return 0;
+  if (!d_src || !d_dst) return (int)hipErrorInvalidValue;
+  return (int)launch_dequant(ttype, d_src, d_dst, (long)nblocks * be, S(stream));
+}
+
+int qhip_launch_dequantize_row(int ttype, const void* d_src_row, float* d_dst, int cols, void* stream) {
+  int be, bb;
+  if (!geom(ttype, be, bb) || cols < 0 || cols % be) return (int)hipErrorInvalidValue;
+  if (cols == 0) return 0;
+  if (!d_src_row || !d_dst) return (int)hipErrorInvalidValue;
+  return (int)launch_dequant(ttype, d_src_row, d_dst, cols, S(stream));
+}
+
 int qhip_launch_mul_mat(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
                         int tokens, int ttype, int path, void* stream) {
   GemvArgs g;

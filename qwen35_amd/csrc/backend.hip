@@ -216,6 +216,13 @@ int qhip_backend_matvec_batch_k(qhip_backend* be, float* d_out, const qhip_linea
   return run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_xK, k);
 }
 
+int qhip_backend_dequant_row(qhip_backend* be, float* d_dst, const qhip_linear* w, int row) {
+  if (!be || !valid_linear(w) || !d_dst || row < 0 || row >= w->rows) return (int)hipErrorInvalidValue;
+  return report("dequantRow", (hipError_t)qhip_launch_dequantize_row(
+                                  w->ttype, (const uint8_t*)w->dev + (size_t)row * w->row_bytes, d_dst,
+                                  w->cols, be->stream));
+}
+
 int qhip_backend_set_stream(qhip_backend* be, void* stream) {
   if (!be) return (int)hipErrorInvalidValue;
   be->stream = (hipStream_t)stream;

@@ -1,0 +1,102 @@
+// dequant.hip -- GGUF blocks to f32, bit-exact with the reference's dequant
+// (src/quant_dequant.zig, the CPU backend's dequantRowInto,
+// src/backend_cpu.zig:661-679), for the embedding lookup (Exec.dequantRow,
+// src/backend.zig:148-151) and whole-tensor expansion (api.h:95-102).
+//
+//   Q8_0    d * q                                    quant_dequant.zig:1388-1402
+//   IQ4_NL  d * codebook[nibble]                     :347-360
+//   Q4_K    (d * sc) * nibble - (dmin * m)           :54-77  (separate roundings)
+//   Q6_K    (d * sc) * (q6 - 32)                     :222-251
+// The library is compiled with -ffp-contract=off, so each product and the
+// Q4_K difference round exactly as the reference's Zig (strict float mode).
+//
+// One thread per four consecutive values; the block header is re-read by the
+// threads of a block (it is in L1), the quantized bytes once.
+#include "qhip_device.hpp"
+#include "qhip_internal.hpp"
+
+namespace qhip {
+
+__device__ __forceinline__ uint32_t ld16b(const uint8_t* p) { return (uint32_t)p[0] | ((uint32_t)p[1] << 8); }
+
+__device__ __forceinline__ int iq4_value(uint32_t nib) {
+  const uint32_t tab = nib < 4 ? IQ4_T0 : nib < 8 ? IQ4_T1 : nib < 12 ? IQ4_T2 : IQ4_T3;
+  return sext8(tab >> (8 * (nib & 3)));
+}
+
+template <int TT>
+__global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src, float* __restrict__ dst,
+                                                  long nvals) {
+  const long v0 = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (v0 >= nvals) return;
+  float o[4];
+  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
+    constexpr int BB = TT == TT_Q8_0 ? 34 : 18;
+    const uint8_t* blk = src + (v0 / 32) * BB;
+    const int j0 = (int)(v0 % 32);
+    const float d = h2f(ld16b(blk));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = j0 + i;
+      int q;
+      if constexpr (TT == TT_Q8_0) {
+        q = (int)(int8_t)blk[2 + j];
+      } else {
+        q = iq4_value(j < 16 ? (blk[2 + j] & 15u) : (uint32_t)(blk[2 + j - 16] >> 4));
+      }
+      o[i] = d * (float)q;
+    }
+  } else if constexpr (TT == TT_Q4_K) {
+    const uint8_t* blk = src + (v0 / 256) * 144;
+    const int e0 = (int)(v0 % 256), sub = e0 / 32;
+    const uint8_t* s12 = blk + 4;
+    int sc, m;  // src/kernels/x86/kernels256.c:105-125
+    if (sub < 4) {
+      sc = s12[sub] & 63;
+      m = s12[sub + 4] & 63;
+    } else {
+      sc = (s12[sub + 4] & 15) | ((s12[sub - 4] >> 6) << 4);
+      m = (s12[sub + 4] >> 4) | ((s12[sub] >> 6) << 4);
+    }
+    const float d1 = h2f(ld16b(blk)) * (float)sc;
+    const float m1 = h2f(ld16b(blk + 2)) * (float)m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int l = (e0 + i) % 32;
+      const uint32_t q = blk[16 + 32 * (sub / 2) + l];
+      const int nib = (int)((sub & 1) ? (q >> 4) : (q & 15u));
+      o[i] = d1 * (float)nib - m1;
+    }
+  } else {  // Q6_K
+    const uint8_t* blk = src + (v0 / 256) * 210;
+    const int e0 = (int)(v0 % 256);
+    const float d = h2f(ld16b(blk + 208));
+    const float ds = d * (float)(int)(int8_t)blk[192 + e0 / 16];  // four values share a 16-group
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + i, h = e / 128, q = (e % 128) / 32, l = e % 32;
+      uint32_t lo = blk[64 * h + 32 * (q & 1) + l];
+      lo = q >= 2 ? (lo >> 4) : (lo & 15u);
+      const uint32_t hb = (blk[128 + 32 * h + l] >> (2 * q)) & 3u;
+      o[i] = ds * (float)((int)(lo | (hb << 4)) - 32);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dst[v0 + i] = o[i];
+}
+
+hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hipStream_t s) {
+  if (nvals <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)((nvals / 4 + 255) / 256);
+  const uint8_t* p = (const uint8_t*)src;
+  switch (ttype) {
+    case TT_Q8_0: hipLaunchKernelGGL(k_dequant<TT_Q8_0>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
+    case TT_IQ4_NL: hipLaunchKernelGGL(k_dequant<TT_IQ4_NL>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
+    case TT_Q4_K: hipLaunchKernelGGL(k_dequant<TT_Q4_K>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
+    case TT_Q6_K: hipLaunchKernelGGL(k_dequant<TT_Q6_K>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace qhip

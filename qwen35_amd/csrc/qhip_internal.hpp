@@ -39,6 +39,8 @@ bool gemv_fused_fits(int ttype, int cols);
 bool gemv_fused_preferred(const GemvArgs& g);
 hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
                              hipStream_t s);
+// GGUF blocks -> f32 (nvals = whole blocks' values)
+hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hipStream_t s);
 // MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)
 hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s);
 

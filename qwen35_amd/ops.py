@@ -61,6 +61,20 @@ def quantize_q8_K(x: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def dequantize(ttype: int, w: torch.Tensor, nblocks: int) -> torch.Tensor:
+    """f32 values of `nblocks` native blocks (bit-exact with the reference dequant)."""
+    be = _GEOM[ttype][0]
+    out = torch.empty(nblocks * be, dtype=torch.float32, device=w.device)
+    check("dequantize", load().qhip_launch_dequantize(ttype, _p(w), _p(out), nblocks, _stream()))
+    return out
+
+
+def dequantize_row(ttype: int, wrow: torch.Tensor, cols: int) -> torch.Tensor:
+    out = torch.empty(cols, dtype=torch.float32, device=wrow.device)
+    check("dequantize_row", load().qhip_launch_dequantize_row(ttype, _p(wrow), _p(out), cols, _stream()))
+    return out
+
+
 def mul_mat(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
             path: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
     """out [tokens, rows] = W . xq_t (xq already quantized)."""
@@ -195,6 +209,9 @@ class Backend:
     def matvec_batch_k(self, out: torch.Tensor, w: QhipLinear, xk: torch.Tensor, k: int) -> None:
         check("matvec_batch_k", self.lib.qhip_backend_matvec_batch_k(self._h, _p(out),
                                                                      ctypes.byref(w), _p(xk), k))
+
+    def dequant_row(self, out: torch.Tensor, w: QhipLinear, row: int) -> None:
+        check("dequant_row", self.lib.qhip_backend_dequant_row(self._h, _p(out), ctypes.byref(w), row))
 
     def sync(self) -> None:
         check("sync", self.lib.qhip_backend_sync(self._h))

@@ -218,3 +218,30 @@ def test_zero_activation_gives_zero(oracle):
     w = synth.make_weight(po.TT_Q4_K, 8, 512, seed=1)
     out = oracle.matvec(po.TT_Q4_K, w, np.zeros((1, 512), np.float32))
     assert np.all(out == 0)
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K])
+def test_dequant_signed_zero_scale(oracle, tt):
+    """The reference dequant converts the f16 scale with @floatCast
+    (quant_dequant.zig:34-37), which keeps -0: d * q then carries the IEEE sign
+    of the product.  Closed form with numpy's exact float16 conversion."""
+    be, bb = po.GEOM[tt]
+    cols = be
+    w = np.zeros(bb, np.uint8)
+    rng = np.random.default_rng(0)
+    w[:] = rng.integers(0, 256, bb)
+    off = 208 if tt == po.TT_Q6_K else 0
+    w[off:off + 2] = [0x00, 0x80]  # -0
+    if tt == po.TT_Q4_K:
+        w[2:4] = [0x00, 0x80]
+    out = oracle.dequant_row(tt, w, cols)
+    assert np.all(out == 0)
+    d = np.float32(np.float16(-0.0))
+    assert np.signbit(d)
+    if tt == po.TT_Q8_0:
+        q = w[2:].view(np.int8).astype(np.float32)
+        assert np.array_equal(np.signbit(out), np.signbit(d * q))
+    elif tt == po.TT_IQ4_NL:
+        idx = np.concatenate([w[2:18] & 15, w[2:18] >> 4])
+        q = IQ4NL[idx].astype(np.float32)
+        assert np.array_equal(np.signbit(out), np.signbit(d * q))
