@@ -335,7 +335,8 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
     [16,256], packed by the ragged quantizer, one launch) and a dense 512-token
     sequence.  Config 5: Q4_K gate [17408,5120] and Q6_K down [5120,17408] at
     T = 1, 4, 16, 64, 512 on the GEMV and on the MMQ, and the crossover.
-    Throughput: tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak."""
+    Throughput: tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak.
+    `mmq_us` is the faster of the tile MMQ and (Q6_K) the image MMQ."""
     PATH_GEMV, PATH_MMQ = 1, 2
     res = {}
 
@@ -390,6 +391,8 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
     sweep = {}
     for name, tt, rows, cols in (("q4_k_17408x5120", 12, 17408, 5120), ("q6_k_5120x17408", 14, 5120, 17408)):
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
+        # the prepared MMQ weight image the Exec mirror uses for Q6_K prefill
+        img = ops.mmq_image(tt, w, rows, cols) if tt == 14 else None
         rows_out = []
         cross = None
         for T in (1, 4, 16, 64, 512):
@@ -399,18 +402,25 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
             it = 100 if T <= 64 else 30
             s_g = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
                                                         PATH_GEMV, stream), it)
-            s_m = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+            s_t = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
                                                         PATH_MMQ, stream), it)
+            pt = {"T": T, "gemv_us": round(s_g * 1e6, 2), "mmq_tile_us": round(s_t * 1e6, 2)}
+            s_m = s_t
+            if img is not None:
+                s_i = timed(lambda: lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows,
+                                                                  cols, T, tt, 0, 0, stream), it)
+                pt["mmq_image_us"] = round(s_i * 1e6, 2)
+                s_m = min(s_t, s_i)
             tops, fr = frac(rows, cols, T, s_m)
-            rows_out.append({"T": T, "gemv_us": round(s_g * 1e6, 2), "mmq_us": round(s_m * 1e6, 2),
-                             "gemv_tokens_per_s": round(T / s_g, 1), "mmq_tokens_per_s": round(T / s_m, 1),
-                             "mmq_int8_tops": tops, "mmq_int8_mfma_frac": fr})
+            pt.update({"mmq_us": round(s_m * 1e6, 2), "gemv_tokens_per_s": round(T / s_g, 1),
+                       "mmq_tokens_per_s": round(T / s_m, 1), "mmq_int8_tops": tops, "mmq_int8_mfma_frac": fr})
+            rows_out.append(pt)
             if cross is None and s_m < s_g:
                 cross = T
         sweep[name] = {"points": rows_out, "crossover_T": cross}
         log(f"mmq cfg5 {name}: " + ", ".join(f"T={p['T']} gemv {p['gemv_us']} / mmq {p['mmq_us']} us"
                                               for p in rows_out) + f"; crossover T={cross}")
-        del w
+        del w, img
         torch.cuda.empty_cache()
     res["cfg5_sweep"] = sweep
     return res

@@ -149,6 +149,23 @@ int qhip_launch_mul_mat_vec_tile(const void *d_w, const void *d_xq, float *d_out
 int qhip_launch_mmq_tuned(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
                           int tokens, int ttype, int tile_tokens, int tile_rows, void *stream);
 
+/* MMQ weight image (no reference counterpart; the reference's CUDA MMQ decodes
+ * the GGUF blocks in every launch, mmq.cu:499-659).  For Q4_K and Q6_K the
+ * integer sub-block scales are folded into the quantized values once,
+ * p = sc*q (Q4_K) or sc*(q6-32) (Q6_K), split exactly into two int8 planes
+ * p = 2^S*hi + lo, so the MMQ accumulates a whole super-block on the matrix
+ * core without per-group integer scaling.  560 (Q4_K) / 528 (Q6_K) bytes per
+ * 256 weights.
+ *   qhip_mmq_image_bytes   image size, -1 for other types or cols % 256 != 0
+ *   qhip_launch_mmq_prepare  build it from GGUF bytes (d_image 16-byte aligned)
+ *   qhip_launch_mul_mat_image  the product from the image: same contract and
+ *     results as qhip_launch_mul_mat_vec_tile; tile 64x64 / 64x128 / 128x64
+ *     tokens x rows, 0 x 0 = default */
+long qhip_mmq_image_bytes(int ttype, int rows, int cols);
+int qhip_launch_mmq_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
+int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
+                              int tokens, int ttype, int tile_tokens, int tile_rows, void *stream);
+
 /* ---- ragged prefill (no reference counterpart: the reference prefills one
  * sequence per chunk, src/engine.zig:1371) -------------------------------------
  * Sequence i owns packed tokens [offsets[i], offsets[i+1]); offsets has

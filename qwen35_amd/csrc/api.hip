@@ -78,6 +78,17 @@ static int mmq_min_tokens(int ttype) {
   }
 }
 
+// The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image
+// (built once per weight).  Measured on MI355X: the image beats the tile path
+// 1.6-1.8x for Q6_K (its per-16-value integer scaling dominates the tile
+// path) and beats the GEMV from 16 tokens ([5120, 17408]: 81 us vs 140 us);
+// for Q4_K the image's 3.9x larger weight bytes, re-read once per 64-token
+// tile, cost more than the scaling they save (202 us vs 183 us at 512
+// tokens), so Q4_K stays on the tile path.
+bool mmq_image_preferred(const GemvArgs& g) {
+  return g.ttype == TT_Q6_K && g.tokens >= 16 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+}
+
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
   if (g.rows == 0 || g.tokens == 0) return hipSuccess;
   const bool fast = fast_ok(g);
@@ -312,6 +323,28 @@ int qhip_launch_mmq_tuned(const void* d_w, const void* d_xq, float* d_out, int r
   if (!bt_ok || !br_ok) return (int)hipErrorInvalidValue;
   if (!fast_ok(g)) return QHIP_DECLINE;
   return (int)launch_mmq(g, tile_tokens, tile_rows, S(stream));
+}
+
+long qhip_mmq_image_bytes(int ttype, int rows, int cols) { return mmq_image_bytes(ttype, rows, cols); }
+
+int qhip_launch_mmq_prepare(int ttype, const void* d_w, int rows, int cols, void* d_image, void* stream) {
+  const long rb = weight_row_bytes(ttype, cols);
+  if (rb < 0 || mmq_image_bytes(ttype, rows, cols) < 0) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!d_w || !d_image || ((uintptr_t)d_image & 15u)) return (int)hipErrorInvalidValue;
+  return (int)launch_mmq_prepare(ttype, d_w, rb, rows, cols, d_image, S(stream));
+}
+
+int qhip_launch_mul_mat_image(const void* d_image, const void* d_xq, float* d_out, int rows, int cols,
+                              int tokens, int ttype, int tile_tokens, int tile_rows, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_image, d_xq, d_out, rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (mmq_image_bytes(ttype, rows, cols) < 0) return (int)hipErrorInvalidValue;
+  const bool tile_ok = (tile_tokens == 0 && tile_rows == 0) || (tile_tokens == 64 && tile_rows == 64) ||
+                       (tile_tokens == 64 && tile_rows == 128) || (tile_tokens == 128 && tile_rows == 64);
+  if (!tile_ok || ((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
+  return (int)launch_mmq_image(g, tile_tokens, tile_rows, S(stream));
 }
 
 int qhip_launch_mul_mat_vec_tile(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,

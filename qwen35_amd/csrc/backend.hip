@@ -10,12 +10,15 @@
 #include "qhip_internal.hpp"
 
 #include <cstdio>
+#include <map>
 #include <mutex>
 #include <new>
+#include <utility>
 #include <vector>
 
 namespace qhip {
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s);
+bool mmq_image_preferred(const GemvArgs& g);
 }
 
 using namespace qhip;
@@ -30,6 +33,10 @@ struct qhip_backend {
   std::vector<void*> bufs;       // allocBuf regions (freed by free_scratch)
   uint8_t* act = nullptr;        // quantized-activation scratch
   size_t act_cap = 0;
+  // MMQ images of K-quant weights, built on first use with many tokens and
+  // kept until free_linear / destroy; keyed by (weight bytes, rows) because a
+  // fused matvecPair multiplies two adjacent weights as one.
+  std::map<std::pair<const void*, int>, void*> images;
   char name[96] = "hip";
 };
 
@@ -104,6 +111,25 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   int rc = qhip_launch_quantize_act(ttype, x, be->act, cols, k, be->stream);
   if (rc) return report("quantize", (hipError_t)rc);
   GemvArgs g{ttype, wdev, be->act, out, rows, cols, k, row_bytes, qhip_act_row_bytes(ttype, cols)};
+  if (mmq_image_preferred(g)) {
+    // prefill of a K-quant weight: MMQ from its image
+    auto key = std::make_pair(wdev, rows);
+    auto it = be->images.find(key);
+    if (it == be->images.end()) {
+      const long n = qhip_mmq_image_bytes(ttype, rows, cols);
+      void* img = nullptr;
+      e = hipMalloc(&img, (size_t)n);
+      if (e != hipSuccess) return report("MMQ image", e);
+      rc = qhip_launch_mmq_prepare(ttype, wdev, rows, cols, img, be->stream);
+      if (rc) {
+        (void)hipFree(img);
+        return report("MMQ image", (hipError_t)rc);
+      }
+      it = be->images.emplace(key, img).first;
+    }
+    return report("matvec", (hipError_t)qhip_launch_mul_mat_image(it->second, be->act, out, rows, cols, k, ttype,
+                                                                   0, 0, be->stream));
+  }
   return report("matvec", dispatch_mul_mat(g, QHIP_PATH_AUTO, be->stream));
 }
 
@@ -128,6 +154,7 @@ void qhip_backend_destroy(qhip_backend* be) {
   (void)hipSetDevice(be->device);
   (void)hipDeviceSynchronize();
   qhip_backend_free_scratch(be);
+  for (auto& kv : be->images) (void)hipFree(kv.second);
   for (auto& c : be->arena) (void)hipFree(c.base);
   delete be;
 }
@@ -157,9 +184,22 @@ int qhip_backend_wrap_linear(qhip_backend* be, int ttype, int rows, int cols, co
 }
 
 void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
-  // Arena memory is returned at destroy; the handle is cleared so a stale use
-  // fails validation instead of reading freed memory.
-  (void)be;
+  // Arena memory is returned at destroy; MMQ images built from this weight are
+  // freed now; the handle is cleared so a stale use fails validation.
+  if (be && w && w->dev) {
+    (void)hipStreamSynchronize(be->stream);
+    for (auto it = be->images.begin(); it != be->images.end();) {
+      const uint8_t* p = (const uint8_t*)it->first.first;
+      const uint8_t* lo = (const uint8_t*)w->dev;
+      // images of this weight, alone or as the first half of a pair
+      if (p == lo) {
+        (void)hipFree(it->second);
+        it = be->images.erase(it);
+      } else {
+        ++it;
+      }
+    }
+  }
   if (w) *w = qhip_linear{nullptr, 0, 0, 0, 0};
 }
 

@@ -150,12 +150,12 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
 // the separate quantize launch (about 2-3 us each on this GPU) from every
 // decode matvec.  Workgroup 0 also writes the quantized activation in the
 // reference layout when `XQ` is not null.
-__host__ __device__ constexpr long fused_lds_qs(int cols) { return cols; }
+__host__ __device__ constexpr long fused_lds_qs(int cols) { return (long)cols / 64 * kSplitUnit; }
 __host__ __device__ constexpr long fused_lds_bytes(int ttype, int cols) {
-  // qs[cols] | d[nblk] f32 (16-aligned) | Q8_K: bs[cols/16] int16
+  // qs (80 B per 64 values) | d[nblk] f32 (16-aligned) | Q8_K: bs[cols/16] int16
   return ttype == TT_Q8_0 || ttype == TT_IQ4_NL
-             ? (long)cols + (((long)cols / 32 * 4 + 15) & ~15L)
-             : (long)cols + (((long)cols / 256 * 4 + 15) & ~15L) + (long)cols / 16 * 2;
+             ? fused_lds_qs(cols) + (((long)cols / 32 * 4 + 15) & ~15L)
+             : fused_lds_qs(cols) + (((long)cols / 256 * 4 + 15) & ~15L) + (long)cols / 16 * 2;
 }
 
 template <int TT, int NR>
@@ -167,8 +167,9 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nblk = K32 ? cols / 32 : cols / 256;
   uint8_t* qs = lds;
-  float* dsc = (float*)(lds + cols);
-  int16_t* bs = (int16_t*)(lds + cols + ((nblk * 4 + 15) & ~15));
+  const int qsb = (int)fused_lds_qs(cols);
+  float* dsc = (float*)(lds + qsb);
+  int16_t* bs = (int16_t*)(lds + qsb + ((nblk * 4 + 15) & ~15));
   const ActSplit sp{qs, dsc, bs};
 
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
       uint32_t hb;
       const int q = quant_q8_0_lane(ok ? X[32 * b + i] : 0.0f, hb);
       if (ok) {
-        qs[32 * b + i] = (uint8_t)(int8_t)q;
+        qs[split_off(32 * b + i)] = (uint8_t)(int8_t)q;
         if (i == 0) dsc[b] = h2f(hb);
         if (out_q) {
           uint8_t* ob = XQ + 34L * b;
@@ -228,7 +229,7 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
       float scale;
       const uint32_t packed = quant_q8_K_lane(v, gsum, scale);
       if (ok) {
-        *(uint32_t*)(qs + 256 * b + 4 * lane) = packed;
+        *(uint32_t*)(qs + split_off(256 * b + 4 * lane)) = packed;
         if ((lane & 3) == 0) bs[16 * b + (lane >> 2)] = (int16_t)gsum;
         if (lane == 0) dsc[b] = scale;
         if (out_q) {

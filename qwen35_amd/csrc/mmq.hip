@@ -184,8 +184,8 @@ __device__ __forceinline__ MmqAct<TT> load_act(const uint8_t* arow, int u) {
   else return Unit<TT_Q4_K>::load_a(arow, u);
 }
 
-template <int TT, int BT, int BR>
-__device__ __forceinline__ void emit_a(MmqSmem<TT, BT, BR>& sm, const MmqAct<TT>& a, int tok, int u4) {
+template <int TT, class SM>
+__device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int u4) {
   uint8_t* dst = sm.aq + tok * kQS + 64 * u4;
   if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
 #pragma unroll
@@ -268,7 +268,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
 #pragma unroll
       for (int i = 0; i < UW; ++i) emit_w<TT, BT, BR>(sm, wreg[i], (tid + 256 * i) >> 2, u4);
 #pragma unroll
-      for (int i = 0; i < UA; ++i) emit_a<TT, BT, BR>(sm, areg[i], (tid + 256 * i) >> 2, u4);
+      for (int i = 0; i < UA; ++i) emit_a<TT>(sm, areg[i], (tid + 256 * i) >> 2, u4);
     }
     __syncthreads();
     if (ch + 1 < nchunks) load_chunk(ch + 1);  // in flight during this chunk's MFMAs
@@ -482,6 +482,340 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         if (row < rows && tok < tokens) Y[(long)tok * rows + row] = acc[a][b][e];
       }
     }
+}
+
+// ---- MMQ on a prepared weight image (Q4_K, Q6_K) -----------------------------------------
+// The K-quants' integer sub-scales are folded into the quantized values once,
+// at weight-load time: p = sc * q (Q4_K, 0..945) or p = sc * (q6 - 32) (Q6_K,
+// -4064..4096), split exactly into two int8 planes p = 2^S * hi + lo (S = 7:
+// hi 0..7, lo 0..127; S = 6: hi -64..64, lo 0..63).  A super-block then needs
+// no per-group scaling: the 32x32x32 int8 MFMAs of both planes accumulate the
+// whole super-block, and isum = (hi_sum << S) + lo_sum is the reference's
+// integer (kernels256.c:474-498 / :720-738) exactly.  Twice the MFMAs, a sixth
+// of the VALU work per output: the loop is bound by the matrix core instead of
+// the vector ALU.  The image costs 560 (Q4_K) / 528 (Q6_K) bytes per 256
+// values (3.9x / 2.5x the GGUF bytes) -- affordable next to 288 GB of HBM.
+//
+// Image layout (two regions, both 16-byte aligned):
+//   planes  [row][super-block] 512 bytes: hi plane [0, 256), lo plane [256, 512),
+//           values in order
+//   headers [row][super-block] Q4_K 48 bytes: min of each 16-value group as
+//           f16 (min[j/2]) [0, 32), d f32 [32, 36), dmin f32 [36, 40);
+//           Q6_K 16 bytes: d f32 [0, 4)
+// Per 256 values: 560 (Q4_K) / 528 (Q6_K) bytes.
+template <int TT>
+__host__ __device__ constexpr int img_hdr_bytes() { return TT == TT_Q4_K ? 48 : 16; }
+__host__ __device__ constexpr int img_shift(int tt) { return tt == TT_Q4_K ? 7 : 6; }
+// one thread per (row, super-block, 16-value group)
+template <int TT>
+__global__ __launch_bounds__(256) void k_mmq_prepare(const uint8_t* __restrict__ W, uint8_t* __restrict__ IMG,
+                                                      long nsb_total, long row_bytes, int nsb) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= nsb_total * 16) return;
+  const int g = (int)(gid & 15);
+  const long sbi = gid >> 4;  // row * nsb + sb
+  const long row = sbi / nsb, sb = sbi % nsb;
+  const uint8_t* blk = W + row * row_bytes + sb * (TT == TT_Q4_K ? 144 : 210);
+  uint8_t* ib = IMG + sbi * 512;
+  uint8_t* hb = IMG + nsb_total * 512 + sbi * img_hdr_bytes<TT>();
+  uint32_t hi[4] = {0, 0, 0, 0}, lo[4] = {0, 0, 0, 0};
+  if constexpr (TT == TT_Q4_K) {
+    const int sub = g >> 1;  // 32-value sub-block, src/kernels/x86/kernels256.c:105-125
+    const uint8_t* s12 = blk + 4;
+    int sc, m;
+    if (sub < 4) {
+      sc = s12[sub] & 63;
+      m = s12[sub + 4] & 63;
+    } else {
+      sc = (s12[sub + 4] & 15) | ((s12[sub - 4] >> 6) << 4);
+      m = (s12[sub + 4] >> 4) | ((s12[sub] >> 6) << 4);
+    }
+    (void)m;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int l = 16 * (g & 1) + i;
+      const uint32_t qb = blk[16 + 32 * (sub >> 1) + l];
+      const int q = (int)((sub & 1) ? (qb >> 4) : (qb & 15u));
+      const int pv = sc * q;
+      hi[i >> 2] |= (uint32_t)(pv >> 7) << (8 * (i & 3));
+      lo[i >> 2] |= (uint32_t)(pv & 127) << (8 * (i & 3));
+    }
+    if (g == 0) {
+      // min of every 16-value group j: min[j/2], as f16 for the mins MFMA
+      uint32_t mw[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int mk = k < 4 ? (s12[k + 4] & 63) : ((s12[k + 4] >> 4) | ((s12[k] >> 6) << 4));
+        mw[k] = f16_pair((uint32_t)mk);
+      }
+      *(uint4*)(hb) = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+      *(uint4*)(hb + 16) = make_uint4(mw[4], mw[5], mw[6], mw[7]);
+      const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+      const float dmin = h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
+      *(uint4*)(hb + 32) = make_uint4(__float_as_uint(d), __float_as_uint(dmin), 0u, 0u);
+    }
+  } else {
+    const int sc = (int)(int8_t)blk[192 + g];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = 16 * g + i, h = e >> 7, q = (e & 127) >> 5, l = e & 31;
+      uint32_t lq = blk[64 * h + 32 * (q & 1) + l];
+      lq = q >= 2 ? (lq >> 4) : (lq & 15u);
+      const uint32_t hb = (blk[128 + 32 * h + l] >> (2 * q)) & 3u;
+      const int pv = sc * ((int)(lq | (hb << 4)) - 32);
+      hi[i >> 2] |= ((uint32_t)(pv >> 6) & 255u) << (8 * (i & 3));  // arithmetic shift: floor
+      lo[i >> 2] |= (uint32_t)(pv & 63) << (8 * (i & 3));
+    }
+    if (g == 0) {
+      const float d = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+      *(uint4*)(hb) = make_uint4(__float_as_uint(d), 0u, 0u, 0u);
+    }
+  }
+  *(uint4*)(ib + 16 * g) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  *(uint4*)(ib + 256 + 16 * g) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+}
+
+template <int TT, int BT, int BR>
+struct alignas(16) ImgSmem {
+  uint8_t aq[BT * kQS];
+  uint8_t bqh[BR * kQS];
+  uint8_t bql[BR * kQS];
+  _Float16 abs[BT][16];
+  _Float16 wmn[BR][16];
+  float ady[BT];
+  float wd[BR], wdmin[BR];
+};
+
+template <int TT, int BT, int BR>
+__global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG, const uint8_t* __restrict__ XQ,
+                                                  float* __restrict__ Y, int rows, int tokens, int nsb,
+                                                  long act_bytes, int ntile_t) {
+  constexpr int HB = img_hdr_bytes<TT>(), NH = HB / 16;
+  constexpr int S = img_shift(TT);
+  constexpr int NA = BT / 64, NB = BR / 64;
+  constexpr int PW = BR * 32 / 256;            // 16-byte plane pieces per thread per chunk
+  constexpr int PH = (BR * NH + 255) / 256;    // header pieces per thread per chunk
+  constexpr int UA = BT / 64;
+  __shared__ ImgSmem<TT, BT, BR> sm;
+
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous row tiles, as k_mmq
+  const int r0 = (g / ntile_t) * BR, t0 = (g % ntile_t) * BT;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  const int tb0 = (wv & 1) * (BT / 2), rb0 = (wv >> 1) * (BR / 2);
+
+  f32x16 acc[NA][NB];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+
+  // plane piece p = tid + 256*i: row p >> 5, piece p & 31 of its 512 bytes;
+  // header piece q = tid + 256*i: row q / NH, piece q % NH
+  const long nsb_total = (long)rows * nsb;
+  const uint8_t* hdr = IMG + nsb_total * 512;
+  i32x4 wreg[PW], hreg[PH];
+  const uint8_t* wsrc[PW];
+  const uint8_t* hsrc[PH];
+#pragma unroll
+  for (int i = 0; i < PW; ++i) {
+    const int p = tid + 256 * i, row = p >> 5;
+    const int rg = r0 + row < rows ? r0 + row : rows - 1;
+    wsrc[i] = IMG + (long)rg * nsb * 512 + 16 * (p & 31);
+  }
+#pragma unroll
+  for (int i = 0; i < PH; ++i) {
+    const int q = tid + 256 * i, row = q / NH < BR ? q / NH : BR - 1;
+    const int rg = r0 + row < rows ? r0 + row : rows - 1;
+    hsrc[i] = hdr + (long)rg * nsb * HB + 16 * (q % NH);
+  }
+  MmqAct<TT> areg[UA];
+  const uint8_t* arow[UA];
+#pragma unroll
+  for (int i = 0; i < UA; ++i) {
+    const int tok = (tid + 256 * i) >> 2;
+    arow[i] = XQ + (long)(t0 + tok < tokens ? t0 + tok : tokens - 1) * act_bytes;
+  }
+  const int u4 = tid & 3;
+  auto load_chunk = [&](int sb) {
+#pragma unroll
+    for (int i = 0; i < PW; ++i) wreg[i] = *(const i32x4*)(wsrc[i] + (long)sb * 512);
+#pragma unroll
+    for (int i = 0; i < PH; ++i)
+      if (tid + 256 * i < BR * NH) hreg[i] = *(const i32x4*)(hsrc[i] + (long)sb * HB);
+#pragma unroll
+    for (int i = 0; i < UA; ++i) areg[i] = load_act<TT>(arow[i], 4 * sb + u4);
+  };
+  load_chunk(0);
+  for (int sb = 0; sb < nsb; ++sb) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PW; ++i) {
+      const int p = tid + 256 * i, row = p >> 5, k = p & 31;
+      uint8_t* dst = (k < 16 ? sm.bqh + 16 * k : sm.bql + 16 * (k - 16)) + row * kQS;
+      *(i32x4*)dst = wreg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < PH; ++i) {
+      const int q = tid + 256 * i;
+      if (q < BR * NH) {
+        const int row = q / NH, k = q % NH;
+        if constexpr (TT == TT_Q4_K) {
+          if (k < 2) {
+            *(i32x4*)((uint8_t*)&sm.wmn[row][0] + 16 * k) = hreg[i];
+          } else {
+            sm.wd[row] = __int_as_float(hreg[i].x);
+            sm.wdmin[row] = __int_as_float(hreg[i].y);
+          }
+        } else {
+          sm.wd[row] = __int_as_float(hreg[i].x);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < UA; ++i) emit_a<TT>(sm, areg[i], (tid + 256 * i) >> 2, u4);
+    __syncthreads();
+    if (sb + 1 < nsb) load_chunk(sb + 1);  // in flight during this chunk's MFMAs
+
+    i32x16 chi[NA][NB], clo[NA][NB];
+    const i32x16 zero = {};
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        chi[a][b] = zero;
+        clo[a][b] = zero;
+      }
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      i32x4 af[NA], bh[NB], bl[NB];
+#pragma unroll
+      for (int a = 0; a < NA; ++a) af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        bh[b] = *(const i32x4*)(sm.bqh + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
+        bl[b] = *(const i32x4*)(sm.bql + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
+      }
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          chi[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bh[b], chi[a][b], 0, 0, 0);
+          clo[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bl[b], clo[a][b], 0, 0, 0);
+        }
+    }
+    f32x4 dy[NA][4];
+    float d[NB];
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dy[a][q] = *(const f32x4*)&sm.ady[tb0 + 32 * a + 8 * q + 4 * lh];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) d[b] = sm.wd[rb0 + 32 * b + li];
+    if constexpr (TT == TT_Q4_K) {
+      f16x8 am[NA], bm[NB];
+      float ndm[NB];
+#pragma unroll
+      for (int a = 0; a < NA; ++a) am[a] = *(const f16x8*)&sm.abs[tb0 + 32 * a + li][8 * lh];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        bm[b] = *(const f16x8*)&sm.wmn[rb0 + 32 * b + li][8 * lh];
+        ndm[b] = -sm.wdmin[rb0 + 32 * b + li];
+      }
+      const f32x16 fz = {};
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[a], bm[b], fz, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int isum = (chi[a][b][e] << S) + clo[a][b][e];
+            const float inner = __builtin_fmaf(d[b], (float)isum, ndm[b] * cm[e]);
+            acc[a][b][e] = __builtin_fmaf(dy[a][e >> 2][e & 3], inner, acc[a][b][e]);
+          }
+        }
+    } else {
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int isum = (chi[a][b][e] << S) + clo[a][b][e];
+            acc[a][b][e] = __builtin_fmaf(d[b] * dy[a][e >> 2][e & 3], (float)isum, acc[a][b][e]);
+          }
+    }
+  }
+
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int row = r0 + rb0 + 32 * b + li;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
+        if (row < rows && tok < tokens) Y[(long)tok * rows + row] = acc[a][b][e];
+      }
+    }
+}
+
+long mmq_image_bytes(int ttype, int rows, int cols) {
+  if ((ttype != TT_Q4_K && ttype != TT_Q6_K) || rows < 0 || cols <= 0 || cols % 256) return -1;
+  return (long)rows * (cols / 256) * (512 + (ttype == TT_Q4_K ? img_hdr_bytes<TT_Q4_K>() : img_hdr_bytes<TT_Q6_K>()));
+}
+
+hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
+                              hipStream_t s) {
+  const long nsb_total = (long)rows * (cols / 256);
+  if (nsb_total <= 0) return hipSuccess;
+  const unsigned grid = (unsigned)((nsb_total * 16 + 255) / 256);
+  if (ttype == TT_Q4_K)
+    hipLaunchKernelGGL(k_mmq_prepare<TT_Q4_K>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img,
+                       nsb_total, row_bytes, cols / 256);
+  else if (ttype == TT_Q6_K)
+    hipLaunchKernelGGL(k_mmq_prepare<TT_Q6_K>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img,
+                       nsb_total, row_bytes, cols / 256);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+template <int TT, int BT, int BR>
+static hipError_t launch_mmq_img_t(const GemvArgs& g, hipStream_t s) {
+  const long ntr = (g.rows + BR - 1) / BR, ntt = (g.tokens + BT - 1) / BT;
+  const long G = ntr * ntt;
+  if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((k_mmq_img<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.cols / 256, g.act_bytes, (int)ntt);
+  return hipGetLastError();
+}
+
+template <int TT>
+static hipError_t launch_mmq_img_type(const GemvArgs& g, int bt, int br, hipStream_t s) {
+  if (bt == 64 && br == 64) return launch_mmq_img_t<TT, 64, 64>(g, s);
+  if (bt == 64 && br == 128) return launch_mmq_img_t<TT, 64, 128>(g, s);
+  if (bt == 128 && br == 64) return launch_mmq_img_t<TT, 128, 64>(g, s);
+  return hipErrorInvalidValue;
+}
+
+// g.w is the image
+hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, hipStream_t s) {
+  if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  if (bt <= 0 || br <= 0) {
+    bt = 64;
+    br = 64;
+  }
+  switch (g.ttype) {
+    case TT_Q4_K: return launch_mmq_img_type<TT_Q4_K>(g, bt, br, s);
+    case TT_Q6_K: return launch_mmq_img_type<TT_Q6_K>(g, bt, br, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 // ---- launchers --------------------------------------------------------------------------

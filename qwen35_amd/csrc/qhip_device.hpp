@@ -183,9 +183,16 @@ template <int TT>
 struct Unit;
 
 // Activation in LDS, split into planes (all 16-byte aligned):
-//   qs  int8 values, `cols` bytes
+//   qs  int8 values, 80 bytes per 64 (split_off)
 //   d   per-block f32 scale (32-value blocks for Q8_0, 256 for Q8_K)
 //   bs  Q8_K only: int16 sums of each 16 values
+// Value v of the split image's int8 plane lives at byte split_off(v): 64-value
+// units padded to 80 bytes, so the 16-byte reads of 16 lanes at consecutive
+// units fall into distinct LDS banks (a 64-byte stride would put lanes j and
+// j+4 on the same banks).
+constexpr int kSplitUnit = 80;
+__host__ __device__ constexpr int split_off(int v) { return (v >> 6) * kSplitUnit + (v & 63); }
+
 struct ActSplit {
   const uint8_t* qs;
   const float* d;
@@ -227,7 +234,7 @@ __device__ __forceinline__ ActPair act_pair_split(const ActSplit& sp, int u) {
   ActPair a;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const u32x4 x = *(const u32x4*)(sp.qs + 64 * u + 16 * i);
+    const u32x4 x = *(const u32x4*)(sp.qs + kSplitUnit * u + 16 * i);
     a.q[4 * i] = x.x; a.q[4 * i + 1] = x.y; a.q[4 * i + 2] = x.z; a.q[4 * i + 3] = x.w;
   }
   a.d0 = sp.d[2 * u];
@@ -356,7 +363,7 @@ struct Unit<TT_Q4_K> {
     A a;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x4 x = *(const u32x4*)(sp.qs + 256 * sb + 64 * c + 16 * i);
+      const u32x4 x = *(const u32x4*)(sp.qs + kSplitUnit * (4 * sb + c) + 16 * i);
       a.y[4 * i] = x.x; a.y[4 * i + 1] = x.y; a.y[4 * i + 2] = x.z; a.y[4 * i + 3] = x.w;
     }
     a.d = sp.d[sb];
@@ -446,7 +453,7 @@ struct Unit<TT_Q6_K> {
     A a;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x4 x = *(const u32x4*)(sp.qs + 256 * sb + 128 * h + 32 * q + 16 * lh);
+      const u32x4 x = *(const u32x4*)(sp.qs + kSplitUnit * (4 * sb + 2 * h + (q >> 1)) + 32 * (q & 1) + 16 * lh);
       a.y[4 * q] = x.x; a.y[4 * q + 1] = x.y; a.y[4 * q + 2] = x.z; a.y[4 * q + 3] = x.w;
     }
     const u32x4 b = *(const u32x4*)(sp.bs + 16 * sb + 8 * h);

@@ -43,5 +43,11 @@ hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, in
 hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hipStream_t s);
 // MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)
 hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s);
+// MMQ weight image of a K-quant weight (sub-scales folded into two int8 planes)
+long mmq_image_bytes(int ttype, int rows, int cols);
+hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
+                              hipStream_t s);
+// g.w = the image; bt x br tile (0 = default)
+hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, hipStream_t s);
 
 }  // namespace qhip

@@ -116,6 +116,24 @@ def mmq_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: in
     return out
 
 
+def mmq_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """The MMQ weight image of a Q4_K / Q6_K weight (sub-scales folded into two int8 planes)."""
+    n = load().qhip_mmq_image_bytes(ttype, rows, cols)
+    if n < 0:
+        raise ValueError(f"no MMQ image for type {ttype} at cols={cols}")
+    img = torch.empty(max(n, 16), dtype=torch.uint8, device=w.device)
+    check("mmq_prepare", load().qhip_launch_mmq_prepare(ttype, _p(w), rows, cols, _p(img), _stream()))
+    return img
+
+
+def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
+                  tile_tokens: int = 0, tile_rows: int = 0) -> torch.Tensor:
+    out = torch.empty((tokens, rows), dtype=torch.float32, device=img.device)
+    check("mul_mat_image", load().qhip_launch_mul_mat_image(_p(img), _p(xq), _p(out), rows, cols, tokens, ttype,
+                                                            tile_tokens, tile_rows, _stream()))
+    return out
+
+
 def block_ints(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
                tokens: int) -> torch.Tensor:
     be = _GEOM[ttype][0]

@@ -169,3 +169,132 @@ def test_cfg4_ragged_batch_through_mmq(gpu, oracle):
     want = oracle.matvec(tt, np.ascontiguousarray(w[idx]), packed)
     assert rel_l2(out[:, idx], want) < TOL
     assert np.all(np.isfinite(out))
+
+
+# ---- MMQ from the prepared weight image (Q4_K, Q6_K) ----------------------------------
+
+def _q4k_p(w, cols):
+    """p = sc * q for every value of Q4_K rows (kernels256.c:105-125, :179-186)."""
+    blk = w.reshape(w.shape[0], cols // 256, 144).astype(np.int64)
+    s12 = blk[:, :, 4:16]
+    sc = np.empty(blk.shape[:2] + (8,), np.int64)
+    for j in range(8):
+        sc[:, :, j] = (s12[:, :, j] & 63) if j < 4 else ((s12[:, :, j + 4] & 15) | ((s12[:, :, j - 4] >> 6) << 4))
+    qs = blk[:, :, 16:144].reshape(blk.shape[0], blk.shape[1], 4, 32)
+    q = np.stack([qs & 15, qs >> 4], axis=3).reshape(blk.shape[0], blk.shape[1], 8, 32)  # sub-block 2c, 2c+1
+    return (sc[:, :, :, None] * q).reshape(blk.shape[0], blk.shape[1], 256)
+
+
+def _q6k_p(w, cols):
+    """p = sc * (q6 - 32) for every value of Q6_K rows (kernels256.c:200-212, :720-738)."""
+    blk = w.reshape(w.shape[0], cols // 256, 210).astype(np.int64)
+    e = np.arange(256)
+    h, q, l = e // 128, (e % 128) // 32, e % 32
+    lo = blk[:, :, 64 * h + 32 * (q & 1) + l]
+    lo = np.where(q >= 2, lo >> 4, lo & 15)
+    hb = (blk[:, :, 128 + 32 * h + l] >> (2 * q)) & 3
+    sc = blk[:, :, 192 + e // 16].astype(np.int8).astype(np.int64)
+    return sc * ((lo | (hb << 4)) - 32)
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
+def test_mmq_image_planes(gpu, tt):
+    rows, cols = 9, 1024
+    w = synth.make_weight(tt, rows, cols, seed=12, tag=tt)
+    img = ops.mmq_image(tt, to_dev(w, gpu), rows, cols).cpu().numpy()
+    nsb = cols // 256
+    planes = img[:rows * nsb * 512].reshape(rows, nsb, 512)
+    S = 7 if tt == po.TT_Q4_K else 6
+    hi = planes[:, :, :256].view(np.int8).astype(np.int64)
+    lo = planes[:, :, 256:].astype(np.int64)
+    p = _q4k_p(w, cols) if tt == po.TT_Q4_K else _q6k_p(w, cols)
+    assert np.array_equal(hi * (1 << S) + lo, p)
+    assert lo.min() >= 0 and lo.max() < (1 << S) and hi.min() >= -128 and hi.max() <= 127
+    hdr = img[rows * nsb * 512:]
+    if tt == po.TT_Q4_K:
+        hdr = hdr.reshape(rows, nsb, 48)
+        d = hdr[:, :, 32:36].copy().view(np.float32)[..., 0]
+        dmin = hdr[:, :, 36:40].copy().view(np.float32)[..., 0]
+        blk = w.reshape(rows, nsb, 144)
+        assert np.array_equal(d, blk[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32))
+        assert np.array_equal(dmin, blk[:, :, 2:4].copy().view(np.float16)[..., 0].astype(np.float32))
+        mins = hdr[:, :, 0:32].copy().view(np.float16).astype(np.int64)  # [rows, nsb, 16]
+        s12 = blk[:, :, 4:16].astype(np.int64)
+        for j in range(16):
+            k = j // 2
+            m = (s12[:, :, k + 4] & 63) if k < 4 else ((s12[:, :, k + 4] >> 4) | ((s12[:, :, k] >> 6) << 4))
+            assert np.array_equal(mins[:, :, j], m)
+    else:
+        hdr = hdr.reshape(rows, nsb, 16)
+        d = hdr[:, :, 0:4].copy().view(np.float32)[..., 0]
+        blk = w.reshape(rows, nsb, 210)
+        assert np.array_equal(d, blk[:, :, 208:210].copy().view(np.float16)[..., 0].astype(np.float32))
+
+
+IMG_CASES = [(po.TT_Q4_K, 150, 512, 65), (po.TT_Q4_K, 64, 2560, 16), (po.TT_Q6_K, 100, 768, 40),
+             (po.TT_Q6_K, 72, 2304, 129)]
+
+
+@pytest.mark.parametrize("tt,rows,cols,tokens", IMG_CASES,
+                         ids=[f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in IMG_CASES])
+def test_mmq_image_matches_oracle(gpu, oracle, tt, rows, cols, tokens):
+    w = synth.make_weight(tt, rows, cols, seed=tokens + 1, tag=tt)
+    x = synth.make_act(cols, tokens, seed=tokens + 1)
+    want = oracle.matvec(tt, w, x)
+    img = ops.mmq_image(tt, to_dev(w, gpu), rows, cols)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    for bt, br in [(64, 64), (64, 128), (128, 64), (0, 0)]:
+        got = ops.mul_mat_image(tt, img, xq, rows, cols, tokens, bt, br).cpu().numpy()
+        assert rel_l2(got, want) < TOL, (bt, br, rel_l2(got, want))
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
+def test_mmq_image_block_integers_exact(gpu, oracle, tt):
+    rows, cols, tokens = 96, 1024, 72
+    w = unit_scale_weight(tt, rows, cols, seed=7)
+    x = unit_scale_act(cols, tokens, seed=7)
+    act = oracle.quantize_act(tt, x)
+    ints = oracle.block_ints(tt, w, act, cols).astype(np.int64)
+    want = ints[:, :, 0::2].sum(-1) - ints[:, :, 1::2].sum(-1) if tt == po.TT_Q4_K else ints.sum(-1)
+    assert np.abs(want).max() < 2 ** 24
+    img = ops.mmq_image(tt, to_dev(w, gpu), rows, cols)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    got = ops.mul_mat_image(tt, img, xq, rows, cols, tokens).cpu().numpy()
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_mmq_image_rejects_other_types(gpu):
+    L = _lib.load()
+    assert L.qhip_mmq_image_bytes(po.TT_Q8_0, 4, 1024) == -1
+    assert L.qhip_mmq_image_bytes(po.TT_Q4_K, 4, 1000) == -1
+    assert L.qhip_mmq_image_bytes(po.TT_Q4_K, 4, 1024) == 4 * 4 * 560
+    assert L.qhip_mmq_image_bytes(po.TT_Q6_K, 4, 1024) == 4 * 4 * 528
+    w = torch.zeros(4 * 34 * 32, dtype=torch.uint8, device=gpu)
+    img = torch.empty(4096, dtype=torch.uint8, device=gpu)
+    assert L.qhip_launch_mmq_prepare(po.TT_Q8_0, w.data_ptr(), 4, 1024, img.data_ptr(), None) != 0
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
+def test_backend_prefill_batch(gpu, oracle, tt):
+    """matvecBatchK above the crossover: the MMQ image for Q6_K, the tile MMQ
+    for Q4_K; the second call reuses the cached image."""
+    rows, cols, k = 130, 2560 if tt == po.TT_Q4_K else 2304, 80
+    w = synth.make_weight(tt, rows, cols, seed=31, tag=tt)
+    x = synth.make_act(cols, k, seed=31)
+    be = ops.Backend(0)
+    try:
+        lin = be.load_linear(tt, rows, cols, w)
+        out = torch.empty((k, rows), device=gpu)
+        for rep in range(2):
+            out.zero_()
+            be.matvec_batch_k(out, lin, to_dev(x, gpu), k)
+            be.sync()
+            assert rel_l2(out.cpu().numpy(), oracle.matvec(tt, w, x)) < TOL, rep
+        be.lib.qhip_backend_free_linear(be._h, ctypes_byref(lin))
+    finally:
+        be.close()
+
+
+def ctypes_byref(x):
+    import ctypes
+    return ctypes.byref(x)
