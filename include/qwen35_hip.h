@@ -245,9 +245,35 @@ int qhip_backend_matvec_batch_k(qhip_backend *be, float *d_out, const qhip_linea
 /* dequantRow (backend.zig:148-151): d_dst[cols] = f32 values of weight row `row`
  * (the embedding lookup). */
 int qhip_backend_dequant_row(qhip_backend *be, float *d_dst, const qhip_linear *w, int row);
-/* Stream for subsequent calls (NULL = default stream) and a host wait. */
+/* Stream for subsequent calls (NULL = default stream) and a host wait.
+ * Changing the stream forgets the memoized activation (below). */
 int qhip_backend_set_stream(qhip_backend *be, void *stream);
 int qhip_backend_sync(qhip_backend *be);
+
+/* Activation-quantization memo (src/backend_cuda.zig:3425-3448 actQValid /
+ * actQMark, used by the matvec slot at :3914-3944).  When on, a matvec whose
+ * x pointer, width, token count and activation family (Q8_0 or Q8_K) match
+ * the last quantization reuses the quantized rows in the scratch instead of
+ * quantizing again (q/k/v of one hidden state, Q4_K and Q6_K weights of one
+ * x, the halves of a non-adjacent matvecPair).  Off by default.  The caller
+ * must call qhip_backend_act_invalidate after anything writes into a buffer
+ * a matvec may read again (the reference clears at the same points,
+ * backend_cuda.zig:6250-6254: rmsnorm, l2norm, add_resid, copy_range,
+ * copy_from_host, swiglu, mul_silu, dequant_row, load_linear, const_buf).
+ * set_act_memo also clears it. */
+int qhip_backend_set_act_memo(qhip_backend *be, int on);
+void qhip_backend_act_invalidate(qhip_backend *be);
+/* Memo hits and misses since create (the reference's QWEN35_QSTAT counters,
+ * backend_cuda.zig:3933-3937); either pointer may be NULL. */
+int qhip_backend_act_stats(const qhip_backend *be, unsigned long long *hits,
+                           unsigned long long *misses);
+/* Decode-step boundary (src/backend.zig:470-491 stepBegin/stepEnd).  A device
+ * backend may ignore the hint; this one clears the activation memo at
+ * step_begin (as backend_cuda.zig:7049-7053 does) and captures nothing: the
+ * library's launches are capture-safe, so an engine can wrap a step in its own
+ * HIP graph. */
+void qhip_backend_step_begin(qhip_backend *be, unsigned pos);
+void qhip_backend_step_end(qhip_backend *be);
 
 #ifdef __cplusplus
 }

@@ -81,6 +81,12 @@ SIGNATURES = {
     "qhip_backend_dequant_row": (c_int, [c_void_p, c_void_p, ctypes.POINTER(QhipLinear), c_int]),
     "qhip_backend_set_stream": (c_int, [c_void_p, c_void_p]),
     "qhip_backend_sync": (c_int, [c_void_p]),
+    "qhip_backend_set_act_memo": (c_int, [c_void_p, c_int]),
+    "qhip_backend_act_invalidate": (None, [c_void_p]),
+    "qhip_backend_act_stats": (c_int, [c_void_p, ctypes.POINTER(ctypes.c_ulonglong),
+                                       ctypes.POINTER(ctypes.c_ulonglong)]),
+    "qhip_backend_step_begin": (None, [c_void_p, ctypes.c_uint]),
+    "qhip_backend_step_end": (None, [c_void_p]),
 }
 
 _lib = None

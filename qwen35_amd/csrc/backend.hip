@@ -37,8 +37,23 @@ struct qhip_backend {
   // kept until free_linear / destroy; keyed by (weight bytes, rows) because a
   // fused matvecPair multiplies two adjacent weights as one.
   std::map<std::pair<const void*, int>, void*> images;
+  // What `act` holds (backend_cuda.zig:3425-3448 actQValid/actQMark): the
+  // source pointer, width, token count and activation family of the last
+  // quantization, so a second matvec of the same x skips its quantize.
+  // Off unless enabled; cleared by step_begin, act_invalidate, set_stream and
+  // a scratch reallocation.
+  bool memo_on = false;
+  const float* memo_src = nullptr;
+  int memo_cols = 0, memo_k = 0, memo_fam = -1;
+  unsigned long long memo_hits = 0, memo_misses = 0;
   char name[96] = "hip";
 };
+
+static void memo_clear(qhip_backend* be) {
+  be->memo_src = nullptr;
+  be->memo_cols = be->memo_k = 0;
+  be->memo_fam = -1;
+}
 
 static constexpr size_t kArenaChunk = size_t(1) << 30;  // 1 GiB
 static constexpr size_t kAlign = 256;
@@ -67,6 +82,7 @@ static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
   if (be->act) (void)hipFree(be->act);
   be->act = nullptr;
   be->act_cap = 0;
+  memo_clear(be);
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess) return e;
@@ -97,7 +113,13 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
                long row_bytes, const float* x, int k) {
   if (!out || !x || k < 0) return (int)hipErrorInvalidValue;
   if (k == 0 || rows == 0) return 0;
-  if (k == 1) {
+  // the activation family: Q8_0 rows for 32-value weight blocks, Q8_K for
+  // 256-value super-blocks (backend_cpu.zig:42-50 actFamily)
+  const int fam = qhip_quant_act_block_elems(ttype);
+  const bool hit = be->memo_on && be->memo_src == x && be->memo_cols == cols && be->memo_k == k &&
+                   be->memo_fam == fam && be->act;
+  if (be->memo_on) (hit ? be->memo_hits : be->memo_misses)++;
+  if (!hit && k == 1) {
     // one launch, the activation quantized inside the GEMV, where that is
     // faster than a separate quantize launch (narrow matrices)
     const GemvArgs g1{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
@@ -106,10 +128,21 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
       if (rc != QHIP_DECLINE) return report("matvec", (hipError_t)rc);
     }
   }
-  hipError_t e = ensure_act(be, act_bytes_for(cols, k));
-  if (e != hipSuccess) return report("activation scratch", e);
-  int rc = qhip_launch_quantize_act(ttype, x, be->act, cols, k, be->stream);
-  if (rc) return report("quantize", (hipError_t)rc);
+  hipError_t e = hipSuccess;
+  int rc = 0;
+  if (!hit) {
+    e = ensure_act(be, act_bytes_for(cols, k));
+    if (e != hipSuccess) return report("activation scratch", e);
+    memo_clear(be);
+    rc = qhip_launch_quantize_act(ttype, x, be->act, cols, k, be->stream);
+    if (rc) return report("quantize", (hipError_t)rc);
+    if (be->memo_on) {
+      be->memo_src = x;
+      be->memo_cols = cols;
+      be->memo_k = k;
+      be->memo_fam = fam;
+    }
+  }
   GemvArgs g{ttype, wdev, be->act, out, rows, cols, k, row_bytes, qhip_act_row_bytes(ttype, cols)};
   if (mmq_image_preferred(g)) {
     // prefill of a K-quant weight: MMQ from its image
@@ -218,6 +251,7 @@ void qhip_backend_free_scratch(qhip_backend* be) {
   if (be->act) (void)hipFree(be->act);
   be->act = nullptr;
   be->act_cap = 0;
+  memo_clear(be);
   for (void* p : be->bufs) (void)hipFree(p);
   be->bufs.clear();
 }
@@ -265,9 +299,35 @@ int qhip_backend_dequant_row(qhip_backend* be, float* d_dst, const qhip_linear* 
 
 int qhip_backend_set_stream(qhip_backend* be, void* stream) {
   if (!be) return (int)hipErrorInvalidValue;
+  if (be->stream != (hipStream_t)stream) memo_clear(be);
   be->stream = (hipStream_t)stream;
   return 0;
 }
+
+int qhip_backend_set_act_memo(qhip_backend* be, int on) {
+  if (!be) return (int)hipErrorInvalidValue;
+  be->memo_on = on != 0;
+  memo_clear(be);
+  return 0;
+}
+
+void qhip_backend_act_invalidate(qhip_backend* be) {
+  if (be) memo_clear(be);
+}
+
+int qhip_backend_act_stats(const qhip_backend* be, unsigned long long* hits, unsigned long long* misses) {
+  if (!be) return (int)hipErrorInvalidValue;
+  if (hits) *hits = be->memo_hits;
+  if (misses) *misses = be->memo_misses;
+  return 0;
+}
+
+void qhip_backend_step_begin(qhip_backend* be, unsigned pos) {
+  (void)pos;
+  if (be) memo_clear(be);
+}
+
+void qhip_backend_step_end(qhip_backend* be) { (void)be; }
 
 int qhip_backend_sync(qhip_backend* be) {
   if (!be) return (int)hipErrorInvalidValue;

@@ -233,3 +233,26 @@ class Backend:
 
     def sync(self) -> None:
         check("sync", self.lib.qhip_backend_sync(self._h))
+
+    def set_stream(self, stream) -> None:
+        """Launch on `stream` (a torch stream or a raw handle) from now on."""
+        h = getattr(stream, "cuda_stream", stream)
+        check("set_stream", self.lib.qhip_backend_set_stream(self._h, ctypes.c_void_p(h)))
+
+    def set_act_memo(self, on: bool) -> None:
+        check("set_act_memo", self.lib.qhip_backend_set_act_memo(self._h, int(bool(on))))
+
+    def act_invalidate(self) -> None:
+        self.lib.qhip_backend_act_invalidate(self._h)
+
+    def act_stats(self) -> tuple[int, int]:
+        hits, misses = ctypes.c_ulonglong(0), ctypes.c_ulonglong(0)
+        check("act_stats", self.lib.qhip_backend_act_stats(self._h, ctypes.byref(hits),
+                                                           ctypes.byref(misses)))
+        return hits.value, misses.value
+
+    def step_begin(self, pos: int) -> None:
+        self.lib.qhip_backend_step_begin(self._h, pos)
+
+    def step_end(self) -> None:
+        self.lib.qhip_backend_step_end(self._h)
