@@ -221,6 +221,113 @@ int32_t orc_blk_q6_k(const uint8_t *w, const uint8_t *a) {
     return isum;
 }
 
+/* kernels256.c:605-629 with :188-198 (value layout: nibble + 16 * high bit)
+ * and :216-226; scales/mins as Q4_K:
+ *   isum  = sum_g sc[g/2] * sum_{l<16} q5[16g+l] * q8[16g+l]
+ *   summs = sum_{j<16} bsum[j] * min[j/2]                                   */
+void orc_blk_q5_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs) {
+    const uint8_t *qh = w + 16, *qs = w + 48;
+    const int8_t *q8 = (const int8_t *)(a + 4);
+    int32_t is = 0, sm = 0;
+    for (int sb = 0; sb < 8; ++sb) {
+        int sc, mn;
+        q4k_scale_min(w + 4, sb, &sc, &mn);
+        int c = sb / 2, hi = sb & 1;
+        int32_t sub = 0;
+        for (int l = 0; l < 32; ++l) {
+            int v = hi ? (qs[32 * c + l] >> 4) : (qs[32 * c + l] & 15);
+            v += ((qh[l] >> sb) & 1) ? 16 : 0;
+            sub += v * (int32_t)q8[32 * sb + l];
+        }
+        is += sc * sub;
+        for (int t = 0; t < 2; ++t) {
+            int16_t bs;
+            memcpy(&bs, a + 260 + 2 * (2 * sb + t), 2);
+            sm += (int32_t)bs * mn;
+        }
+    }
+    *isum = is;
+    *summs = sm;
+}
+
+/* Q3_K 6-bit scales, kernels256.c:129-151: sixteen values 0..63, used - 32. */
+static void q3k_scales(const uint8_t *s12, int *sc) {
+    uint32_t a0, a1, a2;
+    memcpy(&a0, s12, 4);
+    memcpy(&a1, s12 + 4, 4);
+    memcpy(&a2, s12 + 8, 4);
+    const uint32_t m1 = 0x03030303u, m2 = 0x0F0F0F0Fu;
+    uint32_t u[4];
+    u[0] = (a0 & m2) | (((a2 >> 0) & m1) << 4);
+    u[1] = (a1 & m2) | (((a2 >> 2) & m1) << 4);
+    u[2] = ((a0 >> 4) & m2) | (((a2 >> 4) & m1) << 4);
+    u[3] = ((a1 >> 4) & m2) | (((a2 >> 6) & m1) << 4);
+    for (int g = 0; g < 16; ++g) sc[g] = (int)((u[g / 4] >> (8 * (g % 4))) & 255u) - 32;
+}
+
+/* Q3_K value e = 128h + 32g + l: ((qs[32h+l] >> 2g) & 3) - (hmask bit 4h+g of
+ * byte l ? 0 : 4), kernels256.c:162-177. */
+static int q3k_value(const uint8_t *w, int e) {
+    int h = e / 128, g = (e % 128) / 32, l = e % 32;
+    int v = (w[32 + 32 * h + l] >> (2 * g)) & 3;
+    return v - (((w[l] >> (4 * h + g)) & 1) ? 0 : 4);
+}
+
+/* kernels256.c:349-366: isum = sum_g (sc[g] - 32) * sum_{l<16} q3[16g+l] * q8[16g+l] */
+int32_t orc_blk_q3_k(const uint8_t *w, const uint8_t *a) {
+    const int8_t *q8 = (const int8_t *)(a + 4);
+    int sc[16];
+    q3k_scales(w + 96, sc);
+    int32_t isum = 0;
+    for (int g = 0; g < 16; ++g) {
+        int32_t sub = 0;
+        for (int l = 0; l < 16; ++l) sub += q3k_value(w, 16 * g + l) * (int32_t)q8[16 * g + l];
+        isum += sc[g] * sub;
+    }
+    return isum;
+}
+
+/* kernels256.c:232-257 with :153-160 (value e = 128k + 32j + l:
+ * (qs[32k+l] >> 2j) & 3):
+ *   isum  = sum_g (scales[g] & 15) * sum_{l<16} q2[16g+l] * q8[16g+l]
+ *   summs = sum_{j<16} bsum[j] * (scales[j] >> 4)                           */
+void orc_blk_q2_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs) {
+    const int8_t *q8 = (const int8_t *)(a + 4);
+    int32_t is = 0, sm = 0;
+    for (int g = 0; g < 16; ++g) {
+        int32_t sub = 0;
+        for (int l16 = 0; l16 < 16; ++l16) {
+            int e = 16 * g + l16;
+            int k = e / 128, j = (e % 128) / 32, l = e % 32;
+            sub += ((w[16 + 32 * k + l] >> (2 * j)) & 3) * (int32_t)q8[e];
+        }
+        is += (w[g] & 15) * sub;
+        int16_t bs;
+        memcpy(&bs, a + 260 + 2 * g, 2);
+        sm += (int32_t)bs * (w[g] >> 4);
+    }
+    *isum = is;
+    *summs = sm;
+}
+
+/* IQ4_XS 6-bit scale of 32-value block ib, iq_kernels.c:976-979: low nibble
+ * from scales_l[ib/2], two high bits from scales_h. */
+static int iq4xs_ls(const uint8_t *w, int ib) {
+    int sh = ld16(w + 2);
+    return ((w[4 + ib / 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4);
+}
+
+/* iq_kernels.c:967-1001: the integer of 32-value block ib,
+ *   sumi = sum_{j<16} q8[32ib+j] * kv[qs[16ib+j] & 15] + q8[32ib+16+j] * kv[qs[16ib+j] >> 4] */
+int32_t orc_blk_iq4_xs(const uint8_t *w, const uint8_t *a, int ib) {
+    const uint8_t *qs = w + 8 + 16 * ib;
+    const int8_t *q8 = (const int8_t *)(a + 4) + 32 * ib;
+    int32_t s = 0;
+    for (int j = 0; j < 16; ++j)
+        s += (int32_t)q8[j] * orc_iq4nl_values[qs[j] & 15] + (int32_t)q8[16 + j] * orc_iq4nl_values[qs[j] >> 4];
+    return s;
+}
+
 /* ---- geometry ------------------------------------------------------------ */
 
 int orc_geom(int ttype, int *be, int *bb) {
@@ -229,6 +336,10 @@ int orc_geom(int ttype, int *be, int *bb) {
     case ORC_TT_IQ4_NL: *be = 32; *bb = 18; return 1;
     case ORC_TT_Q4_K: *be = 256; *bb = 144; return 1;
     case ORC_TT_Q6_K: *be = 256; *bb = 210; return 1;
+    case ORC_TT_Q2_K: *be = 256; *bb = 84; return 1;
+    case ORC_TT_Q3_K: *be = 256; *bb = 110; return 1;
+    case ORC_TT_Q5_K: *be = 256; *bb = 176; return 1;
+    case ORC_TT_IQ4_XS: *be = 256; *bb = 136; return 1;
     default: return 0;
     }
 }
@@ -301,12 +412,76 @@ static float dot_q6_k(int n, const void *vw, const void *va) {
     return sumf;
 }
 
+/* kernels256.c:605-629 */
+static float dot_q5_k(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 176, a += 292) {
+        int32_t isum, summs;
+        orc_blk_q5_k(w, a, &isum, &summs);
+        float dy;
+        memcpy(&dy, a, 4);
+        float d = dy * orc_f16_to_f32_k256(ld16(w));
+        float dmin = dy * orc_f16_to_f32_k256(ld16(w + 2));
+        sumf += d * (float)isum - dmin * (float)summs;
+    }
+    return sumf;
+}
+
+/* kernels256.c:349-366 */
+static float dot_q3_k(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 110, a += 292) {
+        float dy;
+        memcpy(&dy, a, 4);
+        sumf += orc_f16_to_f32_k256(ld16(w + 108)) * dy * (float)orc_blk_q3_k(w, a);
+    }
+    return sumf;
+}
+
+/* kernels256.c:232-257 */
+static float dot_q2_k(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 84, a += 292) {
+        int32_t isum, summs;
+        orc_blk_q2_k(w, a, &isum, &summs);
+        float dy;
+        memcpy(&dy, a, 4);
+        float dall = dy * orc_f16_to_f32_k256(ld16(w + 80));
+        float dmin = dy * orc_f16_to_f32_k256(ld16(w + 82));
+        sumf += dall * (float)isum - dmin * (float)summs;
+    }
+    return sumf;
+}
+
+/* iq_kernels.c:967-1001 (the f16 decode at :163-196 keeps the sign of zero) */
+static float dot_iq4_xs(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 136, a += 292) {
+        float dy;
+        memcpy(&dy, a, 4);
+        const float d4d8 = orc_f16_to_f32_k256(ld16(w)) * dy;
+        for (int ib = 0; ib < 8; ++ib) {
+            const float dl = d4d8 * (float)(iq4xs_ls(w, ib) - 32);
+            sumf += dl * (float)orc_blk_iq4_xs(w, a, ib);
+        }
+    }
+    return sumf;
+}
+
 orc_dot_fn orc_dot_fn_for(int ttype) {
     switch (ttype) {
     case ORC_TT_Q8_0: return dot_q8_0;
     case ORC_TT_IQ4_NL: return dot_iq4_nl;
     case ORC_TT_Q4_K: return dot_q4_k;
     case ORC_TT_Q6_K: return dot_q6_k;
+    case ORC_TT_Q2_K: return dot_q2_k;
+    case ORC_TT_Q3_K: return dot_q3_k;
+    case ORC_TT_Q5_K: return dot_q5_k;
+    case ORC_TT_IQ4_XS: return dot_iq4_xs;
     default: return 0;
     }
 }
@@ -321,6 +496,16 @@ float orc_dot(int ttype, int n, const void *w, const void *a) {
     return f ? f(n, w, a) : NAN;
 }
 
+/* integers per weight block in orc_row_block_ints: (isum, summs) for the
+ * K-quants with mins, one per 32-value block for IQ4_XS, else one */
+int orc_block_nints(int ttype) {
+    switch (ttype) {
+    case ORC_TT_Q4_K: case ORC_TT_Q5_K: case ORC_TT_Q2_K: return 2;
+    case ORC_TT_IQ4_XS: return 8;
+    default: return 1;
+    }
+}
+
 int orc_row_block_ints(int ttype, int n, const void *vw, const void *va, int32_t *out) {
     const uint8_t *w = vw, *a = va;
     int be, bb;
@@ -332,9 +517,15 @@ int orc_row_block_ints(int ttype, int n, const void *vw, const void *va, int32_t
         case ORC_TT_IQ4_NL: out[b] = orc_blk_iq4_nl(w + 18 * b, a + 34 * b); break;
         case ORC_TT_Q4_K: orc_blk_q4_k(w + 144 * b, a + 292 * b, &out[2 * b], &out[2 * b + 1]); break;
         case ORC_TT_Q6_K: out[b] = orc_blk_q6_k(w + 210 * b, a + 292 * b); break;
+        case ORC_TT_Q5_K: orc_blk_q5_k(w + 176 * b, a + 292 * b, &out[2 * b], &out[2 * b + 1]); break;
+        case ORC_TT_Q2_K: orc_blk_q2_k(w + 84 * b, a + 292 * b, &out[2 * b], &out[2 * b + 1]); break;
+        case ORC_TT_Q3_K: out[b] = orc_blk_q3_k(w + 110 * b, a + 292 * b); break;
+        case ORC_TT_IQ4_XS:
+            for (int ib = 0; ib < 8; ++ib) out[8 * b + ib] = orc_blk_iq4_xs(w + 136 * b, a + 292 * b, ib);
+            break;
         }
     }
-    return ttype == ORC_TT_Q4_K ? 2 * nb : nb;
+    return orc_block_nints(ttype) * nb;
 }
 
 int orc_quantize_act(int ttype, int cols, const float *x, uint8_t *out) {
@@ -405,7 +596,8 @@ int orc_matvec_batch(int ttype, int rows, int cols, int k, const void *w,
 /* ---- dequantization (fixture semantics) --------------------------------- */
 
 /* quant_dequant.zig:1388-1402 (Q8_0), :347-360 (IQ4_NL), :54-77 (Q4_K),
- * :222-251 (Q6_K). */
+ * :222-251 (Q6_K), :188-220 (Q5_K), :252-322 (Q3_K), :892-919 (Q2_K),
+ * :324-345 (IQ4_XS). */
 int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
     const uint8_t *w = vw;
     if (orc_row_bytes(ttype, cols) < 0) return -1;
@@ -438,6 +630,44 @@ int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
                     uint8_t q = blk[16 + 32 * (sb / 2) + l];
                     int nib = (sb & 1) ? (q >> 4) : (q & 15);
                     o[32 * sb + l] = d1 * (float)nib - m1;
+                }
+            }
+        } else if (ttype == ORC_TT_Q5_K) {
+            const uint8_t *blk = w + 176 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk)), mn = orc_f16_to_f32_k256(ld16(blk + 2));
+            for (int sb = 0; sb < 8; ++sb) {
+                int sc, m;
+                q4k_scale_min(blk + 4, sb, &sc, &m);
+                float d1 = d * (float)sc, m1 = mn * (float)m;
+                for (int l = 0; l < 32; ++l) {
+                    uint8_t q = blk[48 + 32 * (sb / 2) + l];
+                    int v = ((sb & 1) ? (q >> 4) : (q & 15)) | (((blk[16 + l] >> sb) & 1) << 4);
+                    o[32 * sb + l] = d1 * (float)v - m1;
+                }
+            }
+        } else if (ttype == ORC_TT_Q3_K) {
+            const uint8_t *blk = w + 110 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk + 108));
+            int sc[16];
+            q3k_scales(blk + 96, sc);
+            for (int e = 0; e < 256; ++e) o[e] = (d * (float)sc[e / 16]) * (float)q3k_value(blk, e);
+        } else if (ttype == ORC_TT_Q2_K) {
+            const uint8_t *blk = w + 84 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk + 80)), mn = orc_f16_to_f32_k256(ld16(blk + 82));
+            for (int e = 0; e < 256; ++e) {
+                int g = e / 16, k = e / 128, j = (e % 128) / 32, l = e % 32;
+                float dl = d * (float)(blk[g] & 15), ml = mn * (float)(blk[g] >> 4);
+                o[e] = dl * (float)((blk[16 + 32 * k + l] >> (2 * j)) & 3) - ml;
+            }
+        } else if (ttype == ORC_TT_IQ4_XS) {
+            const uint8_t *blk = w + 136 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk));
+            for (int ib = 0; ib < 8; ++ib) {
+                float dl = d * (float)(iq4xs_ls(blk, ib) - 32);
+                for (int j = 0; j < 16; ++j) {
+                    uint8_t q = blk[8 + 16 * ib + j];
+                    o[32 * ib + j] = dl * (float)orc_iq4nl_values[q & 15];
+                    o[32 * ib + 16 + j] = dl * (float)orc_iq4nl_values[q >> 4];
                 }
             }
         } else {

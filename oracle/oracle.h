@@ -36,6 +36,10 @@ extern "C" {
 #define ORC_TT_Q4_K  12
 #define ORC_TT_Q6_K  14
 #define ORC_TT_IQ4_NL 20
+#define ORC_TT_Q2_K  10
+#define ORC_TT_Q3_K  11
+#define ORC_TT_Q5_K  13
+#define ORC_TT_IQ4_XS 23
 
 float    orc_f16_to_f32(uint16_t h);        /* kernels32.c:45-66 (+0 for -0)  */
 float    orc_f16_to_f32_k256(uint16_t h);   /* kernels256.c:51-78 (keeps -0) */
@@ -49,6 +53,10 @@ int32_t orc_blk_q8_0(const uint8_t *w, const uint8_t *a);
 int32_t orc_blk_iq4_nl(const uint8_t *w, const uint8_t *a);
 void    orc_blk_q4_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs);
 int32_t orc_blk_q6_k(const uint8_t *w, const uint8_t *a);
+void    orc_blk_q5_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs);
+void    orc_blk_q2_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs);
+int32_t orc_blk_q3_k(const uint8_t *w, const uint8_t *a);
+int32_t orc_blk_iq4_xs(const uint8_t *w, const uint8_t *a, int ib);
 
 /* Geometry: returns 1 and fills the outputs for a supported type, else 0. */
 int orc_geom(int ttype, int *block_elems, int *block_bytes);
@@ -64,6 +72,7 @@ float orc_dot(int ttype, int n, const void *w, const void *a);
 
 /* Per-block integers of one row.  Q8_0 / IQ4_NL / Q6_K write n/block ints;
  * Q4_K writes 2 per super-block: isum then summs.  Returns ints written, or -1. */
+int orc_block_nints(int ttype);
 int orc_row_block_ints(int ttype, int n, const void *w, const void *a, int32_t *out);
 
 /* Quantize one f32 row with the type's activation family. 0 on success. */

@@ -17,8 +17,18 @@ ORACLE_SO = HERE / "liboracle.so"
 REF_SO = HERE / "_ref" / "libqref.so"
 
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20
-GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210)}
-NAMES = {TT_Q8_0: "Q8_0", TT_Q4_K: "Q4_K", TT_Q6_K: "Q6_K", TT_IQ4_NL: "IQ4_NL"}
+TT_Q2_K, TT_Q3_K, TT_Q5_K, TT_IQ4_XS = 10, 11, 13, 23
+GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210),
+        TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136)}
+NAMES = {TT_Q8_0: "Q8_0", TT_Q4_K: "Q4_K", TT_Q6_K: "Q6_K", TT_IQ4_NL: "IQ4_NL",
+         TT_Q2_K: "Q2_K", TT_Q3_K: "Q3_K", TT_Q5_K: "Q5_K", TT_IQ4_XS: "IQ4_XS"}
+# the formats of the benchmark configurations, and the further K-quant family
+BASE_TYPES = [TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL]
+EXTRA_TYPES = [TT_Q5_K, TT_Q3_K, TT_Q2_K, TT_IQ4_XS]
+ALL_TYPES = BASE_TYPES + EXTRA_TYPES
+# integers per weight block in block_ints: (isum, summs) for the K-quants with
+# mins, one per 32-value block for IQ4_XS, else one
+NINTS = {TT_Q4_K: 2, TT_Q5_K: 2, TT_Q2_K: 2, TT_IQ4_XS: 8}
 
 _c_u8p = ctypes.POINTER(ctypes.c_uint8)
 _c_f32p = ctypes.POINTER(ctypes.c_float)
@@ -104,7 +114,7 @@ class Oracle:
         W = np.ascontiguousarray(W).reshape(-1, row_bytes(ttype, cols))
         act = np.ascontiguousarray(act).reshape(-1, act_bytes(ttype, cols))
         nb = cols // GEOM[ttype][0]
-        ni = 2 * nb if ttype == TT_Q4_K else nb
+        ni = NINTS.get(ttype, 1) * nb
         out = np.zeros((act.shape[0], W.shape[0], ni), np.int32)
         for t in range(act.shape[0]):
             for r in range(W.shape[0]):
@@ -148,7 +158,8 @@ class Oracle:
 class RefKernels:
     """The reference's own x86 kernels, compiled from its sources into oracle/_ref."""
 
-    DOTS = {TT_Q8_0: "q8_0_q8_0", TT_Q4_K: "q4_k_q8_k", TT_Q6_K: "q6_k_q8_k"}
+    DOTS = {TT_Q8_0: "q8_0_q8_0", TT_Q4_K: "q4_k_q8_k", TT_Q6_K: "q6_k_q8_k", TT_Q5_K: "q5_k_q8_k",
+            TT_Q3_K: "q3_k_q8_k", TT_Q2_K: "q2_k_q8_k"}
     QUANTS = {32: "quantize_q8_0", 256: "quantize_q8_K"}
 
     def __init__(self, path: Path = REF_SO):

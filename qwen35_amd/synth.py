@@ -8,6 +8,11 @@ inputs.  Block contents follow the generation rules of each configuration:
 * Q4_K    random nibbles and packed 6-bit scales/mins, f16 d and dmin = |N(0,1)| * 1e-3
 * Q6_K    random ql/qh bits, int8 sub-scales uniform in [-64, 63], f16 d = |N(0,1)| * 1e-3
 * IQ4_NL  random 4-bit codebook indices, f16 d = |N(0,1)| * 1e-3
+* Q5_K    as Q4_K plus random high bits; Q3_K random 2-bit values, high-bit
+          mask and packed 6-bit scales; Q2_K random 2-bit values and 4-bit
+          scale/min bytes; IQ4_XS random indices and 6-bit scales; f16 d (and
+          dmin) = |N(0,1)| * 1e-3 (formats beyond the benchmark configurations,
+          same generation style)
 * activations f32 ~ N(0,1) (Box-Muller)
 """
 from __future__ import annotations
@@ -17,8 +22,11 @@ import hashlib
 import numpy as np
 
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20
-GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210)}
-D_SCALE = {TT_Q8_0: 2e-4, TT_IQ4_NL: 1e-3, TT_Q4_K: 1e-3, TT_Q6_K: 1e-3}
+TT_Q2_K, TT_Q3_K, TT_Q5_K, TT_IQ4_XS = 10, 11, 13, 23
+GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210),
+        TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136)}
+D_SCALE = {TT_Q8_0: 2e-4, TT_IQ4_NL: 1e-3, TT_Q4_K: 1e-3, TT_Q6_K: 1e-3, TT_Q2_K: 1e-3, TT_Q3_K: 1e-3,
+           TT_Q5_K: 1e-3, TT_IQ4_XS: 1e-3}
 
 _GAMMA = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -101,6 +109,23 @@ def make_weight(ttype: int, rows: int, cols: int, seed: int = 0, tag: int = 1) -
         sc = rand_uniform_int(substream(s, 4), nb * 16, -64, 63).astype(np.int8)
         blocks[:, 192:208] = sc.view(np.uint8).reshape(nb, 16)
         blocks[:, 208:210] = d.view(np.uint8).reshape(nb, 2)
+    elif ttype == TT_Q5_K:
+        dmin = f16_bits(np.abs(rand_normal(substream(s, 3), nb)) * D_SCALE[ttype])
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:4] = dmin.view(np.uint8).reshape(nb, 2)
+        blocks[:, 4:16] = rand_bytes(substream(s, 4), nb * 12).reshape(nb, 12)
+        blocks[:, 16:] = rand_bytes(substream(s, 2), nb * 160).reshape(nb, 160)
+    elif ttype == TT_Q3_K:
+        blocks[:, 0:108] = rand_bytes(substream(s, 2), nb * 108).reshape(nb, 108)
+        blocks[:, 108:110] = d.view(np.uint8).reshape(nb, 2)
+    elif ttype == TT_Q2_K:
+        dmin = f16_bits(np.abs(rand_normal(substream(s, 3), nb)) * D_SCALE[ttype])
+        blocks[:, 0:80] = rand_bytes(substream(s, 2), nb * 80).reshape(nb, 80)
+        blocks[:, 80:82] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 82:84] = dmin.view(np.uint8).reshape(nb, 2)
+    elif ttype == TT_IQ4_XS:
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:] = rand_bytes(substream(s, 2), nb * 134).reshape(nb, 134)
     else:
         raise ValueError(f"unsupported ttype {ttype}")
     return blocks.reshape(rows, cols // be * bb)

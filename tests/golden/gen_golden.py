@@ -8,7 +8,8 @@ Contents (small seeded inputs and the reference's outputs on them):
   quant_q8_0_x / _act          quantize_q8_0 input rows and output bytes
   quant_q8_k_x / _act          quantize_q8_K input rows and output bytes
   <T>_w, <T>_x, <T>_dot        weight rows, activation rows (f32) and the
-                               reference row dot (T = q8_0, q4_k, q6_k) of each
+                               reference row dot (T = q8_0, q4_k, q6_k, q5_k,
+                               q3_k, q2_k) of each
                                weight row against the reference-quantized row
   <T>_unit_*                   rows with unit scales (d = 1, dmin = 0 / d = 0,
                                dmin = 1) whose float result equals the exact
@@ -26,7 +27,11 @@ sys.path.insert(0, str(ROOT / "oracle"))
 import pyoracle as po  # noqa: E402
 from qwen35_amd import synth  # noqa: E402
 
-TT = {"q8_0": po.TT_Q8_0, "q4_k": po.TT_Q4_K, "q6_k": po.TT_Q6_K}
+TT = {"q8_0": po.TT_Q8_0, "q4_k": po.TT_Q4_K, "q6_k": po.TT_Q6_K, "q5_k": po.TT_Q5_K,
+      "q3_k": po.TT_Q3_K, "q2_k": po.TT_Q2_K}
+# byte offsets of (d, dmin) in each K-quant super-block; dmin None: no mins term
+SCALE_AT = {po.TT_Q4_K: (0, 2), po.TT_Q5_K: (0, 2), po.TT_Q6_K: (208, None), po.TT_Q3_K: (108, None),
+            po.TT_Q2_K: (80, 82)}
 
 
 def edge_rows(n: int) -> np.ndarray:
@@ -80,14 +85,13 @@ def main():
             variants["isum"] = (w1, a1)
         else:
             a1 = ab.copy(); a1[:, 0:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
-            if tt == po.TT_Q4_K:
-                wi = wb.copy(); wi[:, 0:2] = np.frombuffer(one.tobytes(), np.uint8); wi[:, 2:4] = 0
-                wm = wb.copy(); wm[:, 0:2] = 0; wm[:, 2:4] = np.frombuffer(one.tobytes(), np.uint8)
-                variants["isum"] = (wi, a1)
+            od, om = SCALE_AT[tt]
+            wi = wb.copy(); wi[:, od:od + 2] = np.frombuffer(one.tobytes(), np.uint8)
+            if om is not None:
+                wi[:, om:om + 2] = 0
+                wm = wb.copy(); wm[:, od:od + 2] = 0; wm[:, om:om + 2] = np.frombuffer(one.tobytes(), np.uint8)
                 variants["summs"] = (wm, a1)
-            else:
-                wi = wb.copy(); wi[:, 208:210] = np.frombuffer(one.tobytes(), np.uint8)
-                variants["isum"] = (wi, a1)
+            variants["isum"] = (wi, a1)
         for key, (wv, av) in variants.items():
             vals = np.array([ref.dot(tt, wv[i], av[i], be) for i in range(nblk)], np.float32)
             out[f"{name}_unit_{key}_w"], out[f"{name}_unit_{key}_a"] = wv, av

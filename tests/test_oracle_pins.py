@@ -101,12 +101,15 @@ def test_q8_k_bsums_and_clamp(oracle):
 # ---- block integers pinned bit for bit by unit-scale reference rows ---------
 
 @pytest.mark.parametrize("name,tt,key", [("q8_0", po.TT_Q8_0, "isum"), ("q4_k", po.TT_Q4_K, "isum"),
-                                         ("q4_k", po.TT_Q4_K, "summs"), ("q6_k", po.TT_Q6_K, "isum")])
+                                         ("q4_k", po.TT_Q4_K, "summs"), ("q6_k", po.TT_Q6_K, "isum"),
+                                         ("q5_k", po.TT_Q5_K, "isum"), ("q5_k", po.TT_Q5_K, "summs"),
+                                         ("q3_k", po.TT_Q3_K, "isum"), ("q2_k", po.TT_Q2_K, "isum"),
+                                         ("q2_k", po.TT_Q2_K, "summs")])
 def test_block_ints_unit_scale(oracle, gv, name, tt, key):
     w, a, val = gv[f"{name}_unit_{key}_w"], gv[f"{name}_unit_{key}_a"], gv[f"{name}_unit_{key}_val"]
     be = po.GEOM[tt][0]
     got = np.array([oracle.block_ints(tt, w[i:i + 1], a[i:i + 1], be)[0, 0] for i in range(len(w))])
-    if tt == po.TT_Q4_K:
+    if po.NINTS.get(tt, 1) == 2:
         got = got[:, 0] if key == "isum" else -got[:, 1]
     else:
         got = got[:, 0]
@@ -114,7 +117,8 @@ def test_block_ints_unit_scale(oracle, gv, name, tt, key):
     assert np.array_equal(got.astype(np.float32), val)
 
 
-@pytest.mark.parametrize("name,tt", [("q8_0", po.TT_Q8_0), ("q4_k", po.TT_Q4_K), ("q6_k", po.TT_Q6_K)])
+@pytest.mark.parametrize("name,tt", [("q8_0", po.TT_Q8_0), ("q4_k", po.TT_Q4_K), ("q6_k", po.TT_Q6_K),
+                                     ("q5_k", po.TT_Q5_K), ("q3_k", po.TT_Q3_K), ("q2_k", po.TT_Q2_K)])
 def test_row_dot_golden(oracle, gv, name, tt):
     w, x, want = gv[f"{name}_w"], gv[f"{name}_x"], gv[f"{name}_dot"]
     cols = x.shape[1]
@@ -126,7 +130,7 @@ def test_row_dot_golden(oracle, gv, name, tt):
     assert cols % 256 == 0
 
 
-@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K])
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_Q3_K, po.TT_Q2_K])
 def test_row_dot_vs_ref_random(oracle, ref, tt):
     from qwen35_amd import synth
     cols = 2560 if tt != po.TT_Q6_K else 2816
@@ -165,10 +169,53 @@ def test_iq4_nl_equals_q8_0_of_codebook(oracle, ref):
     assert np.array_equal(ints, ints8)
 
 
+def _iq4xs_as_iq4nl(wrow: np.ndarray, cols: int) -> tuple[np.ndarray, np.ndarray]:
+    """IQ4_XS super-blocks -> IQ4_NL blocks with the same indices, and the
+    6-bit scales ls - 32 of each 32-value block (iq_kernels.c:976-979)."""
+    blk = wrow.reshape(cols // 256, 136)
+    nl = np.zeros((cols // 256, 8, 18), np.uint8)
+    nl[:, :, 2:] = blk[:, 8:].reshape(-1, 8, 16)
+    sh = blk[:, 2].astype(np.int64) | (blk[:, 3].astype(np.int64) << 8)
+    ls = np.zeros((cols // 256, 8), np.int64)
+    for ib in range(8):
+        ls[:, ib] = ((blk[:, 4 + ib // 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+    return nl.reshape(-1), (ls - 32).reshape(-1)
+
+
+def test_iq4_xs_block_ints_equal_iq4_nl(oracle):
+    """IQ4_XS uses the IQ4_NL codebook with one index per value: with the same
+    int8 activation values its 32-value block integers ARE the IQ4_NL block
+    integers of the re-packed indices (pinned above by the reference's
+    q8_0_q8_0), and its row dot is sum_b (d*dy*(ls_b - 32)) * int_b."""
+    from qwen35_amd import synth
+    cols, rows = 1024, 16
+    w = synth.make_weight(po.TT_IQ4_XS, rows, cols, seed=8, tag=23)
+    # integer activations with +-127 in every 32-block: Q8_K and Q8_0 both
+    # quantize them to themselves with scale 1
+    rng = np.random.default_rng(8)
+    x = rng.integers(-127, 128, (2, cols)).astype(np.float32)
+    x[:, ::32] = 127.0
+    a_k = oracle.quantize_act(po.TT_IQ4_XS, x)
+    a_0 = oracle.quantize_act(po.TT_IQ4_NL, x)
+    assert np.all(a_k[:, 0:4].view(np.float32) == 1.0)
+    ints_xs = oracle.block_ints(po.TT_IQ4_XS, w, a_k, cols)
+    nl = np.stack([_iq4xs_as_iq4nl(w[r], cols)[0] for r in range(rows)])
+    ints_nl = oracle.block_ints(po.TT_IQ4_NL, nl, a_0, cols)
+    assert np.array_equal(ints_xs, ints_nl)
+    # the float fold against the unpacked scales
+    d = w.reshape(rows, cols // 256, 136)[:, :, 0:2].copy().view(np.float16)[..., 0].astype(np.float32)
+    got = oracle.matvec(po.TT_IQ4_XS, w, x)
+    for r in range(rows):
+        ls = _iq4xs_as_iq4nl(w[r], cols)[1]
+        want = np.sum(np.repeat(d[r], 8).astype(np.float64) * ls * ints_xs[:, r, :], axis=1)
+        assert np.allclose(got[:, r], want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+
+
 # ---- the reference's own fixtures (testdata/udtest) ------------------------------
 
 UD = {po.TT_Q8_0: ("Q8_0", 320), po.TT_Q4_K: ("Q4_K", 144), po.TT_Q6_K: ("Q6_K", 210),
-      po.TT_IQ4_NL: ("IQ4_NL", 144)}
+      po.TT_IQ4_NL: ("IQ4_NL", 144), po.TT_Q5_K: ("Q5_K", 176), po.TT_Q3_K: ("Q3_K", 110),
+      po.TT_IQ4_XS: ("IQ4_XS", 136)}
 
 
 @pytest.mark.parametrize("tt", list(UD))
