@@ -44,6 +44,10 @@ extern "C" {
 #define QHIP_TT_Q4_K 12
 #define QHIP_TT_Q6_K 14
 #define QHIP_TT_IQ4_NL 20
+#define QHIP_TT_Q2_K 10
+#define QHIP_TT_Q3_K 11
+#define QHIP_TT_Q5_K 13
+#define QHIP_TT_IQ4_XS 23
 
 #define QHIP_DECLINE (-1)
 

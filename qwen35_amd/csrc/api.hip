@@ -17,6 +17,10 @@ static bool geom(int ttype, int& be, int& bb) {
     case TT_IQ4_NL: be = 32; bb = 18; return true;
     case TT_Q4_K: be = 256; bb = 144; return true;
     case TT_Q6_K: be = 256; bb = 210; return true;
+    case TT_Q5_K: be = 256; bb = 176; return true;
+    case TT_Q3_K: be = 256; bb = 110; return true;
+    case TT_Q2_K: be = 256; bb = 84; return true;
+    case TT_IQ4_XS: be = 256; bb = 136; return true;
     default: return false;
   }
 }
@@ -78,6 +82,13 @@ static int mmq_min_tokens(int ttype) {
   }
 }
 
+// Formats with an MMQ kernel; the others (Q5_K, Q3_K, Q2_K, IQ4_XS) multiply
+// many tokens with the GEMV, which shares each weight load across up to 8
+// tokens per pass.
+static bool mmq_supported(int ttype) {
+  return ttype == TT_Q8_0 || ttype == TT_IQ4_NL || ttype == TT_Q4_K || ttype == TT_Q6_K;
+}
+
 // The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image
 // (built once per weight).  Measured on MI355X: the image beats the tile path
 // 1.6-1.8x for Q6_K (its per-16-value integer scaling dominates the tile
@@ -95,10 +106,11 @@ hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
   switch (path) {
     case QHIP_PATH_GENERIC: return launch_gemv_generic(g, s);
     case QHIP_PATH_GEMV: return fast ? launch_gemv(g, 0, 0, 0, s) : launch_gemv_generic(g, s);
-    case QHIP_PATH_MMQ: return fast ? launch_mmq(g, 0, 0, s) : (hipError_t)QHIP_DECLINE;
+    case QHIP_PATH_MMQ:
+      return fast && mmq_supported(g.ttype) ? launch_mmq(g, 0, 0, s) : (hipError_t)QHIP_DECLINE;
     case QHIP_PATH_AUTO:
       if (!fast) return launch_gemv_generic(g, s);
-      if (g.tokens >= mmq_min_tokens(g.ttype)) return launch_mmq(g, 0, 0, s);
+      if (mmq_supported(g.ttype) && g.tokens >= mmq_min_tokens(g.ttype)) return launch_mmq(g, 0, 0, s);
       return launch_gemv(g, 0, 0, 0, s);
     default: return hipErrorInvalidValue;
   }
@@ -321,7 +333,7 @@ int qhip_launch_mmq_tuned(const void* d_w, const void* d_xq, float* d_out, int r
   const bool bt_ok = tile_tokens == 0 || tile_tokens == 64 || tile_tokens == 128;
   const bool br_ok = tile_rows == 0 || tile_rows == 64 || tile_rows == 128;
   if (!bt_ok || !br_ok) return (int)hipErrorInvalidValue;
-  if (!fast_ok(g)) return QHIP_DECLINE;
+  if (!fast_ok(g) || !mmq_supported(ttype)) return QHIP_DECLINE;
   return (int)launch_mmq(g, tile_tokens, tile_rows, S(stream));
 }
 

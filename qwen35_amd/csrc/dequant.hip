@@ -7,6 +7,10 @@
 //   IQ4_NL  d * codebook[nibble]                     :347-360
 //   Q4_K    (d * sc) * nibble - (dmin * m)           :54-77  (separate roundings)
 //   Q6_K    (d * sc) * (q6 - 32)                     :222-251
+//   Q5_K    (d * sc) * (nibble + 16 * bit) - (dmin * m)  :188-220
+//   Q3_K    (d * (sc - 32)) * q3                      :252-322
+//   Q2_K    (d * (sc & 15)) * q2 - (dmin * (sc >> 4)) :892-919
+//   IQ4_XS  (d * (ls - 32)) * codebook[nibble]        :324-345
 // The library is compiled with -ffp-contract=off, so each product and the
 // Q4_K difference round exactly as the reference's Zig (strict float mode).
 //
@@ -67,6 +71,63 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
       const int nib = (int)((sub & 1) ? (q >> 4) : (q & 15u));
       o[i] = d1 * (float)nib - m1;
     }
+  } else if constexpr (TT == TT_Q5_K) {  // quant_dequant.zig:188-220
+    const uint8_t* blk = src + (v0 / 256) * 176;
+    const int e0 = (int)(v0 % 256), sub = e0 / 32;
+    const uint8_t* s12 = blk + 4;
+    int sc, m;
+    if (sub < 4) {
+      sc = s12[sub] & 63;
+      m = s12[sub + 4] & 63;
+    } else {
+      sc = (s12[sub + 4] & 15) | ((s12[sub - 4] >> 6) << 4);
+      m = (s12[sub + 4] >> 4) | ((s12[sub] >> 6) << 4);
+    }
+    const float d1 = h2f(ld16b(blk)) * (float)sc;
+    const float m1 = h2f(ld16b(blk + 2)) * (float)m;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int l = (e0 + i) % 32;
+      const uint32_t q = blk[48 + 32 * (sub / 2) + l];
+      const int v = (int)((sub & 1) ? (q >> 4) : (q & 15u)) | (int)(((blk[16 + l] >> sub) & 1u) << 4);
+      o[i] = d1 * (float)v - m1;
+    }
+  } else if constexpr (TT == TT_Q3_K) {  // quant_dequant.zig:252-322
+    const uint8_t* blk = src + (v0 / 256) * 110;
+    const int e0 = (int)(v0 % 256), g = e0 / 16, c = g / 4;
+    const uint32_t a0 = ld16b(blk + 96) | (ld16b(blk + 98) << 16), a1 = ld16b(blk + 100) | (ld16b(blk + 102) << 16);
+    const uint32_t a2 = ld16b(blk + 104) | (ld16b(blk + 106) << 16);
+    const uint32_t base = (c & 1) ? a1 : a0;
+    const uint32_t scw = ((c >= 2 ? (base >> 4) : base) & 0x0F0F0F0Fu) | (((a2 >> (2 * c)) & 0x03030303u) << 4);
+    const float dl = h2f(ld16b(blk + 108)) * (float)((int)((scw >> (8 * (g % 4))) & 0xFFu) - 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + i, h = e / 128, j = (e % 128) / 32, l = e % 32;
+      const int v = (int)((blk[32 + 32 * h + l] >> (2 * j)) & 3u) - (((blk[l] >> (4 * h + j)) & 1u) ? 0 : 4);
+      o[i] = dl * (float)v;
+    }
+  } else if constexpr (TT == TT_Q2_K) {  // quant_dequant.zig:892-919
+    const uint8_t* blk = src + (v0 / 256) * 84;
+    const int e0 = (int)(v0 % 256), g = e0 / 16;
+    const float dl = h2f(ld16b(blk + 80)) * (float)(blk[g] & 15);
+    const float ml = h2f(ld16b(blk + 82)) * (float)(blk[g] >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + i, k = e / 128, j = (e % 128) / 32, l = e % 32;
+      o[i] = dl * (float)((blk[16 + 32 * k + l] >> (2 * j)) & 3u) - ml;
+    }
+  } else if constexpr (TT == TT_IQ4_XS) {  // quant_dequant.zig:324-345
+    const uint8_t* blk = src + (v0 / 256) * 136;
+    const int e0 = (int)(v0 % 256), ib = e0 / 32;
+    const uint32_t sh = ld16b(blk + 2);
+    const int ls = (int)(((blk[4 + ib / 2] >> (4 * (ib % 2))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+    const float dl = h2f(ld16b(blk)) * (float)(ls - 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = (e0 + i) % 32;
+      const uint32_t q = blk[8 + 16 * ib + (j & 15)];
+      o[i] = dl * (float)iq4_value(j < 16 ? (q & 15u) : (q >> 4));
+    }
   } else {  // Q6_K
     const uint8_t* blk = src + (v0 / 256) * 210;
     const int e0 = (int)(v0 % 256);
@@ -89,14 +150,10 @@ hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hi
   if (nvals <= 0) return hipSuccess;
   const unsigned grid = (unsigned)((nvals / 4 + 255) / 256);
   const uint8_t* p = (const uint8_t*)src;
-  switch (ttype) {
-    case TT_Q8_0: hipLaunchKernelGGL(k_dequant<TT_Q8_0>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
-    case TT_IQ4_NL: hipLaunchKernelGGL(k_dequant<TT_IQ4_NL>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
-    case TT_Q4_K: hipLaunchKernelGGL(k_dequant<TT_Q4_K>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
-    case TT_Q6_K: hipLaunchKernelGGL(k_dequant<TT_Q6_K>, dim3(grid), dim3(256), 0, s, p, dst, nvals); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  return dispatch_type(ttype, [&](auto tt) {
+    hipLaunchKernelGGL(k_dequant<decltype(tt)::value>, dim3(grid), dim3(256), 0, s, p, dst, nvals);
+    return hipGetLastError();
+  });
 }
 
 }  // namespace qhip

@@ -277,10 +277,13 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
 }
 
 // Exact per-block integers through the same unit decode as k_gemv.  One
-// thread per (token, row, block group): a 2-block unit for Q8_0 / IQ4_NL, a
-// whole super-block (its four units summed) for Q4_K / Q6_K.  Layout of
-// `ints`: [tokens][rows][nints]; nints = blocks per row, or 2 per super-block
-// for Q4_K (isum, summs).
+// thread per (token, row, block group): a unit of two 32-value blocks for
+// Q8_0 / IQ4_NL / IQ4_XS (whose integers are per 32-value block), a whole
+// super-block (its four units summed) for the other K-quants.  Layout of
+// `ints`: [tokens][rows][nints]; nints = 32-value blocks per row, or per
+// super-block 2 (isum, summs: Q4_K, Q5_K, Q2_K) or 1 (Q6_K, Q3_K).
+constexpr bool per_block_ints(int tt) { return tt == TT_Q8_0 || tt == TT_IQ4_NL || tt == TT_IQ4_XS; }
+
 template <int TT>
 __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ W,
                                                      const uint8_t* __restrict__ XQ,
@@ -294,7 +297,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ 
   const long row = rt % rows, t = rt / rows;
   const uint8_t* wrow = W + row * row_bytes;
   const uint8_t* arow = XQ + t * act_bytes;
-  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
+  if constexpr (per_block_ints(TT)) {
     int out[2];
     U::ints(U::load_w(wrow, g), U::load_a(arow, g), out);
     int* o = ints + rt * (2L * groups) + 2 * g;
@@ -309,7 +312,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ 
       acc[0] += part[0];
       acc[1] += part[1];
     }
-    if constexpr (TT == TT_Q4_K) {
+    if constexpr (U::kInts == 2) {
       int* o = ints + rt * (2L * groups) + 2 * g;
       o[0] = acc[0];
       o[1] = acc[1];
@@ -351,45 +354,96 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
       }
       acc += h2f(ldb16(w)) * h2f(ldb16(a)) * (float)s;
     }
-  } else if constexpr (TT == TT_Q4_K) {
-    for (int b = 0; b < cols / 256; ++b, w += 144, a += 292) {
-      int is = 0, sm = 0;
-      for (int sb = 0; sb < 8; ++sb) {
-        int sc, mn;
-        const uint8_t* s12 = w + 4;
-        if (sb < 4) {
-          sc = s12[sb] & 63; mn = s12[sb + 4] & 63;
-        } else {
-          sc = (s12[sb + 4] & 15) | ((s12[sb - 4] >> 6) << 4);
-          mn = (s12[sb + 4] >> 4) | ((s12[sb] >> 6) << 4);
-        }
-        int sub = 0;
-        for (int l = 0; l < 32; ++l) {
-          const uint8_t q = w[16 + 32 * (sb / 2) + l];
-          sub += ((sb & 1) ? (q >> 4) : (q & 15)) * (int)(int8_t)a[4 + 32 * sb + l];
-        }
-        is += sc * sub;
-        sm += mn * (sext16(ldb16(a + 260 + 4 * sb)) + sext16(ldb16(a + 262 + 4 * sb)));
-      }
-      const float dy = __builtin_bit_cast(float, ldb16(a) | (ldb16(a + 2) << 16));
-      acc += (dy * h2f(ldb16(w))) * (float)is - (dy * h2f(ldb16(w + 2))) * (float)sm;
-    }
   } else {
-    for (int b = 0; b < cols / 256; ++b, w += 210, a += 292) {
-      int isum = 0;
-      for (int g = 0; g < 16; ++g) {
-        int sub = 0;
-        for (int l16 = 0; l16 < 16; ++l16) {
-          const int e = 16 * g + l16, h = e / 128, q = (e % 128) / 32, l = e % 32;
-          int lo = (q & 1) ? w[64 * h + 32 + l] : w[64 * h + l];
-          lo = q >= 2 ? (lo >> 4) : (lo & 15);
-          const int hb = (w[128 + 32 * h + l] >> (2 * q)) & 3;
-          sub += ((lo | (hb << 4)) - 32) * (int)(int8_t)a[4 + e];
-        }
-        isum += (int)(int8_t)w[192 + g] * sub;
-      }
+    constexpr int BB = TT == TT_Q4_K ? 144 : TT == TT_Q6_K ? 210 : TT == TT_Q5_K ? 176 : TT == TT_Q3_K ? 110
+                     : TT == TT_Q2_K ? 84 : 136;
+    for (int b = 0; b < cols / 256; ++b, w += BB, a += 292) {
       const float dy = __builtin_bit_cast(float, ldb16(a) | (ldb16(a + 2) << 16));
-      acc += (h2f(ldb16(w + 208)) * dy) * (float)isum;
+      const int8_t* q8 = (const int8_t*)(a + 4);
+      if constexpr (TT == TT_Q4_K || TT == TT_Q5_K) {
+        constexpr int QS = TT == TT_Q4_K ? 16 : 48;
+        int is = 0, sm = 0;
+        for (int sb = 0; sb < 8; ++sb) {
+          int sc, mn;
+          const uint8_t* s12 = w + 4;
+          if (sb < 4) {
+            sc = s12[sb] & 63; mn = s12[sb + 4] & 63;
+          } else {
+            sc = (s12[sb + 4] & 15) | ((s12[sb - 4] >> 6) << 4);
+            mn = (s12[sb + 4] >> 4) | ((s12[sb] >> 6) << 4);
+          }
+          int sub = 0;
+          for (int l = 0; l < 32; ++l) {
+            const uint8_t q = w[QS + 32 * (sb / 2) + l];
+            int v = (sb & 1) ? (q >> 4) : (q & 15);
+            if constexpr (TT == TT_Q5_K) v |= ((w[16 + l] >> sb) & 1) << 4;
+            sub += v * (int)q8[32 * sb + l];
+          }
+          is += sc * sub;
+          sm += mn * (sext16(ldb16(a + 260 + 4 * sb)) + sext16(ldb16(a + 262 + 4 * sb)));
+        }
+        acc += (dy * h2f(ldb16(w))) * (float)is - (dy * h2f(ldb16(w + 2))) * (float)sm;
+      } else if constexpr (TT == TT_Q6_K) {
+        int isum = 0;
+        for (int g = 0; g < 16; ++g) {
+          int sub = 0;
+          for (int l16 = 0; l16 < 16; ++l16) {
+            const int e = 16 * g + l16, h = e / 128, q = (e % 128) / 32, l = e % 32;
+            int lo = (q & 1) ? w[64 * h + 32 + l] : w[64 * h + l];
+            lo = q >= 2 ? (lo >> 4) : (lo & 15);
+            const int hb = (w[128 + 32 * h + l] >> (2 * q)) & 3;
+            sub += ((lo | (hb << 4)) - 32) * (int)q8[e];
+          }
+          isum += (int)(int8_t)w[192 + g] * sub;
+        }
+        acc += (h2f(ldb16(w + 208)) * dy) * (float)isum;
+      } else if constexpr (TT == TT_Q3_K) {
+        uint32_t u[3];
+        for (int i = 0; i < 3; ++i)
+          u[i] = (uint32_t)w[96 + 4 * i] | ((uint32_t)w[97 + 4 * i] << 8) | ((uint32_t)w[98 + 4 * i] << 16) |
+                 ((uint32_t)w[99 + 4 * i] << 24);
+        int isum = 0;
+        for (int g = 0; g < 16; ++g) {
+          const int c = g / 4, k = g % 4;
+          const uint32_t base = (c & 1) ? u[1] : u[0];
+          const uint32_t scw = ((c >= 2 ? (base >> 4) : base) & 0x0F0F0F0Fu) | (((u[2] >> (2 * c)) & 0x03030303u) << 4);
+          const int sc = (int)((scw >> (8 * k)) & 0xFFu) - 32;
+          int sub = 0;
+          for (int l16 = 0; l16 < 16; ++l16) {
+            const int e = 16 * g + l16, h = e / 128, j = (e % 128) / 32, l = e % 32;
+            const int v = ((w[32 + 32 * h + l] >> (2 * j)) & 3) - (((w[l] >> (4 * h + j)) & 1) ? 0 : 4);
+            sub += v * (int)q8[e];
+          }
+          isum += sc * sub;
+        }
+        acc += (h2f(ldb16(w + 108)) * dy) * (float)isum;
+      } else if constexpr (TT == TT_Q2_K) {
+        int isum = 0, summs = 0;
+        for (int g = 0; g < 16; ++g) {
+          int sub = 0;
+          for (int l16 = 0; l16 < 16; ++l16) {
+            const int e = 16 * g + l16, k = e / 128, j = (e % 128) / 32, l = e % 32;
+            sub += ((w[16 + 32 * k + l] >> (2 * j)) & 3) * (int)q8[e];
+          }
+          isum += (w[g] & 15) * sub;
+          summs += (w[g] >> 4) * sext16(ldb16(a + 260 + 2 * g));
+        }
+        acc += (dy * h2f(ldb16(w + 80))) * (float)isum - (dy * h2f(ldb16(w + 82))) * (float)summs;
+      } else {  // IQ4_XS
+        const float d4d8 = h2f(ldb16(w)) * dy;
+        const uint32_t sh = ldb16(w + 2);
+        for (int ib = 0; ib < 8; ++ib) {
+          const int ls = (int)(((w[4 + ib / 2] >> (4 * (ib % 2))) & 15u) | (((sh >> (2 * ib)) & 3u) << 4));
+          int sumi = 0;
+          for (int j = 0; j < 32; ++j) {
+            const uint32_t q = w[8 + 16 * ib + (j & 15)];
+            const uint32_t nib = j < 16 ? (q & 15u) : (q >> 4);
+            const uint32_t tab = nib < 4 ? IQ4_T0 : nib < 8 ? IQ4_T1 : nib < 12 ? IQ4_T2 : IQ4_T3;
+            sumi += sext8(tab >> (8 * (nib & 3))) * (int)q8[32 * ib + j];
+          }
+          acc += (d4d8 * (float)(ls - 32)) * (float)sumi;
+        }
+      }
     }
   }
   Y[t * rows + row] = acc;
@@ -474,15 +528,16 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
     nr = g.rows >= 4096 ? 4 : 2;
     return;
   }
-  if (g.ttype == TT_Q4_K && upr >= 64) {
+  if ((g.ttype == TT_Q4_K || g.ttype == TT_Q5_K) && upr >= 64) {
     team = 128;
     nr = 4;
     return;
   }
   switch (g.ttype) {
     case TT_Q6_K: nr = g.rows >= 4096 ? 2 : 1; team = 64; break;
-    case TT_Q4_K: nr = g.rows >= 16384 && upr <= 40 ? 4 : 2; team = upr <= 40 ? 40 : 20; break;
-    case TT_IQ4_NL: nr = 4; team = 20; break;
+    case TT_Q4_K: case TT_Q5_K:
+      nr = g.rows >= 16384 && upr <= 40 ? 4 : 2; team = upr <= 40 ? 40 : 20; break;
+    case TT_IQ4_NL: case TT_IQ4_XS: case TT_Q2_K: case TT_Q3_K: nr = 4; team = 20; break;
     default: nr = g.rows >= 4096 ? 2 : 1; team = 16; break;
   }
   if (team > upr) team = upr;
@@ -506,13 +561,7 @@ hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t 
   }
   if (team > 64) return launch_gemv_multiwave(g, nr, team / 64, s);
   if (nt <= 0) nt = gemv_pick_nt(g.tokens);
-  switch (g.ttype) {
-    case TT_Q8_0: return launch_gemv_type<TT_Q8_0>(g, team, nt, nr, s);
-    case TT_IQ4_NL: return launch_gemv_type<TT_IQ4_NL>(g, team, nt, nr, s);
-    case TT_Q4_K: return launch_gemv_type<TT_Q4_K>(g, team, nt, nr, s);
-    case TT_Q6_K: return launch_gemv_type<TT_Q6_K>(g, team, nt, nr, s);
-    default: return hipErrorInvalidValue;
-  }
+  return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_type<decltype(tt)::value>(g, team, nt, nr, s); });
 }
 
 template <int TT, int NR, int WV>
@@ -546,13 +595,7 @@ static hipError_t launch_gemv_mw_type(const GemvArgs& g, int nr, int wv, hipStre
 // one token, teams of wv = 2 or 4 waves
 static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipStream_t s) {
   if (g.tokens != 1) return hipErrorInvalidValue;
-  switch (g.ttype) {
-    case TT_Q8_0: return launch_gemv_mw_type<TT_Q8_0>(g, nr, wv, s);
-    case TT_IQ4_NL: return launch_gemv_mw_type<TT_IQ4_NL>(g, nr, wv, s);
-    case TT_Q4_K: return launch_gemv_mw_type<TT_Q4_K>(g, nr, wv, s);
-    case TT_Q6_K: return launch_gemv_mw_type<TT_Q6_K>(g, nr, wv, s);
-    default: return hipErrorInvalidValue;
-  }
+  return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_mw_type<decltype(tt)::value>(g, nr, wv, s); });
 }
 
 template <int TT, int NR>
@@ -609,13 +652,7 @@ hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, in
     if (nr <= 0) nr = 1;
     if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);
   }
-  switch (g.ttype) {
-    case TT_Q8_0: return launch_gemv_q_type<TT_Q8_0>(g, x, xq_out, team, nr, s);
-    case TT_IQ4_NL: return launch_gemv_q_type<TT_IQ4_NL>(g, x, xq_out, team, nr, s);
-    case TT_Q4_K: return launch_gemv_q_type<TT_Q4_K>(g, x, xq_out, team, nr, s);
-    case TT_Q6_K: return launch_gemv_q_type<TT_Q6_K>(g, x, xq_out, team, nr, s);
-    default: return hipErrorInvalidValue;
-  }
+  return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_q_type<decltype(tt)::value>(g, x, xq_out, team, nr, s); });
 }
 
 hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s) {
@@ -624,19 +661,16 @@ hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s) {
   const unsigned grid = (unsigned)((n + 255) / 256);
   const uint8_t* w = (const uint8_t*)g.w;
   const uint8_t* a = (const uint8_t*)g.xq;
-  switch (g.ttype) {
-    case TT_Q8_0: hipLaunchKernelGGL(k_gemv_generic<TT_Q8_0>, dim3(grid), dim3(256), 0, s, w, a, g.out, g.rows, g.cols, g.row_bytes, g.act_bytes, g.tokens); break;
-    case TT_IQ4_NL: hipLaunchKernelGGL(k_gemv_generic<TT_IQ4_NL>, dim3(grid), dim3(256), 0, s, w, a, g.out, g.rows, g.cols, g.row_bytes, g.act_bytes, g.tokens); break;
-    case TT_Q4_K: hipLaunchKernelGGL(k_gemv_generic<TT_Q4_K>, dim3(grid), dim3(256), 0, s, w, a, g.out, g.rows, g.cols, g.row_bytes, g.act_bytes, g.tokens); break;
-    case TT_Q6_K: hipLaunchKernelGGL(k_gemv_generic<TT_Q6_K>, dim3(grid), dim3(256), 0, s, w, a, g.out, g.rows, g.cols, g.row_bytes, g.act_bytes, g.tokens); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  return dispatch_type(g.ttype, [&](auto tt) {
+    hipLaunchKernelGGL(k_gemv_generic<decltype(tt)::value>, dim3(grid), dim3(256), 0, s, w, a, g.out, g.rows,
+                       g.cols, g.row_bytes, g.act_bytes, g.tokens);
+    return hipGetLastError();
+  });
 }
 
 template <int TT>
 static hipError_t launch_ints_t(const GemvArgs& g, int* ints, hipStream_t s) {
-  const int groups = (TT == TT_Q8_0 || TT == TT_IQ4_NL) ? g.cols / 64 : g.cols / 256;
+  const int groups = per_block_ints(TT) ? g.cols / 64 : g.cols / 256;
   const long n = (long)g.tokens * g.rows * groups;
   const unsigned grid = (unsigned)((n + 255) / 256);
   hipLaunchKernelGGL(k_block_ints<TT>, dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
@@ -646,13 +680,7 @@ static hipError_t launch_ints_t(const GemvArgs& g, int* ints, hipStream_t s) {
 
 hipError_t launch_block_ints(const GemvArgs& g, int* ints, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
-  switch (g.ttype) {
-    case TT_Q8_0: return launch_ints_t<TT_Q8_0>(g, ints, s);
-    case TT_IQ4_NL: return launch_ints_t<TT_IQ4_NL>(g, ints, s);
-    case TT_Q4_K: return launch_ints_t<TT_Q4_K>(g, ints, s);
-    case TT_Q6_K: return launch_ints_t<TT_Q6_K>(g, ints, s);
-    default: return hipErrorInvalidValue;
-  }
+  return dispatch_type(g.ttype, [&](auto tt) { return launch_ints_t<decltype(tt)::value>(g, ints, s); });
 }
 
 }  // namespace qhip

@@ -15,15 +15,21 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace qhip {
 
-enum : int { TT_Q8_0 = 8, TT_Q4_K = 12, TT_Q6_K = 14, TT_IQ4_NL = 20 };
+enum : int {
+  TT_Q8_0 = 8, TT_Q2_K = 10, TT_Q3_K = 11, TT_Q4_K = 12, TT_Q5_K = 13, TT_Q6_K = 14, TT_IQ4_NL = 20,
+  TT_IQ4_XS = 23
+};
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
 // unaligned views (byte-aligned addresses; global memory only)
 typedef uint32_t u32x4_u __attribute__((ext_vector_type(4), aligned(1)));
 typedef uint32_t u32x2_u __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t u32_a2 __attribute__((aligned(2)));
 
 // ---- loads (addresses are 4-byte aligned; see each caller) -----------------
 __device__ __forceinline__ uint32_t ld32(const uint8_t* p) { return *(const uint32_t*)p; }
@@ -489,5 +495,238 @@ struct Unit<TT_Q6_K> {
     return (h2f(w.d) * a.d) * (float)s[0];
   }
 };
+
+
+// ---- the further K-quant family (Q8_K activations, 64-value quarter units) ----
+// Every unit below covers values 64c..64c+63 of super-block u>>2 (c = u&3) in
+// order, so it takes the Q4_K activation unit (values, block scale, the four
+// 16-value sums of groups 4c..4c+3).
+
+template <>
+struct Unit<TT_Q5_K> {
+  // 176-byte super-block: d, dmin, 12 scale bytes, qh[32], qs[128]
+  // (value layout src/kernels/x86/kernels256.c:188-198: nibble + 16 * bit)
+  static constexpr int kWBytes = 80, kInts = 2;
+  struct W { uint32_t hdr[4]; uint32_t q[8]; uint32_t qh[8]; int c; };
+  using A = ActQ8K;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* blk = row + 176 * (u >> 2);
+    W w;
+    w.c = u & 3;
+    const u32x4 h = ld128(blk), m0 = ld128(blk + 16), m1 = ld128(blk + 32);
+    const u32x4 a = ld128(blk + 48 + 32 * w.c), b = ld128(blk + 64 + 32 * w.c);
+    w.hdr[0] = h.x; w.hdr[1] = h.y; w.hdr[2] = h.z; w.hdr[3] = h.w;
+    w.qh[0] = m0.x; w.qh[1] = m0.y; w.qh[2] = m0.z; w.qh[3] = m0.w;
+    w.qh[4] = m1.x; w.qh[5] = m1.y; w.qh[6] = m1.z; w.qh[7] = m1.w;
+    w.q[0] = a.x; w.q[1] = a.y; w.q[2] = a.z; w.q[3] = a.w;
+    w.q[4] = b.x; w.q[5] = b.y; w.q[6] = b.z; w.q[7] = b.w;
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return Unit<TT_Q4_K>::load_a(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    return Unit<TT_Q4_K>::load_a_split(sp, u);
+  }
+  // sub-blocks 2c (low nibbles, qh bit 2c) and 2c+1 (high nibbles, bit 2c+1);
+  // scales and mins exactly as Q4_K (kernels256.c:605-629)
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
+    int lo = 0, hi = 0;
+    const uint32_t s0 = 2u * (uint32_t)w.c;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t h0 = ((w.qh[i] >> s0) & 0x01010101u) << 4;
+      const uint32_t h1 = ((w.qh[i] >> (s0 + 1)) & 0x01010101u) << 4;
+      lo = dot4((w.q[i] & 0x0F0F0F0Fu) | h0, a.y[i], lo);
+      hi = dot4(((w.q[i] >> 4) & 0x0F0F0F0Fu) | h1, a.y[8 + i], hi);
+    }
+    const uint32_t S0 = w.hdr[1], S1 = w.hdr[2], S2 = w.hdr[3];
+    const bool upper = w.c >= 2;
+    const uint32_t scw = upper ? ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u)) : (S0 & 0x3F3F3F3Fu);
+    const uint32_t mnw = upper ? (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) : (S1 & 0x3F3F3F3Fu);
+    const uint32_t sh = 16u * (uint32_t)(w.c & 1);
+    const int sc0 = (int)((scw >> sh) & 0xFFu), sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+    const int m0 = (int)((mnw >> sh) & 0xFFu), m1 = (int)((mnw >> (sh + 8)) & 0xFFu);
+    out[0] = sc0 * lo + sc1 * hi;
+    out[1] = m0 * (a.bs[0] + a.bs[1]) + m1 * (a.bs[2] + a.bs[3]);
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[2];
+    ints(w, a, s);
+    const float d = a.d * h2f(w.hdr[0]);
+    const float dmin = a.d * h2f(w.hdr[0] >> 16);
+    return d * (float)s[0] - dmin * (float)s[1];
+  }
+};
+
+template <>
+struct Unit<TT_Q3_K> {
+  // 110-byte super-block: hmask[32], qs[64], 12 scale bytes, d.  Value
+  // 128h + 32g + l = ((qs[32h+l] >> 2g) & 3) - (hmask bit 4h+g of byte l ? 0 : 4)
+  // (kernels256.c:162-177).  Super-blocks start 2-byte aligned: unaligned
+  // loads, each inside the super-block (see Unit<TT_Q6_K>).
+  static constexpr int kWBytes = 78, kInts = 1;
+  struct W { uint32_t q[8], hm[8]; uint32_t s0, s1, s2; uint32_t d; int c; };
+  using A = ActQ8K;
+  static __device__ __forceinline__ void load16(const uint8_t* p, uint32_t* out) {
+    const u32x4_u v = *(const u32x4_u*)p;
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  }
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* blk = row + 110 * (u >> 2);
+    W w;
+    w.c = u & 3;
+    const int h = w.c >> 1;
+    load16(blk, w.hm);
+    load16(blk + 16, w.hm + 4);
+    load16(blk + 32 + 32 * h, w.q);
+    load16(blk + 48 + 32 * h, w.q + 4);
+    const u32x2_u sc = *(const u32x2_u*)(blk + 96);
+    w.s0 = sc.x;
+    w.s1 = sc.y;
+    w.s2 = *(const u32_a2*)(blk + 104);
+    w.d = *(const uint16_t*)(blk + 108);
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return Unit<TT_Q4_K>::load_a(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    return Unit<TT_Q4_K>::load_a_split(sp, u);
+  }
+  // groups 4c+k, k = 0..3: shift g = 2(c&1) + k/2, bytes 16(k&1).. of the qs
+  // slice and of hmask.  sum (q3 - 4) * q8 = sum u3 * q8 - 4 * bsum with
+  // u3 = q2 | (hbit << 2).  Scales: dword c of the 16 unpacked 6-bit values
+  // (kernels256.c:129-151), used - 32.
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
+    const int h = w.c >> 1;
+    const uint32_t base = (w.c & 1) ? w.s1 : w.s0;
+    const uint32_t scw = ((w.c >= 2 ? (base >> 4) : base) & 0x0F0F0F0Fu) |
+                         (((w.s2 >> (2 * w.c)) & 0x03030303u) << 4);
+    int isum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t g = 2u * (uint32_t)(w.c & 1) + (uint32_t)(k >> 1);
+      const uint32_t hs = 4u * (uint32_t)h + g;
+      int sk = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t q2 = (w.q[4 * (k & 1) + i] >> (2 * g)) & 0x03030303u;
+        const uint32_t hb = (w.hm[4 * (k & 1) + i] >> hs) & 0x01010101u;
+        sk = dot4(q2 | (hb << 2), a.y[4 * k + i], sk);
+      }
+      const int sc = (int)((scw >> (8 * k)) & 0xFFu) - 32;
+      isum += sc * (sk - 4 * a.bs[k]);
+    }
+    out[0] = isum;
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[1];
+    ints(w, a, s);
+    return (h2f(w.d) * a.d) * (float)s[0];
+  }
+};
+
+template <>
+struct Unit<TT_Q2_K> {
+  // 84-byte super-block: scales[16] (low nibble scale, high nibble min),
+  // qs[64], d, dmin.  Value 128k + 32j + l = (qs[32k+l] >> 2j) & 3
+  // (kernels256.c:153-160).
+  static constexpr int kWBytes = 40, kInts = 2;
+  struct W { uint32_t q[8]; uint32_t sc; uint32_t dd; int c; };
+  using A = ActQ8K;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* blk = row + 84 * (u >> 2);
+    W w;
+    w.c = u & 3;
+    const int k = w.c >> 1;
+    const u32x4 a = ld128(blk + 16 + 32 * k), b = ld128(blk + 32 + 32 * k);
+    w.q[0] = a.x; w.q[1] = a.y; w.q[2] = a.z; w.q[3] = a.w;
+    w.q[4] = b.x; w.q[5] = b.y; w.q[6] = b.z; w.q[7] = b.w;
+    w.sc = ld32(blk + 4 * w.c);
+    w.dd = ld32(blk + 80);
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return Unit<TT_Q4_K>::load_a(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    return Unit<TT_Q4_K>::load_a_split(sp, u);
+  }
+  // groups 4c+k: shift 2j with j = 2(c&1) + k/2, bytes 16(k&1).. of the slice
+  // (kernels256.c:232-257)
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
+    int isum = 0, summs = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t j = 2u * (uint32_t)(w.c & 1) + (uint32_t)(k >> 1);
+      int sk = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sk = dot4((w.q[4 * (k & 1) + i] >> (2 * j)) & 0x03030303u, a.y[4 * k + i], sk);
+      const uint32_t b = (w.sc >> (8 * k)) & 0xFFu;
+      isum += (int)(b & 15u) * sk;
+      summs += (int)(b >> 4) * a.bs[k];
+    }
+    out[0] = isum;
+    out[1] = summs;
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[2];
+    ints(w, a, s);
+    const float dall = a.d * h2f(w.dd);
+    const float dmin = a.d * h2f(w.dd >> 16);
+    return dall * (float)s[0] - dmin * (float)s[1];
+  }
+};
+
+template <>
+struct Unit<TT_IQ4_XS> {
+  // 136-byte super-block: d, scales_h (u16), scales_l[4], qs[128]; 32-value
+  // block ib has index bytes qs[16ib..16ib+15] (low nibble -> value j, high ->
+  // j+16) into the IQ4_NL codebook and the 6-bit scale
+  // ls = scales_l nibble | 2 bits of scales_h, used - 32 (iq_kernels.c:967-1001)
+  static constexpr int kWBytes = 40, kInts = 2;
+  struct W { uint32_t q[8]; uint32_t h0, sl; int c; };
+  using A = ActQ8K;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* blk = row + 136 * (u >> 2);
+    W w;
+    w.c = u & 3;
+    const u32x4 a = ld128(blk + 8 + 32 * w.c), b = ld128(blk + 24 + 32 * w.c);
+    w.q[0] = a.x; w.q[1] = a.y; w.q[2] = a.z; w.q[3] = a.w;
+    w.q[4] = b.x; w.q[5] = b.y; w.q[6] = b.z; w.q[7] = b.w;
+    w.h0 = ld32(blk);
+    w.sl = ld32(blk + 4);
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return Unit<TT_Q4_K>::load_a(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    return Unit<TT_Q4_K>::load_a_split(sp, u);
+  }
+  // the integers of blocks 2c and 2c+1, the IQ4_NL block core
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
+    out[0] = Unit<TT_IQ4_NL>::block(w.q, a.y);
+    out[1] = Unit<TT_IQ4_NL>::block(w.q + 4, a.y + 8);
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[2];
+    ints(w, a, s);
+    const uint32_t sh = w.h0 >> 16, sl = (w.sl >> (8 * w.c)) & 0xFFu;
+    const int ls0 = (int)((sl & 15u) | (((sh >> (4 * w.c)) & 3u) << 4));
+    const int ls1 = (int)((sl >> 4) | (((sh >> (4 * w.c + 2)) & 3u) << 4));
+    const float d4d8 = h2f(w.h0) * a.d;
+    return (d4d8 * (float)(ls0 - 32)) * (float)s[0] + (d4d8 * (float)(ls1 - 32)) * (float)s[1];
+  }
+};
+
+// Calls f(std::integral_constant<int, TT>{}) for the format id `ttype`.
+template <class F>
+__host__ inline auto dispatch_type(int ttype, F&& f) -> decltype(f(std::integral_constant<int, TT_Q8_0>{})) {
+  switch (ttype) {
+    case TT_Q8_0: return f(std::integral_constant<int, TT_Q8_0>{});
+    case TT_IQ4_NL: return f(std::integral_constant<int, TT_IQ4_NL>{});
+    case TT_Q4_K: return f(std::integral_constant<int, TT_Q4_K>{});
+    case TT_Q6_K: return f(std::integral_constant<int, TT_Q6_K>{});
+    case TT_Q5_K: return f(std::integral_constant<int, TT_Q5_K>{});
+    case TT_Q3_K: return f(std::integral_constant<int, TT_Q3_K>{});
+    case TT_Q2_K: return f(std::integral_constant<int, TT_Q2_K>{});
+    case TT_IQ4_XS: return f(std::integral_constant<int, TT_IQ4_XS>{});
+    default: return hipErrorInvalidValue;
+  }
+}
 
 }  // namespace qhip

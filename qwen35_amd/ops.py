@@ -11,7 +11,11 @@ import torch
 
 from ._lib import QhipLinear, check, load
 
-_GEOM = {8: (32, 34), 20: (32, 18), 12: (256, 144), 14: (256, 210)}
+_GEOM = {8: (32, 34), 20: (32, 18), 12: (256, 144), 14: (256, 210), 13: (256, 176), 11: (256, 110),
+         10: (256, 84), 23: (256, 136)}
+# integers per super-block in the block-integer export: (isum, summs) for
+# Q4_K / Q5_K / Q2_K, one per 32-value block for IQ4_XS, else one
+_NINTS_SB = {12: 2, 13: 2, 10: 2, 23: 8}
 
 
 def _stream() -> ctypes.c_void_p:
@@ -137,7 +141,7 @@ def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, co
 def block_ints(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
                tokens: int) -> torch.Tensor:
     be = _GEOM[ttype][0]
-    nints = 2 * cols // 256 if ttype == 12 else cols // be
+    nints = cols // be if be == 32 else _NINTS_SB.get(ttype, 1) * (cols // 256)
     out = torch.empty((tokens, rows, nints), dtype=torch.int32, device=w.device)
     check("block_ints", load().qhip_launch_block_ints(_p(w), _p(xq), _p(out), rows, cols, tokens,
                                                       ttype, _stream()))

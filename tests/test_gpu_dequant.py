@@ -10,7 +10,7 @@ import qwen35_amd
 from qwen35_amd import _lib, ops, synth
 
 pytestmark = pytest.mark.gpu
-TYPES = [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K]
+TYPES = po.ALL_TYPES
 
 
 def to_dev(a, dev):
@@ -24,16 +24,17 @@ def with_edge_scales(tt, w):
     blk = w.reshape(-1, bb).copy()
     edge = np.array([0x0001, 0x03FF, 0x8400, 0x0000, 0x8000, 0x7BFF, 0xFBFF], np.uint16).view(np.uint8)
     n = min(len(blk), 7)
-    off = 208 if tt == po.TT_Q6_K else 0
+    off = {po.TT_Q6_K: 208, po.TT_Q3_K: 108, po.TT_Q2_K: 80}.get(tt, 0)
     blk[:n, off:off + 2] = edge.reshape(-1, 2)[:n]
-    if tt == po.TT_Q4_K:
-        blk[:n, 2:4] = edge.reshape(-1, 2)[::-1][:n]
+    dmin = {po.TT_Q4_K: 2, po.TT_Q5_K: 2, po.TT_Q2_K: 82}.get(tt)
+    if dmin is not None:
+        blk[:n, dmin:dmin + 2] = edge.reshape(-1, 2)[::-1][:n]
     return blk.reshape(w.shape)
 
 
 @pytest.mark.parametrize("tt", TYPES)
 def test_dequantize_rows_bit_exact(gpu, oracle, tt):
-    rows, cols = 7, 2560 if tt != po.TT_Q6_K else 2304
+    rows, cols = 7, 2560 if tt not in (po.TT_Q6_K, po.TT_Q3_K) else 2304
     w = with_edge_scales(tt, synth.make_weight(tt, rows, cols, seed=4, tag=tt))
     wd = to_dev(w, gpu)
     for r in range(rows):

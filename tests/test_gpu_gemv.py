@@ -15,7 +15,7 @@ from qwen35_amd import ops, synth
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5  # relative L2, float outputs
-TYPES = [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K]
+TYPES = po.ALL_TYPES
 
 
 def rel_l2(got, want):
@@ -80,6 +80,10 @@ SHAPES = {
     po.TT_IQ4_NL: [(200, 2560), (37, 256)],
     po.TT_Q4_K: [(100, 2560), (33, 256)],
     po.TT_Q6_K: [(50, 9728), (18, 256), (16, 2304)],
+    po.TT_Q5_K: [(100, 2560), (33, 256)],
+    po.TT_Q3_K: [(60, 2560), (18, 256), (16, 2304)],
+    po.TT_Q2_K: [(70, 2560), (21, 256)],
+    po.TT_IQ4_XS: [(80, 2560), (19, 256)],
 }
 CASES = [(tt, r, c) for tt in TYPES for (r, c) in SHAPES[tt]]
 
@@ -177,7 +181,8 @@ def test_zero_weights_and_zero_activation(gpu, oracle):
 
 FUSED = [(po.TT_Q8_0, 300, 1024), (po.TT_Q8_0, 6144, 1024), (po.TT_IQ4_NL, 200, 2560),
          (po.TT_Q4_K, 100, 2560), (po.TT_Q4_K, 19456, 2560), (po.TT_Q6_K, 50, 9728),
-         (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 16, 2304)]
+         (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 16, 2304), (po.TT_Q5_K, 100, 2560), (po.TT_Q3_K, 60, 2304),
+         (po.TT_Q2_K, 70, 2560), (po.TT_IQ4_XS, 80, 2560)]
 
 
 @pytest.mark.parametrize("tt,rows,cols", FUSED, ids=[case_id(*c) for c in FUSED])

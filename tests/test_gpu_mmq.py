@@ -298,3 +298,23 @@ def test_backend_prefill_batch(gpu, oracle, tt):
 def ctypes_byref(x):
     import ctypes
     return ctypes.byref(x)
+
+
+@pytest.mark.parametrize("tt", po.EXTRA_TYPES)
+def test_formats_without_mmq_decline_and_auto_uses_gemv(gpu, oracle, tt):
+    """Q5_K / Q3_K / Q2_K / IQ4_XS have no MMQ kernel: the explicit MMQ entry
+    points decline, the automatic path serves any token count with the GEMV."""
+    rows, cols, tokens = 72, 1024, 70
+    w = synth.make_weight(tt, rows, cols, seed=12, tag=tt)
+    x = synth.make_act(cols, tokens, seed=12)
+    wd = to_dev(w, gpu)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    out = torch.empty((tokens, rows), device=gpu)
+    L = _lib.load()
+    assert L.qhip_launch_mmq_tuned(wd.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt,
+                                   64, 64, None) == qwen35_amd.DECLINE
+    assert L.qhip_launch_mul_mat_vec_tile(wd.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt,
+                                          None) == qwen35_amd.DECLINE
+    assert L.qhip_mmq_image_bytes(tt, rows, cols) == -1
+    got = ops.mul_mat(tt, wd, xq, rows, cols, tokens).cpu().numpy()
+    assert rel_l2(got, oracle.matvec(tt, w, x)) < TOL
