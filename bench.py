@@ -136,8 +136,10 @@ def main() -> int:
         return 0
 
     # ---- headline workload: cfg2 FFN step through the Exec mirror --------------
-    # matvecPair(gate, up, x) + matvec(down, h): one launch each, the activation
-    # quantized inside the GEMV (src/backend.zig:153-176 slots).
+    # matvecPair(gate, up, x) + matvec(down, h) (src/backend.zig:153-176 slots):
+    # the mirror quantizes x and h on the device and runs one GEMV per slot
+    # (adjacent gate/up weights are one launch); at these widths it picks the
+    # separate quantize launch over the fused quantize+GEMV.
     import ctypes
     H, F = 2560, 9728
     t0 = time.time()
@@ -262,7 +264,12 @@ def main() -> int:
         for name, tt, rows, cols in (("cfg1_q8_0_6144x1024", TQ8, 6144, 1024),
                                      ("cfg3_iq4_nl_248320x2560", TIQ, 248320, 2560),
                                      ("cfg5_q4_k_17408x5120", TQ4, 17408, 5120),
-                                     ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408)):
+                                     ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408),
+                                     # further formats at the config-5 gate/up shape
+                                     ("q5_k_17408x5120", 13, 17408, 5120),
+                                     ("q3_k_17408x5120", 11, 17408, 5120),
+                                     ("q2_k_17408x5120", 10, 17408, 5120),
+                                     ("iq4_xs_17408x5120", 23, 17408, 5120)):
             t1 = time.time()
             w = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
             st = Stream(torch, w.reshape(-1), dev)
@@ -303,7 +310,8 @@ def main() -> int:
         "data": "synthetic (SplitMix64 seed 0, BASELINE.json config rules)",
         "config": {"workload": "cfg2 decode FFN step, batch 1, through the Exec mirror: matvecPair "
                                "Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down [2560,9728] "
-                               "from f32 h[9728] (Q8_K quantization inside each GEMV launch)",
+                               "from f32 h[9728] (Q8_K quantization of x and h on the device, one quantize "
+                               "and one GEMV launch per slot)",
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": step_bytes,
                    "weight_copies_rotated": copies, "parallelism": "single GPU",
                    "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2)},

@@ -76,17 +76,17 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
 // MMQ's most VALU-heavy format) between 16 and 64.
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
-    case TT_Q4_K: case TT_IQ4_NL: return 16;
+    case TT_Q4_K: case TT_IQ4_NL: case TT_Q5_K: case TT_IQ4_XS: return 16;
     case TT_Q8_0: return 32;
     default: return 48;
   }
 }
 
-// Formats with an MMQ kernel; the others (Q5_K, Q3_K, Q2_K, IQ4_XS) multiply
-// many tokens with the GEMV, which shares each weight load across up to 8
-// tokens per pass.
+// Formats with an MMQ kernel; the others (Q3_K, Q2_K) multiply many tokens
+// with the GEMV, which shares each weight load across up to 8 tokens per pass.
 static bool mmq_supported(int ttype) {
-  return ttype == TT_Q8_0 || ttype == TT_IQ4_NL || ttype == TT_Q4_K || ttype == TT_Q6_K;
+  return ttype == TT_Q8_0 || ttype == TT_IQ4_NL || ttype == TT_Q4_K || ttype == TT_Q6_K || ttype == TT_Q5_K ||
+         ttype == TT_IQ4_XS;
 }
 
 // The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image

@@ -520,6 +520,10 @@ static hipError_t launch_gemv_type(const GemvArgs& g, int team, int nt, int nr, 
 // [17408, 5120]: 11.4 vs 12.9 us).  Otherwise Q6_K uses 64 lanes per row,
 // Q4_K and IQ4_NL reuse the activation over two or four rows per lane, and
 // Q8_0 over two rows when the matrix is large enough to fill the GPU anyway.
+// The further formats, swept at [17408, 5120] and [9728, 2560]: Q5_K as Q4_K;
+// Q3_K (its decode is VALU-heavy) two-wave teams of four rows on long rows
+// (20.5 vs 28.3 us) and 64 lanes per row otherwise; Q2_K and IQ4_XS two rows
+// per 20-lane team (10.4 vs 14.2 us, 14.2 vs 17.2 us).
 static void default_shape(const GemvArgs& g, int& team, int& nr) {
   const int upr = g.cols / 64;
   // long rows: teams of whole waves (k_gemv_mw), several rows per team
@@ -528,7 +532,7 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
     nr = g.rows >= 4096 ? 4 : 2;
     return;
   }
-  if ((g.ttype == TT_Q4_K || g.ttype == TT_Q5_K) && upr >= 64) {
+  if ((g.ttype == TT_Q4_K || g.ttype == TT_Q5_K || g.ttype == TT_Q3_K) && upr >= 64) {
     team = 128;
     nr = 4;
     return;
@@ -537,7 +541,9 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
     case TT_Q6_K: nr = g.rows >= 4096 ? 2 : 1; team = 64; break;
     case TT_Q4_K: case TT_Q5_K:
       nr = g.rows >= 16384 && upr <= 40 ? 4 : 2; team = upr <= 40 ? 40 : 20; break;
-    case TT_IQ4_NL: case TT_IQ4_XS: case TT_Q2_K: case TT_Q3_K: nr = 4; team = 20; break;
+    case TT_IQ4_NL: nr = 4; team = 20; break;
+    case TT_IQ4_XS: case TT_Q2_K: nr = 2; team = 20; break;
+    case TT_Q3_K: nr = 1; team = 64; break;
     default: nr = g.rows >= 4096 ? 2 : 1; team = 16; break;
   }
   if (team > upr) team = upr;

@@ -26,6 +26,9 @@
 //                 bsums, all partial sums < 2^24)  (kernels256.c:474-498)
 //   Q6_K          v_mfma_i32_32x32x16_i8 per 16-value group, times its int8
 //                 scale in integer arithmetic  (kernels256.c:720-738)
+//   Q5_K          as Q4_K on the 5-bit values  (kernels256.c:605-629)
+//   IQ4_XS        as Q4_K on the codebook values with the signed scale
+//                 ls - 32, no mins  (iq_kernels.c:967-1001)
 // and the float scaling follows per block / super-block.  For the 32-value
 // formats the accumulator input is the bit pattern of 1.5*2^23, so the MFMA
 // result read as a float is 1.5*2^23 + sumi exactly (|sumi| <= 2^19); one
@@ -73,6 +76,13 @@ struct alignas(16) MmqSmem<TT_Q4_K, BT, BR, false> {
   float wd[BR], wdmin[BR];
   uint32_t wsc[BR][2];  // eight 6-bit sub-block scales, one per byte
 };
+
+// Q5_K shares Q4_K's scales and mins; IQ4_XS uses the same per-sub-block
+// integer scale bytes (ls - 32, signed) and d, without mins.
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_Q5_K, BT, BR, false> : MmqSmem<TT_Q4_K, BT, BR, false> {};
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_IQ4_XS, BT, BR, false> : MmqSmem<TT_Q4_K, BT, BR, false> {};
 
 template <int BT, int BR>
 struct alignas(16) MmqSmem<TT_Q6_K, BT, BR, false> {
@@ -148,6 +158,49 @@ __device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename U
       sm.wd[row] = h2f(w.hdr[0]);
       sm.wdmin[row] = h2f(w.hdr[0] >> 16);
     }
+  } else if constexpr (TT == TT_Q5_K) {
+    // nibble + 16 * high bit (src/kernels/x86/kernels256.c:188-198)
+    const uint32_t m = 0x0F0F0F0Fu, s0 = 2u * (uint32_t)u4;
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo[i] = (w.q[i] & m) | (((w.qh[i] >> s0) & 0x01010101u) << 4);
+      hi[i] = ((w.q[i] >> 4) & m) | (((w.qh[i] >> (s0 + 1)) & 0x01010101u) << 4);
+    }
+    st16(dst, lo[0], lo[1], lo[2], lo[3]);
+    st16(dst + 16, lo[4], lo[5], lo[6], lo[7]);
+    st16(dst + 32, hi[0], hi[1], hi[2], hi[3]);
+    st16(dst + 48, hi[4], hi[5], hi[6], hi[7]);
+    if (u4 == 0) {
+      const uint32_t S0 = w.hdr[1], S1 = w.hdr[2], S2 = w.hdr[3];
+      const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
+      const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+      const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+      sm.wsc[row][0] = sc_lo;
+      sm.wsc[row][1] = sc_hi;
+      uint8_t* mp = (uint8_t*)&sm.wmn[row][0];
+      st16(mp, f16_pair(mn_lo & 255u), f16_pair((mn_lo >> 8) & 255u), f16_pair((mn_lo >> 16) & 255u),
+           f16_pair(mn_lo >> 24));
+      st16(mp + 16, f16_pair(mn_hi & 255u), f16_pair((mn_hi >> 8) & 255u), f16_pair((mn_hi >> 16) & 255u),
+           f16_pair(mn_hi >> 24));
+      sm.wd[row] = h2f(w.hdr[0]);
+      sm.wdmin[row] = h2f(w.hdr[0] >> 16);
+    }
+  } else if constexpr (TT == TT_IQ4_XS) {
+    // blocks 2u4 and 2u4+1: codebook values as for IQ4_NL, scale bytes ls - 32
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t* q = w.q + 4 * b;
+      st16(dst + 32 * b, iq4_lo(q[0]), iq4_lo(q[1]), iq4_lo(q[2]), iq4_lo(q[3]));
+      st16(dst + 32 * b + 16, iq4_hi(q[0]), iq4_hi(q[1]), iq4_hi(q[2]), iq4_hi(q[3]));
+    }
+    const uint32_t sh = w.h0 >> 16, sl = (w.sl >> (8 * u4)) & 0xFFu;
+    const int ls0 = (int)((sl & 15u) | (((sh >> (4 * u4)) & 3u) << 4));
+    const int ls1 = (int)((sl >> 4) | (((sh >> (4 * u4 + 2)) & 3u) << 4));
+    uint8_t* sp = (uint8_t*)&sm.wsc[row][0] + 2 * u4;
+    sp[0] = (uint8_t)(ls0 - 32);
+    sp[1] = (uint8_t)(ls1 - 32);
+    if (u4 == 0) sm.wd[row] = h2f(w.h0);
   } else {  // Q6_K: unit (h, lh) holds values 128h + 32q + 16lh + (0..15), q = 0..3
     const int h = (u4 >> 1) & 1, lh = u4 & 1;
     uint32_t v[4][4];
@@ -195,7 +248,7 @@ __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(dst + 16 * i, a.y[4 * i], a.y[4 * i + 1], a.y[4 * i + 2], a.y[4 * i + 3]);
-    if constexpr (TT == TT_Q4_K) {
+    if constexpr (TT == TT_Q4_K || TT == TT_Q5_K) {
       _Float16* bp = &sm.abs[tok][4 * u4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) bp[i] = (_Float16)(float)a.bs[i];
@@ -335,7 +388,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
           finish(s2, c0, dw0);
         }
       }
-    } else if constexpr (TT == TT_Q4_K) {
+    } else if constexpr (TT == TT_Q4_K || TT == TT_Q5_K || TT == TT_IQ4_XS) {
       i32x16 isum[NA][NB];
       const i32x16 zero = {};
 #pragma unroll
@@ -364,7 +417,8 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
       auto finish = [&](int s, const i32x16 (&c)[NA][NB]) {
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          const int sc = (int)((scw[b][s >> 2] >> (8 * (s & 3))) & 0xFFu);
+          const uint32_t sb = scw[b][s >> 2] >> (8 * (s & 3));
+          const int sc = TT == TT_IQ4_XS ? sext8(sb) : (int)(sb & 0xFFu);
 #pragma unroll
           for (int a = 0; a < NA; ++a)
 #pragma unroll
@@ -380,6 +434,25 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         if (s + 2 < 8) issue(s + 2, c0);
         finish(s + 1, c1);
       }
+      if constexpr (TT == TT_IQ4_XS) {
+        // no mins: acc += (d * dy) * isum  (iq_kernels.c:967-1001, one
+        // rounding of the exact super-block integer instead of one per block)
+        f32x4 dy[NA][4];
+        float d[NB];
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) dy[a][q] = *(const f32x4*)&sm.ady[tb0 + 32 * a + 8 * q + 4 * lh];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) d[b] = sm.wd[rb0 + 32 * b + li];
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              acc[a][b][e] = __builtin_fmaf(d[b] * dy[a][e >> 2][e & 3], (float)isum[a][b][e], acc[a][b][e]);
+      } else {
       // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
       f16x8 am[NA], bm[NB];
       f32x4 dy[NA][4];
@@ -408,6 +481,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
             acc[a][b][e] = __builtin_fmaf(dy[a][e >> 2][e & 3], inner, acc[a][b][e]);
           }
         }
+      }
     } else {  // Q6_K
       i32x16 isum[NA][NB];
       const i32x16 zero = {};
@@ -857,6 +931,8 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
     case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, s);
     case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, s);
     case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, s);
+    case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, s);
+    case TT_IQ4_XS: return launch_mmq_type<TT_IQ4_XS>(g, bt, br, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -40,6 +40,10 @@ CASES = [
     (po.TT_Q4_K, 64, 2560, 16),
     (po.TT_Q6_K, 100, 768, 40),
     (po.TT_Q6_K, 72, 2304, 129),
+    (po.TT_Q5_K, 150, 512, 65),
+    (po.TT_Q5_K, 64, 2560, 16),
+    (po.TT_IQ4_XS, 130, 768, 70),
+    (po.TT_IQ4_XS, 33, 2560, 20),
 ]
 IDS = [f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in CASES]
 
@@ -67,9 +71,9 @@ def unit_scale_weight(tt, rows, cols, seed):
     w = synth.make_weight(tt, rows, cols, seed=seed, tag=tt).copy()
     be, bb = po.GEOM[tt]
     blk = w.reshape(rows, cols // be, bb)
-    if tt in (po.TT_Q8_0, po.TT_IQ4_NL):
+    if tt in (po.TT_Q8_0, po.TT_IQ4_NL, po.TT_IQ4_XS):
         blk[:, :, 0:2] = F16_ONE
-    elif tt == po.TT_Q4_K:
+    elif tt in (po.TT_Q4_K, po.TT_Q5_K):
         blk[:, :, 0:2] = F16_ONE
         blk[:, :, 2:4] = F16_ONE
     else:
@@ -86,15 +90,24 @@ def unit_scale_act(cols, tokens, seed):
     return x
 
 
-@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K])
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS])
 def test_mmq_block_integers_exact(gpu, oracle, tt):
-    rows, cols, tokens = 96, 1024, 72
+    # IQ4_XS: the super-block sums carry the scales (up to 31), so half the
+    # width keeps every result below 2^24
+    rows, cols, tokens = 96, 512 if tt == po.TT_IQ4_XS else 1024, 72
     w = unit_scale_weight(tt, rows, cols, seed=5)
     x = unit_scale_act(cols, tokens, seed=5)
     act = oracle.quantize_act(tt, x)
     ints = oracle.block_ints(tt, w, act, cols).astype(np.int64)  # [tokens][rows][nints]
-    if tt == po.TT_Q4_K:
+    if tt in (po.TT_Q4_K, po.TT_Q5_K):
         want = ints[:, :, 0::2].sum(-1) - ints[:, :, 1::2].sum(-1)  # isum - summs
+    elif tt == po.TT_IQ4_XS:
+        # per-block integers times the block's ls - 32 (d = 1, dy = 1)
+        blk = w.reshape(rows, cols // 256, 136)
+        sh = blk[:, :, 2].astype(np.int64) | (blk[:, :, 3].astype(np.int64) << 8)
+        ls = np.stack([((blk[:, :, 4 + ib // 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+                       for ib in range(8)], axis=-1).reshape(rows, -1) - 32
+        want = (ints * ls[None, :, :]).sum(-1)
     else:
         want = ints.sum(-1)
     assert np.abs(want).max() < 2 ** 24  # every partial float sum is exact
@@ -300,10 +313,10 @@ def ctypes_byref(x):
     return ctypes.byref(x)
 
 
-@pytest.mark.parametrize("tt", po.EXTRA_TYPES)
+@pytest.mark.parametrize("tt", [po.TT_Q3_K, po.TT_Q2_K])
 def test_formats_without_mmq_decline_and_auto_uses_gemv(gpu, oracle, tt):
-    """Q5_K / Q3_K / Q2_K / IQ4_XS have no MMQ kernel: the explicit MMQ entry
-    points decline, the automatic path serves any token count with the GEMV."""
+    """Q3_K / Q2_K have no MMQ kernel: the explicit MMQ entry points decline,
+    the automatic path serves any token count with the GEMV."""
     rows, cols, tokens = 72, 1024, 70
     w = synth.make_weight(tt, rows, cols, seed=12, tag=tt)
     x = synth.make_act(cols, tokens, seed=12)
