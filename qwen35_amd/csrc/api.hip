@@ -69,16 +69,15 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
   return hipSuccess;
 }
 
-// Token count from which the MMQ tiles beat the weight-streaming GEMV (the
-// GEMV re-reads the weights once per 8 tokens; the MMQ once per 64 tokens),
-// from the GEMV-vs-MMQ sweep at the BASELINE shapes on MI355X: Q4_K and
-// IQ4_NL cross between 4 and 16 tokens, Q8_0 between 16 and 64, Q6_K (the
-// MMQ's most VALU-heavy format) between 16 and 64.
+// Token count from which the MMQ tiles beat the weight-streaming GEMV.
+// Measured on MI355X at the BASELINE shapes with split-K MMQ for small token
+// counts: Q4_K [17408, 5120] GEMV 23.6 us / MMQ 31.2 us at 4 tokens, 39.2 /
+// 30.3 us at 8; Q6_K [5120, 17408] 44.5 / 42.4 us at 8; Q8_0 [3584, 1024]
+// 5.3 / 7.9 us at 8, 8.1 / 8.0 us at 16.
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
-    case TT_Q4_K: case TT_IQ4_NL: case TT_Q5_K: case TT_IQ4_XS: return 16;
-    case TT_Q8_0: return 32;
-    default: return 48;
+    case TT_Q4_K: case TT_Q5_K: case TT_IQ4_XS: case TT_Q6_K: return 8;
+    default: return 16;
   }
 }
 
@@ -90,14 +89,13 @@ static bool mmq_supported(int ttype) {
 }
 
 // The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image
-// (built once per weight).  Measured on MI355X: the image beats the tile path
-// 1.6-1.8x for Q6_K (its per-16-value integer scaling dominates the tile
-// path) and beats the GEMV from 16 tokens ([5120, 17408]: 81 us vs 140 us);
-// for Q4_K the image's 3.9x larger weight bytes, re-read once per 64-token
-// tile, cost more than the scaling they save (202 us vs 183 us at 512
-// tokens), so Q4_K stays on the tile path.
+// (built once per weight).  Measured on MI355X, [5120, 17408]: image 32.6 us,
+// tile 42.4 us, GEMV 44.5 us at 8 tokens; 190 / 294 us (image / tile) at 512
+// -- the tile path's per-16-value integer scaling dominates it.  For Q4_K the
+// image's 3.9x larger weight bytes cost more than the scaling they save (43 /
+// 30 us at 16 tokens, 201 / 172 us at 512), so Q4_K stays on the tile path.
 bool mmq_image_preferred(const GemvArgs& g) {
-  return g.ttype == TT_Q6_K && g.tokens >= 16 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+  return g.ttype == TT_Q6_K && g.tokens >= 8 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
@@ -318,8 +316,7 @@ int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int 
   const bool multiwave = lanes_per_row == 128 || lanes_per_row == 256;
   if (lanes_per_row < 0 || (lanes_per_row > 64 && !multiwave) || n < 0 || n > 8 || (n & (n - 1)))
     return (int)hipErrorInvalidValue;
-  if (nr < 0 || nr > 4 || nr == 3 || (nr > 2 && n > 1) || (nr > 1 && n > 2))
-    return (int)hipErrorInvalidValue;
+  if (nr < 0 || nr > 4 || nr == 3) return (int)hipErrorInvalidValue;
   if (multiwave && (tokens != 1 || n > 1)) return (int)hipErrorInvalidValue;
   if (!fast_ok(g)) return QHIP_DECLINE;
   return (int)launch_gemv(g, lanes_per_row, n, nr, S(stream));

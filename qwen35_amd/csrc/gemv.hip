@@ -505,9 +505,9 @@ template <int TT>
 static hipError_t launch_gemv_type(const GemvArgs& g, int team, int nt, int nr, hipStream_t s) {
   switch (nt) {
     case 1: return launch_gemv_nr<TT, 1>(g, team, nr, s);
-    case 2: return launch_gemv_nr<TT, 2>(g, team, nr > 2 ? 2 : nr, s);
-    case 4: return launch_gemv_t<TT, 4, 1>(g, team, s);
-    case 8: return launch_gemv_t<TT, 8, 1>(g, team, s);
+    case 2: return launch_gemv_nr<TT, 2>(g, team, nr, s);
+    case 4: return launch_gemv_nr<TT, 4>(g, team, nr, s);
+    case 8: return launch_gemv_nr<TT, 8>(g, team, nr, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -561,6 +561,12 @@ hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t 
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   if (team <= 0 && nr <= 0 && g.tokens == 1) {
     default_shape(g, team, nr);
+  } else if (team <= 0 && nr <= 0 && nt <= 0) {
+    // several tokens: two rows per lane halve the activation loads per weight
+    // load (swept at T = 2..32 on [17408, 5120] Q4_K and [5120, 17408] Q6_K:
+    // 1.6-1.8x over one row per lane; Q8_0 is launch-bound either way)
+    nr = g.ttype == TT_Q8_0 ? 1 : 2;
+    team = g.ttype == TT_Q6_K ? 64 : g.ttype == TT_Q8_0 ? 32 : 16;
   } else {
     if (nr <= 0) nr = 1;
     if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);

@@ -261,17 +261,21 @@ __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int
 template <int TT, int BT, int BR>
 __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                               float* __restrict__ Y, int rows, int tokens, long row_bytes,
-                                              long act_bytes, int upr, int ntile_t) {
+                                              long act_bytes, int upr, int ntile_t, int ksplit, int cps) {
   constexpr bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL);
   constexpr int NA = BT / 64, NB = BR / 64;
   __shared__ MmqSmem<TT, BT, BR> sm;
 
   // Tile order: the hardware deals workgroups round-robin to the 8 XCDs;
   // give each XCD a contiguous run of row tiles (all their token tiles), so
-  // a weight chunk is fetched into one XCD's L2 and reused there.
+  // a weight chunk is fetched into one XCD's L2 and reused there.  With
+  // ksplit > 1 the K range is cut into ksplit slices of cps chunks; each
+  // workgroup adds its slice's partial tile into the zero-filled output.
   const int G = gridDim.x;
   int g = blockIdx.x;
   if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);
+  const int ks = g % ksplit;
+  g /= ksplit;
   const int r0 = (g / ntile_t) * BR, t0 = (g % ntile_t) * BT;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -304,7 +308,9 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
     arow[i] = XQ + (long)(t0 + tok < tokens ? t0 + tok : tokens - 1) * act_bytes;
   }
   const int u4 = tid & 3;
-  const int nchunks = (upr + 3) >> 2;
+  const int nchunks_all = (upr + 3) >> 2;
+  const int ch_begin = ks * cps;
+  const int nchunks = ch_begin + cps < nchunks_all ? ch_begin + cps : nchunks_all;
   auto load_chunk = [&](int ch) {
     if (4 * ch + u4 < upr) {
 #pragma unroll
@@ -313,8 +319,8 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
       for (int i = 0; i < UA; ++i) areg[i] = load_act<TT>(arow[i], 4 * ch + u4);
     }
   };
-  load_chunk(0);
-  for (int ch = 0; ch < nchunks; ++ch) {
+  if (ch_begin < nchunks) load_chunk(ch_begin);
+  for (int ch = ch_begin; ch < nchunks; ++ch) {
     const int nu = upr - 4 * ch < 4 ? upr - 4 * ch : 4;  // units in this chunk
     __syncthreads();  // the previous chunk's fragments have been read
     if (u4 < nu) {
@@ -553,9 +559,39 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
-        if (row < rows && tok < tokens) Y[(long)tok * rows + row] = acc[a][b][e];
+        if (row < rows && tok < tokens) {
+          float* y = Y + (long)tok * rows + row;
+          if (ksplit > 1) unsafeAtomicAdd(y, acc[a][b][e]);
+          else *y = acc[a][b][e];
+        }
       }
     }
+}
+
+// ---- split-K for small grids ----------------------------------------------------------
+// With fewer than two tile workgroups per CU the K loop of each tile is one
+// long dependent chain and the GPU idles.  For at most two token tiles (where
+// the output is small) K is cut into slices of at least `min_chunks` chunks,
+// aiming at about four workgroups per CU, and the slices' partial tiles are
+// added into the zero-filled output with float atomics (the summation order
+// of the slices is not fixed; every per-block integer stays exact).
+static int mmq_ksplit_for(const GemvArgs& g, int bt, int br, int nchunks, int min_chunks) {
+  const long ntt = (g.tokens + bt - 1) / bt;
+  const long tiles = (long)((g.rows + br - 1) / br) * ntt;
+  if (tiles >= 512 || ntt > 2 || nchunks < 2 * min_chunks) return 1;
+  const long want = (1024 + tiles - 1) / tiles;
+  const int cap = nchunks / min_chunks;
+  return (int)(want < cap ? want : cap);
+}
+
+__global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ y, long n) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) y[i] = 0.0f;
+}
+
+// a kernel, not a memset node, so the launch sequence stays capture-safe
+static void launch_fill_zero(float* y, long n, hipStream_t s) {
+  const long blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)blocks), dim3(256), 0, s, y, n);
 }
 
 // ---- MMQ on a prepared weight image (Q4_K, Q6_K) -----------------------------------------
@@ -663,7 +699,7 @@ struct alignas(16) ImgSmem {
 template <int TT, int BT, int BR>
 __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG, const uint8_t* __restrict__ XQ,
                                                   float* __restrict__ Y, int rows, int tokens, int nsb,
-                                                  long act_bytes, int ntile_t) {
+                                                  long act_bytes, int ntile_t, int ksplit, int cps) {
   constexpr int HB = img_hdr_bytes<TT>(), NH = HB / 16;
   constexpr int S = img_shift(TT);
   constexpr int NA = BT / 64, NB = BR / 64;
@@ -675,7 +711,10 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
   const int G = gridDim.x;
   int g = blockIdx.x;
   if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous row tiles, as k_mmq
+  const int ks = g % ksplit;  // K slice: super-blocks [ks*cps, ks*cps + cps), as k_mmq
+  g /= ksplit;
   const int r0 = (g / ntile_t) * BR, t0 = (g % ntile_t) * BT;
+  const int sb_begin = ks * cps, sb_end = sb_begin + cps < nsb ? sb_begin + cps : nsb;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int li = lane & 31, lh = lane >> 5;
   const int tb0 = (wv & 1) * (BT / 2), rb0 = (wv >> 1) * (BR / 2);
@@ -724,8 +763,8 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
 #pragma unroll
     for (int i = 0; i < UA; ++i) areg[i] = load_act<TT>(arow[i], 4 * sb + u4);
   };
-  load_chunk(0);
-  for (int sb = 0; sb < nsb; ++sb) {
+  if (sb_begin < sb_end) load_chunk(sb_begin);
+  for (int sb = sb_begin; sb < sb_end; ++sb) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < PW; ++i) {
@@ -753,7 +792,7 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
 #pragma unroll
     for (int i = 0; i < UA; ++i) emit_a<TT>(sm, areg[i], (tid + 256 * i) >> 2, u4);
     __syncthreads();
-    if (sb + 1 < nsb) load_chunk(sb + 1);  // in flight during this chunk's MFMAs
+    if (sb + 1 < sb_end) load_chunk(sb + 1);  // in flight during this chunk's MFMAs
 
     i32x16 chi[NA][NB], clo[NA][NB];
     const i32x16 zero = {};
@@ -834,7 +873,11 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
-        if (row < rows && tok < tokens) Y[(long)tok * rows + row] = acc[a][b][e];
+        if (row < rows && tok < tokens) {
+          float* y = Y + (long)tok * rows + row;
+          if (ksplit > 1) unsafeAtomicAdd(y, acc[a][b][e]);
+          else *y = acc[a][b][e];
+        }
       }
     }
 }
@@ -861,55 +904,71 @@ hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows
 }
 
 template <int TT, int BT, int BR>
-static hipError_t launch_mmq_img_t(const GemvArgs& g, hipStream_t s) {
+static hipError_t launch_mmq_img_t(const GemvArgs& g, int ksplit, hipStream_t s) {
+  const int nsb = g.cols / 256;
   const long ntr = (g.rows + BR - 1) / BR, ntt = (g.tokens + BT - 1) / BT;
-  const long G = ntr * ntt;
+  if (ksplit < 1) ksplit = 1;
+  if (ksplit > nsb) ksplit = nsb;
+  const int cps = (nsb + ksplit - 1) / ksplit;
+  ksplit = (nsb + cps - 1) / cps;
+  const long G = ntr * ntt * ksplit;
   if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  if (ksplit > 1) launch_fill_zero(g.out, (long)g.tokens * g.rows, s);
   hipLaunchKernelGGL((k_mmq_img<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
-                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.cols / 256, g.act_bytes, (int)ntt);
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, nsb, g.act_bytes, (int)ntt, ksplit, cps);
   return hipGetLastError();
 }
 
 template <int TT>
-static hipError_t launch_mmq_img_type(const GemvArgs& g, int bt, int br, hipStream_t s) {
-  if (bt == 64 && br == 64) return launch_mmq_img_t<TT, 64, 64>(g, s);
-  if (bt == 64 && br == 128) return launch_mmq_img_t<TT, 64, 128>(g, s);
-  if (bt == 128 && br == 64) return launch_mmq_img_t<TT, 128, 64>(g, s);
+static hipError_t launch_mmq_img_type(const GemvArgs& g, int bt, int br, int ksplit, hipStream_t s) {
+  if (bt == 64 && br == 64) return launch_mmq_img_t<TT, 64, 64>(g, ksplit, s);
+  if (bt == 64 && br == 128) return launch_mmq_img_t<TT, 64, 128>(g, ksplit, s);
+  if (bt == 128 && br == 64) return launch_mmq_img_t<TT, 128, 64>(g, ksplit, s);
   return hipErrorInvalidValue;
 }
 
 // g.w is the image
 hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  int ksplit = 1;
   if (bt <= 0 || br <= 0) {
     bt = 64;
     br = 64;
+    // small grids: split K over super-blocks (k_mmq's rule, one chunk = one super-block)
+    ksplit = mmq_ksplit_for(g, bt, br, g.cols / 256, 1);
   }
   switch (g.ttype) {
-    case TT_Q4_K: return launch_mmq_img_type<TT_Q4_K>(g, bt, br, s);
-    case TT_Q6_K: return launch_mmq_img_type<TT_Q6_K>(g, bt, br, s);
+    case TT_Q4_K: return launch_mmq_img_type<TT_Q4_K>(g, bt, br, ksplit, s);
+    case TT_Q6_K: return launch_mmq_img_type<TT_Q6_K>(g, bt, br, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 // ---- launchers --------------------------------------------------------------------------
 template <int TT, int BT, int BR>
-static hipError_t launch_mmq_t(const GemvArgs& g, hipStream_t s) {
+static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
   const int upr = g.cols / 64;
+  const int nchunks = (upr + 3) / 4;
   const long ntr = (g.rows + BR - 1) / BR, ntt = (g.tokens + BT - 1) / BT;
-  const long G = ntr * ntt;
+  if (ksplit < 1) ksplit = 1;
+  if (ksplit > nchunks) ksplit = nchunks;
+  const int cps = (nchunks + ksplit - 1) / ksplit;
+  ksplit = (nchunks + cps - 1) / cps;  // no empty slices
+  const long G = ntr * ntt * ksplit;
   if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  if (ksplit > 1) launch_fill_zero(g.out, (long)g.tokens * g.rows, s);
   hipLaunchKernelGGL((k_mmq<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
-                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt);
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
+                     ksplit, cps);
   return hipGetLastError();
 }
 
 template <int TT>
-static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, hipStream_t s) {
-  if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, s);
-  if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, s);
-  if (bt == 128 && br == 64) return launch_mmq_t<TT, 128, 64>(g, s);
-  if (bt == 128 && br == 128) return launch_mmq_t<TT, 128, 128>(g, s);
+static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit, hipStream_t s) {
+  if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, s);
+  if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, ksplit, s);
+  if (bt == 128 && br == 64) return launch_mmq_t<TT, 128, 64>(g, ksplit, s);
+  if (bt == 128 && br == 128) return launch_mmq_t<TT, 128, 128>(g, ksplit, s);
   return hipErrorInvalidValue;
 }
 
@@ -923,16 +982,21 @@ static void mmq_default_tile(const GemvArgs& /*g*/, int& bt, int& br) {
   br = 64;
 }
 
+
 hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
-  if (bt <= 0 || br <= 0) mmq_default_tile(g, bt, br);
+  int ksplit = 1;
+  if (bt <= 0 || br <= 0) {
+    mmq_default_tile(g, bt, br);
+    ksplit = mmq_ksplit_for(g, bt, br, (g.cols / 64 + 3) / 4, 2);
+  }
   switch (g.ttype) {
-    case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, s);
-    case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, s);
-    case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, s);
-    case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, s);
-    case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, s);
-    case TT_IQ4_XS: return launch_mmq_type<TT_IQ4_XS>(g, bt, br, s);
+    case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, ksplit, s);
+    case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, ksplit, s);
+    case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, ksplit, s);
+    case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, ksplit, s);
+    case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, ksplit, s);
+    case TT_IQ4_XS: return launch_mmq_type<TT_IQ4_XS>(g, bt, br, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }

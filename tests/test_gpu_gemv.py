@@ -130,7 +130,7 @@ def test_every_launch_shape(gpu, oracle, tt):
     want = oracle.matvec(tt, w, x)
     xq = ops.quantize_act(tt, xd)
     units = cols // 64
-    shapes = [(1, 1), (1, 2), (1, 4), (2, 1), (4, 1), (2, 2), (1, 8)]  # (rows/lane, tokens/pass)
+    shapes = [(1, 1), (1, 2), (1, 4), (2, 1), (4, 1), (2, 2), (1, 8), (2, 4), (4, 4), (2, 8), (4, 8)]  # (rows/lane, tokens/pass)
     for lpr in sorted({1, 2, 3, 4, 7, 13, 31, 40, 64, units - 1}):
         for nr, tpp in shapes:
             got = ops.gemv_tuned(tt, wd, xq, rows, cols, tokens, lpr, tpp, nr).cpu().numpy()
