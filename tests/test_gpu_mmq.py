@@ -16,7 +16,7 @@ from qwen35_amd import _lib, ops, synth
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-TILES = [(64, 64), (64, 128), (128, 64), (128, 128)]
+TILES = [(64, 64), (64, 128), (128, 64), (128, 128), (32, 128)]
 F16_ONE = np.array([0x00, 0x3C], np.uint8)  # 1.0 as little-endian binary16
 
 
