@@ -66,10 +66,24 @@ class Stream:
         return self.buf.data_ptr() + (i % self.copies) * self.stride
 
 
+WARM_SECONDS = 0.1  # GPU clocks ramp down while the host prepares inputs
+
+
 def time_loop(torch, fn, iters: int, warmup: int) -> float:
-    """Average seconds per call of fn(i), HIP events on the current stream."""
-    for i in range(warmup):
+    """Average seconds per call of fn(i), HIP events on the current stream.
+
+    Warm-up is at least `warmup` calls and at least WARM_SECONDS of back-to-back
+    calls: after host-side setup the GPU's clocks have dropped, and the first
+    ~10 ms of launches run measurably slower (a 357 MB GEMV read 81 us cold
+    against 72 us warm on MI355X)."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - t0 < WARM_SECONDS:
         fn(i)
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
+    warmup = i
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
