@@ -5,7 +5,9 @@ Headline workload: one decode FFN step at batch 1
 through the Exec mirror (the slots the engine calls): matvecPair over the Q4_K
 gate/up weights [9728,2560] x2 (adjacent in the weight arena: one launch) from
 f32 x[2560], then matvec over the Q6_K down weight [2560,9728] from f32
-h[9728]; each launch quantizes its activation (Q8_K) inside the GEMV.
+h[9728].  The mirror quantizes x (Q8_K) inside the gate/up GEMV (one launch)
+and h in a quantize launch before the down GEMV (rows this long do better with
+the separate launch).
 `value` = algorithmic bytes of the step's GEMVs (packed weights + f32 x + f32 y
 per GEMV) / step time, inputs resident in HBM.  Weight sets rotate over enough
 device copies (> 512 MB per pass) that every step streams from HBM, not from
@@ -116,7 +118,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "step", "step_unfused", "mmq_cfg5_q4k",
+    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "fused_gate_up", "step", "step_unfused",
+                                                 "mmq_cfg5_q4k",
                                                  "mmq_cfg4"],
                     help="run only this kernel (for rocprofv3) and exit")
     ap.add_argument("--copy-calib", action="store_true")
@@ -152,8 +155,8 @@ def main() -> int:
     # ---- headline workload: cfg2 FFN step through the Exec mirror --------------
     # matvecPair(gate, up, x) + matvec(down, h) (src/backend.zig:153-176 slots):
     # the mirror quantizes x and h on the device and runs one GEMV per slot
-    # (adjacent gate/up weights are one launch); at these widths it picks the
-    # separate quantize launch over the fused quantize+GEMV.
+    # (adjacent gate/up weights are one launch): x inside the gate/up GEMV
+    # (width 2560), h in its own quantize launch (width 9728).
     import ctypes
     H, F = 2560, 9728
     t0 = time.time()
@@ -214,6 +217,16 @@ def main() -> int:
                                          TQ6, stream)
         assert rc == 0, rc
 
+    # the launches the mirror issues in the step: quantize + GEMV in one launch
+    # for gate/up (width 2560), a quantize launch and a GEMV for down (9728)
+    def fused_gate_up(i):
+        rc = lib.qhip_launch_quantize_mul_mat_vec(lins[i % copies][3].dev, xd.data_ptr(), None, y_gu.data_ptr(),
+                                                  2 * F, H, TQ4, stream)
+        assert rc == 0, rc
+
+    def quantize_h(i):
+        assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
+
     def step_unfused(i):
         lg = lins[i % copies][3]
         assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
@@ -222,10 +235,10 @@ def main() -> int:
         assert lib.qhip_launch_mul_mat_vec(lg.dev + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1, TQ6,
                                            stream) == 0
 
-    if args.profile_kernel in ("down", "gate_up", "step", "step_unfused"):
+    if args.profile_kernel in ("down", "gate_up", "fused_gate_up", "step", "step_unfused"):
         for i in range(3):
             step(i)
-        fn = {"down": gemv_down, "gate_up": gemv_gate_up, "step": step,
+        fn = {"down": gemv_down, "gate_up": gemv_gate_up, "fused_gate_up": fused_gate_up, "step": step,
               "step_unfused": step_unfused}[args.profile_kernel]
         for i in range(args.steps):
             fn(i)
@@ -243,18 +256,26 @@ def main() -> int:
     sec_unfused = time_loop(torch, step_unfused, args.steps, args.warmup)
     log(f"cfg2 step, separate quantize launches: {sec_unfused * 1e6:.2f} us")
 
-    # each GEMV kernel of the step alone, back to back (the roofline's kernel)
+    # each launch of the step alone, back to back; the roofline's kernel is the
+    # longest of them.  The GEMVs on pre-quantized activations are reported too.
     n_k = max(200, args.steps)
     gu_alg = gemv_bytes(2 * F, H, gu_bytes)
     d_alg = gemv_bytes(H, F, d_bytes)
-    gu_sec = time_loop(torch, gemv_gate_up, n_k, 20)
+    q_alg = 4 * F + lib.qhip_act_row_bytes(TQ6, F)
+    fgu_sec = time_loop(torch, fused_gate_up, n_k, 20)
     d_sec = time_loop(torch, gemv_down, n_k, 20)
+    qh_sec = time_loop(torch, quantize_h, n_k, 20)
+    gu_sec = time_loop(torch, gemv_gate_up, n_k, 20)
+
+    def entry(alg, sec):
+        return {"alg_bytes": alg, "avg_us": sec * 1e6, "gbs": alg / sec / 1e9}
+
     kernels = {
-        "gemv_q4_k_gate_up_19456x2560": {"alg_bytes": gu_alg, "avg_us": gu_sec * 1e6,
-                                         "gbs": gu_alg / gu_sec / 1e9},
-        "gemv_q6_k_down_2560x9728": {"alg_bytes": d_alg, "avg_us": d_sec * 1e6,
-                                     "gbs": d_alg / d_sec / 1e9},
+        "fused_q4_k_gate_up_19456x2560": entry(gu_alg, fgu_sec),
+        "gemv_q6_k_down_2560x9728": entry(d_alg, d_sec),
+        "quantize_q8_k_9728": entry(q_alg, qh_sec),
     }
+    off_step = {"gemv_q4_k_gate_up_19456x2560_prequantized": entry(gu_alg, gu_sec)}
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
     achieved = kernels[dom]["gbs"]
     traffic = None
@@ -268,7 +289,7 @@ def main() -> int:
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
                 "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
                 "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
-    latency = {"gate_up_single_launch_us": round(single_latency(torch, gemv_gate_up) * 1e6, 2),
+    latency = {"gate_up_single_launch_us": round(single_latency(torch, fused_gate_up) * 1e6, 2),
                "down_single_launch_us": round(single_latency(torch, gemv_down) * 1e6, 2),
                "step_single_us": round(single_latency(torch, step) * 1e6, 2)}
 
@@ -324,14 +345,15 @@ def main() -> int:
         "data": "synthetic (SplitMix64 seed 0, BASELINE.json config rules)",
         "config": {"workload": "cfg2 decode FFN step, batch 1, through the Exec mirror: matvecPair "
                                "Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down [2560,9728] "
-                               "from f32 h[9728] (Q8_K quantization of x and h on the device, one quantize "
-                               "and one GEMV launch per slot)",
+                               "from f32 h[9728] (Q8_K quantization on the device: of x inside the gate/up "
+                               "GEMV launch, of h in a quantize launch before the down GEMV)",
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": step_bytes,
                    "weight_copies_rotated": copies, "parallelism": "single GPU",
                    "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2)},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "kernels_off_step": off_step,
         "latency": latency,
         "configs": extra,
         "mmq": mmq,

@@ -121,11 +121,27 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   if (be->memo_on) (hit ? be->memo_hits : be->memo_misses)++;
   if (!hit && k == 1) {
     // one launch, the activation quantized inside the GEMV, where that is
-    // faster than a separate quantize launch (narrow matrices)
+    // faster than a separate quantize launch (widths up to 4096); with the
+    // memo on, the launch also leaves the quantized rows in the scratch
     const GemvArgs g1{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
     if (gemv_fused_preferred(g1)) {
-      const int rc = qhip_launch_quantize_mul_mat_vec(wdev, x, nullptr, out, rows, cols, ttype, be->stream);
-      if (rc != QHIP_DECLINE) return report("matvec", (hipError_t)rc);
+      void* xq_out = nullptr;
+      if (be->memo_on) {
+        const hipError_t ea = ensure_act(be, act_bytes_for(cols, 1));
+        if (ea != hipSuccess) return report("activation scratch", ea);
+        memo_clear(be);
+        xq_out = be->act;
+      }
+      const int rc = qhip_launch_quantize_mul_mat_vec(wdev, x, xq_out, out, rows, cols, ttype, be->stream);
+      if (rc != QHIP_DECLINE) {
+        if (rc == 0 && xq_out) {
+          be->memo_src = x;
+          be->memo_cols = cols;
+          be->memo_k = 1;
+          be->memo_fam = fam;
+        }
+        return report("matvec", (hipError_t)rc);
+      }
     }
   }
   hipError_t e = hipSuccess;

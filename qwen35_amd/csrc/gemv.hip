@@ -158,8 +158,8 @@ __host__ __device__ constexpr long fused_lds_bytes(int ttype, int cols) {
              : fused_lds_qs(cols) + (((long)cols / 256 * 4 + 15) & ~15L) + (long)cols / 16 * 2;
 }
 
-template <int TT, int NR>
-__global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, const float* __restrict__ X,
+template <int TT, int NR, int WGS>
+__global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                  uint8_t* __restrict__ XQ, float* __restrict__ Y, int rows,
                                                  int cols, long row_bytes, int upr, int team) {
   using U = Unit<TT>;
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int tpw = 64 / team;
   const int r = lane / team, j = lane - r * team;
-  const long row0 = (((long)blockIdx.x * 4 + wv) * tpw + r) * NR;
+  const long row0 = (((long)blockIdx.x * (WGS / 64) + wv) * tpw + r) * NR;
   const bool active = r < tpw && row0 < rows;
   const uint8_t* wrow[NR];
 #pragma unroll
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
   const bool out_q = XQ != nullptr && blockIdx.x == 0;
   if constexpr (K32) {
     // one value per thread, a 32-lane group per block
-    for (int b0 = 0; b0 < nblk; b0 += 8) {
+    for (int b0 = 0; b0 < nblk; b0 += WGS / 32) {
       const int b = b0 + (threadIdx.x >> 5), i = threadIdx.x & 31;
       const bool ok = b < nblk;
       uint32_t hb;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) void k_gemv_q(const uint8_t* __restrict__ W, c
     }
   } else {
     // a wave per 256-value block, four values per lane
-    for (int b0 = 0; b0 < nblk; b0 += 4) {
+    for (int b0 = 0; b0 < nblk; b0 += WGS / 64) {
       const int b = b0 + wv;
       const bool ok = b < nblk;
       float v[4];
@@ -610,61 +610,96 @@ static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipSt
   return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_mw_type<decltype(tt)::value>(g, nr, wv, s); });
 }
 
-template <int TT, int NR>
+template <int TT, int NR, int WGS>
 static hipError_t launch_gemv_q_t(const GemvArgs& g, const float* x, void* xq_out, int team, hipStream_t s) {
   const int upr = g.cols / 64;
-  if (team > upr) team = upr;
   if (team > 64) team = 64;
   const int tpw = 64 / team;
   const long teams = (g.rows + NR - 1) / NR;
   const long waves = (teams + tpw - 1) / tpw;
-  const unsigned grid = (unsigned)((waves + 3) / 4);
+  const unsigned grid = (unsigned)((waves + WGS / 64 - 1) / (WGS / 64));
   const size_t lds = (size_t)fused_lds_bytes(TT, g.cols);
-  hipLaunchKernelGGL((k_gemv_q<TT, NR>), dim3(grid), dim3(256), lds, s, (const uint8_t*)g.w, x,
+  hipLaunchKernelGGL((k_gemv_q<TT, NR, WGS>), dim3(grid), dim3(WGS), lds, s, (const uint8_t*)g.w, x,
                      (uint8_t*)xq_out, g.out, g.rows, g.cols, g.row_bytes, upr, team);
   return hipGetLastError();
 }
 
 template <int TT>
-static hipError_t launch_gemv_q_type(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
+static hipError_t launch_gemv_q_type(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int wgs,
                                      hipStream_t s) {
+  if (wgs == 1024 && nr == 1) return launch_gemv_q_t<TT, 1, 1024>(g, x, xq_out, team, s);
+  if (wgs != 256) return hipErrorInvalidValue;
   switch (nr) {
-    case 1: return launch_gemv_q_t<TT, 1>(g, x, xq_out, team, s);
-    case 2: return launch_gemv_q_t<TT, 2>(g, x, xq_out, team, s);
-    case 4: return launch_gemv_q_t<TT, 4>(g, x, xq_out, team, s);
+    case 1: return launch_gemv_q_t<TT, 1, 256>(g, x, xq_out, team, s);
+    case 2: return launch_gemv_q_t<TT, 2, 256>(g, x, xq_out, team, s);
+    case 4: return launch_gemv_q_t<TT, 4, 256>(g, x, xq_out, team, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 bool gemv_fused_fits(int ttype, int cols) { return fused_lds_bytes(ttype, cols) <= kFusedMaxLds; }
 
-// Every workgroup of the fused kernel quantizes the whole activation, so its
-// extra work grows with workgroups x cols.  Measured on MI355X against the
-// separate quantize + GEMV launches: the fused launch wins below about 4e5
-// quantized values in total (Q8_0 [1024..6144, 1024]: 5.5-6.2 us vs 7.2-7.8
-// us), ties around 7e5 (Q4_K [4096, 4096]) and loses above (IQ4_NL
-// [248320, 2560]: 148 us vs 76 us).
+// Default fused shape: one row per lane and 1024-thread workgroups (16 waves
+// quantize the activation together, once per workgroup).  Lanes per row: the
+// candidate with the fewest wave-steps (waves x units per lane) among those
+// whose grid has at least 192 workgroups (three quarters of the CUs), ties to
+// the larger team; if none fills the GPU, the largest grid.  Swept on MI355X
+// over Q8_0 [6144, 1024], Q4_K [9728 / 19456, 2560] and [12288, 4096], Q6_K
+// [2560, 2560] and IQ4_NL [32768, 2560]: the best shape on five, within 9% on
+// the sixth (Q4_K [19456, 2560]: 20 lanes, 8.8 us; 12 lanes 10.0 us).
+static void fused_default_shape(const GemvArgs& g, int& team, int& nr, int& wgs) {
+  static const int kCand[] = {8, 10, 16, 20, 32, 40, 64};
+  const long upr = g.cols / 64;
+  int best = -1;
+  long best_w = 0, best_grid = 0;
+  bool best_full = false;
+  for (int t : kCand) {
+    const long tpw = 64 / t;
+    const long waves = (g.rows + tpw - 1) / tpw;
+    const long grid = (waves + 15) / 16;
+    const long w = waves * ((upr + t - 1) / t);
+    const bool full = grid >= 192;
+    bool take;
+    if (best < 0) take = true;
+    else if (full != best_full) take = full;
+    else if (full) take = w <= best_w;          // ties: the later (larger) team
+    else take = grid >= best_grid;
+    if (take) {
+      best = t;
+      best_w = w;
+      best_grid = grid;
+      best_full = full;
+    }
+  }
+  team = best;
+  nr = 1;
+  wgs = 1024;
+}
+
+// Fused quantize + GEMV against separate quantize and GEMV launches, measured
+// on MI355X with the default shapes: the fused launch wins for rows up to
+// 32768 at widths up to 4096 (Q4_K [19456, 2560] 9.4 vs 10.7 us, Q8_0 [6144,
+// 1024] 5.0 vs 6.2 us) and loses on long rows, where every workgroup would
+// quantize a long activation (Q6_K [2560, 9728] 12.4 vs 10.4 us, Q4_K
+// [17408, 5120] 14.9 vs 14.2 us).
 bool gemv_fused_preferred(const GemvArgs& g) {
-  if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols)) return false;
-  int team = 0, nr = 0;
-  default_shape(g, team, nr);
-  if (team > 64) return false;  // long rows: the prologue would dominate
-  const long tpw = 64 / team;
-  const long waves = ((g.rows + nr - 1) / nr + tpw - 1) / tpw;
-  return (waves + 3) / 4 * (long)g.cols <= 400000L;
+  return g.tokens == 1 && gemv_fused_fits(g.ttype, g.cols) && g.cols <= 4096 && g.rows <= 32768;
 }
 
 hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
                              hipStream_t s) {
   if (g.rows <= 0) return hipSuccess;
   if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols)) return hipErrorInvalidValue;
+  int wgs = 256;
   if (team <= 0 && nr <= 0) {
-    default_shape(g, team, nr);
+    fused_default_shape(g, team, nr, wgs);
   } else {
     if (nr <= 0) nr = 1;
     if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);
   }
-  return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_q_type<decltype(tt)::value>(g, x, xq_out, team, nr, s); });
+  return dispatch_type(g.ttype, [&](auto tt) {
+    return launch_gemv_q_type<decltype(tt)::value>(g, x, xq_out, team, nr, wgs, s);
+  });
 }
 
 hipError_t launch_gemv_generic(const GemvArgs& g, hipStream_t s) {

@@ -2,9 +2,12 @@
 :3914-3944), the decode-step hints (backend.zig:470-491) and a decode step
 captured in a HIP graph by the caller and replayed.
 
-Shapes are chosen wide enough that the mirror quantizes into its scratch
-(the fused quantize+GEMV launch is only used for narrow matrices, and it
-leaves the scratch alone)."""
+For widths up to 4096 the mirror quantizes inside the GEMV (one fused
+launch); with the memo on, that launch also leaves the quantized rows in the
+scratch, so a memo hit then runs the plain GEMV on them.  The two kernels fold
+the block terms in different orders, so results are compared to 1e-6 relative
+L2 where a hit replaces a fused launch, and bit for bit where the same kernel
+runs."""
 import numpy as np
 import pytest
 import torch
@@ -53,8 +56,10 @@ def test_memo_hits_same_family_and_matches(gpu, oracle, weights):
         be.matvec(o6, l6, xd)   # Q6_K takes the same Q8_K rows: hit
         be.sync()
         assert be.act_stats() == (1, 1)
-        # the memo only skips work: results are identical to the memo-off ones
-        assert torch.equal(ou, ou0) and torch.equal(o6, o60)
+        # the memo only skips work: the miss ran the same fused launch as the
+        # memo-off call; the hit ran the plain GEMV on the same quantized rows
+        assert torch.equal(ou, ou0)
+        assert rel_l2(o6.cpu().numpy(), o60.cpu().numpy()) < 1e-6
         assert rel_l2(ou.cpu().numpy(), want_u) < TOL
         assert rel_l2(o6.cpu().numpy(), want_6) < TOL
         # another pointer, or another width, or a new step: miss
@@ -84,7 +89,7 @@ def test_memo_invalidate_after_write(gpu, oracle, weights):
         be.act_invalidate()
         be.matvec(o_c, l6, xd)
         be.sync()
-        assert torch.equal(o_b, o_a)
+        assert rel_l2(o_b.cpu().numpy(), o_a.cpu().numpy()) < 1e-6
         x_new = (x[0] * np.float32(-0.5))[None, :]
         assert rel_l2(o_c.cpu().numpy(), oracle.matvec(po.TT_Q6_K, q6, x_new)[0]) < TOL
         assert be.act_stats() == (1, 2)
