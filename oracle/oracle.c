@@ -160,6 +160,30 @@ int32_t orc_blk_iq4_nl(const uint8_t *w, const uint8_t *a) {
     return s;
 }
 
+/* kernels32.c:297-316: Q4_0 block (f16 d @0, 16 nibble bytes @2); low
+ * nibble of byte j minus 8 pairs with a[j], high nibble minus 8 with a[j+16]. */
+int32_t orc_blk_q4_0(const uint8_t *w, const uint8_t *a) {
+    int32_t s = 0;
+    for (int j = 0; j < 16; ++j) {
+        s += ((int32_t)(w[2 + j] & 15) - 8) * (int32_t)(int8_t)a[2 + j];
+        s += ((int32_t)(w[2 + j] >> 4) - 8) * (int32_t)(int8_t)a[18 + j];
+    }
+    return s;
+}
+
+/* kernels32.c:318-340: Q4_1 block (f16 d @0, f16 m @2, 16 nibble bytes @4);
+ * unsigned nibbles against a, and the sum of the block's 32 activations. */
+void orc_blk_q4_1(const uint8_t *w, const uint8_t *a, int32_t *sumi, int32_t *sumy) {
+    int32_t s = 0, y = 0;
+    for (int j = 0; j < 16; ++j) {
+        s += (int32_t)(w[4 + j] & 15) * (int32_t)(int8_t)a[2 + j];
+        s += (int32_t)(w[4 + j] >> 4) * (int32_t)(int8_t)a[18 + j];
+    }
+    for (int j = 0; j < 32; ++j) y += (int32_t)(int8_t)a[2 + j];
+    *sumi = s;
+    *sumy = y;
+}
+
 /* 6-bit scale / min of sub-block sb (0..7) from the 12 packed bytes; the
  * ggml get_scale_min_k4 rule, equal to kernels256.c:105-125 (sm[sb] / sm[8+sb]). */
 static void q4k_scale_min(const uint8_t *s12, int sb, int *sc, int *mn) {
@@ -340,6 +364,8 @@ int orc_geom(int ttype, int *be, int *bb) {
     case ORC_TT_Q3_K: *be = 256; *bb = 110; return 1;
     case ORC_TT_Q5_K: *be = 256; *bb = 176; return 1;
     case ORC_TT_IQ4_XS: *be = 256; *bb = 136; return 1;
+    case ORC_TT_Q4_0: *be = 32; *bb = 18; return 1;
+    case ORC_TT_Q4_1: *be = 32; *bb = 20; return 1;
     default: return 0;
     }
 }
@@ -382,6 +408,30 @@ static float dot_iq4_nl(int n, const void *vw, const void *va) {
     for (int b = 0; b < n / 32; ++b, w += 18, a += 34) {
         float dx = orc_f16_to_f32(ld16(w)), dy = orc_f16_to_f32(ld16(a));
         sumf += dx * dy * (float)orc_blk_iq4_nl(w, a);
+    }
+    return sumf;
+}
+
+/* kernels32.c:297-316, one sequential per-block fold (both tiers) */
+static float dot_q4_0(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 32; ++b, w += 18, a += 34) {
+        float dx = orc_f16_to_f32(ld16(w)), dy = orc_f16_to_f32(ld16(a));
+        sumf += dx * dy * (float)orc_blk_q4_0(w, a);
+    }
+    return sumf;
+}
+
+/* kernels32.c:318-340: sumf += dx*dy*sumi + mx*dy*sumy per block */
+static float dot_q4_1(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 32; ++b, w += 20, a += 34) {
+        float dx = orc_f16_to_f32(ld16(w)), mx = orc_f16_to_f32(ld16(w + 2)), dy = orc_f16_to_f32(ld16(a));
+        int32_t sumi, sumy;
+        orc_blk_q4_1(w, a, &sumi, &sumy);
+        sumf += dx * dy * (float)sumi + mx * dy * (float)sumy;
     }
     return sumf;
 }
@@ -482,6 +532,8 @@ orc_dot_fn orc_dot_fn_for(int ttype) {
     case ORC_TT_Q3_K: return dot_q3_k;
     case ORC_TT_Q5_K: return dot_q5_k;
     case ORC_TT_IQ4_XS: return dot_iq4_xs;
+    case ORC_TT_Q4_0: return dot_q4_0;
+    case ORC_TT_Q4_1: return dot_q4_1;
     default: return 0;
     }
 }
@@ -497,10 +549,11 @@ float orc_dot(int ttype, int n, const void *w, const void *a) {
 }
 
 /* integers per weight block in orc_row_block_ints: (isum, summs) for the
- * K-quants with mins, one per 32-value block for IQ4_XS, else one */
+ * K-quants with mins, (sumi, sumy) for Q4_1, one per 32-value block for
+ * IQ4_XS, else one */
 int orc_block_nints(int ttype) {
     switch (ttype) {
-    case ORC_TT_Q4_K: case ORC_TT_Q5_K: case ORC_TT_Q2_K: return 2;
+    case ORC_TT_Q4_K: case ORC_TT_Q5_K: case ORC_TT_Q2_K: case ORC_TT_Q4_1: return 2;
     case ORC_TT_IQ4_XS: return 8;
     default: return 1;
     }
@@ -515,6 +568,8 @@ int orc_row_block_ints(int ttype, int n, const void *vw, const void *va, int32_t
         switch (ttype) {
         case ORC_TT_Q8_0: out[b] = orc_blk_q8_0(w + 34 * b, a + 34 * b); break;
         case ORC_TT_IQ4_NL: out[b] = orc_blk_iq4_nl(w + 18 * b, a + 34 * b); break;
+        case ORC_TT_Q4_0: out[b] = orc_blk_q4_0(w + 18 * b, a + 34 * b); break;
+        case ORC_TT_Q4_1: orc_blk_q4_1(w + 20 * b, a + 34 * b, &out[2 * b], &out[2 * b + 1]); break;
         case ORC_TT_Q4_K: orc_blk_q4_k(w + 144 * b, a + 292 * b, &out[2 * b], &out[2 * b + 1]); break;
         case ORC_TT_Q6_K: out[b] = orc_blk_q6_k(w + 210 * b, a + 292 * b); break;
         case ORC_TT_Q5_K: orc_blk_q5_k(w + 176 * b, a + 292 * b, &out[2 * b], &out[2 * b + 1]); break;
@@ -595,12 +650,27 @@ int orc_matvec_batch(int ttype, int rows, int cols, int k, const void *w,
 
 /* ---- dequantization (fixture semantics) --------------------------------- */
 
-/* quant_dequant.zig:1388-1402 (Q8_0), :347-360 (IQ4_NL), :54-77 (Q4_K),
+/* quant_dequant.zig:1388-1402 (Q8_0), :347-360 (IQ4_NL), :78-103 (Q4_0,
+ * Q4_1), :54-77 (Q4_K),
  * :222-251 (Q6_K), :188-220 (Q5_K), :252-322 (Q3_K), :892-919 (Q2_K),
  * :324-345 (IQ4_XS). */
 int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
     const uint8_t *w = vw;
     if (orc_row_bytes(ttype, cols) < 0) return -1;
+    if (ttype == ORC_TT_Q4_0 || ttype == ORC_TT_Q4_1) {
+        const int bb = ttype == ORC_TT_Q4_0 ? 18 : 20, qo = ttype == ORC_TT_Q4_0 ? 2 : 4;
+        for (int b = 0; b < cols / 32; ++b) {
+            const uint8_t *blk = w + bb * b;
+            float d = orc_f16_to_f32_k256(ld16(blk));
+            float m = ttype == ORC_TT_Q4_1 ? orc_f16_to_f32_k256(ld16(blk + 2)) : 0.0f;
+            for (int j = 0; j < 32; ++j) {
+                int q = j < 16 ? (blk[qo + j] & 15) : (blk[qo + j - 16] >> 4);
+                /* Q4_0: (q - 8) * d; Q4_1: q * d + m (two roundings) */
+                out[32 * b + j] = ttype == ORC_TT_Q4_0 ? ((float)q - 8.0f) * d : (float)q * d + m;
+            }
+        }
+        return 0;
+    }
     if (ttype == ORC_TT_Q8_0 || ttype == ORC_TT_IQ4_NL) {
         int bb = ttype == ORC_TT_Q8_0 ? 34 : 18;
         for (int b = 0; b < cols / 32; ++b) {

@@ -12,10 +12,11 @@
  *   quantize_q8_K          src/kernels/x86/kernels256.c:865-896
  *   Q8_0 x Q8_0            src/kernels/x86/kernels32.c:447-464, kernels512.c:53-81
  *   IQ4_NL x Q8_0          src/kernels/x86/kernels32.c:342-361 (+ iq_tables.zig:429-432)
+ *   Q4_0 / Q4_1 x Q8_0     src/kernels/x86/kernels32.c:297-340
  *   Q4_K x Q8_K            src/kernels/x86/kernels256.c:105-125, :179-186, :474-498
  *   Q6_K x Q8_K            src/kernels/x86/kernels256.c:200-212, :720-738
  *   matvec / batch driver  src/backend_cpu.zig:167-289, :328-446; src/pool.zig:300-336, :468-550
- *   dequant (fixtures)     src/quant_dequant.zig:54-77, :222-251, :347-360, :1388-1402
+ *   dequant (fixtures)     src/quant_dequant.zig:54-77, :78-103, :222-251, :347-360, :1388-1402
  *
  * Float results follow the scalar / AVX-512-VNNI tier order (one sequential
  * per-block fold).  The reference's AVX2 tier folds Q4_K/Q6_K with 8-lane
@@ -40,6 +41,8 @@ extern "C" {
 #define ORC_TT_Q3_K  11
 #define ORC_TT_Q5_K  13
 #define ORC_TT_IQ4_XS 23
+#define ORC_TT_Q4_0   2
+#define ORC_TT_Q4_1   3
 
 float    orc_f16_to_f32(uint16_t h);        /* kernels32.c:45-66 (+0 for -0)  */
 float    orc_f16_to_f32_k256(uint16_t h);   /* kernels256.c:51-78 (keeps -0) */
@@ -57,6 +60,8 @@ void    orc_blk_q5_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t 
 void    orc_blk_q2_k(const uint8_t *w, const uint8_t *a, int32_t *isum, int32_t *summs);
 int32_t orc_blk_q3_k(const uint8_t *w, const uint8_t *a);
 int32_t orc_blk_iq4_xs(const uint8_t *w, const uint8_t *a, int ib);
+int32_t orc_blk_q4_0(const uint8_t *w, const uint8_t *a);
+void    orc_blk_q4_1(const uint8_t *w, const uint8_t *a, int32_t *sumi, int32_t *sumy);
 
 /* Geometry: returns 1 and fills the outputs for a supported type, else 0. */
 int orc_geom(int ttype, int *block_elems, int *block_bytes);
@@ -70,8 +75,9 @@ long orc_row_bytes(int ttype, int cols);
 /* One weight row against one quantized activation row (n = cols). */
 float orc_dot(int ttype, int n, const void *w, const void *a);
 
-/* Per-block integers of one row.  Q8_0 / IQ4_NL / Q6_K write n/block ints;
- * Q4_K writes 2 per super-block: isum then summs.  Returns ints written, or -1. */
+/* Per-block integers of one row.  Q8_0 / IQ4_NL / Q4_0 / Q6_K write n/block ints;
+ * Q4_K writes 2 per super-block: isum then summs; Q4_1 2 per block: sumi then
+ * sumy (the activation's block sum).  Returns ints written, or -1. */
 int orc_block_nints(int ttype);
 int orc_row_block_ints(int ttype, int n, const void *w, const void *a, int32_t *out);
 

@@ -18,17 +18,21 @@ REF_SO = HERE / "_ref" / "libqref.so"
 
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20
 TT_Q2_K, TT_Q3_K, TT_Q5_K, TT_IQ4_XS = 10, 11, 13, 23
+TT_Q4_0, TT_Q4_1 = 2, 3
 GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210),
-        TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136)}
+        TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136),
+        TT_Q4_0: (32, 18), TT_Q4_1: (32, 20)}
 NAMES = {TT_Q8_0: "Q8_0", TT_Q4_K: "Q4_K", TT_Q6_K: "Q6_K", TT_IQ4_NL: "IQ4_NL",
-         TT_Q2_K: "Q2_K", TT_Q3_K: "Q3_K", TT_Q5_K: "Q5_K", TT_IQ4_XS: "IQ4_XS"}
-# the formats of the benchmark configurations, and the further K-quant family
+         TT_Q2_K: "Q2_K", TT_Q3_K: "Q3_K", TT_Q5_K: "Q5_K", TT_IQ4_XS: "IQ4_XS",
+         TT_Q4_0: "Q4_0", TT_Q4_1: "Q4_1"}
+# the formats of the benchmark configurations, the further K-quant family, and
+# the legacy 32-value formats of real GGUF files (Q8_0 activations)
 BASE_TYPES = [TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL]
-EXTRA_TYPES = [TT_Q5_K, TT_Q3_K, TT_Q2_K, TT_IQ4_XS]
+EXTRA_TYPES = [TT_Q5_K, TT_Q3_K, TT_Q2_K, TT_IQ4_XS, TT_Q4_0, TT_Q4_1]
 ALL_TYPES = BASE_TYPES + EXTRA_TYPES
 # integers per weight block in block_ints: (isum, summs) for the K-quants with
-# mins, one per 32-value block for IQ4_XS, else one
-NINTS = {TT_Q4_K: 2, TT_Q5_K: 2, TT_Q2_K: 2, TT_IQ4_XS: 8}
+# mins, (sumi, sumy) for Q4_1, one per 32-value block for IQ4_XS, else one
+NINTS = {TT_Q4_K: 2, TT_Q5_K: 2, TT_Q2_K: 2, TT_IQ4_XS: 8, TT_Q4_1: 2}
 
 _c_u8p = ctypes.POINTER(ctypes.c_uint8)
 _c_f32p = ctypes.POINTER(ctypes.c_float)
@@ -159,7 +163,7 @@ class RefKernels:
     """The reference's own x86 kernels, compiled from its sources into oracle/_ref."""
 
     DOTS = {TT_Q8_0: "q8_0_q8_0", TT_Q4_K: "q4_k_q8_k", TT_Q6_K: "q6_k_q8_k", TT_Q5_K: "q5_k_q8_k",
-            TT_Q3_K: "q3_k_q8_k", TT_Q2_K: "q2_k_q8_k"}
+            TT_Q3_K: "q3_k_q8_k", TT_Q2_K: "q2_k_q8_k", TT_Q4_0: "q4_0_q8_0", TT_Q4_1: "q4_1_q8_0"}
     QUANTS = {32: "quantize_q8_0", 256: "quantize_q8_K"}
 
     def __init__(self, path: Path = REF_SO):

@@ -15,6 +15,8 @@ static bool geom(int ttype, int& be, int& bb) {
   switch (ttype) {
     case TT_Q8_0: be = 32; bb = 34; return true;
     case TT_IQ4_NL: be = 32; bb = 18; return true;
+    case TT_Q4_0: be = 32; bb = 18; return true;
+    case TT_Q4_1: be = 32; bb = 20; return true;
     case TT_Q4_K: be = 256; bb = 144; return true;
     case TT_Q6_K: be = 256; bb = 210; return true;
     case TT_Q5_K: be = 256; bb = 176; return true;
@@ -84,8 +86,7 @@ static int mmq_min_tokens(int ttype) {
 // Formats with an MMQ kernel; the others (Q3_K, Q2_K) multiply many tokens
 // with the GEMV, which shares each weight load across up to 8 tokens per pass.
 static bool mmq_supported(int ttype) {
-  return ttype == TT_Q8_0 || ttype == TT_IQ4_NL || ttype == TT_Q4_K || ttype == TT_Q6_K || ttype == TT_Q5_K ||
-         ttype == TT_IQ4_XS;
+  return act32(ttype) || ttype == TT_Q4_K || ttype == TT_Q6_K || ttype == TT_Q5_K || ttype == TT_IQ4_XS;
 }
 
 // The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image

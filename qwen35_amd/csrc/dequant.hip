@@ -11,6 +11,8 @@
 //   Q3_K    (d * (sc - 32)) * q3                      :252-322
 //   Q2_K    (d * (sc & 15)) * q2 - (dmin * (sc >> 4)) :892-919
 //   IQ4_XS  (d * (ls - 32)) * codebook[nibble]        :324-345
+//   Q4_0    (nibble - 8) * d                          :78-88
+//   Q4_1    nibble * d + m                            :90-103
 // The library is compiled with -ffp-contract=off, so each product and the
 // Q4_K difference round exactly as the reference's Zig (strict float mode).
 //
@@ -34,21 +36,24 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
   const long v0 = ((long)blockIdx.x * 256 + threadIdx.x) * 4;
   if (v0 >= nvals) return;
   float o[4];
-  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
-    constexpr int BB = TT == TT_Q8_0 ? 34 : 18;
+  if constexpr (act32(TT)) {
+    constexpr int BB = blk32_bytes(TT);
     const uint8_t* blk = src + (v0 / 32) * BB;
     const int j0 = (int)(v0 % 32);
     const float d = h2f(ld16b(blk));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = j0 + i;
-      int q;
       if constexpr (TT == TT_Q8_0) {
-        q = (int)(int8_t)blk[2 + j];
-      } else {
-        q = iq4_value(j < 16 ? (blk[2 + j] & 15u) : (uint32_t)(blk[2 + j - 16] >> 4));
+        o[i] = d * (float)(int)(int8_t)blk[2 + j];
+      } else if constexpr (TT == TT_IQ4_NL) {
+        o[i] = d * (float)iq4_value(j < 16 ? (blk[2 + j] & 15u) : (uint32_t)(blk[2 + j - 16] >> 4));
+      } else {  // Q4_0: (q - 8) * d; Q4_1: q * d + m (quant_dequant.zig:78-103)
+        constexpr int QO = TT == TT_Q4_1 ? 4 : 2;
+        const uint32_t q = j < 16 ? (blk[QO + j] & 15u) : (uint32_t)(blk[QO + j - 16] >> 4);
+        if constexpr (TT == TT_Q4_0) o[i] = ((float)q - 8.0f) * d;
+        else o[i] = (float)q * d + h2f(ld16b(blk + 2));
       }
-      o[i] = d * (float)q;
     }
   } else if constexpr (TT == TT_Q4_K) {
     const uint8_t* blk = src + (v0 / 256) * 144;

@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
 __host__ __device__ constexpr long fused_lds_qs(int cols) { return (long)cols / 64 * kSplitUnit; }
 __host__ __device__ constexpr long fused_lds_bytes(int ttype, int cols) {
   // qs (80 B per 64 values) | d[nblk] f32 (16-aligned) | Q8_K: bs[cols/16] int16
-  return ttype == TT_Q8_0 || ttype == TT_IQ4_NL
+  return act32(ttype)
              ? fused_lds_qs(cols) + (((long)cols / 32 * 4 + 15) & ~15L)
              : fused_lds_qs(cols) + (((long)cols / 256 * 4 + 15) & ~15L) + (long)cols / 16 * 2;
 }
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
                                                  uint8_t* __restrict__ XQ, float* __restrict__ Y, int rows,
                                                  int cols, long row_bytes, int upr, int team) {
   using U = Unit<TT>;
-  constexpr bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL);
+  constexpr bool K32 = act32(TT);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nblk = K32 ? cols / 32 : cols / 256;
   uint8_t* qs = lds;
@@ -277,12 +277,13 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
 }
 
 // Exact per-block integers through the same unit decode as k_gemv.  One
-// thread per (token, row, block group): a unit of two 32-value blocks for
-// Q8_0 / IQ4_NL / IQ4_XS (whose integers are per 32-value block), a whole
+// thread per (token, row, block group): a unit of two 32-value blocks for the
+// 32-value formats and IQ4_XS (whose integers are per 32-value block), a whole
 // super-block (its four units summed) for the other K-quants.  Layout of
-// `ints`: [tokens][rows][nints]; nints = 32-value blocks per row, or per
-// super-block 2 (isum, summs: Q4_K, Q5_K, Q2_K) or 1 (Q6_K, Q3_K).
-constexpr bool per_block_ints(int tt) { return tt == TT_Q8_0 || tt == TT_IQ4_NL || tt == TT_IQ4_XS; }
+// `ints`: [tokens][rows][nints]; nints = 32-value blocks per row (twice that
+// for Q4_1: sumi, sumy per block), or per super-block 2 (isum, summs: Q4_K,
+// Q5_K, Q2_K) or 1 (Q6_K, Q3_K).
+constexpr bool per_block_ints(int tt) { return act32(tt) || tt == TT_IQ4_XS; }
 
 template <int TT>
 __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ W,
@@ -298,11 +299,12 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ 
   const uint8_t* wrow = W + row * row_bytes;
   const uint8_t* arow = XQ + t * act_bytes;
   if constexpr (per_block_ints(TT)) {
-    int out[2];
+    constexpr int NI = U::kInts;
+    int out[NI];
     U::ints(U::load_w(wrow, g), U::load_a(arow, g), out);
-    int* o = ints + rt * (2L * groups) + 2 * g;
-    o[0] = out[0];
-    o[1] = out[1];
+    int* o = ints + rt * ((long)NI * groups) + NI * g;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) o[i] = out[i];
   } else {
     int acc[2] = {0, 0};
 #pragma unroll
@@ -336,23 +338,30 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
   const uint8_t* w = W + row * row_bytes;
   const uint8_t* a = XQ + t * act_bytes;
   float acc = 0.0f;
-  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
-    constexpr int BB = TT == TT_Q8_0 ? 34 : 18;
+  if constexpr (act32(TT)) {
+    constexpr int BB = blk32_bytes(TT), QO = TT == TT_Q4_1 ? 4 : 2;
     for (int b = 0; b < cols / 32; ++b, w += BB, a += 34) {
-      int s = 0;
+      int s = 0, sy = 0;
       for (int j = 0; j < 32; ++j) {
         int wv;
         if constexpr (TT == TT_Q8_0) {
           wv = (int8_t)w[2 + j];
         } else {
-          const uint32_t q = w[2 + (j & 15)];
+          const uint32_t q = w[QO + (j & 15)];
           const uint32_t nib = j < 16 ? (q & 15u) : (q >> 4);
-          const uint32_t tab = nib < 4 ? IQ4_T0 : nib < 8 ? IQ4_T1 : nib < 12 ? IQ4_T2 : IQ4_T3;
-          wv = sext8(tab >> (8 * (nib & 3)));
+          if constexpr (TT == TT_IQ4_NL) {
+            const uint32_t tab = nib < 4 ? IQ4_T0 : nib < 8 ? IQ4_T1 : nib < 12 ? IQ4_T2 : IQ4_T3;
+            wv = sext8(tab >> (8 * (nib & 3)));
+          } else {
+            wv = TT == TT_Q4_0 ? (int)nib - 8 : (int)nib;
+          }
         }
         s += wv * (int)(int8_t)a[2 + j];
+        sy += (int)(int8_t)a[2 + j];
       }
-      acc += h2f(ldb16(w)) * h2f(ldb16(a)) * (float)s;
+      const float dy = h2f(ldb16(a));
+      acc += h2f(ldb16(w)) * dy * (float)s;
+      if constexpr (TT == TT_Q4_1) acc += h2f(ldb16(w + 2)) * dy * (float)sy;
     }
   } else {
     constexpr int BB = TT == TT_Q4_K ? 144 : TT == TT_Q6_K ? 210 : TT == TT_Q5_K ? 176 : TT == TT_Q3_K ? 110
@@ -523,13 +532,29 @@ static hipError_t launch_gemv_type(const GemvArgs& g, int team, int nt, int nr, 
 // The further formats, swept at [17408, 5120] and [9728, 2560]: Q5_K as Q4_K;
 // Q3_K (its decode is VALU-heavy) two-wave teams of four rows on long rows
 // (20.5 vs 28.3 us) and 64 lanes per row otherwise; Q2_K and IQ4_XS two rows
-// per 20-lane team (10.4 vs 14.2 us, 14.2 vs 17.2 us).
+// per 20-lane team (10.4 vs 14.2 us, 14.2 vs 17.2 us).  The 4-bit 32-value
+// formats, swept at [17408, 5120], [19456, 2560] and [2560, 9728]: four-wave
+// teams on rows of >= 8192 values (IQ4_NL 5.8 vs 6.7 us, Q4_0 5.5 vs 6.4,
+// Q4_1 5.2 vs 6.4), two-wave teams for Q4_0 / Q4_1 from 4096 values (Q4_1
+// 11.5 vs 15.8 us: its 40-byte units need no realignment and stream at
+// 4.8 TB/s), else two rows per 40- or 20-lane team.
 static void default_shape(const GemvArgs& g, int& team, int& nr) {
   const int upr = g.cols / 64;
+  const bool nib32 = g.ttype == TT_Q4_0 || g.ttype == TT_Q4_1 || g.ttype == TT_IQ4_NL;
   // long rows: teams of whole waves (k_gemv_mw), several rows per team
   if (g.ttype == TT_Q6_K && upr >= 128) {
     team = 256;
     nr = g.rows >= 4096 ? 4 : 2;
+    return;
+  }
+  if (nib32 && upr >= 128) {
+    team = 256;
+    nr = g.ttype == TT_Q4_1 ? 2 : 1;
+    return;
+  }
+  if ((g.ttype == TT_Q4_0 || g.ttype == TT_Q4_1) && upr >= 64) {
+    team = 128;
+    nr = g.ttype == TT_Q4_1 ? 4 : 2;
     return;
   }
   if ((g.ttype == TT_Q4_K || g.ttype == TT_Q5_K || g.ttype == TT_Q3_K) && upr >= 64) {
@@ -542,6 +567,7 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
     case TT_Q4_K: case TT_Q5_K:
       nr = g.rows >= 16384 && upr <= 40 ? 4 : 2; team = upr <= 40 ? 40 : 20; break;
     case TT_IQ4_NL: nr = 4; team = 20; break;
+    case TT_Q4_0: case TT_Q4_1: nr = 2; team = upr <= 40 ? 40 : 20; break;
     case TT_IQ4_XS: case TT_Q2_K: nr = 2; team = 20; break;
     case TT_Q3_K: nr = 1; team = 64; break;
     default: nr = g.rows >= 4096 ? 2 : 1; team = 16; break;
@@ -681,9 +707,16 @@ static void fused_default_shape(const GemvArgs& g, int& team, int& nr, int& wgs)
 // 32768 at widths up to 4096 (Q4_K [19456, 2560] 9.4 vs 10.7 us, Q8_0 [6144,
 // 1024] 5.0 vs 6.2 us) and loses on long rows, where every workgroup would
 // quantize a long activation (Q6_K [2560, 9728] 12.4 vs 10.4 us, Q4_K
-// [17408, 5120] 14.9 vs 14.2 us).
+// [17408, 5120] 14.9 vs 14.2 us).  The 32-value formats' separate GEMV takes
+// multi-row shapes the fused launch does not, and wins on larger matrices:
+// Q8_0 from width 4096 ([12288, 4096] 19.2 vs 22.1 us; [32768, 2560] fused
+// 21.0 vs 27.9), the 4-bit ones from 2^24 weights (Q4_0 [19456, 2560] 10.5
+// vs 11.9 us, IQ4_NL 11.8 vs 13.7; [6144, 1024] fused 4.7 vs 6.8).
 bool gemv_fused_preferred(const GemvArgs& g) {
-  return g.tokens == 1 && gemv_fused_fits(g.ttype, g.cols) && g.cols <= 4096 && g.rows <= 32768;
+  if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols) || g.cols > 4096 || g.rows > 32768) return false;
+  if (g.ttype == TT_Q8_0) return g.cols <= 2560;
+  if (act32(g.ttype)) return (long)g.rows * g.cols <= (1L << 24);
+  return true;
 }
 
 hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,

@@ -20,6 +20,9 @@
 // int32 result is the reference's per-block integer:
 //   Q8_0, IQ4_NL  v_mfma_i32_32x32x32_i8 per 32-value block
 //                 (src/kernels/x86/kernels32.c:447-464, :342-361)
+//   Q4_0, Q4_1    the same on nib - 8 (Q4_0) or the unsigned nibble (Q4_1,
+//                 whose min term m * dy * sumy is a rank-1 update in the
+//                 epilogue)  (kernels32.c:297-340)
 //   Q4_K          v_mfma_i32_32x32x32_i8 per 32-value sub-block, times its
 //                 6-bit scale in integer arithmetic; the mins term
 //                 sum_j bsum[j]*min[j/2] as an exact f16 MFMA (K = 16
@@ -55,7 +58,7 @@ constexpr float kBias = 12582912.0f;  // 1.5 * 2^23
 constexpr int kBiasBits = 0x4B400000;
 
 // ---- LDS images ---------------------------------------------------------------------
-template <int TT, int BT, int BR, bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL)>
+template <int TT, int BT, int BR, bool K32 = act32(TT)>
 struct MmqSmem;
 
 template <int TT, int BT, int BR>
@@ -64,6 +67,18 @@ struct alignas(16) MmqSmem<TT, BT, BR, true> {
   uint8_t bq[BR * kQS];
   float ad[8][BT];  // activation block scales of the chunk
   float wd[8][BR];  // weight block scales
+};
+
+// Q4_1 adds the block mins: ay = dy * (sum of the activation block's int8s),
+// wm = m, so a block contributes wm[r] * ay[t] beside its integer product.
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_Q4_1, BT, BR, true> {
+  uint8_t aq[BT * kQS];
+  uint8_t bq[BR * kQS];
+  float ad[8][BT];
+  float wd[8][BR];
+  float ay[8][BT];
+  float wm[8][BR];
 };
 
 template <int BT, int BR>
@@ -135,6 +150,30 @@ __device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename U
     }
     sm.wd[2 * u4][row] = h2f(w.d0);
     sm.wd[2 * u4 + 1][row] = h2f(w.d1);
+  } else if constexpr (TT == TT_Q4_0 || TT == TT_Q4_1) {
+    // Q4_0: nib - 8; Q4_1: the unsigned nibble (its min is added apart)
+    const uint32_t m = 0x0F0F0F0Fu;
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const uint32_t* q = w.q + 4 * b;
+      if constexpr (TT == TT_Q4_0) {
+        st16(dst + 32 * b, nib_minus8(q[0] & m), nib_minus8(q[1] & m), nib_minus8(q[2] & m), nib_minus8(q[3] & m));
+        st16(dst + 32 * b + 16, nib_minus8((q[0] >> 4) & m), nib_minus8((q[1] >> 4) & m),
+             nib_minus8((q[2] >> 4) & m), nib_minus8((q[3] >> 4) & m));
+      } else {
+        st16(dst + 32 * b, q[0] & m, q[1] & m, q[2] & m, q[3] & m);
+        st16(dst + 32 * b + 16, (q[0] >> 4) & m, (q[1] >> 4) & m, (q[2] >> 4) & m, (q[3] >> 4) & m);
+      }
+    }
+    if constexpr (TT == TT_Q4_0) {
+      sm.wd[2 * u4][row] = h2f(w.d0);
+      sm.wd[2 * u4 + 1][row] = h2f(w.d1);
+    } else {
+      sm.wd[2 * u4][row] = h2f(w.h0);
+      sm.wd[2 * u4 + 1][row] = h2f(w.h1);
+      sm.wm[2 * u4][row] = h2f(w.h0 >> 16);
+      sm.wm[2 * u4 + 1][row] = h2f(w.h1 >> 16);
+    }
   } else if constexpr (TT == TT_Q4_K) {
     const uint32_t m = 0x0F0F0F0Fu;
     st16(dst, w.q[0] & m, w.q[1] & m, w.q[2] & m, w.q[3] & m);
@@ -229,22 +268,32 @@ __device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename U
 // The 32-value formats take Q8_0 activations (two blocks per unit); the
 // K-quants take a Q8_K quarter in plain value order: values 64*u4 .. 64*u4+63.
 template <int TT>
-using MmqAct = typename std::conditional<(TT == TT_Q8_0 || TT == TT_IQ4_NL), ActPair, ActQ8K>::type;
+using MmqAct = typename std::conditional<act32(TT), ActPair, ActQ8K>::type;
 
 template <int TT>
 __device__ __forceinline__ MmqAct<TT> load_act(const uint8_t* arow, int u) {
-  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) return act_pair_ref(arow, u);
+  if constexpr (act32(TT)) return act_pair_ref(arow, u);
   else return Unit<TT_Q4_K>::load_a(arow, u);
 }
 
 template <int TT, class SM>
 __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int u4) {
   uint8_t* dst = sm.aq + tok * kQS + 64 * u4;
-  if constexpr (TT == TT_Q8_0 || TT == TT_IQ4_NL) {
+  if constexpr (act32(TT)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(dst + 16 * i, a.q[4 * i], a.q[4 * i + 1], a.q[4 * i + 2], a.q[4 * i + 3]);
     sm.ad[2 * u4][tok] = a.d0;
     sm.ad[2 * u4 + 1][tok] = a.d1;
+    if constexpr (TT == TT_Q4_1) {
+      int y0 = 0, y1 = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        y0 = dot4(0x01010101u, a.q[i], y0);
+        y1 = dot4(0x01010101u, a.q[8 + i], y1);
+      }
+      sm.ay[2 * u4][tok] = a.d0 * (float)y0;
+      sm.ay[2 * u4 + 1][tok] = a.d1 * (float)y1;
+    }
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(dst + 16 * i, a.y[4 * i], a.y[4 * i + 1], a.y[4 * i + 2], a.y[4 * i + 3]);
@@ -262,7 +311,7 @@ template <int TT, int BT, int BR>
 __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                               float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                               long act_bytes, int upr, int ntile_t, int ksplit, int cps) {
-  constexpr bool K32 = (TT == TT_Q8_0 || TT == TT_IQ4_NL);
+  constexpr bool K32 = act32(TT);
   // waves: 2 x 2 over (tokens, rows), or 1 x 4 (stacked along rows) for a
   // 32-token tile
   constexpr int WT = BT >= 64 ? 2 : 1, WR = 4 / WT;
@@ -384,6 +433,22 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
               const float t = __builtin_fmaf(__int_as_float(ce), dw[b], cw);
               acc[a][b][e] = __builtin_fmaf(t, da[e >> 2][e & 3], acc[a][b][e]);
             }
+          }
+        }
+        if constexpr (TT == TT_Q4_1) {
+          // the mins: acc += m[r] * (dy * sumy)[t]
+          float wm[NB];
+#pragma unroll
+          for (int b = 0; b < NB; ++b) wm[b] = sm.wm[s][rb0 + 32 * b + li];
+#pragma unroll
+          for (int a = 0; a < NA; ++a) {
+            f32x4 ay[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ay[q] = *(const f32x4*)&sm.ay[s][tb0 + 32 * a + 8 * q + 4 * lh];
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc[a][b][e] = __builtin_fmaf(wm[b], ay[e >> 2][e & 3], acc[a][b][e]);
           }
         }
       };
@@ -993,7 +1058,7 @@ static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit,
 // 23.5 vs 30.5 us, Q6_K 33.8 vs 42.9 us.  The 32-value formats keep 64 x 64:
 // their (small) config-4 matrix needs the wider grid.
 static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
-  const bool small = g.tokens <= 32 && g.ttype != TT_Q8_0 && g.ttype != TT_IQ4_NL;
+  const bool small = g.tokens <= 32 && !act32(g.ttype);
   bt = small ? 32 : 64;
   br = small ? 128 : 64;
 }
@@ -1009,6 +1074,8 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
   switch (g.ttype) {
     case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, ksplit, s);
     case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, ksplit, s);
+    case TT_Q4_0: return launch_mmq_type<TT_Q4_0>(g, bt, br, ksplit, s);
+    case TT_Q4_1: return launch_mmq_type<TT_Q4_1>(g, bt, br, ksplit, s);
     case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, ksplit, s);
     case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, ksplit, s);
     case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, ksplit, s);

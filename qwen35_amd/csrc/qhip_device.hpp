@@ -3,9 +3,10 @@
 // primitives, the IQ4_NL codebook lookup and the per-format decode of one
 // 64-value work unit.
 //
-// Q8_0 and IQ4_NL weights pair with a Q8_0 activation (34 B / 32 values),
-// Q4_K and Q6_K with a Q8_K activation (292 B / 256 values), as the
-// reference's actFamily (src/backend_cpu.zig:42-50) prescribes.
+// The 32-value formats (Q8_0, IQ4_NL, Q4_0, Q4_1) pair with a Q8_0 activation
+// (34 B / 32 values), the K-quants and IQ4_XS with a Q8_K activation (292 B /
+// 256 values), as the reference's actFamily (src/backend_cpu.zig:42-50)
+// prescribes.
 //
 // Integer arithmetic inside a block is exact and equals the reference's
 // per-block integers (src/kernels/x86/kernels32.c:342-361, :447-464;
@@ -20,9 +21,18 @@
 namespace qhip {
 
 enum : int {
-  TT_Q8_0 = 8, TT_Q2_K = 10, TT_Q3_K = 11, TT_Q4_K = 12, TT_Q5_K = 13, TT_Q6_K = 14, TT_IQ4_NL = 20,
-  TT_IQ4_XS = 23
+  TT_Q4_0 = 2, TT_Q4_1 = 3, TT_Q8_0 = 8, TT_Q2_K = 10, TT_Q3_K = 11, TT_Q4_K = 12, TT_Q5_K = 13,
+  TT_Q6_K = 14, TT_IQ4_NL = 20, TT_IQ4_XS = 23
 };
+
+// Formats of 32-value blocks, which take a Q8_0 activation; the others take Q8_K.
+__host__ __device__ constexpr bool act32(int tt) {
+  return tt == TT_Q8_0 || tt == TT_IQ4_NL || tt == TT_Q4_0 || tt == TT_Q4_1;
+}
+// bytes of one 32-value weight block (act32 formats)
+__host__ __device__ constexpr int blk32_bytes(int tt) {
+  return tt == TT_Q8_0 ? 34 : tt == TT_Q4_1 ? 20 : 18;
+}
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2), aligned(4)));
@@ -168,7 +178,8 @@ __device__ __forceinline__ uint32_t iq4_hi(uint32_t q) {
 // ---- per-format unit decode ------------------------------------------------------
 // Every GEMV lane walks a weight row in units of 64 values:
 //   Q8_0    two 34-byte blocks (68 B, blocks 2u and 2u+1)
-//   IQ4_NL  two 18-byte blocks (36 B)
+//   IQ4_NL  two 18-byte blocks (36 B); Q4_0 the same
+//   Q4_1    two 20-byte blocks (40 B)
 //   Q4_K    one quarter of a 144-byte super-block: 32 B of nibbles (sub-blocks
 //           2c and 2c+1) plus the shared 16-byte header
 //   Q6_K    one quarter of a 210-byte super-block: the (h, l-half) slice of the
@@ -320,6 +331,91 @@ struct Unit<TT_IQ4_NL> {
     int s[2];
     ints(w, a, s);
     return (h2f(w.d0) * a.d0) * (float)s[0] + (h2f(w.d1) * a.d1) * (float)s[1];
+  }
+};
+
+// 4 packed nibbles, one per byte (0..15) -> the int8 bytes nib - 8.  Setting
+// bit 7 of every byte first keeps the per-byte subtraction from borrowing
+// into its neighbour; flipping it back restores the two's complement byte.
+__device__ __forceinline__ uint32_t nib_minus8(uint32_t n) {
+  return ((n | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+}
+
+// Q4_0 (src/kernels/x86/kernels32.c:297-316): 18-byte blocks of f16 d and 16
+// nibble bytes, byte j holding value j (low nibble) and j+16 (high), each
+// value nib - 8.  The unit layout is IQ4_NL's.
+template <>
+struct Unit<TT_Q4_0> {
+  static constexpr int kWBytes = 36, kInts = 2;
+  using W = Unit<TT_IQ4_NL>::W;
+  using A = ActPair;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) { return Unit<TT_IQ4_NL>::load_w(row, u); }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return act_pair_ref(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) { return act_pair_split(sp, u); }
+  static __device__ __forceinline__ int block(const uint32_t* q, const uint32_t* y) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s = dot4(nib_minus8(q[i] & 0x0F0F0F0Fu), y[i], s);
+      s = dot4(nib_minus8((q[i] >> 4) & 0x0F0F0F0Fu), y[4 + i], s);
+    }
+    return s;
+  }
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* s) {
+    s[0] = block(w.q, a.q);
+    s[1] = block(w.q + 4, a.q + 8);
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[2];
+    ints(w, a, s);
+    return (h2f(w.d0) * a.d0) * (float)s[0] + (h2f(w.d1) * a.d1) * (float)s[1];
+  }
+};
+
+// Q4_1 (src/kernels/x86/kernels32.c:318-340): 20-byte blocks of f16 d, f16 m
+// and 16 nibble bytes (unsigned values, same order as Q4_0); a block's term is
+// d*dy*sumi + m*dy*sumy with sumy the sum of the activation block's int8s.
+// A 40-byte unit of two blocks is dword aligned throughout: no funnel shifts.
+template <>
+struct Unit<TT_Q4_1> {
+  static constexpr int kWBytes = 40, kInts = 4;
+  struct W { uint32_t q[8]; uint32_t h0, h1; };  // h: d | m << 16
+  using A = ActPair;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* p = row + 40 * u;
+    const u32x4 x0 = ld128(p), x1 = ld128(p + 16);
+    const u32x2 x2 = *(const u32x2*)(p + 32);
+    W w;
+    w.h0 = x0.x;
+    w.q[0] = x0.y; w.q[1] = x0.z; w.q[2] = x0.w; w.q[3] = x1.x;
+    w.h1 = x1.y;
+    w.q[4] = x1.z; w.q[5] = x1.w; w.q[6] = x2.x; w.q[7] = x2.y;
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return act_pair_ref(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) { return act_pair_split(sp, u); }
+  // (sumi, sumy) of one block; nibbles 0..15 are exact as signed int8
+  static __device__ __forceinline__ void block(const uint32_t* q, const uint32_t* y, int& si, int& sy) {
+    si = 0;
+    sy = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      si = dot4(q[i] & 0x0F0F0F0Fu, y[i], si);
+      si = dot4((q[i] >> 4) & 0x0F0F0F0Fu, y[4 + i], si);
+      sy = dot4(0x01010101u, y[i], sy);
+      sy = dot4(0x01010101u, y[4 + i], sy);
+    }
+  }
+  // s = {sumi0, sumy0, sumi1, sumy1}
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* s) {
+    block(w.q, a.q, s[0], s[1]);
+    block(w.q + 4, a.q + 8, s[2], s[3]);
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[4];
+    ints(w, a, s);
+    return (h2f(w.h0) * a.d0) * (float)s[0] + (h2f(w.h0 >> 16) * a.d0) * (float)s[1] +
+           (h2f(w.h1) * a.d1) * (float)s[2] + (h2f(w.h1 >> 16) * a.d1) * (float)s[3];
   }
 };
 
@@ -725,6 +821,8 @@ __host__ inline auto dispatch_type(int ttype, F&& f) -> decltype(f(std::integral
     case TT_Q3_K: return f(std::integral_constant<int, TT_Q3_K>{});
     case TT_Q2_K: return f(std::integral_constant<int, TT_Q2_K>{});
     case TT_IQ4_XS: return f(std::integral_constant<int, TT_IQ4_XS>{});
+    case TT_Q4_0: return f(std::integral_constant<int, TT_Q4_0>{});
+    case TT_Q4_1: return f(std::integral_constant<int, TT_Q4_1>{});
     default: return hipErrorInvalidValue;
   }
 }

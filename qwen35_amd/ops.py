@@ -12,7 +12,9 @@ import torch
 from ._lib import QhipLinear, check, load
 
 _GEOM = {8: (32, 34), 20: (32, 18), 12: (256, 144), 14: (256, 210), 13: (256, 176), 11: (256, 110),
-         10: (256, 84), 23: (256, 136)}
+         10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20)}
+# integers per 32-value block in the block-integer export: (sumi, sumy) for Q4_1
+_NINTS_32 = {3: 2}
 # integers per super-block in the block-integer export: (isum, summs) for
 # Q4_K / Q5_K / Q2_K, one per 32-value block for IQ4_XS, else one
 _NINTS_SB = {12: 2, 13: 2, 10: 2, 23: 8}
@@ -141,7 +143,7 @@ def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, co
 def block_ints(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
                tokens: int) -> torch.Tensor:
     be = _GEOM[ttype][0]
-    nints = cols // be if be == 32 else _NINTS_SB.get(ttype, 1) * (cols // 256)
+    nints = _NINTS_32.get(ttype, 1) * (cols // 32) if be == 32 else _NINTS_SB.get(ttype, 1) * (cols // 256)
     out = torch.empty((tokens, rows, nints), dtype=torch.int32, device=w.device)
     check("block_ints", load().qhip_launch_block_ints(_p(w), _p(xq), _p(out), rows, cols, tokens,
                                                       ttype, _stream()))

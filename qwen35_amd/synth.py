@@ -13,6 +13,8 @@ inputs.  Block contents follow the generation rules of each configuration:
           scale/min bytes; IQ4_XS random indices and 6-bit scales; f16 d (and
           dmin) = |N(0,1)| * 1e-3 (formats beyond the benchmark configurations,
           same generation style)
+* Q4_0    random nibbles, f16 d = |N(0,1)| * 1e-3; Q4_1 the same plus an f16
+          min m = N(0,1) * 8e-3
 * activations f32 ~ N(0,1) (Box-Muller)
 """
 from __future__ import annotations
@@ -23,10 +25,12 @@ import numpy as np
 
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20
 TT_Q2_K, TT_Q3_K, TT_Q5_K, TT_IQ4_XS = 10, 11, 13, 23
+TT_Q4_0, TT_Q4_1 = 2, 3
 GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210),
-        TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136)}
+        TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136),
+        TT_Q4_0: (32, 18), TT_Q4_1: (32, 20)}
 D_SCALE = {TT_Q8_0: 2e-4, TT_IQ4_NL: 1e-3, TT_Q4_K: 1e-3, TT_Q6_K: 1e-3, TT_Q2_K: 1e-3, TT_Q3_K: 1e-3,
-           TT_Q5_K: 1e-3, TT_IQ4_XS: 1e-3}
+           TT_Q5_K: 1e-3, TT_IQ4_XS: 1e-3, TT_Q4_0: 1e-3, TT_Q4_1: 1e-3}
 
 _GAMMA = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -126,6 +130,15 @@ def make_weight(ttype: int, rows: int, cols: int, seed: int = 0, tag: int = 1) -
     elif ttype == TT_IQ4_XS:
         blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         blocks[:, 2:] = rand_bytes(substream(s, 2), nb * 134).reshape(nb, 134)
+    elif ttype == TT_Q4_0:
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:] = rand_bytes(substream(s, 2), nb * 16).reshape(nb, 16)
+    elif ttype == TT_Q4_1:
+        # m: the block minimum, signed, of the magnitude of 8 * d
+        m = f16_bits(rand_normal(substream(s, 3), nb) * (8 * D_SCALE[ttype]))
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:4] = m.view(np.uint8).reshape(nb, 2)
+        blocks[:, 4:] = rand_bytes(substream(s, 2), nb * 16).reshape(nb, 16)
     else:
         raise ValueError(f"unsupported ttype {ttype}")
     return blocks.reshape(rows, cols // be * bb)

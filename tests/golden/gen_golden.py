@@ -9,11 +9,12 @@ Contents (small seeded inputs and the reference's outputs on them):
   quant_q8_k_x / _act          quantize_q8_K input rows and output bytes
   <T>_w, <T>_x, <T>_dot        weight rows, activation rows (f32) and the
                                reference row dot (T = q8_0, q4_k, q6_k, q5_k,
-                               q3_k, q2_k) of each
+                               q3_k, q2_k, q4_0, q4_1) of each
                                weight row against the reference-quantized row
   <T>_unit_*                   rows with unit scales (d = 1, dmin = 0 / d = 0,
-                               dmin = 1) whose float result equals the exact
-                               integer sums, pinning them bit for bit
+                               dmin = 1; Q4_1: d = 1, m = 0 / d = 0, m = 1)
+                               whose float result equals the exact integer
+                               sums, pinning them bit for bit
   meta_tier                    CPU tier the reference dispatched to
 """
 import sys
@@ -28,10 +29,10 @@ import pyoracle as po  # noqa: E402
 from qwen35_amd import synth  # noqa: E402
 
 TT = {"q8_0": po.TT_Q8_0, "q4_k": po.TT_Q4_K, "q6_k": po.TT_Q6_K, "q5_k": po.TT_Q5_K,
-      "q3_k": po.TT_Q3_K, "q2_k": po.TT_Q2_K}
-# byte offsets of (d, dmin) in each K-quant super-block; dmin None: no mins term
+      "q3_k": po.TT_Q3_K, "q2_k": po.TT_Q2_K, "q4_0": po.TT_Q4_0, "q4_1": po.TT_Q4_1}
+# byte offsets of (d, dmin) in each weight block; dmin None: no mins term
 SCALE_AT = {po.TT_Q4_K: (0, 2), po.TT_Q5_K: (0, 2), po.TT_Q6_K: (208, None), po.TT_Q3_K: (108, None),
-            po.TT_Q2_K: (80, 82)}
+            po.TT_Q2_K: (80, 82), po.TT_Q8_0: (0, None), po.TT_Q4_0: (0, None), po.TT_Q4_1: (0, 2)}
 
 
 def edge_rows(n: int) -> np.ndarray:
@@ -64,7 +65,7 @@ def main():
         out[f"quant_{name}_x"] = x
         out[f"quant_{name}_act"] = ref.quantize_act(tt, x)
     for name, tt in TT.items():
-        cols = 512 if tt == po.TT_Q8_0 else 768
+        cols = 512 if po.GEOM[tt][0] == 32 else 768
         rows = 12
         w = synth.make_weight(tt, rows, cols, seed=11, tag=tt)
         x = synth.make_act(cols, 3, seed=11)
@@ -79,19 +80,18 @@ def main():
         ab = ref.quantize_act(tt, synth.make_act(be, nblk, seed=13))
         one = np.float16(1.0).view(np.uint16)
         variants = {}
-        if tt == po.TT_Q8_0:
-            w1 = wb.copy(); w1[:, 0:2] = np.frombuffer(one.tobytes(), np.uint8)
-            a1 = ab.copy(); a1[:, 0:2] = np.frombuffer(one.tobytes(), np.uint8)
-            variants["isum"] = (w1, a1)
-        else:
-            a1 = ab.copy(); a1[:, 0:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
-            od, om = SCALE_AT[tt]
-            wi = wb.copy(); wi[:, od:od + 2] = np.frombuffer(one.tobytes(), np.uint8)
-            if om is not None:
-                wi[:, om:om + 2] = 0
-                wm = wb.copy(); wm[:, od:od + 2] = 0; wm[:, om:om + 2] = np.frombuffer(one.tobytes(), np.uint8)
-                variants["summs"] = (wm, a1)
-            variants["isum"] = (wi, a1)
+        a1 = ab.copy()
+        if be == 32:  # Q8_0 activation blocks: f16 scale
+            a1[:, 0:2] = np.frombuffer(one.tobytes(), np.uint8)
+        else:         # Q8_K activation blocks: f32 scale
+            a1[:, 0:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
+        od, om = SCALE_AT[tt]
+        wi = wb.copy(); wi[:, od:od + 2] = np.frombuffer(one.tobytes(), np.uint8)
+        if om is not None:
+            wi[:, om:om + 2] = 0
+            wm = wb.copy(); wm[:, od:od + 2] = 0; wm[:, om:om + 2] = np.frombuffer(one.tobytes(), np.uint8)
+            variants["summs"] = (wm, a1)
+        variants["isum"] = (wi, a1)
         for key, (wv, av) in variants.items():
             vals = np.array([ref.dot(tt, wv[i], av[i], be) for i in range(nblk)], np.float32)
             out[f"{name}_unit_{key}_w"], out[f"{name}_unit_{key}_a"] = wv, av

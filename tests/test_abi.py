@@ -49,12 +49,14 @@ def test_python_binding_covers_header(lib):
 
 def test_geometry(lib):
     be, bb = ctypes.c_int(), ctypes.c_int()
-    table = {8: (32, 34), 12: (256, 144), 14: (256, 210), 20: (32, 18)}
+    table = {8: (32, 34), 12: (256, 144), 14: (256, 210), 20: (32, 18), 13: (256, 176), 11: (256, 110),
+             10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20)}
     for tt, (e, b) in table.items():
         assert lib.qhip_quant_geom(tt, ctypes.byref(be), ctypes.byref(bb)) == 1
         assert (be.value, bb.value) == (e, b)
         assert lib.qhip_quant_act_block_elems(tt) == (32 if e == 32 else 256)
-    assert lib.qhip_quant_geom(2, ctypes.byref(be), ctypes.byref(bb)) == 0  # Q4_0 unsupported
+    assert lib.qhip_quant_geom(6, ctypes.byref(be), ctypes.byref(bb)) == 0  # Q5_0 unsupported
+    assert lib.qhip_quant_geom(1, ctypes.byref(be), ctypes.byref(bb)) == 0  # F16: not a quant format
     assert lib.qhip_quant_act_block_elems(99) == 0
     assert lib.qhip_act_row_bytes(8, 1024) == 1088
     assert lib.qhip_act_row_bytes(12, 2560) == 2920
@@ -76,7 +78,7 @@ def test_ragged_offsets(lib):
 def test_invalid_arguments_rejected_before_launch(lib):
     p = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
     # unknown type id
-    assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 256, 1, 2, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 256, 1, 6, None) == INVALID
     # cols not a multiple of the block size
     assert lib.qhip_launch_mul_mat_vec(p, p, p, 16, 100, 1, 12, None) == INVALID
     # NULL buffers

@@ -28,7 +28,8 @@ def backend(gpu):
 @pytest.mark.parametrize("tt,rows,cols", [(po.TT_Q8_0, 256, 1024), (po.TT_Q4_K, 128, 2560),
                                           (po.TT_Q6_K, 64, 9728), (po.TT_IQ4_NL, 96, 2560),
                                           (po.TT_Q5_K, 128, 2560), (po.TT_Q3_K, 80, 2304),
-                                          (po.TT_Q2_K, 96, 2560), (po.TT_IQ4_XS, 112, 2560)])
+                                          (po.TT_Q2_K, 96, 2560), (po.TT_IQ4_XS, 112, 2560),
+                                          (po.TT_Q4_0, 96, 2560), (po.TT_Q4_1, 96, 2560)])
 def test_backend_matvec(gpu, oracle, backend, tt, rows, cols):
     w = synth.make_weight(tt, rows, cols, seed=21, tag=tt)
     x = synth.make_act(cols, 1, seed=21)

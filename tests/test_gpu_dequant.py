@@ -26,7 +26,7 @@ def with_edge_scales(tt, w):
     n = min(len(blk), 7)
     off = {po.TT_Q6_K: 208, po.TT_Q3_K: 108, po.TT_Q2_K: 80}.get(tt, 0)
     blk[:n, off:off + 2] = edge.reshape(-1, 2)[:n]
-    dmin = {po.TT_Q4_K: 2, po.TT_Q5_K: 2, po.TT_Q2_K: 82}.get(tt)
+    dmin = {po.TT_Q4_K: 2, po.TT_Q5_K: 2, po.TT_Q2_K: 82, po.TT_Q4_1: 2}.get(tt)
     if dmin is not None:
         blk[:n, dmin:dmin + 2] = edge.reshape(-1, 2)[::-1][:n]
     return blk.reshape(w.shape)

@@ -84,6 +84,8 @@ SHAPES = {
     po.TT_Q3_K: [(60, 2560), (18, 256), (16, 2304)],
     po.TT_Q2_K: [(70, 2560), (21, 256)],
     po.TT_IQ4_XS: [(80, 2560), (19, 256)],
+    po.TT_Q4_0: [(200, 2560), (37, 256), (11, 224)],
+    po.TT_Q4_1: [(150, 2560), (29, 256), (9, 224)],
 }
 CASES = [(tt, r, c) for tt in TYPES for (r, c) in SHAPES[tt]]
 
@@ -100,7 +102,7 @@ def test_block_ints_bit_exact(gpu, oracle, tt, rows, cols):
     act = oracle.quantize_act(tt, x)
     xq = ops.quantize_act(tt, xd)
     assert np.array_equal(xq.cpu().numpy(), act)
-    if cols % (64 if tt in (po.TT_Q8_0, po.TT_IQ4_NL) else 256):
+    if cols % (64 if po.GEOM[tt][0] == 32 else 256):
         # the export walks whole per-lane chunks; other widths are refused
         with pytest.raises(qwen35_amd.QhipError):
             ops.block_ints(tt, wd, xq, rows, cols, 2)
@@ -182,7 +184,8 @@ def test_zero_weights_and_zero_activation(gpu, oracle):
 FUSED = [(po.TT_Q8_0, 300, 1024), (po.TT_Q8_0, 6144, 1024), (po.TT_IQ4_NL, 200, 2560),
          (po.TT_Q4_K, 100, 2560), (po.TT_Q4_K, 19456, 2560), (po.TT_Q6_K, 50, 9728),
          (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 16, 2304), (po.TT_Q5_K, 100, 2560), (po.TT_Q3_K, 60, 2304),
-         (po.TT_Q2_K, 70, 2560), (po.TT_IQ4_XS, 80, 2560)]
+         (po.TT_Q2_K, 70, 2560), (po.TT_IQ4_XS, 80, 2560), (po.TT_Q4_0, 200, 2560),
+         (po.TT_Q4_1, 150, 2560), (po.TT_Q4_1, 4096, 1024)]
 
 
 @pytest.mark.parametrize("tt,rows,cols", FUSED, ids=[case_id(*c) for c in FUSED])

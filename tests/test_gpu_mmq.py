@@ -44,6 +44,10 @@ CASES = [
     (po.TT_Q5_K, 64, 2560, 16),
     (po.TT_IQ4_XS, 130, 768, 70),
     (po.TT_IQ4_XS, 33, 2560, 20),
+    (po.TT_Q4_0, 200, 320, 37),
+    (po.TT_Q4_0, 64, 2560, 16),
+    (po.TT_Q4_1, 96, 576, 70),
+    (po.TT_Q4_1, 130, 1024, 130),
 ]
 IDS = [f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in CASES]
 
@@ -71,9 +75,9 @@ def unit_scale_weight(tt, rows, cols, seed):
     w = synth.make_weight(tt, rows, cols, seed=seed, tag=tt).copy()
     be, bb = po.GEOM[tt]
     blk = w.reshape(rows, cols // be, bb)
-    if tt in (po.TT_Q8_0, po.TT_IQ4_NL, po.TT_IQ4_XS):
+    if tt in (po.TT_Q8_0, po.TT_IQ4_NL, po.TT_IQ4_XS, po.TT_Q4_0):
         blk[:, :, 0:2] = F16_ONE
-    elif tt in (po.TT_Q4_K, po.TT_Q5_K):
+    elif tt in (po.TT_Q4_K, po.TT_Q5_K, po.TT_Q4_1):  # d = 1 and dmin (Q4_1: m) = 1
         blk[:, :, 0:2] = F16_ONE
         blk[:, :, 2:4] = F16_ONE
     else:
@@ -90,7 +94,8 @@ def unit_scale_act(cols, tokens, seed):
     return x
 
 
-@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS])
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS,
+                                po.TT_Q4_0, po.TT_Q4_1])
 def test_mmq_block_integers_exact(gpu, oracle, tt):
     # IQ4_XS: the super-block sums carry the scales (up to 31), so half the
     # width keeps every result below 2^24
@@ -101,6 +106,8 @@ def test_mmq_block_integers_exact(gpu, oracle, tt):
     ints = oracle.block_ints(tt, w, act, cols).astype(np.int64)  # [tokens][rows][nints]
     if tt in (po.TT_Q4_K, po.TT_Q5_K):
         want = ints[:, :, 0::2].sum(-1) - ints[:, :, 1::2].sum(-1)  # isum - summs
+    elif tt == po.TT_Q4_1:
+        want = ints[:, :, 0::2].sum(-1) + ints[:, :, 1::2].sum(-1)  # sumi + sumy
     elif tt == po.TT_IQ4_XS:
         # per-block integers times the block's ls - 32 (d = 1, dy = 1)
         blk = w.reshape(rows, cols // 256, 136)

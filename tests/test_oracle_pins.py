@@ -104,13 +104,16 @@ def test_q8_k_bsums_and_clamp(oracle):
                                          ("q4_k", po.TT_Q4_K, "summs"), ("q6_k", po.TT_Q6_K, "isum"),
                                          ("q5_k", po.TT_Q5_K, "isum"), ("q5_k", po.TT_Q5_K, "summs"),
                                          ("q3_k", po.TT_Q3_K, "isum"), ("q2_k", po.TT_Q2_K, "isum"),
-                                         ("q2_k", po.TT_Q2_K, "summs")])
+                                         ("q2_k", po.TT_Q2_K, "summs"), ("q4_0", po.TT_Q4_0, "isum"),
+                                         ("q4_1", po.TT_Q4_1, "isum"), ("q4_1", po.TT_Q4_1, "summs")])
 def test_block_ints_unit_scale(oracle, gv, name, tt, key):
     w, a, val = gv[f"{name}_unit_{key}_w"], gv[f"{name}_unit_{key}_a"], gv[f"{name}_unit_{key}_val"]
     be = po.GEOM[tt][0]
     got = np.array([oracle.block_ints(tt, w[i:i + 1], a[i:i + 1], be)[0, 0] for i in range(len(w))])
     if po.NINTS.get(tt, 1) == 2:
-        got = got[:, 0] if key == "isum" else -got[:, 1]
+        # the K-quant mins term is subtracted (dmin * summs), the Q4_1 one added (m * sumy)
+        sign = 1 if tt == po.TT_Q4_1 else -1
+        got = got[:, 0] if key == "isum" else sign * got[:, 1]
     else:
         got = got[:, 0]
     assert np.all(np.abs(val) < 2 ** 24)  # exactly representable
@@ -118,7 +121,8 @@ def test_block_ints_unit_scale(oracle, gv, name, tt, key):
 
 
 @pytest.mark.parametrize("name,tt", [("q8_0", po.TT_Q8_0), ("q4_k", po.TT_Q4_K), ("q6_k", po.TT_Q6_K),
-                                     ("q5_k", po.TT_Q5_K), ("q3_k", po.TT_Q3_K), ("q2_k", po.TT_Q2_K)])
+                                     ("q5_k", po.TT_Q5_K), ("q3_k", po.TT_Q3_K), ("q2_k", po.TT_Q2_K),
+                                     ("q4_0", po.TT_Q4_0), ("q4_1", po.TT_Q4_1)])
 def test_row_dot_golden(oracle, gv, name, tt):
     w, x, want = gv[f"{name}_w"], gv[f"{name}_x"], gv[f"{name}_dot"]
     cols = x.shape[1]
@@ -130,7 +134,8 @@ def test_row_dot_golden(oracle, gv, name, tt):
     assert cols % 256 == 0
 
 
-@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_Q3_K, po.TT_Q2_K])
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_Q3_K, po.TT_Q2_K,
+                                po.TT_Q4_0, po.TT_Q4_1])
 def test_row_dot_vs_ref_random(oracle, ref, tt):
     from qwen35_amd import synth
     cols = 2560 if tt != po.TT_Q6_K else 2816
@@ -215,7 +220,7 @@ def test_iq4_xs_block_ints_equal_iq4_nl(oracle):
 
 UD = {po.TT_Q8_0: ("Q8_0", 320), po.TT_Q4_K: ("Q4_K", 144), po.TT_Q6_K: ("Q6_K", 210),
       po.TT_IQ4_NL: ("IQ4_NL", 144), po.TT_Q5_K: ("Q5_K", 176), po.TT_Q3_K: ("Q3_K", 110),
-      po.TT_IQ4_XS: ("IQ4_XS", 136)}
+      po.TT_IQ4_XS: ("IQ4_XS", 136), po.TT_Q4_0: ("Q4_0", 144), po.TT_Q4_1: ("Q4_1", 160)}
 
 
 @pytest.mark.parametrize("tt", list(UD))
