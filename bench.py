@@ -306,7 +306,9 @@ def main() -> int:
                                      ("q2_k_17408x5120", 10, 17408, 5120),
                                      ("iq4_xs_17408x5120", 23, 17408, 5120),
                                      ("q4_0_17408x5120", 2, 17408, 5120),
-                                     ("q4_1_17408x5120", 3, 17408, 5120)):
+                                     ("q4_1_17408x5120", 3, 17408, 5120),
+                                     ("iq3_xxs_17408x5120", 18, 17408, 5120),
+                                     ("iq3_s_17408x5120", 21, 17408, 5120)):
             t1 = time.time()
             w = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
             st = Stream(torch, w.reshape(-1), dev)

@@ -19,7 +19,7 @@
  *
  * Type ids are the GGUF TensorType numbers (src/gguf.zig TensorType,
  * src/kernels/cuda/api.h:52-75).  Supported: Q8_0, Q4_K, Q6_K, IQ4_NL (the
- * benchmark formats), Q5_K, Q3_K, Q2_K, IQ4_XS, Q4_0, Q4_1.
+ * benchmark formats), Q5_K, Q3_K, Q2_K, IQ4_XS, Q4_0, Q4_1, IQ3_XXS, IQ3_S.
  *
  * Layouts (all little-endian, GGUF block formats, src/gguf.zig:168-207):
  *   weight rows   rows x (cols / block_elems) blocks, rows contiguous
@@ -51,6 +51,8 @@ extern "C" {
 #define QHIP_TT_IQ4_XS 23
 #define QHIP_TT_Q4_0 2
 #define QHIP_TT_Q4_1 3
+#define QHIP_TT_IQ3_XXS 18
+#define QHIP_TT_IQ3_S 21
 
 #define QHIP_DECLINE (-1)
 
@@ -198,8 +200,9 @@ int qhip_launch_mul_mat_ragged(const void *d_w, const void *d_xq_packed, float *
  * Exact per-block integers through the same unit decode as the GEMV kernels:
  * ints[(t*rows + r)*nints + i], nints = cols/block_elems, except the formats
  * with mins: Q4_K, Q5_K, Q2_K store (isum, summs) per super-block (nints =
- * 2*cols/256), Q4_1 (sumi, sumy) per block (nints = 2*cols/32); IQ4_XS one
- * integer per 32-value block (nints = cols/32).  The integers of
+ * 2*cols/256), Q4_1 (sumi, sumy) per block (nints = 2*cols/32); IQ4_XS,
+ * IQ3_XXS and IQ3_S one integer per 32-value sub-block before its scale
+ * (nints = cols/32).  The integers of
  * src/kernels/x86/kernels32.c:447-464 / :342-361 / :297-340 and
  * kernels256.c:474-498 / :720-738. */
 int qhip_launch_block_ints(const void *d_w, const void *d_xq, int32_t *d_ints, int rows, int cols,

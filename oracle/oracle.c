@@ -11,6 +11,7 @@
  * per-rounding statements.
  */
 #include "oracle.h"
+#include "../qwen35_amd/csrc/iq_grids.h"
 
 #include <math.h>
 #include <stdlib.h>
@@ -352,6 +353,74 @@ int32_t orc_blk_iq4_xs(const uint8_t *w, const uint8_t *a, int ib) {
     return s;
 }
 
+/* ---- IQ3_XXS / IQ3_S ------------------------------------------------------
+ * Grids: the 12-bit codes of iq_grids.h expanded to the u32 entries of
+ * src/iq_tables.zig:323-356 / :360-425. */
+#define ORC_XXS_ENTRY(c) QHIP_IQ3_EXPAND(QHIP_IQ3XXS_LEVEL, c),
+#define ORC_S_ENTRY(c) QHIP_IQ3_EXPAND(QHIP_IQ3S_LEVEL, c),
+static const uint32_t orc_iq3xxs_tab[256] = {QHIP_IQ3XXS_CODES(ORC_XXS_ENTRY)};
+static const uint32_t orc_iq3s_tab[512] = {QHIP_IQ3S_CODES(ORC_S_ENTRY)};
+
+uint32_t orc_iq3xxs_grid(int i) { return orc_iq3xxs_tab[i & 255]; }
+uint32_t orc_iq3s_grid(int i) { return orc_iq3s_tab[i & 511]; }
+
+/* ksigns_iq2xs (iq_tables.zig:42-61): the 7-bit index with bit 7 set when the
+ * index has an odd number of ones, so every mask has even parity.  Bit j set
+ * negates value j of the 8 (kmask_iq2xs, iq_tables.zig:36-38: 1 << j). */
+uint8_t orc_ksigns(int i) {
+    int p = 0;
+    for (int b = 0; b < 7; ++b) p ^= (i >> b) & 1;
+    return (uint8_t)((i & 127) | (p << 7));
+}
+
+/* 8 values: grid entries g1 (values 0..3), g2 (4..7) against q8, signs by mask */
+static int32_t iq3_group(uint32_t g1, uint32_t g2, uint8_t sg, const int8_t *q8) {
+    int32_t s = 0;
+    for (int j = 0; j < 4; ++j) {
+        s += (int32_t)((g1 >> (8 * j)) & 255) * q8[j] * ((sg >> j) & 1 ? -1 : 1);
+        s += (int32_t)((g2 >> (8 * j)) & 255) * q8[4 + j] * ((sg >> (4 + j)) & 1 ? -1 : 1);
+    }
+    return s;
+}
+
+/* iq_kernels.c:612-643: sub-block ib of a 98-byte IQ3_XXS super-block (d,
+ * qs[64] grid indices, 8 u32 aux words: four 7-bit sign indices, then the
+ * 4-bit scale in bits 28..31) */
+int32_t orc_blk_iq3_xxs(const uint8_t *w, const uint8_t *a, int ib) {
+    const uint8_t *q3 = w + 2 + 8 * ib;
+    uint32_t aux;
+    memcpy(&aux, w + 66 + 4 * ib, 4);
+    const int8_t *q8 = (const int8_t *)(a + 4) + 32 * ib;
+    int32_t s = 0;
+    for (int l = 0; l < 4; ++l)
+        s += iq3_group(orc_iq3xxs_tab[q3[2 * l]], orc_iq3xxs_tab[q3[2 * l + 1]],
+                       orc_ksigns((aux >> (7 * l)) & 127), q8 + 8 * l);
+    return s;
+}
+static int iq3xxs_ls(const uint8_t *w, int ib) {
+    uint32_t aux;
+    memcpy(&aux, w + 66 + 4 * ib, 4);
+    return 2 * (int)(aux >> 28) + 1;
+}
+
+/* iq_kernels.c:1728-1772: sub-block ib of a 110-byte IQ3_S super-block (d,
+ * qs[64] low index bytes, qh[8] index bit 8, signs[32] explicit masks,
+ * scales[4] 4-bit pairs); index of group k: qs[8ib+k] | bit k of qh[ib] << 8 */
+int32_t orc_blk_iq3_s(const uint8_t *w, const uint8_t *a, int ib) {
+    const uint8_t *qs = w + 2 + 8 * ib;
+    const unsigned qh = w[66 + ib];
+    const uint8_t *signs = w + 74 + 4 * ib;
+    const int8_t *q8 = (const int8_t *)(a + 4) + 32 * ib;
+    int32_t s = 0;
+    for (int l = 0; l < 4; ++l) {
+        const int i1 = qs[2 * l] | ((qh << (8 - 2 * l)) & 256);
+        const int i2 = qs[2 * l + 1] | ((qh << (7 - 2 * l)) & 256);
+        s += iq3_group(orc_iq3s_tab[i1], orc_iq3s_tab[i2], signs[l], q8 + 8 * l);
+    }
+    return s;
+}
+static int iq3s_ls(const uint8_t *w, int ib) { return 2 * ((w[106 + ib / 2] >> (4 * (ib % 2))) & 15) + 1; }
+
 /* ---- geometry ------------------------------------------------------------ */
 
 int orc_geom(int ttype, int *be, int *bb) {
@@ -364,6 +433,8 @@ int orc_geom(int ttype, int *be, int *bb) {
     case ORC_TT_Q3_K: *be = 256; *bb = 110; return 1;
     case ORC_TT_Q5_K: *be = 256; *bb = 176; return 1;
     case ORC_TT_IQ4_XS: *be = 256; *bb = 136; return 1;
+    case ORC_TT_IQ3_XXS: *be = 256; *bb = 98; return 1;
+    case ORC_TT_IQ3_S: *be = 256; *bb = 110; return 1;
     case ORC_TT_Q4_0: *be = 32; *bb = 18; return 1;
     case ORC_TT_Q4_1: *be = 32; *bb = 20; return 1;
     default: return 0;
@@ -522,6 +593,37 @@ static float dot_iq4_xs(int n, const void *vw, const void *va) {
     return sumf;
 }
 
+/* iq_kernels.c:612-643: bsum = sum_ib sumi_ib * (2 ls + 1) per super-block,
+ * sumf += (d * dy) * bsum, and 0.25 * sumf at the end */
+static float dot_iq3_xxs(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 98, a += 292) {
+        float dy;
+        memcpy(&dy, a, 4);
+        const float d = orc_f16_to_f32_k256(ld16(w)) * dy;
+        int32_t bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) bsum += orc_blk_iq3_xxs(w, a, ib) * iq3xxs_ls(w, ib);
+        sumf += d * (float)bsum;
+    }
+    return 0.25f * sumf;
+}
+
+/* iq_kernels.c:1728-1772: as IQ3_XXS without the final 0.25 */
+static float dot_iq3_s(int n, const void *vw, const void *va) {
+    const uint8_t *w = vw, *a = va;
+    float sumf = 0.0f;
+    for (int b = 0; b < n / 256; ++b, w += 110, a += 292) {
+        float dy;
+        memcpy(&dy, a, 4);
+        const float d = orc_f16_to_f32_k256(ld16(w)) * dy;
+        int32_t bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) bsum += orc_blk_iq3_s(w, a, ib) * iq3s_ls(w, ib);
+        sumf += d * (float)bsum;
+    }
+    return sumf;
+}
+
 orc_dot_fn orc_dot_fn_for(int ttype) {
     switch (ttype) {
     case ORC_TT_Q8_0: return dot_q8_0;
@@ -534,6 +636,8 @@ orc_dot_fn orc_dot_fn_for(int ttype) {
     case ORC_TT_IQ4_XS: return dot_iq4_xs;
     case ORC_TT_Q4_0: return dot_q4_0;
     case ORC_TT_Q4_1: return dot_q4_1;
+    case ORC_TT_IQ3_XXS: return dot_iq3_xxs;
+    case ORC_TT_IQ3_S: return dot_iq3_s;
     default: return 0;
     }
 }
@@ -550,11 +654,11 @@ float orc_dot(int ttype, int n, const void *w, const void *a) {
 
 /* integers per weight block in orc_row_block_ints: (isum, summs) for the
  * K-quants with mins, (sumi, sumy) for Q4_1, one per 32-value block for
- * IQ4_XS, else one */
+ * IQ4_XS and the IQ3 formats (before the block scales), else one */
 int orc_block_nints(int ttype) {
     switch (ttype) {
     case ORC_TT_Q4_K: case ORC_TT_Q5_K: case ORC_TT_Q2_K: case ORC_TT_Q4_1: return 2;
-    case ORC_TT_IQ4_XS: return 8;
+    case ORC_TT_IQ4_XS: case ORC_TT_IQ3_XXS: case ORC_TT_IQ3_S: return 8;
     default: return 1;
     }
 }
@@ -577,6 +681,12 @@ int orc_row_block_ints(int ttype, int n, const void *vw, const void *va, int32_t
         case ORC_TT_Q3_K: out[b] = orc_blk_q3_k(w + 110 * b, a + 292 * b); break;
         case ORC_TT_IQ4_XS:
             for (int ib = 0; ib < 8; ++ib) out[8 * b + ib] = orc_blk_iq4_xs(w + 136 * b, a + 292 * b, ib);
+            break;
+        case ORC_TT_IQ3_XXS:
+            for (int ib = 0; ib < 8; ++ib) out[8 * b + ib] = orc_blk_iq3_xxs(w + 98 * b, a + 292 * b, ib);
+            break;
+        case ORC_TT_IQ3_S:
+            for (int ib = 0; ib < 8; ++ib) out[8 * b + ib] = orc_blk_iq3_s(w + 110 * b, a + 292 * b, ib);
             break;
         }
     }
@@ -653,7 +763,7 @@ int orc_matvec_batch(int ttype, int rows, int cols, int k, const void *w,
 /* quant_dequant.zig:1388-1402 (Q8_0), :347-360 (IQ4_NL), :78-103 (Q4_0,
  * Q4_1), :54-77 (Q4_K),
  * :222-251 (Q6_K), :188-220 (Q5_K), :252-322 (Q3_K), :892-919 (Q2_K),
- * :324-345 (IQ4_XS). */
+ * :324-345 (IQ4_XS), :362-415 (IQ3_S), :417-445 (IQ3_XXS). */
 int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
     const uint8_t *w = vw;
     if (orc_row_bytes(ttype, cols) < 0) return -1;
@@ -728,6 +838,43 @@ int orc_dequant_row(int ttype, int cols, const void *vw, float *out) {
                 int g = e / 16, k = e / 128, j = (e % 128) / 32, l = e % 32;
                 float dl = d * (float)(blk[g] & 15), ml = mn * (float)(blk[g] >> 4);
                 o[e] = dl * (float)((blk[16 + 32 * k + l] >> (2 * j)) & 3) - ml;
+            }
+        } else if (ttype == ORC_TT_IQ3_XXS) {
+            /* db = d * (0.5 + ls4) * 0.5; value = (db * g) * (+-1) */
+            const uint8_t *blk = w + 98 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk));
+            for (int ib = 0; ib < 8; ++ib) {
+                uint32_t aux;
+                memcpy(&aux, blk + 66 + 4 * ib, 4);
+                const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+                for (int l = 0; l < 4; ++l) {
+                    const uint8_t sg = orc_ksigns((aux >> (7 * l)) & 127);
+                    const uint32_t g1 = orc_iq3xxs_tab[blk[2 + 8 * ib + 2 * l]];
+                    const uint32_t g2 = orc_iq3xxs_tab[blk[2 + 8 * ib + 2 * l + 1]];
+                    for (int j = 0; j < 4; ++j) {
+                        o[32 * ib + 8 * l + j] = db * (float)((g1 >> (8 * j)) & 255) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                        o[32 * ib + 8 * l + 4 + j] =
+                            db * (float)((g2 >> (8 * j)) & 255) * ((sg >> (4 + j)) & 1 ? -1.0f : 1.0f);
+                    }
+                }
+            }
+        } else if (ttype == ORC_TT_IQ3_S) {
+            /* db = d * (1 + 2 * nibble); value = (db * g) * (+-1) */
+            const uint8_t *blk = w + 110 * b;
+            float d = orc_f16_to_f32_k256(ld16(blk));
+            for (int ib = 0; ib < 8; ++ib) {
+                const float db = d * (float)iq3s_ls(blk, ib);
+                const unsigned qh = blk[66 + ib];
+                for (int l = 0; l < 4; ++l) {
+                    const uint8_t sg = blk[74 + 4 * ib + l];
+                    const uint32_t g1 = orc_iq3s_tab[blk[2 + 8 * ib + 2 * l] | ((qh << (8 - 2 * l)) & 256)];
+                    const uint32_t g2 = orc_iq3s_tab[blk[2 + 8 * ib + 2 * l + 1] | ((qh << (7 - 2 * l)) & 256)];
+                    for (int j = 0; j < 4; ++j) {
+                        o[32 * ib + 8 * l + j] = db * (float)((g1 >> (8 * j)) & 255) * ((sg >> j) & 1 ? -1.0f : 1.0f);
+                        o[32 * ib + 8 * l + 4 + j] =
+                            db * (float)((g2 >> (8 * j)) & 255) * ((sg >> (4 + j)) & 1 ? -1.0f : 1.0f);
+                    }
+                }
             }
         } else if (ttype == ORC_TT_IQ4_XS) {
             const uint8_t *blk = w + 136 * b;

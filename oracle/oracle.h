@@ -13,10 +13,13 @@
  *   Q8_0 x Q8_0            src/kernels/x86/kernels32.c:447-464, kernels512.c:53-81
  *   IQ4_NL x Q8_0          src/kernels/x86/kernels32.c:342-361 (+ iq_tables.zig:429-432)
  *   Q4_0 / Q4_1 x Q8_0     src/kernels/x86/kernels32.c:297-340
+ *   IQ3_XXS / IQ3_S x Q8_K src/kernels/x86/iq_kernels.c:612-643, :1728-1772
+ *                          (grids: src/iq_tables.zig:323-425, ksigns :42-61)
  *   Q4_K x Q8_K            src/kernels/x86/kernels256.c:105-125, :179-186, :474-498
  *   Q6_K x Q8_K            src/kernels/x86/kernels256.c:200-212, :720-738
  *   matvec / batch driver  src/backend_cpu.zig:167-289, :328-446; src/pool.zig:300-336, :468-550
- *   dequant (fixtures)     src/quant_dequant.zig:54-77, :78-103, :222-251, :347-360, :1388-1402
+ *   dequant (fixtures)     src/quant_dequant.zig:54-77, :78-103, :222-251, :347-360,
+ *                          :362-415, :417-445, :1388-1402
  *
  * Float results follow the scalar / AVX-512-VNNI tier order (one sequential
  * per-block fold).  The reference's AVX2 tier folds Q4_K/Q6_K with 8-lane
@@ -43,6 +46,8 @@ extern "C" {
 #define ORC_TT_IQ4_XS 23
 #define ORC_TT_Q4_0   2
 #define ORC_TT_Q4_1   3
+#define ORC_TT_IQ3_XXS 18
+#define ORC_TT_IQ3_S  21
 
 float    orc_f16_to_f32(uint16_t h);        /* kernels32.c:45-66 (+0 for -0)  */
 float    orc_f16_to_f32_k256(uint16_t h);   /* kernels256.c:51-78 (keeps -0) */
@@ -62,6 +67,14 @@ int32_t orc_blk_q3_k(const uint8_t *w, const uint8_t *a);
 int32_t orc_blk_iq4_xs(const uint8_t *w, const uint8_t *a, int ib);
 int32_t orc_blk_q4_0(const uint8_t *w, const uint8_t *a);
 void    orc_blk_q4_1(const uint8_t *w, const uint8_t *a, int32_t *sumi, int32_t *sumy);
+/* IQ3 32-value sub-block ib of a super-block: the signed grid values times q8,
+ * before the sub-block scale 2*ls+1 */
+int32_t orc_blk_iq3_xxs(const uint8_t *w, const uint8_t *a, int ib);
+int32_t orc_blk_iq3_s(const uint8_t *w, const uint8_t *a, int ib);
+/* grid entry i (u32, byte j = value j) and the sign mask of 7-bit index i */
+uint32_t orc_iq3xxs_grid(int i);
+uint32_t orc_iq3s_grid(int i);
+uint8_t  orc_ksigns(int i);
 
 /* Geometry: returns 1 and fills the outputs for a supported type, else 0. */
 int orc_geom(int ttype, int *block_elems, int *block_bytes);

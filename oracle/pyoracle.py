@@ -19,20 +19,23 @@ REF_SO = HERE / "_ref" / "libqref.so"
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20
 TT_Q2_K, TT_Q3_K, TT_Q5_K, TT_IQ4_XS = 10, 11, 13, 23
 TT_Q4_0, TT_Q4_1 = 2, 3
+TT_IQ3_XXS, TT_IQ3_S = 18, 21
 GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210),
         TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136),
-        TT_Q4_0: (32, 18), TT_Q4_1: (32, 20)}
+        TT_Q4_0: (32, 18), TT_Q4_1: (32, 20), TT_IQ3_XXS: (256, 98), TT_IQ3_S: (256, 110)}
 NAMES = {TT_Q8_0: "Q8_0", TT_Q4_K: "Q4_K", TT_Q6_K: "Q6_K", TT_IQ4_NL: "IQ4_NL",
          TT_Q2_K: "Q2_K", TT_Q3_K: "Q3_K", TT_Q5_K: "Q5_K", TT_IQ4_XS: "IQ4_XS",
-         TT_Q4_0: "Q4_0", TT_Q4_1: "Q4_1"}
-# the formats of the benchmark configurations, the further K-quant family, and
-# the legacy 32-value formats of real GGUF files (Q8_0 activations)
+         TT_Q4_0: "Q4_0", TT_Q4_1: "Q4_1", TT_IQ3_XXS: "IQ3_XXS", TT_IQ3_S: "IQ3_S"}
+# the formats of the benchmark configurations, the further K-quant family, the
+# legacy 32-value formats (Q8_0 activations) and the 3-bit grid formats of real
+# GGUF files
 BASE_TYPES = [TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL]
-EXTRA_TYPES = [TT_Q5_K, TT_Q3_K, TT_Q2_K, TT_IQ4_XS, TT_Q4_0, TT_Q4_1]
+EXTRA_TYPES = [TT_Q5_K, TT_Q3_K, TT_Q2_K, TT_IQ4_XS, TT_Q4_0, TT_Q4_1, TT_IQ3_XXS, TT_IQ3_S]
 ALL_TYPES = BASE_TYPES + EXTRA_TYPES
 # integers per weight block in block_ints: (isum, summs) for the K-quants with
-# mins, (sumi, sumy) for Q4_1, one per 32-value block for IQ4_XS, else one
-NINTS = {TT_Q4_K: 2, TT_Q5_K: 2, TT_Q2_K: 2, TT_IQ4_XS: 8, TT_Q4_1: 2}
+# mins, (sumi, sumy) for Q4_1, one per 32-value block (before its scale) for
+# IQ4_XS and the IQ3 formats, else one
+NINTS = {TT_Q4_K: 2, TT_Q5_K: 2, TT_Q2_K: 2, TT_IQ4_XS: 8, TT_Q4_1: 2, TT_IQ3_XXS: 8, TT_IQ3_S: 8}
 
 _c_u8p = ctypes.POINTER(ctypes.c_uint8)
 _c_f32p = ctypes.POINTER(ctypes.c_float)
@@ -92,6 +95,11 @@ class Oracle:
         L.orc_dot_fn_for.argtypes = [ctypes.c_int]
         L.orc_quant_fn_for.restype = ctypes.c_void_p
         L.orc_quant_fn_for.argtypes = [ctypes.c_int]
+        for name in ("orc_iq3xxs_grid", "orc_iq3s_grid"):
+            getattr(L, name).restype = ctypes.c_uint32
+            getattr(L, name).argtypes = [ctypes.c_int]
+        L.orc_ksigns.restype = ctypes.c_uint8
+        L.orc_ksigns.argtypes = [ctypes.c_int]
 
     def f16_to_f32(self, h: int) -> float:
         return self.lib.orc_f16_to_f32(h)
@@ -157,6 +165,14 @@ class Oracle:
 
     def dot_fn_addr(self, ttype: int) -> int:
         return self.lib.orc_dot_fn_for(ttype)
+
+    def iq3_grid(self, ttype: int) -> np.ndarray:
+        """The oracle's IQ3_XXS (256) or IQ3_S (512) grid as u32 entries."""
+        n, f = (256, self.lib.orc_iq3xxs_grid) if ttype == TT_IQ3_XXS else (512, self.lib.orc_iq3s_grid)
+        return np.array([f(i) for i in range(n)], np.uint32)
+
+    def ksigns(self) -> np.ndarray:
+        return np.array([self.lib.orc_ksigns(i) for i in range(128)], np.uint8)
 
 
 class RefKernels:

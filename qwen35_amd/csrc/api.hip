@@ -23,6 +23,8 @@ static bool geom(int ttype, int& be, int& bb) {
     case TT_Q3_K: be = 256; bb = 110; return true;
     case TT_Q2_K: be = 256; bb = 84; return true;
     case TT_IQ4_XS: be = 256; bb = 136; return true;
+    case TT_IQ3_XXS: be = 256; bb = 98; return true;
+    case TT_IQ3_S: be = 256; bb = 110; return true;
     default: return false;
   }
 }
@@ -78,7 +80,7 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
 // 5.3 / 7.9 us at 8, 8.1 / 8.0 us at 16.
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
-    case TT_Q4_K: case TT_Q5_K: case TT_IQ4_XS: case TT_Q6_K: return 8;
+    case TT_Q4_K: case TT_Q5_K: case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: return 8;
     default: return 16;
   }
 }
@@ -86,7 +88,8 @@ static int mmq_min_tokens(int ttype) {
 // Formats with an MMQ kernel; the others (Q3_K, Q2_K) multiply many tokens
 // with the GEMV, which shares each weight load across up to 8 tokens per pass.
 static bool mmq_supported(int ttype) {
-  return act32(ttype) || ttype == TT_Q4_K || ttype == TT_Q6_K || ttype == TT_Q5_K || ttype == TT_IQ4_XS;
+  return act32(ttype) || iq3(ttype) || ttype == TT_Q4_K || ttype == TT_Q6_K || ttype == TT_Q5_K ||
+         ttype == TT_IQ4_XS;
 }
 
 // The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image

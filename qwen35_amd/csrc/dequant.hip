@@ -13,6 +13,8 @@
 //   IQ4_XS  (d * (ls - 32)) * codebook[nibble]        :324-345
 //   Q4_0    (nibble - 8) * d                          :78-88
 //   Q4_1    nibble * d + m                            :90-103
+//   IQ3_XXS (d * (0.5 + ls) * 0.5) * grid * sign      :417-445
+//   IQ3_S   (d * (1 + 2 ls)) * grid * sign            :362-415
 // The library is compiled with -ffp-contract=off, so each product and the
 // Q4_K difference round exactly as the reference's Zig (strict float mode).
 //
@@ -132,6 +134,31 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ src
       const int j = (e0 + i) % 32;
       const uint32_t q = blk[8 + 16 * ib + (j & 15)];
       o[i] = dl * (float)iq4_value(j < 16 ? (q & 15u) : (q >> 4));
+    }
+  } else if constexpr (iq3(TT)) {
+    // the four values are one grid entry: group k of sub-block ib
+    // (IQ3_XXS quant_dequant.zig:417-445: db = d * (0.5 + ls) * 0.5;
+    //  IQ3_S :362-415: db = d * (1 + 2 ls); value = (db * g) * (+-1))
+    constexpr int BB = TT == TT_IQ3_XXS ? 98 : 110;
+    const uint8_t* blk = src + (v0 / 256) * BB;
+    const int e0 = (int)(v0 % 256), ib = e0 / 32, k = (e0 % 32) / 4;
+    const float d = h2f(ld16b(blk));
+    uint32_t e, s8;
+    float db;
+    if constexpr (TT == TT_IQ3_XXS) {
+      const uint32_t aux = ld16b(blk + 66 + 4 * ib) | (ld16b(blk + 68 + 4 * ib) << 16);
+      e = kIq3xxsGrid[blk[2 + 8 * ib + k]];
+      s8 = iq_sign8((aux >> (7 * (k >> 1))) & 127u);
+      db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+    } else {
+      e = kIq3sGrid[blk[2 + 8 * ib + k] | (((blk[66 + ib] >> k) & 1u) << 8)];
+      s8 = blk[74 + 4 * ib + (k >> 1)];
+      db = d * (float)(1 + 2 * (int)((blk[106 + ib / 2] >> (4 * (ib % 2))) & 15u));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float g = (float)((e >> (8 * i)) & 255u);
+      o[i] = db * g * (((s8 >> (4 * (k & 1) + i)) & 1u) ? -1.0f : 1.0f);
     }
   } else {  // Q6_K
     const uint8_t* blk = src + (v0 / 256) * 210;

@@ -29,6 +29,7 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
                                                float* __restrict__ Y, int rows, long row_bytes,
                                                long act_bytes, int upr, int team, int tokens) {
   using U = Unit<TT>;
+  grid_prologue<TT>();
   const int lane = threadIdx.x & 63;
   const int tpw = 64 / team;                       // teams per wave
   const int r = lane / team, j = lane - r * team;  // team index, lane in team
@@ -98,6 +99,7 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
                                                   float* __restrict__ Y, int rows, long row_bytes,
                                                   int upr) {
   using U = Unit<TT>;
+  grid_prologue<TT>();
   constexpr int TPB = 4 / WV;  // teams per workgroup
   __shared__ float part[4][NR];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
@@ -163,6 +165,7 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
                                                  uint8_t* __restrict__ XQ, float* __restrict__ Y, int rows,
                                                  int cols, long row_bytes, int upr, int team) {
   using U = Unit<TT>;
+  grid_prologue<TT>();
   constexpr bool K32 = act32(TT);
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nblk = K32 ? cols / 32 : cols / 256;
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
 // `ints`: [tokens][rows][nints]; nints = 32-value blocks per row (twice that
 // for Q4_1: sumi, sumy per block), or per super-block 2 (isum, summs: Q4_K,
 // Q5_K, Q2_K) or 1 (Q6_K, Q3_K).
-constexpr bool per_block_ints(int tt) { return act32(tt) || tt == TT_IQ4_XS; }
+constexpr bool per_block_ints(int tt) { return act32(tt) || tt == TT_IQ4_XS || iq3(tt); }
 
 template <int TT>
 __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ W,
@@ -291,6 +294,7 @@ __global__ __launch_bounds__(256) void k_block_ints(const uint8_t* __restrict__ 
                                                      int* __restrict__ ints, int rows, int groups,
                                                      long row_bytes, long act_bytes, int tokens) {
   using U = Unit<TT>;
+  grid_prologue<TT>();
   const long gid = (long)blockIdx.x * 256 + threadIdx.x;
   if (gid >= (long)tokens * rows * groups) return;
   const int g = (int)(gid % groups);
@@ -365,7 +369,7 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
     }
   } else {
     constexpr int BB = TT == TT_Q4_K ? 144 : TT == TT_Q6_K ? 210 : TT == TT_Q5_K ? 176 : TT == TT_Q3_K ? 110
-                     : TT == TT_Q2_K ? 84 : 136;
+                     : TT == TT_Q2_K ? 84 : TT == TT_IQ3_XXS ? 98 : TT == TT_IQ3_S ? 110 : 136;
     for (int b = 0; b < cols / 256; ++b, w += BB, a += 292) {
       const float dy = __builtin_bit_cast(float, ldb16(a) | (ldb16(a + 2) << 16));
       const int8_t* q8 = (const int8_t*)(a + 4);
@@ -438,6 +442,34 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
           summs += (w[g] >> 4) * sext16(ldb16(a + 260 + 2 * g));
         }
         acc += (dy * h2f(ldb16(w + 80))) * (float)isum - (dy * h2f(ldb16(w + 82))) * (float)summs;
+      } else if constexpr (iq3(TT)) {
+        // grid entries from constant memory; value j of entry e is byte j
+        int bsum = 0;
+        for (int ib = 0; ib < 8; ++ib) {
+          int sumi = 0, ls;
+          for (int k = 0; k < 8; ++k) {  // 4-value group k of the sub-block
+            uint32_t e, s8;
+            if constexpr (TT == TT_IQ3_XXS) {
+              const uint32_t aux = (uint32_t)w[66 + 4 * ib] | ((uint32_t)w[67 + 4 * ib] << 8) |
+                                   ((uint32_t)w[68 + 4 * ib] << 16) | ((uint32_t)w[69 + 4 * ib] << 24);
+              e = kIq3xxsGrid[w[2 + 8 * ib + k]];
+              s8 = iq_sign8((aux >> (7 * (k >> 1))) & 127u);
+              ls = 2 * (int)(aux >> 28) + 1;
+            } else {
+              e = kIq3sGrid[w[2 + 8 * ib + k] | (((w[66 + ib] >> k) & 1u) << 8)];
+              s8 = w[74 + 4 * ib + (k >> 1)];
+              ls = 2 * (int)((w[106 + ib / 2] >> (4 * (ib % 2))) & 15u) + 1;
+            }
+            for (int j = 0; j < 4; ++j) {
+              const int v = (int)((e >> (8 * j)) & 255u);
+              const bool neg = (s8 >> (4 * (k & 1) + j)) & 1u;
+              sumi += (neg ? -v : v) * (int)q8[32 * ib + 4 * k + j];
+            }
+          }
+          bsum += ls * sumi;
+        }
+        const float dd = h2f(ldb16(w)) * dy;
+        acc += TT == TT_IQ3_XXS ? dd * (float)bsum * 0.25f : dd * (float)bsum;
       } else {  // IQ4_XS
         const float d4d8 = h2f(ldb16(w)) * dy;
         const uint32_t sh = ldb16(w + 2);
@@ -537,7 +569,10 @@ static hipError_t launch_gemv_type(const GemvArgs& g, int team, int nt, int nr, 
 // teams on rows of >= 8192 values (IQ4_NL 5.8 vs 6.7 us, Q4_0 5.5 vs 6.4,
 // Q4_1 5.2 vs 6.4), two-wave teams for Q4_0 / Q4_1 from 4096 values (Q4_1
 // 11.5 vs 15.8 us: its 40-byte units need no realignment and stream at
-// 4.8 TB/s), else two rows per 40- or 20-lane team.
+// 4.8 TB/s), else two rows per 40- or 20-lane team.  IQ3_XXS / IQ3_S (grid
+// lookups in LDS make their decode VALU-heavy), swept at the same shapes:
+// four-wave teams of two rows on rows of >= 8192 values (6.1 vs 7.5 us),
+// one row per 20-lane team at width 2560 (9.3 vs 10.1 us), two from 4096.
 static void default_shape(const GemvArgs& g, int& team, int& nr) {
   const int upr = g.cols / 64;
   const bool nib32 = g.ttype == TT_Q4_0 || g.ttype == TT_Q4_1 || g.ttype == TT_IQ4_NL;
@@ -550,6 +585,11 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
   if (nib32 && upr >= 128) {
     team = 256;
     nr = g.ttype == TT_Q4_1 ? 2 : 1;
+    return;
+  }
+  if (iq3(g.ttype) && upr >= 128) {
+    team = 256;
+    nr = 2;
     return;
   }
   if ((g.ttype == TT_Q4_0 || g.ttype == TT_Q4_1) && upr >= 64) {
@@ -569,6 +609,7 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
     case TT_IQ4_NL: nr = 4; team = 20; break;
     case TT_Q4_0: case TT_Q4_1: nr = 2; team = upr <= 40 ? 40 : 20; break;
     case TT_IQ4_XS: case TT_Q2_K: nr = 2; team = 20; break;
+    case TT_IQ3_XXS: case TT_IQ3_S: nr = upr >= 64 ? 2 : 1; team = 20; break;
     case TT_Q3_K: nr = 1; team = 64; break;
     default: nr = g.rows >= 4096 ? 2 : 1; team = 16; break;
   }

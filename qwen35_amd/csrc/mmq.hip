@@ -32,6 +32,8 @@
 //   Q5_K          as Q4_K on the 5-bit values  (kernels256.c:605-629)
 //   IQ4_XS        as Q4_K on the codebook values with the signed scale
 //                 ls - 32, no mins  (iq_kernels.c:967-1001)
+//   IQ3_XXS/IQ3_S the same on the signed grid values with the odd scale
+//                 2 ls + 1  (iq_kernels.c:612-643, :1728-1772)
 // and the float scaling follows per block / super-block.  For the 32-value
 // formats the accumulator input is the bit pattern of 1.5*2^23, so the MFMA
 // result read as a float is 1.5*2^23 + sumi exactly (|sumi| <= 2^19); one
@@ -98,6 +100,11 @@ template <int BT, int BR>
 struct alignas(16) MmqSmem<TT_Q5_K, BT, BR, false> : MmqSmem<TT_Q4_K, BT, BR, false> {};
 template <int BT, int BR>
 struct alignas(16) MmqSmem<TT_IQ4_XS, BT, BR, false> : MmqSmem<TT_Q4_K, BT, BR, false> {};
+// the IQ3 formats: the same image with the odd sub-block scale 2 ls + 1
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_IQ3_XXS, BT, BR, false> : MmqSmem<TT_Q4_K, BT, BR, false> {};
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_IQ3_S, BT, BR, false> : MmqSmem<TT_Q4_K, BT, BR, false> {};
 
 template <int BT, int BR>
 struct alignas(16) MmqSmem<TT_Q6_K, BT, BR, false> {
@@ -240,6 +247,42 @@ __device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename U
     sp[0] = (uint8_t)(ls0 - 32);
     sp[1] = (uint8_t)(ls1 - 32);
     if (u4 == 0) sm.wd[row] = h2f(w.h0);
+  } else if constexpr (iq3(TT)) {
+    // signed grid values of sub-blocks 2u4 and 2u4+1 (Unit<>::sub's decode),
+    // their scale bytes 2 ls + 1; IQ3_XXS folds its 1/4 into d (exact)
+    uint32_t v[16];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int l = 0; l < 4; ++l) {
+        const uint32_t qq = w.q[2 * b + (l >> 1)] >> (16 * (l & 1));
+        uint32_t e1, e2, s8;
+        if constexpr (TT == TT_IQ3_XXS) {
+          e1 = g_iq3_grid[qq & 255u];
+          e2 = g_iq3_grid[(qq >> 8) & 255u];
+          s8 = iq_sign8((w.aux[b] >> (7 * l)) & 127u);
+        } else {
+          const uint32_t qh = w.qh >> (8 * b);
+          e1 = Unit<TT_IQ3_S>::entry(qq, qh, 2 * l);
+          e2 = Unit<TT_IQ3_S>::entry(qq >> 8, qh, 2 * l + 1);
+          s8 = w.sg[b] >> (8 * l);
+        }
+        v[8 * b + 2 * l] = apply_signs4(e1, s8);
+        v[8 * b + 2 * l + 1] = apply_signs4(e2, s8 >> 4);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st16(dst + 16 * i, v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    uint8_t* sp = (uint8_t*)&sm.wsc[row][0] + 2 * u4;
+    if constexpr (TT == TT_IQ3_XXS) {
+      sp[0] = (uint8_t)(2 * (w.aux[0] >> 28) + 1);
+      sp[1] = (uint8_t)(2 * (w.aux[1] >> 28) + 1);
+      if (u4 == 0) sm.wd[row] = h2f(w.d) * 0.25f;
+    } else {
+      sp[0] = (uint8_t)(2 * (w.sc & 15u) + 1);
+      sp[1] = (uint8_t)(2 * (w.sc >> 4) + 1);
+      if (u4 == 0) sm.wd[row] = h2f(w.d);
+    }
   } else {  // Q6_K: unit (h, lh) holds values 128h + 32q + 16lh + (0..15), q = 0..3
     const int h = (u4 >> 1) & 1, lh = u4 & 1;
     uint32_t v[4][4];
@@ -311,6 +354,7 @@ template <int TT, int BT, int BR>
 __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                               float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                               long act_bytes, int upr, int ntile_t, int ksplit, int cps) {
+  grid_prologue<TT>();
   constexpr bool K32 = act32(TT);
   // waves: 2 x 2 over (tokens, rows), or 1 x 4 (stacked along rows) for a
   // 32-token tile
@@ -469,7 +513,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
           finish(s2, c0, dw0);
         }
       }
-    } else if constexpr (TT == TT_Q4_K || TT == TT_Q5_K || TT == TT_IQ4_XS) {
+    } else if constexpr (TT == TT_Q4_K || TT == TT_Q5_K || TT == TT_IQ4_XS || iq3(TT)) {
       i32x16 isum[NA][NB];
       const i32x16 zero = {};
 #pragma unroll
@@ -515,7 +559,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         if (s + 2 < 8) issue(s + 2, c0);
         finish(s + 1, c1);
       }
-      if constexpr (TT == TT_IQ4_XS) {
+      if constexpr (TT == TT_IQ4_XS || iq3(TT)) {
         // no mins: acc += (d * dy) * isum  (iq_kernels.c:967-1001, one
         // rounding of the exact super-block integer instead of one per block)
         f32x4 dy[NA][4];
@@ -1076,6 +1120,8 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
     case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, ksplit, s);
     case TT_Q4_0: return launch_mmq_type<TT_Q4_0>(g, bt, br, ksplit, s);
     case TT_Q4_1: return launch_mmq_type<TT_Q4_1>(g, bt, br, ksplit, s);
+    case TT_IQ3_XXS: return launch_mmq_type<TT_IQ3_XXS>(g, bt, br, ksplit, s);
+    case TT_IQ3_S: return launch_mmq_type<TT_IQ3_S>(g, bt, br, ksplit, s);
     case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, ksplit, s);
     case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, ksplit, s);
     case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, ksplit, s);

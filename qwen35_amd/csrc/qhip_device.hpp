@@ -4,9 +4,9 @@
 // 64-value work unit.
 //
 // The 32-value formats (Q8_0, IQ4_NL, Q4_0, Q4_1) pair with a Q8_0 activation
-// (34 B / 32 values), the K-quants and IQ4_XS with a Q8_K activation (292 B /
-// 256 values), as the reference's actFamily (src/backend_cpu.zig:42-50)
-// prescribes.
+// (34 B / 32 values), the K-quants, IQ4_XS and the IQ3 grid formats with a
+// Q8_K activation (292 B / 256 values), as the reference's actFamily
+// (src/backend_cpu.zig:42-50) prescribes.
 //
 // Integer arithmetic inside a block is exact and equals the reference's
 // per-block integers (src/kernels/x86/kernels32.c:342-361, :447-464;
@@ -16,14 +16,18 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "iq_grids.h"
+
 #include <type_traits>
 
 namespace qhip {
 
 enum : int {
   TT_Q4_0 = 2, TT_Q4_1 = 3, TT_Q8_0 = 8, TT_Q2_K = 10, TT_Q3_K = 11, TT_Q4_K = 12, TT_Q5_K = 13,
-  TT_Q6_K = 14, TT_IQ4_NL = 20, TT_IQ4_XS = 23
+  TT_Q6_K = 14, TT_IQ3_XXS = 18, TT_IQ4_NL = 20, TT_IQ3_S = 21, TT_IQ4_XS = 23
 };
+
+__host__ __device__ constexpr bool iq3(int tt) { return tt == TT_IQ3_XXS || tt == TT_IQ3_S; }
 
 // Formats of 32-value blocks, which take a Q8_0 activation; the others take Q8_K.
 __host__ __device__ constexpr bool act32(int tt) {
@@ -173,6 +177,44 @@ __device__ __forceinline__ uint32_t iq4_lo(uint32_t q) {
 }
 __device__ __forceinline__ uint32_t iq4_hi(uint32_t q) {
   return iq4_lookup((q >> 4) & 0x07070707u, ((q >> 5) & 0x04040404u) | 0x03020100u);
+}
+
+// ---- IQ3 grids and signs --------------------------------------------------------
+// The grids of iq_grids.h expanded to u32 entries (byte j = value j) in
+// constant memory.  Kernels of an IQ3 format first stage their grid into LDS
+// (grid_prologue), so the per-lane lookups are LDS reads, not divergent
+// global loads; the byte-granular generic and dequant kernels read constant
+// memory directly.
+#define QHIP_XXS_ENTRY(c) QHIP_IQ3_EXPAND(QHIP_IQ3XXS_LEVEL, c),
+#define QHIP_S_ENTRY(c) QHIP_IQ3_EXPAND(QHIP_IQ3S_LEVEL, c),
+static __constant__ uint32_t kIq3xxsGrid[256] = {QHIP_IQ3XXS_CODES(QHIP_XXS_ENTRY)};
+static __constant__ uint32_t kIq3sGrid[512] = {QHIP_IQ3S_CODES(QHIP_S_ENTRY)};
+#undef QHIP_XXS_ENTRY
+#undef QHIP_S_ENTRY
+static __shared__ uint32_t g_iq3_grid[512];
+
+// Every thread of the workgroup must call it before any early exit.
+template <int TT>
+__device__ __forceinline__ void grid_prologue() {
+  if constexpr (iq3(TT)) {
+    constexpr int N = TT == TT_IQ3_XXS ? 256 : 512;
+    for (int i = threadIdx.x; i < N; i += blockDim.x) g_iq3_grid[i] = TT == TT_IQ3_XXS ? kIq3xxsGrid[i] : kIq3sGrid[i];
+    __syncthreads();
+  }
+}
+
+// ksigns_iq2xs (src/iq_tables.zig:42-61): a 7-bit index completed by bit 7 to
+// an even number of set bits; bit j negates value j of the 8.
+__device__ __forceinline__ uint32_t iq_sign8(uint32_t idx7) {
+  return idx7 | (((uint32_t)__builtin_popcount(idx7) & 1u) << 7);
+}
+// Four unsigned grid bytes (each >= 1) with the low 4 bits of `s` as per-byte
+// signs: t holds a 1 in each negated byte, m = 255 * t is 0xFF there, and
+// (g ^ m) + t is 256 - g in those bytes (no carry leaves a byte as g >= 1).
+__device__ __forceinline__ uint32_t apply_signs4(uint32_t g, uint32_t s) {
+  const uint32_t t = ((s & 15u) * 0x00204081u) & 0x01010101u;
+  const uint32_t m = (t << 8) - t;
+  return (g ^ m) + t;
 }
 
 // ---- per-format unit decode ------------------------------------------------------
@@ -809,6 +851,111 @@ struct Unit<TT_IQ4_XS> {
   }
 };
 
+// ---- IQ3 (Q8_K activations, quarter units as above) ------------------------------
+template <>
+struct Unit<TT_IQ3_XXS> {
+  // 98-byte super-block: f16 d, qs[64] grid indices (one per 4 values), 8 u32
+  // words (four 7-bit sign indices, the 4-bit scale in bits 28..31), one per
+  // 32-value sub-block.  Unit c: indices qs[16c..16c+15], words 2c and 2c+1
+  // (src/kernels/x86/iq_kernels.c:612-643).
+  static constexpr int kWBytes = 26, kInts = 2;
+  struct W { uint32_t q[4]; uint32_t aux[2]; uint32_t d; };
+  using A = ActQ8K;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* blk = row + 98 * (u >> 2);
+    const int c = u & 3;
+    W w;
+    const u32x4_u q = *(const u32x4_u*)(blk + 2 + 16 * c);
+    w.q[0] = q.x; w.q[1] = q.y; w.q[2] = q.z; w.q[3] = q.w;
+    const u32x2_u x = *(const u32x2_u*)(blk + 66 + 8 * c);
+    w.aux[0] = x.x;
+    w.aux[1] = x.y;
+    w.d = *(const uint16_t*)blk;
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return Unit<TT_Q4_K>::load_a(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    return Unit<TT_Q4_K>::load_a_split(sp, u);
+  }
+  // one 32-value sub-block: 8 index bytes q[0..1], its word, values y[0..7]
+  static __device__ __forceinline__ int sub(const uint32_t* q, uint32_t aux, const uint32_t* y) {
+    int s = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t qq = q[l >> 1] >> (16 * (l & 1));
+      const uint32_t sg = iq_sign8((aux >> (7 * l)) & 127u);
+      s = dot4(apply_signs4(g_iq3_grid[qq & 255u], sg), y[2 * l], s);
+      s = dot4(apply_signs4(g_iq3_grid[(qq >> 8) & 255u], sg >> 4), y[2 * l + 1], s);
+    }
+    return s;
+  }
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
+    out[0] = sub(w.q, w.aux[0], a.y);
+    out[1] = sub(w.q + 2, w.aux[1], a.y + 8);
+  }
+  // (d * dy) * sum (2 ls + 1) * sumi, times 1/4 (exact below 2^24)
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[2];
+    ints(w, a, s);
+    const int ls0 = 2 * (int)(w.aux[0] >> 28) + 1, ls1 = 2 * (int)(w.aux[1] >> 28) + 1;
+    return (h2f(w.d) * a.d) * (float)(ls0 * s[0] + ls1 * s[1]) * 0.25f;
+  }
+};
+
+template <>
+struct Unit<TT_IQ3_S> {
+  // 110-byte super-block: f16 d, qs[64] low index bytes, qh[8] (bit k of
+  // qh[ib] is index bit 8 of group k of sub-block ib), signs[32] (one mask per
+  // 8 values), scales[4] (4-bit pairs).  Unit c: qs[16c..16c+15], qh[2c..2c+1],
+  // signs[8c..8c+7], scales[c] (src/kernels/x86/iq_kernels.c:1728-1772).
+  static constexpr int kWBytes = 30, kInts = 2;
+  struct W { uint32_t q[4]; uint32_t sg[2]; uint32_t qh, sc, d; };
+  using A = ActQ8K;
+  static __device__ __forceinline__ W load_w(const uint8_t* row, int u) {
+    const uint8_t* blk = row + 110 * (u >> 2);
+    const int c = u & 3;
+    W w;
+    const u32x4_u q = *(const u32x4_u*)(blk + 2 + 16 * c);
+    w.q[0] = q.x; w.q[1] = q.y; w.q[2] = q.z; w.q[3] = q.w;
+    const u32x2_u s = *(const u32x2_u*)(blk + 74 + 8 * c);
+    w.sg[0] = s.x;
+    w.sg[1] = s.y;
+    w.qh = *(const uint16_t*)(blk + 66 + 2 * c);
+    w.sc = blk[106 + c];
+    w.d = *(const uint16_t*)blk;
+    return w;
+  }
+  static __device__ __forceinline__ A load_a(const uint8_t* act, int u) { return Unit<TT_Q4_K>::load_a(act, u); }
+  static __device__ __forceinline__ A load_a_split(const ActSplit& sp, int u) {
+    return Unit<TT_Q4_K>::load_a_split(sp, u);
+  }
+  static __device__ __forceinline__ uint32_t entry(uint32_t qq, uint32_t qh, int k) {
+    return g_iq3_grid[(qq & 255u) | (((qh >> k) & 1u) << 8)];
+  }
+  // one 32-value sub-block: 8 low index bytes q[0..1], its qh byte, 4 sign masks
+  static __device__ __forceinline__ int sub(const uint32_t* q, uint32_t qh, uint32_t sg, const uint32_t* y) {
+    int s = 0;
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const uint32_t qq = q[l >> 1] >> (16 * (l & 1));
+      const uint32_t s8 = sg >> (8 * l);
+      s = dot4(apply_signs4(entry(qq, qh, 2 * l), s8), y[2 * l], s);
+      s = dot4(apply_signs4(entry(qq >> 8, qh, 2 * l + 1), s8 >> 4), y[2 * l + 1], s);
+    }
+    return s;
+  }
+  static __device__ __forceinline__ void ints(const W& w, const A& a, int* out) {
+    out[0] = sub(w.q, w.qh & 255u, w.sg[0], a.y);
+    out[1] = sub(w.q + 2, w.qh >> 8, w.sg[1], a.y + 8);
+  }
+  static __device__ __forceinline__ float dot(const W& w, const A& a) {
+    int s[2];
+    ints(w, a, s);
+    const int ls0 = 2 * (int)(w.sc & 15u) + 1, ls1 = 2 * (int)(w.sc >> 4) + 1;
+    return (h2f(w.d) * a.d) * (float)(ls0 * s[0] + ls1 * s[1]);
+  }
+};
+
 // Calls f(std::integral_constant<int, TT>{}) for the format id `ttype`.
 template <class F>
 __host__ inline auto dispatch_type(int ttype, F&& f) -> decltype(f(std::integral_constant<int, TT_Q8_0>{})) {
@@ -823,6 +970,8 @@ __host__ inline auto dispatch_type(int ttype, F&& f) -> decltype(f(std::integral
     case TT_IQ4_XS: return f(std::integral_constant<int, TT_IQ4_XS>{});
     case TT_Q4_0: return f(std::integral_constant<int, TT_Q4_0>{});
     case TT_Q4_1: return f(std::integral_constant<int, TT_Q4_1>{});
+    case TT_IQ3_XXS: return f(std::integral_constant<int, TT_IQ3_XXS>{});
+    case TT_IQ3_S: return f(std::integral_constant<int, TT_IQ3_S>{});
     default: return hipErrorInvalidValue;
   }
 }

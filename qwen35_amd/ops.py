@@ -12,12 +12,12 @@ import torch
 from ._lib import QhipLinear, check, load
 
 _GEOM = {8: (32, 34), 20: (32, 18), 12: (256, 144), 14: (256, 210), 13: (256, 176), 11: (256, 110),
-         10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20)}
+         10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20), 18: (256, 98), 21: (256, 110)}
 # integers per 32-value block in the block-integer export: (sumi, sumy) for Q4_1
 _NINTS_32 = {3: 2}
 # integers per super-block in the block-integer export: (isum, summs) for
-# Q4_K / Q5_K / Q2_K, one per 32-value block for IQ4_XS, else one
-_NINTS_SB = {12: 2, 13: 2, 10: 2, 23: 8}
+# Q4_K / Q5_K / Q2_K, one per 32-value block for IQ4_XS and the IQ3 formats, else one
+_NINTS_SB = {12: 2, 13: 2, 10: 2, 23: 8, 18: 8, 21: 8}
 
 
 def _stream() -> ctypes.c_void_p:

@@ -15,6 +15,8 @@ inputs.  Block contents follow the generation rules of each configuration:
           same generation style)
 * Q4_0    random nibbles, f16 d = |N(0,1)| * 1e-3; Q4_1 the same plus an f16
           min m = N(0,1) * 8e-3
+* IQ3_XXS, IQ3_S  random grid indices, sign words and scale nibbles, f16 d =
+          |N(0,1)| * 1e-3
 * activations f32 ~ N(0,1) (Box-Muller)
 """
 from __future__ import annotations
@@ -26,11 +28,12 @@ import numpy as np
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20
 TT_Q2_K, TT_Q3_K, TT_Q5_K, TT_IQ4_XS = 10, 11, 13, 23
 TT_Q4_0, TT_Q4_1 = 2, 3
+TT_IQ3_XXS, TT_IQ3_S = 18, 21
 GEOM = {TT_Q8_0: (32, 34), TT_IQ4_NL: (32, 18), TT_Q4_K: (256, 144), TT_Q6_K: (256, 210),
         TT_Q2_K: (256, 84), TT_Q3_K: (256, 110), TT_Q5_K: (256, 176), TT_IQ4_XS: (256, 136),
-        TT_Q4_0: (32, 18), TT_Q4_1: (32, 20)}
+        TT_Q4_0: (32, 18), TT_Q4_1: (32, 20), TT_IQ3_XXS: (256, 98), TT_IQ3_S: (256, 110)}
 D_SCALE = {TT_Q8_0: 2e-4, TT_IQ4_NL: 1e-3, TT_Q4_K: 1e-3, TT_Q6_K: 1e-3, TT_Q2_K: 1e-3, TT_Q3_K: 1e-3,
-           TT_Q5_K: 1e-3, TT_IQ4_XS: 1e-3, TT_Q4_0: 1e-3, TT_Q4_1: 1e-3}
+           TT_Q5_K: 1e-3, TT_IQ4_XS: 1e-3, TT_Q4_0: 1e-3, TT_Q4_1: 1e-3, TT_IQ3_XXS: 1e-3, TT_IQ3_S: 1e-3}
 
 _GAMMA = np.uint64(0x9E3779B97F4A7C15)
 _M1 = np.uint64(0xBF58476D1CE4E5B9)
@@ -130,6 +133,10 @@ def make_weight(ttype: int, rows: int, cols: int, seed: int = 0, tag: int = 1) -
     elif ttype == TT_IQ4_XS:
         blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         blocks[:, 2:] = rand_bytes(substream(s, 2), nb * 134).reshape(nb, 134)
+    elif ttype in (TT_IQ3_XXS, TT_IQ3_S):
+        # every byte after d is free: grid indices, sign indices / masks, scales
+        blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
+        blocks[:, 2:] = rand_bytes(substream(s, 2), nb * (bb - 2)).reshape(nb, bb - 2)
     elif ttype == TT_Q4_0:
         blocks[:, 0:2] = d.view(np.uint8).reshape(nb, 2)
         blocks[:, 2:] = rand_bytes(substream(s, 2), nb * 16).reshape(nb, 16)

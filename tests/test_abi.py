@@ -50,7 +50,7 @@ def test_python_binding_covers_header(lib):
 def test_geometry(lib):
     be, bb = ctypes.c_int(), ctypes.c_int()
     table = {8: (32, 34), 12: (256, 144), 14: (256, 210), 20: (32, 18), 13: (256, 176), 11: (256, 110),
-             10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20)}
+             10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20), 18: (256, 98), 21: (256, 110)}
     for tt, (e, b) in table.items():
         assert lib.qhip_quant_geom(tt, ctypes.byref(be), ctypes.byref(bb)) == 1
         assert (be.value, bb.value) == (e, b)

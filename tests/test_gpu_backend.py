@@ -29,7 +29,8 @@ def backend(gpu):
                                           (po.TT_Q6_K, 64, 9728), (po.TT_IQ4_NL, 96, 2560),
                                           (po.TT_Q5_K, 128, 2560), (po.TT_Q3_K, 80, 2304),
                                           (po.TT_Q2_K, 96, 2560), (po.TT_IQ4_XS, 112, 2560),
-                                          (po.TT_Q4_0, 96, 2560), (po.TT_Q4_1, 96, 2560)])
+                                          (po.TT_Q4_0, 96, 2560), (po.TT_Q4_1, 96, 2560),
+                                          (po.TT_IQ3_XXS, 96, 2560), (po.TT_IQ3_S, 96, 2560)])
 def test_backend_matvec(gpu, oracle, backend, tt, rows, cols):
     w = synth.make_weight(tt, rows, cols, seed=21, tag=tt)
     x = synth.make_act(cols, 1, seed=21)
@@ -64,7 +65,7 @@ def test_backend_matvec_pair_adjacent_and_not(gpu, oracle, backend):
 
 
 @pytest.mark.parametrize("k", [1, 7, 16])
-@pytest.mark.parametrize("tt", [po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS])
+@pytest.mark.parametrize("tt", [po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS, po.TT_IQ3_XXS])
 def test_backend_batch_k(gpu, oracle, backend, k, tt):
     rows, cols = 80, 2560
     w = synth.make_weight(tt, rows, cols, seed=5, tag=tt)

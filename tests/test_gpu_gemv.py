@@ -86,6 +86,8 @@ SHAPES = {
     po.TT_IQ4_XS: [(80, 2560), (19, 256)],
     po.TT_Q4_0: [(200, 2560), (37, 256), (11, 224)],
     po.TT_Q4_1: [(150, 2560), (29, 256), (9, 224)],
+    po.TT_IQ3_XXS: [(90, 2560), (21, 256), (16, 2304)],
+    po.TT_IQ3_S: [(90, 2560), (21, 256), (16, 2304)],
 }
 CASES = [(tt, r, c) for tt in TYPES for (r, c) in SHAPES[tt]]
 
@@ -102,8 +104,9 @@ def test_block_ints_bit_exact(gpu, oracle, tt, rows, cols):
     act = oracle.quantize_act(tt, x)
     xq = ops.quantize_act(tt, xd)
     assert np.array_equal(xq.cpu().numpy(), act)
-    if cols % (64 if po.GEOM[tt][0] == 32 else 256):
-        # the export walks whole per-lane chunks; other widths are refused
+    if cols % (64 if po.GEOM[tt][0] == 32 else 256) or rows * po.row_bytes(tt, cols) % 4:
+        # the export walks whole per-lane chunks of a dword-sized weight
+        # buffer; other widths and sizes are refused
         with pytest.raises(qwen35_amd.QhipError):
             ops.block_ints(tt, wd, xq, rows, cols, 2)
         return
@@ -185,7 +188,8 @@ FUSED = [(po.TT_Q8_0, 300, 1024), (po.TT_Q8_0, 6144, 1024), (po.TT_IQ4_NL, 200, 
          (po.TT_Q4_K, 100, 2560), (po.TT_Q4_K, 19456, 2560), (po.TT_Q6_K, 50, 9728),
          (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 16, 2304), (po.TT_Q5_K, 100, 2560), (po.TT_Q3_K, 60, 2304),
          (po.TT_Q2_K, 70, 2560), (po.TT_IQ4_XS, 80, 2560), (po.TT_Q4_0, 200, 2560),
-         (po.TT_Q4_1, 150, 2560), (po.TT_Q4_1, 4096, 1024)]
+         (po.TT_Q4_1, 150, 2560), (po.TT_Q4_1, 4096, 1024), (po.TT_IQ3_XXS, 90, 2560),
+         (po.TT_IQ3_XXS, 6144, 2560), (po.TT_IQ3_S, 90, 2560), (po.TT_IQ3_S, 16, 2304)]
 
 
 @pytest.mark.parametrize("tt,rows,cols", FUSED, ids=[case_id(*c) for c in FUSED])

@@ -48,6 +48,10 @@ CASES = [
     (po.TT_Q4_0, 64, 2560, 16),
     (po.TT_Q4_1, 96, 576, 70),
     (po.TT_Q4_1, 130, 1024, 130),
+    (po.TT_IQ3_XXS, 150, 512, 65),
+    (po.TT_IQ3_XXS, 64, 2560, 16),
+    (po.TT_IQ3_S, 130, 768, 70),
+    (po.TT_IQ3_S, 33, 2560, 20),
 ]
 IDS = [f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in CASES]
 
@@ -75,7 +79,7 @@ def unit_scale_weight(tt, rows, cols, seed):
     w = synth.make_weight(tt, rows, cols, seed=seed, tag=tt).copy()
     be, bb = po.GEOM[tt]
     blk = w.reshape(rows, cols // be, bb)
-    if tt in (po.TT_Q8_0, po.TT_IQ4_NL, po.TT_IQ4_XS, po.TT_Q4_0):
+    if tt in (po.TT_Q8_0, po.TT_IQ4_NL, po.TT_IQ4_XS, po.TT_Q4_0, po.TT_IQ3_XXS, po.TT_IQ3_S):
         blk[:, :, 0:2] = F16_ONE
     elif tt in (po.TT_Q4_K, po.TT_Q5_K, po.TT_Q4_1):  # d = 1 and dmin (Q4_1: m) = 1
         blk[:, :, 0:2] = F16_ONE
@@ -95,11 +99,13 @@ def unit_scale_act(cols, tokens, seed):
 
 
 @pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS,
-                                po.TT_Q4_0, po.TT_Q4_1])
+                                po.TT_Q4_0, po.TT_Q4_1, po.TT_IQ3_XXS, po.TT_IQ3_S])
 def test_mmq_block_integers_exact(gpu, oracle, tt):
-    # IQ4_XS: the super-block sums carry the scales (up to 31), so half the
-    # width keeps every result below 2^24
-    rows, cols, tokens = 96, 512 if tt == po.TT_IQ4_XS else 1024, 72
+    # IQ4_XS / IQ3: the super-block sums carry the scales (up to 31), so a
+    # narrower width keeps every result below 2^24; IQ3_XXS's 1/4 leaves
+    # quarter values, exact with one super-block
+    cols = {po.TT_IQ4_XS: 512, po.TT_IQ3_S: 512, po.TT_IQ3_XXS: 256}.get(tt, 1024)
+    rows, tokens = 96, 72
     w = unit_scale_weight(tt, rows, cols, seed=5)
     x = unit_scale_act(cols, tokens, seed=5)
     act = oracle.quantize_act(tt, x)
@@ -115,6 +121,14 @@ def test_mmq_block_integers_exact(gpu, oracle, tt):
         ls = np.stack([((blk[:, :, 4 + ib // 2] >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
                        for ib in range(8)], axis=-1).reshape(rows, -1) - 32
         want = (ints * ls[None, :, :]).sum(-1)
+    elif tt in (po.TT_IQ3_XXS, po.TT_IQ3_S):
+        # per-block integers times 2 ls + 1 (d = 1, dy = 1); IQ3_XXS times 1/4
+        blk = w.reshape(rows, cols // 256, -1)
+        if tt == po.TT_IQ3_XXS:
+            ls = np.stack([blk[:, :, 66 + 4 * ib + 3] >> 4 for ib in range(8)], axis=-1)
+        else:
+            ls = np.stack([(blk[:, :, 106 + ib // 2] >> (4 * (ib % 2))) & 15 for ib in range(8)], axis=-1)
+        want = (ints * (2 * ls.reshape(rows, -1).astype(np.int64) + 1)[None, :, :]).sum(-1)
     else:
         want = ints.sum(-1)
     assert np.abs(want).max() < 2 ** 24  # every partial float sum is exact
@@ -123,6 +137,8 @@ def test_mmq_block_integers_exact(gpu, oracle, tt):
     wd = to_dev(w, gpu)
     for bt, br in TILES:
         got = ops.mmq_tuned(tt, wd, xq, rows, cols, tokens, bt, br).cpu().numpy()
+        if tt == po.TT_IQ3_XXS:
+            got = got * np.float32(4.0)  # exact: the 1/4 is a power of two
         assert np.array_equal(got.astype(np.int64), want), (bt, br)
         assert np.array_equal(got, want.astype(np.float32))
 
