@@ -23,8 +23,10 @@
 //   Q4_0, Q4_1    the same on nib - 8 (Q4_0) or the unsigned nibble (Q4_1,
 //                 whose min term m * dy * sumy is a rank-1 update in the
 //                 epilogue)  (kernels32.c:297-340)
-//   Q4_K          v_mfma_i32_32x32x32_i8 per 32-value sub-block, times its
-//                 6-bit scale in integer arithmetic; the mins term
+//   Q4_K          v_mfma_i32_32x32x32_i8 per 32-value sub-block on the
+//                 nibbles times the two halves of its 6-bit scale (sc = 8 sh
+//                 + sl, each product <= 105 fits int8), accumulated over the
+//                 super-block in two chains, isum = 8 C_hi + C_lo; the mins term
 //                 sum_j bsum[j]*min[j/2] as an exact f16 MFMA (K = 16
 //                 bsums, all partial sums < 2^24)  (kernels256.c:474-498)
 //   Q6_K          v_mfma_i32_32x32x16_i8 per 16-value group, times its int8
@@ -53,6 +55,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef long i64x1_a8 __attribute__((aligned(8)));
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kChunk = 256;         // values per staged K-chunk
 constexpr int kQS = kChunk + 16;    // LDS bytes per int8 row (pad: rows 4 banks apart)
@@ -526,6 +529,62 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         scw[b][0] = sm.wsc[rb0 + 32 * b + li][0];
         scw[b][1] = sm.wsc[rb0 + 32 * b + li][1];
       }
+      if constexpr (TT == TT_Q4_K) {
+        // Split scales: the 6-bit sub-block scale sc = 8 sh + sl (sh, sl <= 7),
+        // so sh*q and sl*q (q <= 15) fit int8.  Both products are formed on the
+        // weight fragment (bytewise: a 16-bit lane multiply of two packed
+        // bytes carries nothing across them, each product being < 256), and
+        // two MFMA chains accumulate the whole super-block with the scales
+        // already applied: isum = 8 C_hi + C_lo, the same exact integer as
+        // sum_s sc_s * sumi_s, with no per-sub-block integer scaling.
+        i32x16 chi[NA][NB], clo[NA][NB];
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            chi[a][b] = zero;
+            clo[a][b] = zero;
+          }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          i32x4 af[NA], bh[NB], bl[NB];
+#pragma unroll
+          for (int a = 0; a < NA; ++a) af[a] = *(const i32x4*)(sm.aq + (tb0 + 32 * a + li) * kQS + 32 * s + 16 * lh);
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const i32x4 q = *(const i32x4*)(sm.bq + (rb0 + 32 * b + li) * kQS + 32 * s + 16 * lh);
+            const uint32_t sc = (scw[b][s >> 2] >> (8 * (s & 3))) & 63u;
+            const u16x2 mh = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
+            const u16x2 ml = {(uint16_t)(sc & 7u), (uint16_t)(sc & 7u)};
+            // (scalar copies first: bit-casting a vector element expression
+            // reads element 0 for every index)
+            const uint32_t q0 = q.x, q1 = q.y, q2 = q.z, q3 = q.w;
+            const uint32_t h0 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q0) * mh));
+            const uint32_t h1 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q1) * mh));
+            const uint32_t h2 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q2) * mh));
+            const uint32_t h3 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q3) * mh));
+            const uint32_t l0 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q0) * ml));
+            const uint32_t l1 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q1) * ml));
+            const uint32_t l2 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q2) * ml));
+            const uint32_t l3 = __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, q3) * ml));
+            bh[b] = i32x4{(int)h0, (int)h1, (int)h2, (int)h3};
+            bl[b] = i32x4{(int)l0, (int)l1, (int)l2, (int)l3};
+          }
+#pragma unroll
+          for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+              chi[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bh[b], chi[a][b], 0, 0, 0);
+              clo[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[a], bl[b], clo[a][b], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) isum[a][b][e] = 8 * chi[a][b][e] + clo[a][b][e];
+      } else {
       // pipelined as in the 32-value path: sub-block s+1's MFMAs are issued
       // before sub-block s's integer scaling
       auto issue = [&](int s, i32x16 (&c)[NA][NB]) {
@@ -558,6 +617,7 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
         finish(s, c0);
         if (s + 2 < 8) issue(s + 2, c0);
         finish(s + 1, c1);
+      }
       }
       if constexpr (TT == TT_IQ4_XS || iq3(TT)) {
         // no mins: acc += (d * dy) * isum  (iq_kernels.c:967-1001, one
