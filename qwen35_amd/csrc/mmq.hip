@@ -56,6 +56,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef long i64x1_a8 __attribute__((aligned(8)));
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kChunk = 256;         // values per staged K-chunk
 constexpr int kQS = kChunk + 16;    // LDS bytes per int8 row (pad: rows 4 banks apart)
@@ -1123,6 +1124,183 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, hipStream_t s) {
   }
 }
 
+// ---- weights-direct MMQ (Q4_K, 64 tokens x 128 rows) --------------------------------------
+// Each wave owns 32 weight rows and reads their Q4_K bytes from global memory
+// straight into MFMA B fragments, with no LDS image of the weights: lane l
+// holds row l%32, and each 16-byte qs piece gives it values 16*(l/32)..+15 of
+// two sub-blocks (low / high nibbles), scaled by the split sub-block scale as
+// in k_mmq.  The workgroup's 64 tokens of Q8_K activation are copied into LDS
+// by global_load_lds (DMA, no registers), double-buffered: chunk c+1 (one
+// super-block) lands while chunk c is multiplied.  LDS token row: qs[256] |
+// bsums[16] | d, 304 bytes, so 16-byte fragment reads of 32 consecutive
+// tokens fall 12 banks apart (conflict-free).  Measured on MI355X, config 5
+// Q4_K [17408, 5120]: T = 512 146-150 us against 184 us for the 64 x 64 tile
+// kernel in the same harness, T = 128 56 against 62 us; it loses below 128
+// tokens (no split-K), where the tile kernel stays the default.
+constexpr int kWdRow = 304, kWdPieces = 19, kWdBT = 64, kWdBR = 128;
+constexpr int kWdStage = kWdBT * kWdRow;
+constexpr int kWdDma = (kWdBT * kWdPieces + 255) / 256;  // DMA pieces per thread
+
+__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
+  return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
+}
+
+__global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                     float* __restrict__ Y, int rows, int tokens, long row_bytes,
+                                                     long act_bytes, int nsb, int ntile_t) {
+  constexpr int NA = 2;
+  __shared__ __attribute__((aligned(16))) uint8_t act[2][kWdStage];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
+  const int r0 = (g / ntile_t) * kWdBR, t0 = (g % ntile_t) * kWdBT;
+  const int row = r0 + 32 * wv + li;
+  const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+
+  // DMA piece p = 64*(4i + wave) + lane of the stage: token p/19, 16-byte
+  // slot p%19 (16 qs slots, two bsum slots, one slot holding d); tokens past
+  // the end re-read the last one
+  long goff[kWdDma];
+  bool gon[kWdDma];
+#pragma unroll
+  for (int i = 0; i < kWdDma; ++i) {
+    const int p = 64 * (4 * i + wv) + lane;
+    gon[i] = p < kWdBT * kWdPieces;
+    const int tp = p / kWdPieces, j = p - tp * kWdPieces;
+    int tok = t0 + tp;
+    tok = tok < tokens ? tok : tokens - 1;
+    goff[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
+  }
+  auto issue_act = [&](int sb, int buf) {
+#pragma unroll
+    for (int i = 0; i < kWdDma; ++i) {
+      if (4 * i + wv < (kWdBT * kWdPieces + 63) / 64 && gon[i])
+        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
+                                         (__attribute__((address_space(3))) void*)(&act[buf][0] + 1024 * (4 * i + wv)),
+                                         16, 0, 0);
+    }
+  };
+  u32x4 wh, wq[4];
+  auto issue_w = [&](int sb, u32x4& h, u32x4 (&q)[4]) {
+    const uint8_t* b = wrow + 144L * sb;
+    h = *(const u32x4*)b;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
+  };
+
+  f32x16 acc[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
+  const i32x16 zero = {};
+  const f32x16 fz = {};
+
+  issue_act(0, 0);
+  issue_w(0, wh, wq);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int cur = sb & 1;
+    u32x4 nh, nq[4];
+    if (sb + 1 < nsb) {
+      issue_act(sb + 1, cur ^ 1);
+      issue_w(sb + 1, nh, nq);
+    }
+    const uint8_t* A = &act[cur][0];
+    __builtin_amdgcn_iglp_opt(0);
+    // 6-bit scales and mins of this lane's row (kernels256.c:105-125)
+    const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
+    const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+    i32x16 chi[NA], clo[NA];
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      chi[a] = zero;
+      clo[a] = zero;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t q0 = wq[c].x, q1 = wq[c].y, q2 = wq[c].z, q3 = wq[c].w;
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int s = 2 * c + hi;
+        const uint32_t n0 = (hi ? q0 >> 4 : q0) & 0x0F0F0F0Fu, n1 = (hi ? q1 >> 4 : q1) & 0x0F0F0F0Fu;
+        const uint32_t n2 = (hi ? q2 >> 4 : q2) & 0x0F0F0F0Fu, n3 = (hi ? q3 >> 4 : q3) & 0x0F0F0F0Fu;
+        const uint32_t sc = ((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 63u;
+        const u16x2 mh = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
+        const u16x2 ml = {(uint16_t)(sc & 7u), (uint16_t)(sc & 7u)};
+        const i32x4 bh = {(int)pk_mul_u16(n0, mh), (int)pk_mul_u16(n1, mh), (int)pk_mul_u16(n2, mh),
+                          (int)pk_mul_u16(n3, mh)};
+        const i32x4 bl = {(int)pk_mul_u16(n0, ml), (int)pk_mul_u16(n1, ml), (int)pk_mul_u16(n2, ml),
+                          (int)pk_mul_u16(n3, ml)};
+#pragma unroll
+        for (int a = 0; a < NA; ++a) {
+          const i32x4 af = *(const i32x4*)(A + (32 * a + li) * kWdRow + 32 * s + 16 * lh);
+          chi[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bh, chi[a], 0, 0, 0);
+          clo[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, clo[a], 0, 0, 0);
+        }
+      }
+    }
+    // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
+    const uint32_t mn = lh ? mn_hi : mn_lo;
+    f16x8 bm;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const _Float16 m = (_Float16)(float)((mn >> (8 * k)) & 255u);
+      bm[2 * k] = m;
+      bm[2 * k + 1] = m;
+    }
+    const float d = h2f(wh.x), ndm = -h2f(wh.x >> 16);
+#pragma unroll
+    for (int a = 0; a < NA; ++a) {
+      const i16x8 bs = *(const i16x8*)(A + (32 * a + li) * kWdRow + 256 + 16 * lh);
+      f16x8 am;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const short v = bs[k];
+        am[k] = (_Float16)v;
+      }
+      const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, fz, 0, 0, 0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
+        const float dy = *(const float*)(A + t * kWdRow + 288);
+        const int ci = chi[a][e], cl = clo[a][e];  // (scalar copies: see k_mmq)
+        const int isum = 8 * ci + cl;
+        const float inner = __builtin_fmaf(d, (float)isum, ndm * cm[e]);
+        acc[a][e] = __builtin_fmaf(dy, inner, acc[a][e]);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
+    __syncthreads();
+    if (sb + 1 < nsb) {
+      wh = nh;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wq[c] = nq[c];
+    }
+  }
+  if (row < rows) {
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int t = t0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
+        if (t < tokens) Y[(long)t * rows + row] = acc[a][e];
+      }
+  }
+}
+
+static hipError_t launch_mmq_wd(const GemvArgs& g, hipStream_t s) {
+  const long ntt = (g.tokens + kWdBT - 1) / kWdBT, ntr = (g.rows + kWdBR - 1) / kWdBR;
+  if (ntt * ntr > 0x7FFFFFFFL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mmq_wd_q4k, dim3((unsigned)(ntt * ntr)), dim3(256), 0, s, (const uint8_t*)g.w,
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, g.cols / 256, (int)ntt);
+  return hipGetLastError();
+}
+
 // ---- launchers --------------------------------------------------------------------------
 template <int TT, int BT, int BR>
 static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
@@ -1144,6 +1322,9 @@ static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
 
 template <int TT>
 static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit, hipStream_t s) {
+  // Q4_K's 64 x 128 tile is the weights-direct kernel (never split)
+  if constexpr (TT == TT_Q4_K)
+    if (bt == 64 && br == 128) return launch_mmq_wd(g, s);
   if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, s);
   if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, s);
   if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, ksplit, s);
@@ -1152,7 +1333,8 @@ static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit,
   return hipErrorInvalidValue;
 }
 
-// Default tile: 64 x 64.  Measured on MI355X at the benchmark shapes (T = 16..512,
+// Default tile: 64 x 64 (Q4_K from 128 tokens: the weights-direct kernel
+// above).  Measured on MI355X at the benchmark shapes (T = 16..512,
 // all four formats) it beats the larger tiles everywhere: with one 32x32
 // accumulator per wave it stays at 3-4 waves per SIMD, and the larger tiles'
 // extra fragment reuse does not pay for their lower occupancy while the
@@ -1165,6 +1347,7 @@ static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
   const bool small = g.tokens <= 32 && !act32(g.ttype);
   bt = small ? 32 : 64;
   br = small ? 128 : 64;
+  if (g.ttype == TT_Q4_K && g.tokens >= 128) br = 128;  // the weights-direct kernel
 }
 
 

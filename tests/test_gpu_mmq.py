@@ -38,6 +38,8 @@ CASES = [
     (po.TT_IQ4_NL, 33, 2560, 20),
     (po.TT_Q4_K, 150, 512, 65),
     (po.TT_Q4_K, 64, 2560, 16),
+    (po.TT_Q4_K, 200, 768, 130),   # >= 128 tokens: the weights-direct kernel by default
+    (po.TT_Q4_K, 333, 512, 257),
     (po.TT_Q6_K, 100, 768, 40),
     (po.TT_Q6_K, 72, 2304, 129),
     (po.TT_Q5_K, 150, 512, 65),
