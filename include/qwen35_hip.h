@@ -152,7 +152,7 @@ int qhip_launch_gemv_tuned(const void *d_w, const void *d_xq, float *d_out, int 
 int qhip_launch_mul_mat_vec_tile(const void *d_w, const void *d_xq, float *d_out, int rows,
                                  int cols, int tokens, int ttype, void *stream);
 /* The MMQ with an explicit workgroup tile: `tile_tokens` x `tile_rows`
- * outputs, each 64 or 128 (0 picks).  Replaces the reference's compile-time
+ * outputs, each 64 or 128, or 32 x 128 / 32 x 64 (0 picks).  Replaces the reference's compile-time
  * tile constants (mmq.cu, 128 rows x 8 tokens per CTA) with arguments.
  * Returns QHIP_DECLINE when the fast-path preconditions do not hold. */
 int qhip_launch_mmq_tuned(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,

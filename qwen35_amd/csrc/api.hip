@@ -332,7 +332,7 @@ int qhip_launch_mmq_tuned(const void* d_w, const void* d_xq, float* d_out, int r
   hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
   const bool bt_ok = tile_tokens == 0 || tile_tokens == 64 || tile_tokens == 128 ||
-                     (tile_tokens == 32 && tile_rows == 128);
+                     (tile_tokens == 32 && (tile_rows == 128 || tile_rows == 64));
   const bool br_ok = tile_rows == 0 || tile_rows == 64 || tile_rows == 128;
   if (!bt_ok || !br_ok) return (int)hipErrorInvalidValue;
   if (!fast_ok(g) || !mmq_supported(ttype)) return QHIP_DECLINE;

@@ -354,15 +354,16 @@ __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int
 }
 
 // ---- the kernel -------------------------------------------------------------------------
-template <int TT, int BT, int BR>
-__global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+template <int TT, int BT, int BR, int NT = 256>
+__global__ __launch_bounds__(NT) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                               float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                               long act_bytes, int upr, int ntile_t, int ksplit, int cps) {
   grid_prologue<TT>();
   constexpr bool K32 = act32(TT);
-  // waves: 2 x 2 over (tokens, rows), or 1 x 4 (stacked along rows) for a
-  // 32-token tile
-  constexpr int WT = BT >= 64 ? 2 : 1, WR = 4 / WT;
+  // waves: 2 x 2 over (tokens, rows), or stacked along rows for a 32-token
+  // tile (four waves for 128 rows, two for 64)
+  constexpr int NW = NT / 64;
+  constexpr int WT = BT >= 64 ? 2 : 1, WR = NW / WT;
   constexpr int NA = BT / (32 * WT), NB = BR / (32 * WR);
   static_assert(NA >= 1 && NB >= 1, "tile too small for the wave layout");
   __shared__ MmqSmem<TT, BT, BR> sm;
@@ -391,23 +392,24 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
 
-  // Thread tid stages weight units tid + 256*i (row q>>2, unit q&3) and the
-  // activation units likewise (threads 0..127 only for a 32-token tile); rows
-  // / tokens past the end re-read the last one.
-  constexpr int UW = BR / 64, UA = BT >= 64 ? BT / 64 : 1;
-  const bool a_on = BT >= 64 || tid < 4 * BT;
+  // Thread tid stages weight units tid + NT*i (row q>>2, unit q&3) and the
+  // activation units likewise (threads 0..4*BT-1 only when the tile has
+  // fewer tokens than NT/4); rows / tokens past the end re-read the last one.
+  constexpr int UW = 4 * BR / NT, UA = 4 * BT >= NT ? 4 * BT / NT : 1;
+  static_assert(UW >= 1, "too few rows for the workgroup");
+  const bool a_on = 4 * BT >= NT || tid < 4 * BT;
   typename Unit<TT>::W wreg[UW];
   MmqAct<TT> areg[UA];
   const uint8_t* wrow[UW];
   const uint8_t* arow[UA];
 #pragma unroll
   for (int i = 0; i < UW; ++i) {
-    const int row = (tid + 256 * i) >> 2;
+    const int row = (tid + NT * i) >> 2;
     wrow[i] = W + (long)(r0 + row < rows ? r0 + row : rows - 1) * row_bytes;
   }
 #pragma unroll
   for (int i = 0; i < UA; ++i) {
-    const int tok = (tid + 256 * i) >> 2;
+    const int tok = (tid + NT * i) >> 2;
     arow[i] = XQ + (long)(t0 + tok < tokens ? t0 + tok : tokens - 1) * act_bytes;
   }
   const int u4 = tid & 3;
@@ -430,10 +432,10 @@ __global__ __launch_bounds__(256) void k_mmq(const uint8_t* __restrict__ W, cons
     __syncthreads();  // the previous chunk's fragments have been read
     if (u4 < nu) {
 #pragma unroll
-      for (int i = 0; i < UW; ++i) emit_w<TT, BT, BR>(sm, wreg[i], (tid + 256 * i) >> 2, u4);
+      for (int i = 0; i < UW; ++i) emit_w<TT, BT, BR>(sm, wreg[i], (tid + NT * i) >> 2, u4);
       if (a_on) {
 #pragma unroll
-        for (int i = 0; i < UA; ++i) emit_a<TT>(sm, areg[i], (tid + 256 * i) >> 2, u4);
+        for (int i = 0; i < UA; ++i) emit_a<TT>(sm, areg[i], (tid + NT * i) >> 2, u4);
       }
     }
     __syncthreads();
@@ -1302,7 +1304,7 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, hipStream_t s) {
 }
 
 // ---- launchers --------------------------------------------------------------------------
-template <int TT, int BT, int BR>
+template <int TT, int BT, int BR, int NT = 256>
 static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
   const int upr = g.cols / 64;
   const int nchunks = (upr + 3) / 4;
@@ -1314,7 +1316,7 @@ static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
   const long G = ntr * ntt * ksplit;
   if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
   if (ksplit > 1) launch_fill_zero(g.out, (long)g.tokens * g.rows, s);
-  hipLaunchKernelGGL((k_mmq<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+  hipLaunchKernelGGL((k_mmq<TT, BT, BR, NT>), dim3((unsigned)G), dim3(NT), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
                      ksplit, cps);
   return hipGetLastError();
@@ -1326,6 +1328,7 @@ static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit,
   if constexpr (TT == TT_Q4_K)
     if (bt == 64 && br == 128) return launch_mmq_wd(g, s);
   if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, s);
+  if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, s);
   if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, s);
   if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, ksplit, s);
   if (bt == 128 && br == 64) return launch_mmq_t<TT, 128, 64>(g, ksplit, s);

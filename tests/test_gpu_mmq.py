@@ -16,7 +16,7 @@ from qwen35_amd import _lib, ops, synth
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-5
-TILES = [(64, 64), (64, 128), (128, 64), (128, 128), (32, 128)]
+TILES = [(64, 64), (64, 128), (128, 64), (128, 128), (32, 128), (32, 64)]
 F16_ONE = np.array([0x00, 0x3C], np.uint8)  # 1.0 as little-endian binary16
 
 
@@ -172,7 +172,7 @@ def test_mmq_rejects_bad_tiles(gpu):
     xq = torch.zeros(tokens * 292, dtype=torch.uint8, device=gpu)
     out = torch.empty((tokens, rows), device=gpu)
     L = _lib.load()
-    for bt, br in [(32, 64), (64, 256), (-1, 64)]:
+    for bt, br in [(32, 32), (64, 256), (-1, 64), (16, 64)]:
         rc = L.qhip_launch_mmq_tuned(w.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt, bt,
                                      br, None)
         assert rc not in (0, qwen35_amd.DECLINE), (bt, br)
