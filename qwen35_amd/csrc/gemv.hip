@@ -188,60 +188,85 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
   }
   const int u_end = active ? upr : 0;
 
-  // first weight unit in flight before the prologue
+  // The activation loads of the first RX quantize rounds are issued before
+  // the first weight unit's: loads complete in order, so the quantize can
+  // start as soon as x arrives instead of after the weights.
+  constexpr int RX = 4;
+  constexpr int STEP = K32 ? WGS / 32 : WGS / 64;  // blocks per round
+  const bool out_q = XQ != nullptr && blockIdx.x == 0;
+  float xs[RX];
+  float4 xf[RX];
+#pragma unroll
+  for (int rd = 0; rd < RX; ++rd) {
+    if constexpr (K32) {
+      const int b = rd * STEP + (threadIdx.x >> 5);
+      xs[rd] = b < nblk ? X[32 * b + (threadIdx.x & 31)] : 0.0f;
+    } else {
+      const int b = rd * STEP + wv;
+      xf[rd] = b < nblk ? *(const float4*)(X + 256L * b + 4 * lane) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  }
+
   typename U::W wcur[NR];
   if (j < u_end) {
 #pragma unroll
     for (int k = 0; k < NR; ++k) wcur[k] = U::load_w(wrow[k], j);
   }
 
-  const bool out_q = XQ != nullptr && blockIdx.x == 0;
-  if constexpr (K32) {
-    // one value per thread, a 32-lane group per block
-    for (int b0 = 0; b0 < nblk; b0 += WGS / 32) {
-      const int b = b0 + (threadIdx.x >> 5), i = threadIdx.x & 31;
-      const bool ok = b < nblk;
-      uint32_t hb;
-      const int q = quant_q8_0_lane(ok ? X[32 * b + i] : 0.0f, hb);
-      if (ok) {
-        qs[split_off(32 * b + i)] = (uint8_t)(int8_t)q;
-        if (i == 0) dsc[b] = h2f(hb);
-        if (out_q) {
-          uint8_t* ob = XQ + 34L * b;
-          ob[2 + i] = (uint8_t)(int8_t)q;
-          if (i == 0) {
-            ob[0] = (uint8_t)hb;
-            ob[1] = (uint8_t)(hb >> 8);
-          }
+  // one quantize round: block b from the value(s) v
+  auto quant32 = [&](int b, float v) {
+    const int i = threadIdx.x & 31;
+    const bool ok = b < nblk;
+    uint32_t hb;
+    const int q = quant_q8_0_lane(v, hb);
+    if (ok) {
+      qs[split_off(32 * b + i)] = (uint8_t)(int8_t)q;
+      if (i == 0) dsc[b] = h2f(hb);
+      if (out_q) {
+        uint8_t* ob = XQ + 34L * b;
+        ob[2 + i] = (uint8_t)(int8_t)q;
+        if (i == 0) {
+          ob[0] = (uint8_t)hb;
+          ob[1] = (uint8_t)(hb >> 8);
         }
       }
     }
-  } else {
-    // a wave per 256-value block, four values per lane
-    for (int b0 = 0; b0 < nblk; b0 += WGS / 64) {
+  };
+  auto quant256 = [&](int b, float4 f) {
+    const bool ok = b < nblk;
+    float v[4] = {f.x, f.y, f.z, f.w};
+    int gsum;
+    float scale;
+    const uint32_t packed = quant_q8_K_lane(v, gsum, scale);
+    if (ok) {
+      *(uint32_t*)(qs + split_off(256 * b + 4 * lane)) = packed;
+      if ((lane & 3) == 0) bs[16 * b + (lane >> 2)] = (int16_t)gsum;
+      if (lane == 0) dsc[b] = scale;
+      if (out_q) {
+        uint8_t* ob = XQ + 292L * b;
+        *(uint32_t*)(ob + 4 + 4 * lane) = packed;
+        if ((lane & 3) == 0) *(int16_t*)(ob + 260 + 2 * (lane >> 2)) = (int16_t)gsum;
+        if (lane == 0) *(float*)ob = scale;
+      }
+    }
+  };
+  // K32: one value per thread, a 32-lane group per block; else a wave per
+  // 256-value block, four values per lane.  Rounds are uniform over the
+  // workgroup (every lane takes part in the shuffles).
+#pragma unroll
+  for (int rd = 0; rd < RX; ++rd) {
+    if (rd * STEP < nblk) {
+      if constexpr (K32) quant32(rd * STEP + (threadIdx.x >> 5), xs[rd]);
+      else quant256(rd * STEP + wv, xf[rd]);
+    }
+  }
+  for (int b0 = RX * STEP; b0 < nblk; b0 += STEP) {
+    if constexpr (K32) {
+      const int b = b0 + (threadIdx.x >> 5);
+      quant32(b, b < nblk ? X[32 * b + (threadIdx.x & 31)] : 0.0f);
+    } else {
       const int b = b0 + wv;
-      const bool ok = b < nblk;
-      float v[4];
-      if (ok) {
-        const float4 f = *(const float4*)(X + 256L * b + 4 * lane);
-        v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
-      } else {
-        v[0] = v[1] = v[2] = v[3] = 0.0f;
-      }
-      int gsum;
-      float scale;
-      const uint32_t packed = quant_q8_K_lane(v, gsum, scale);
-      if (ok) {
-        *(uint32_t*)(qs + split_off(256 * b + 4 * lane)) = packed;
-        if ((lane & 3) == 0) bs[16 * b + (lane >> 2)] = (int16_t)gsum;
-        if (lane == 0) dsc[b] = scale;
-        if (out_q) {
-          uint8_t* ob = XQ + 292L * b;
-          *(uint32_t*)(ob + 4 + 4 * lane) = packed;
-          if ((lane & 3) == 0) *(int16_t*)(ob + 260 + 2 * (lane >> 2)) = (int16_t)gsum;
-          if (lane == 0) *(float*)ob = scale;
-        }
-      }
+      quant256(b, b < nblk ? *(const float4*)(X + 256L * b + 4 * lane) : make_float4(0.0f, 0.0f, 0.0f, 0.0f));
     }
   }
   __syncthreads();
