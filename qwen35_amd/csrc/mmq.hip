@@ -260,19 +260,21 @@ __device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename U
 #pragma unroll
       for (int l = 0; l < 4; ++l) {
         const uint32_t qq = w.q[2 * b + (l >> 1)] >> (16 * (l & 1));
-        uint32_t e1, e2, s8;
+        uint32_t e1, e2;
+        uint2 m;
         if constexpr (TT == TT_IQ3_XXS) {
           e1 = g_iq3_grid[qq & 255u];
           e2 = g_iq3_grid[(qq >> 8) & 255u];
-          s8 = iq_sign8((w.aux[b] >> (7 * l)) & 127u);
+          m = g_iq3_sign[(w.aux[b] >> (7 * l)) & 127u];
         } else {
           const uint32_t qh = w.qh >> (8 * b);
           e1 = Unit<TT_IQ3_S>::entry(qq, qh, 2 * l);
           e2 = Unit<TT_IQ3_S>::entry(qq >> 8, qh, 2 * l + 1);
-          s8 = w.sg[b] >> (8 * l);
+          const uint32_t s8 = w.sg[b] >> (8 * l);
+          m = make_uint2(sign_bytes4(s8), sign_bytes4(s8 >> 4));
         }
-        v[8 * b + 2 * l] = apply_signs4(e1, s8);
-        v[8 * b + 2 * l + 1] = apply_signs4(e2, s8 >> 4);
+        v[8 * b + 2 * l] = apply_mask4(e1, m.x);
+        v[8 * b + 2 * l + 1] = apply_mask4(e2, m.y);
       }
     }
 #pragma unroll

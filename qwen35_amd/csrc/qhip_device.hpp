@@ -192,6 +192,22 @@ static __constant__ uint32_t kIq3sGrid[512] = {QHIP_IQ3S_CODES(QHIP_S_ENTRY)};
 #undef QHIP_XXS_ENTRY
 #undef QHIP_S_ENTRY
 static __shared__ uint32_t g_iq3_grid[512];
+// IQ3_XXS sign masks in LDS: entry s holds the parity-completed mask of the
+// 7-bit index s as 0xFF / 0x00 bytes, .x for values 0..3, .y for 4..7 (one
+// LDS read instead of the parity and byte spreading per 8 values; IQ3_S's
+// explicit masks are spread in registers, which measured no slower).
+static __shared__ uint2 g_iq3_sign[128];
+
+// ksigns_iq2xs (src/iq_tables.zig:42-61): a 7-bit index completed by bit 7 to
+// an even number of set bits; bit j negates value j of the 8.
+__device__ __forceinline__ uint32_t iq_sign8(uint32_t idx7) {
+  return idx7 | (((uint32_t)__builtin_popcount(idx7) & 1u) << 7);
+}
+// the low 4 bits of s as 0xFF / 0x00 bytes
+__device__ __forceinline__ uint32_t sign_bytes4(uint32_t s) {
+  const uint32_t t = ((s & 15u) * 0x00204081u) & 0x01010101u;
+  return (t << 8) - t;
+}
 
 // Every thread of the workgroup must call it before any early exit.
 template <int TT>
@@ -199,23 +215,18 @@ __device__ __forceinline__ void grid_prologue() {
   if constexpr (iq3(TT)) {
     constexpr int N = TT == TT_IQ3_XXS ? 256 : 512;
     for (int i = threadIdx.x; i < N; i += blockDim.x) g_iq3_grid[i] = TT == TT_IQ3_XXS ? kIq3xxsGrid[i] : kIq3sGrid[i];
+    if constexpr (TT == TT_IQ3_XXS) {
+      for (int i = threadIdx.x; i < 128; i += blockDim.x) {
+        const uint32_t s8 = iq_sign8((uint32_t)i);
+        g_iq3_sign[i] = make_uint2(sign_bytes4(s8), sign_bytes4(s8 >> 4));
+      }
+    }
     __syncthreads();
   }
 }
-
-// ksigns_iq2xs (src/iq_tables.zig:42-61): a 7-bit index completed by bit 7 to
-// an even number of set bits; bit j negates value j of the 8.
-__device__ __forceinline__ uint32_t iq_sign8(uint32_t idx7) {
-  return idx7 | (((uint32_t)__builtin_popcount(idx7) & 1u) << 7);
-}
-// Four unsigned grid bytes (each >= 1) with the low 4 bits of `s` as per-byte
-// signs: t holds a 1 in each negated byte, m = 255 * t is 0xFF there, and
-// (g ^ m) + t is 256 - g in those bytes (no carry leaves a byte as g >= 1).
-__device__ __forceinline__ uint32_t apply_signs4(uint32_t g, uint32_t s) {
-  const uint32_t t = ((s & 15u) * 0x00204081u) & 0x01010101u;
-  const uint32_t m = (t << 8) - t;
-  return (g ^ m) + t;
-}
+// Four unsigned grid bytes (each >= 1) negated where the mask m is 0xFF:
+// (g ^ m) + (m & 1) is 256 - g in those bytes, and no carry leaves a byte.
+__device__ __forceinline__ uint32_t apply_mask4(uint32_t g, uint32_t m) { return (g ^ m) + (m & 0x01010101u); }
 
 // ---- per-format unit decode ------------------------------------------------------
 // Every GEMV lane walks a weight row in units of 64 values:
@@ -883,9 +894,9 @@ struct Unit<TT_IQ3_XXS> {
 #pragma unroll
     for (int l = 0; l < 4; ++l) {
       const uint32_t qq = q[l >> 1] >> (16 * (l & 1));
-      const uint32_t sg = iq_sign8((aux >> (7 * l)) & 127u);
-      s = dot4(apply_signs4(g_iq3_grid[qq & 255u], sg), y[2 * l], s);
-      s = dot4(apply_signs4(g_iq3_grid[(qq >> 8) & 255u], sg >> 4), y[2 * l + 1], s);
+      const uint2 m = g_iq3_sign[(aux >> (7 * l)) & 127u];
+      s = dot4(apply_mask4(g_iq3_grid[qq & 255u], m.x), y[2 * l], s);
+      s = dot4(apply_mask4(g_iq3_grid[(qq >> 8) & 255u], m.y), y[2 * l + 1], s);
     }
     return s;
   }
@@ -939,8 +950,8 @@ struct Unit<TT_IQ3_S> {
     for (int l = 0; l < 4; ++l) {
       const uint32_t qq = q[l >> 1] >> (16 * (l & 1));
       const uint32_t s8 = sg >> (8 * l);
-      s = dot4(apply_signs4(entry(qq, qh, 2 * l), s8), y[2 * l], s);
-      s = dot4(apply_signs4(entry(qq >> 8, qh, 2 * l + 1), s8 >> 4), y[2 * l + 1], s);
+      s = dot4(apply_mask4(entry(qq, qh, 2 * l), sign_bytes4(s8)), y[2 * l], s);
+      s = dot4(apply_mask4(entry(qq >> 8, qh, 2 * l + 1), sign_bytes4(s8 >> 4)), y[2 * l + 1], s);
     }
     return s;
   }
