@@ -54,6 +54,10 @@ CASES = [
     (po.TT_IQ3_XXS, 64, 2560, 16),
     (po.TT_IQ3_S, 130, 768, 70),
     (po.TT_IQ3_S, 33, 2560, 20),
+    (po.TT_IQ4_NL, 96, 1024, 100),   # small grids with 4+ chunks per tile
+    (po.TT_Q4_0, 200, 1280, 75),     # an odd chunk count
+    (po.TT_Q8_0, 70, 2048, 66),
+    (po.TT_Q4_1, 64, 1024, 128),
 ]
 IDS = [f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in CASES]
 
