@@ -6,8 +6,9 @@ through the Exec mirror (the slots the engine calls): matvecPair over the Q4_K
 gate/up weights [9728,2560] x2 (adjacent in the weight arena: one launch) from
 f32 x[2560], then matvec over the Q6_K down weight [2560,9728] from f32
 h[9728].  The mirror quantizes x (Q8_K) inside the gate/up GEMV (one launch)
-and h in a quantize launch before the down GEMV (rows this long do better with
-the separate launch).
+and h inside the down GEMV, split over K: each workgroup quantizes and
+multiplies one 1024-value slice of h, the last one of a row tile to finish
+adds the partial sums (one launch).
 `value` = algorithmic bytes of the step's GEMVs (packed weights + f32 x + f32 y
 per GEMV) / step time, inputs resident in HBM.  Weight sets rotate over enough
 device copies (> 512 MB per pass) that every step streams from HBM, not from
@@ -118,7 +119,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "fused_gate_up", "step", "step_unfused",
+    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "fused_gate_up", "split_down", "step",
+                                                 "step_unfused",
                                                  "mmq_cfg5_q4k",
                                                  "mmq_cfg4"],
                     help="run only this kernel (for rocprofv3) and exit")
@@ -156,7 +158,7 @@ def main() -> int:
     # matvecPair(gate, up, x) + matvec(down, h) (src/backend.zig:153-176 slots):
     # the mirror quantizes x and h on the device and runs one GEMV per slot
     # (adjacent gate/up weights are one launch): x inside the gate/up GEMV
-    # (width 2560), h in its own quantize launch (width 9728).
+    # (width 2560), h inside the split-K down launch (width 9728).
     import ctypes
     H, F = 2560, 9728
     t0 = time.time()
@@ -218,7 +220,15 @@ def main() -> int:
         assert rc == 0, rc
 
     # the launches the mirror issues in the step: quantize + GEMV in one launch
-    # for gate/up (width 2560), a quantize launch and a GEMV for down (9728)
+    # for gate/up (width 2560) and, split over K, for down (9728)
+    skwork = ops.split_work(H, F, dev)
+
+    def split_down(i):
+        rc = lib.qhip_launch_quantize_mul_mat_vec_split(lins[i % copies][3].dev + gu_bytes, hd.data_ptr(), None,
+                                                        y_d.data_ptr(), H, F, TQ6, 0, 0, 0, skwork.data_ptr(),
+                                                        skwork.numel(), stream)
+        assert rc == 0, rc
+
     def fused_gate_up(i):
         rc = lib.qhip_launch_quantize_mul_mat_vec(lins[i % copies][3].dev, xd.data_ptr(), None, y_gu.data_ptr(),
                                                   2 * F, H, TQ4, stream)
@@ -235,10 +245,11 @@ def main() -> int:
         assert lib.qhip_launch_mul_mat_vec(lg.dev + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1, TQ6,
                                            stream) == 0
 
-    if args.profile_kernel in ("down", "gate_up", "fused_gate_up", "step", "step_unfused"):
+    if args.profile_kernel in ("down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused"):
         for i in range(3):
             step(i)
-        fn = {"down": gemv_down, "gate_up": gemv_gate_up, "fused_gate_up": fused_gate_up, "step": step,
+        fn = {"down": gemv_down, "gate_up": gemv_gate_up, "fused_gate_up": fused_gate_up,
+              "split_down": split_down, "step": step,
               "step_unfused": step_unfused}[args.profile_kernel]
         for i in range(args.steps):
             fn(i)
@@ -263,6 +274,7 @@ def main() -> int:
     d_alg = gemv_bytes(H, F, d_bytes)
     q_alg = 4 * F + lib.qhip_act_row_bytes(TQ6, F)
     fgu_sec = time_loop(torch, fused_gate_up, n_k, 20)
+    sd_sec = time_loop(torch, split_down, n_k, 20)
     d_sec = time_loop(torch, gemv_down, n_k, 20)
     qh_sec = time_loop(torch, quantize_h, n_k, 20)
     gu_sec = time_loop(torch, gemv_gate_up, n_k, 20)
@@ -272,10 +284,13 @@ def main() -> int:
 
     kernels = {
         "fused_q4_k_gate_up_19456x2560": entry(gu_alg, fgu_sec),
-        "gemv_q6_k_down_2560x9728": entry(d_alg, d_sec),
-        "quantize_q8_k_9728": entry(q_alg, qh_sec),
+        "split_q6_k_down_2560x9728": entry(d_alg, sd_sec),
     }
-    off_step = {"gemv_q4_k_gate_up_19456x2560_prequantized": entry(gu_alg, gu_sec)}
+    # the separate launches the split-K down replaces, and the gate/up GEMV on
+    # a pre-quantized activation
+    off_step = {"gemv_q4_k_gate_up_19456x2560_prequantized": entry(gu_alg, gu_sec),
+                "gemv_q6_k_down_2560x9728_prequantized": entry(d_alg, d_sec),
+                "quantize_q8_k_9728": entry(q_alg, qh_sec)}
     dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
     achieved = kernels[dom]["gbs"]
     traffic = None
@@ -290,7 +305,7 @@ def main() -> int:
                 "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
                 "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
     latency = {"gate_up_single_launch_us": round(single_latency(torch, fused_gate_up) * 1e6, 2),
-               "down_single_launch_us": round(single_latency(torch, gemv_down) * 1e6, 2),
+               "down_single_launch_us": round(single_latency(torch, split_down) * 1e6, 2),
                "step_single_us": round(single_latency(torch, step) * 1e6, 2)}
 
     # ---- other configurations (GEMV bandwidth per launch, back-to-back) ------
@@ -350,7 +365,7 @@ def main() -> int:
         "config": {"workload": "cfg2 decode FFN step, batch 1, through the Exec mirror: matvecPair "
                                "Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down [2560,9728] "
                                "from f32 h[9728] (Q8_K quantization on the device: of x inside the gate/up "
-                               "GEMV launch, of h in a quantize launch before the down GEMV)",
+                               "GEMV launch, of h inside the split-K down GEMV launch)",
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": step_bytes,
                    "weight_copies_rotated": copies, "parallelism": "single GPU",
                    "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2)},

@@ -130,6 +130,25 @@ int qhip_launch_mul_mat(const void *d_w, const void *d_xq, float *d_out, int row
 int qhip_launch_quantize_mul_mat_vec(const void *d_w, const float *d_x, void *d_xq_out, float *d_out,
                                      int rows, int cols, int ttype, void *stream);
 
+/* The same product for long rows, split over K: each workgroup quantizes and
+ * multiplies one slice of `slice_values` values (a multiple of 256; 0 picks)
+ * of a tile of rows, writes its partial sums into d_work, and the last
+ * workgroup of each row tile to finish adds the partials in slice order
+ * (deterministic).  `lanes_per_row` (4, 8, 16, 32 or 64) and `rows_per_lane`
+ * (1, 2 or 4) set the shape; 0 picks.  d_work holds
+ * qhip_quantize_mul_mat_vec_work_bytes(rows, cols) bytes; its first 32 KiB
+ * must be zero before the first launch (hipMemset once at allocation) and
+ * are zero again after every launch.  Launches that share a d_work must not
+ * overlap (one stream).  Replaces the same reference pair as above for the
+ * FFN down projection's long rows, where quantizing the whole activation in
+ * every workgroup does not pay; no reference kernel splits K.  Returns
+ * QHIP_DECLINE when the fast-path preconditions do not hold. */
+long qhip_quantize_mul_mat_vec_work_bytes(int rows, int cols);
+int qhip_launch_quantize_mul_mat_vec_split(const void *d_w, const float *d_x, void *d_xq_out, float *d_out,
+                                           int rows, int cols, int ttype, int slice_values,
+                                           int lanes_per_row, int rows_per_lane, void *d_work,
+                                           long work_bytes, void *stream);
+
 /* The GEMV with explicit launch shape: `lanes_per_row` (1..64, or 128 / 256
  * = two / four whole waves, one token only) lanes share `rows_per_lane` (1, 2
  * or 4) weight rows, walking their 64-value units in turn, and fold their

@@ -48,6 +48,10 @@ SIGNATURES = {
                                       c_int, c_void_p]),
     "qhip_launch_quantize_mul_mat_vec": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                                  c_void_p]),
+    "qhip_quantize_mul_mat_vec_work_bytes": (c_long, [c_int, c_int]),
+    "qhip_launch_quantize_mul_mat_vec_split": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                                       c_int, c_int, c_int, c_int, c_void_p, c_long,
+                                                       c_void_p]),
     "qhip_mmq_image_bytes": (c_long, [c_int, c_int, c_int]),
     "qhip_launch_mmq_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "qhip_launch_mul_mat_image": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,

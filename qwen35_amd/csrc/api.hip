@@ -310,6 +310,31 @@ int qhip_launch_quantize_mul_mat_vec(const void* d_w, const float* d_x, void* d_
   return (int)launch_gemv_fused(g, d_x, d_xq_out, 0, 0, S(stream));
 }
 
+long qhip_quantize_mul_mat_vec_work_bytes(int rows, int cols) {
+  if (rows < 0 || cols < 0) return 0;
+  return gemv_splitk_work_bytes(rows, cols);
+}
+
+int qhip_launch_quantize_mul_mat_vec_split(const void* d_w, const float* d_x, void* d_xq_out, float* d_out,
+                                           int rows, int cols, int ttype, int slice_values, int lanes_per_row,
+                                           int rows_per_lane, void* d_work, long work_bytes, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_x, d_out, rows, cols, 1, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (d_xq_out && !aligned4(d_xq_out)) return (int)hipErrorInvalidValue;
+  if (slice_values < 0 || slice_values % 256 || lanes_per_row < 0 || lanes_per_row > 64 ||
+      (lanes_per_row & (lanes_per_row - 1)) || (lanes_per_row > 0 && lanes_per_row < 4) || rows_per_lane < 0 ||
+      rows_per_lane > 4 || rows_per_lane == 3)
+    return (int)hipErrorInvalidValue;
+  if (!d_work || ((uintptr_t)d_work & 15u) || work_bytes < gemv_splitk_work_bytes(rows, cols))
+    return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!fast_ok(g) || ((uintptr_t)d_x & 15u) || cols % 256) return QHIP_DECLINE;
+  if (slice_values && !gemv_fused_fits(ttype, slice_values)) return QHIP_DECLINE;
+  return (int)launch_gemv_splitk(g, d_x, d_xq_out, lanes_per_row, rows_per_lane, slice_values, d_work, work_bytes,
+                                 S(stream));
+}
+
 int qhip_launch_gemv_tuned(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
                            int tokens, int ttype, int lanes_per_row, int tokens_per_pass,
                            int rows_per_lane, void* stream) {

@@ -33,6 +33,9 @@ struct qhip_backend {
   std::vector<void*> bufs;       // allocBuf regions (freed by free_scratch)
   uint8_t* act = nullptr;        // quantized-activation scratch
   size_t act_cap = 0;
+  // split-K partials and row-tile counters (counters zero between launches)
+  uint8_t* skwork = nullptr;
+  size_t skwork_cap = 0;
   // MMQ images of K-quant weights, built on first use with many tokens and
   // kept until free_linear / destroy; keyed by (weight bytes, rows) because a
   // fused matvecPair multiplies two adjacent weights as one.
@@ -91,6 +94,26 @@ static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
   return hipSuccess;
 }
 
+static hipError_t ensure_skwork(qhip_backend* be, size_t bytes) {
+  if (be->skwork_cap >= bytes) return hipSuccess;
+  if (be->skwork) (void)hipFree(be->skwork);
+  be->skwork = nullptr;
+  be->skwork_cap = 0;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, bytes);
+  if (e != hipSuccess) return e;
+  // the counters start at zero; a fill kernel on the backend's stream orders
+  // it before the first split launch
+  e = launch_fill_zero(p, kSkCountBytes, be->stream);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return e;
+  }
+  be->skwork = (uint8_t*)p;
+  be->skwork_cap = bytes;
+  return hipSuccess;
+}
+
 // Bytes per value of the widest activation family (Q8_K: 292/256), so one
 // scratch serves every weight type.
 static size_t act_bytes_for(int cols, int k) {
@@ -121,10 +144,12 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   if (be->memo_on) (hit ? be->memo_hits : be->memo_misses)++;
   if (!hit && k == 1) {
     // one launch, the activation quantized inside the GEMV, where that is
-    // faster than a separate quantize launch (widths up to 4096); with the
-    // memo on, the launch also leaves the quantized rows in the scratch
+    // faster than a separate quantize launch (widths up to 4096 whole; long
+    // rows split over K); with the memo on, the launch also leaves the
+    // quantized rows in the scratch
     const GemvArgs g1{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
-    if (gemv_fused_preferred(g1)) {
+    const bool split = gemv_splitk_preferred(g1);
+    if (split || gemv_fused_preferred(g1)) {
       void* xq_out = nullptr;
       if (be->memo_on) {
         const hipError_t ea = ensure_act(be, act_bytes_for(cols, 1));
@@ -132,7 +157,16 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
         memo_clear(be);
         xq_out = be->act;
       }
-      const int rc = qhip_launch_quantize_mul_mat_vec(wdev, x, xq_out, out, rows, cols, ttype, be->stream);
+      int rc;
+      if (split) {
+        const long wb = gemv_splitk_work_bytes(rows, cols);
+        const hipError_t ew = ensure_skwork(be, (size_t)wb);
+        if (ew != hipSuccess) return report("split-K workspace", ew);
+        rc = qhip_launch_quantize_mul_mat_vec_split(wdev, x, xq_out, out, rows, cols, ttype, 0, 0, 0, be->skwork,
+                                                    (long)be->skwork_cap, be->stream);
+      } else {
+        rc = qhip_launch_quantize_mul_mat_vec(wdev, x, xq_out, out, rows, cols, ttype, be->stream);
+      }
       if (rc != QHIP_DECLINE) {
         if (rc == 0 && xq_out) {
           be->memo_src = x;
@@ -268,6 +302,9 @@ void qhip_backend_free_scratch(qhip_backend* be) {
   be->act = nullptr;
   be->act_cap = 0;
   memo_clear(be);
+  if (be->skwork) (void)hipFree(be->skwork);
+  be->skwork = nullptr;
+  be->skwork_cap = 0;
   for (void* p : be->bufs) (void)hipFree(p);
   be->bufs.clear();
 }

@@ -160,13 +160,33 @@ __host__ __device__ constexpr long fused_lds_bytes(int ttype, int cols) {
              : fused_lds_qs(cols) + (((long)cols / 256 * 4 + 15) & ~15L) + (long)cols / 16 * 2;
 }
 
-template <int TT, int NR, int WGS>
+//
+// Split-K form (SK): the rows' units are cut into slices of `slice_units`
+// (whole super-blocks); workgroup column blockIdx.y owns slice blockIdx.y of
+// the rows of its row tile blockIdx.x and quantizes only that slice of x, so
+// a long activation is quantized once per row tile rather than once per
+// row group.  Each workgroup writes its partial sums to part[slice][row];
+// the last workgroup of a row tile to finish (counted by an atomic in
+// cnt[tile]) adds the partials in slice order, writes y and puts the counter
+// back to zero, so the result does not depend on completion order.  No
+// workgroup waits for another: the last one to arrive does the sum.
+template <int TT, int NR, int WGS, bool SK = false>
 __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, const float* __restrict__ X,
                                                  uint8_t* __restrict__ XQ, float* __restrict__ Y, int rows,
-                                                 int cols, long row_bytes, int upr, int team) {
+                                                 int cols, long row_bytes, int upr, int team,
+                                                 float* __restrict__ part, unsigned* __restrict__ cnt,
+                                                 int slice_units, long slice_wbytes) {
   using U = Unit<TT>;
   grid_prologue<TT>();
   constexpr bool K32 = act32(TT);
+  if constexpr (SK) {
+    const int u0 = (int)blockIdx.y * slice_units;
+    X += 64L * u0;
+    W += (long)blockIdx.y * slice_wbytes;
+    if (XQ) XQ += K32 ? 68L * u0 : 73L * u0;  // 2 x 34 B per unit (Q8_0), 292 B per 4 units (Q8_K)
+    upr = min(slice_units, upr - u0);
+    cols = 64 * upr;
+  }
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int nblk = K32 ? cols / 32 : cols / 256;
   uint8_t* qs = lds;
@@ -297,10 +317,54 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
       }
     }
   }
-  if (active && j == 0) {
+  if constexpr (!SK) {
+    if (active && j == 0) {
 #pragma unroll
-    for (int k = 0; k < NR; ++k)
-      if (row0 + k < rows) Y[row0 + k] = acc[k];
+      for (int k = 0; k < NR; ++k)
+        if (row0 + k < rows) Y[row0 + k] = acc[k];
+    }
+  } else {
+    // The partials and the counter are device-scope atomic accesses, coherent
+    // across the XCDs' L2s by themselves; a full device fence would instead
+    // write back and invalidate the whole L2 of every workgroup's XCD.
+    float* pp = part + (long)blockIdx.y * rows;
+    if (active && j == 0) {
+#pragma unroll
+      for (int k = 0; k < NR; ++k)
+        if (row0 + k < rows) __hip_atomic_store(pp + row0 + k, acc[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // every partial store performed before the slice is counted in
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    __shared__ unsigned last;
+    if (threadIdx.x == 0)
+      last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     gridDim.y - 1
+                 ? 1u
+                 : 0u;
+    __syncthreads();
+    if (last) {
+      const int rpw = (WGS / 64) * tpw * NR;
+      const int ns = (int)gridDim.y;
+      for (int i = threadIdx.x; i < rpw; i += WGS) {
+        const long rr = (long)blockIdx.x * rpw + i;
+        if (rr < rows) {
+          float v = 0.0f;
+          int q = 0;
+          for (; q + 8 <= ns; q += 8) {
+            float t[8];
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
+              t[c] = __hip_atomic_load(part + (long)(q + c) * rows + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int c = 0; c < 8; ++c) v += t[c];
+          }
+          for (; q < ns; ++q) v += __hip_atomic_load(part + (long)q * rows + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          Y[rr] = v;
+        }
+      }
+      if (threadIdx.x == 0) __hip_atomic_store(cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -712,7 +776,7 @@ static hipError_t launch_gemv_q_t(const GemvArgs& g, const float* x, void* xq_ou
   const unsigned grid = (unsigned)((waves + WGS / 64 - 1) / (WGS / 64));
   const size_t lds = (size_t)fused_lds_bytes(TT, g.cols);
   hipLaunchKernelGGL((k_gemv_q<TT, NR, WGS>), dim3(grid), dim3(WGS), lds, s, (const uint8_t*)g.w, x,
-                     (uint8_t*)xq_out, g.out, g.rows, g.cols, g.row_bytes, upr, team);
+                     (uint8_t*)xq_out, g.out, g.rows, g.cols, g.row_bytes, upr, team, nullptr, nullptr, 0, 0L);
   return hipGetLastError();
 }
 
@@ -798,6 +862,88 @@ hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, in
   }
   return dispatch_type(g.ttype, [&](auto tt) {
     return launch_gemv_q_type<decltype(tt)::value>(g, x, xq_out, team, nr, wgs, s);
+  });
+}
+
+// ---- split-K quantize + GEMV (batch 1, long rows) ---------------------------------
+// Workspace: kSkCountBytes of row-tile counters (zero before the first launch,
+// zero again after every launch), then the partials [slices][rows] f32.
+long gemv_splitk_work_bytes(int rows, int cols) { return kSkCountBytes + 4L * rows * ((cols + 255) / 256); }
+
+__global__ __launch_bounds__(256) void k_fill_zero(uint32_t* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) p[i] = 0u;
+}
+
+hipError_t launch_fill_zero(void* p, long bytes, hipStream_t s) {
+  const long n = bytes / 4;
+  if (n <= 0) return hipSuccess;
+  const long g = (n + 255) / 256;
+  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)(g < 1024 ? g : 1024)), dim3(256), 0, s, (uint32_t*)p, n);
+  return hipGetLastError();
+}
+
+template <int TT, int NR>
+static hipError_t launch_gemv_qsk_t(const GemvArgs& g, const float* x, void* xq_out, int team, int su, void* work,
+                                    hipStream_t s) {
+  constexpr int WGS = 256;
+  const int upr = g.cols / 64;
+  const long rpw = (long)(WGS / 64) * (64 / team) * NR;
+  const long tiles = (g.rows + rpw - 1) / rpw;
+  if (tiles > kSkMaxTiles || tiles > 65535) return hipErrorInvalidValue;
+  const int ns = (upr + su - 1) / su;
+  const long swb = g.row_bytes * su / upr;  // exact: su * 64 values are whole blocks
+  const size_t lds = (size_t)fused_lds_bytes(TT, 64 * su);
+  unsigned* cnt = (unsigned*)work;
+  float* part = (float*)((uint8_t*)work + kSkCountBytes);
+  hipLaunchKernelGGL((k_gemv_q<TT, NR, WGS, true>), dim3((unsigned)tiles, (unsigned)ns), dim3(WGS), lds, s,
+                     (const uint8_t*)g.w, x, (uint8_t*)xq_out, g.out, g.rows, g.cols, g.row_bytes, upr, team, part,
+                     cnt, su, swb);
+  return hipGetLastError();
+}
+
+// Default split-K shape, from a sweep on MI355X (slices of 256..2048 values,
+// 4..32 lanes per row, 1..4 rows per lane) over Q6_K [2560, 9728] and
+// [5120, 17408], Q4_K [5120, 17408], and Q5_K, Q3_K, IQ4_XS, Q8_0 at
+// [2560, 9728]: eight lanes and one row per lane throughout; slices of 1024
+// values (within 0.4 us of the best on every shape), 2048 from width 16384
+// (Q4_K [5120, 17408] 14.0 vs 15.9 us).
+static void splitk_default_shape(const GemvArgs& g, int& team, int& nr, int& slice) {
+  team = 8;
+  nr = 1;
+  slice = g.cols >= 16384 ? 2048 : 1024;
+}
+
+// Split-K against the separate quantize + GEMV launches, same sweep (default
+// shape): Q6_K [2560, 9728] 10.3 vs 10.4 us, [5120, 17408] 20.8 vs 21.1;
+// Q4_K [5120, 17408] 14.0 vs 17.1; Q5_K 9.7 vs 11.3, Q3_K 9.8 vs 13.8,
+// IQ4_XS 9.5 vs 9.7, Q8_0 11.5 vs 13.0 at [2560, 9728].  Rows of >= 8192
+// values; narrower rows keep the whole-row fused launch.
+bool gemv_splitk_preferred(const GemvArgs& g) {
+  return g.tokens == 1 && g.cols >= 8192 && g.cols % 256 == 0 && g.rows <= 65536 &&
+         fused_lds_bytes(g.ttype, g.cols >= 16384 ? 2048 : 1024) <= kFusedMaxLds;
+}
+
+hipError_t launch_gemv_splitk(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int slice,
+                              void* work, long work_bytes, hipStream_t s) {
+  if (g.rows <= 0) return hipSuccess;
+  if (g.tokens != 1 || work == nullptr || work_bytes < gemv_splitk_work_bytes(g.rows, g.cols))
+    return hipErrorInvalidValue;
+  int dt = 0, dn = 0, ds = 0;
+  splitk_default_shape(g, dt, dn, ds);
+  if (team <= 0) team = dt;
+  if (nr <= 0) nr = dn;
+  if (slice <= 0) slice = ds;
+  if (slice % 256 || (team & (team - 1)) || team < 4 || team > 64) return hipErrorInvalidValue;
+  const int su = slice / 64;
+  if (fused_lds_bytes(g.ttype, slice) > kFusedMaxLds) return hipErrorInvalidValue;
+  return dispatch_type(g.ttype, [&](auto tt) -> hipError_t {
+    constexpr int T = decltype(tt)::value;
+    switch (nr) {
+      case 1: return launch_gemv_qsk_t<T, 1>(g, x, xq_out, team, su, work, s);
+      case 2: return launch_gemv_qsk_t<T, 2>(g, x, xq_out, team, su, work, s);
+      case 4: return launch_gemv_qsk_t<T, 4>(g, x, xq_out, team, su, work, s);
+      default: return hipErrorInvalidValue;
+    }
   });
 }
 

@@ -39,6 +39,18 @@ bool gemv_fused_fits(int ttype, int cols);
 bool gemv_fused_preferred(const GemvArgs& g);
 hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
                              hipStream_t s);
+// Split-K quantize + GEMV for one token on long rows: slices of `slice`
+// values (a multiple of 256) per workgroup, partial sums in `work`
+// (gemv_splitk_work_bytes; its first kSkCountBytes must be zero before the
+// first launch and are zero again after each).  0 picks team / nr / slice.
+constexpr long kSkMaxTiles = 8192;
+constexpr long kSkCountBytes = 4 * kSkMaxTiles;
+long gemv_splitk_work_bytes(int rows, int cols);
+// zero `bytes` (a multiple of 4) with a fill kernel (no memset node in graphs)
+hipError_t launch_fill_zero(void* p, long bytes, hipStream_t s);
+bool gemv_splitk_preferred(const GemvArgs& g);
+hipError_t launch_gemv_splitk(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int slice,
+                              void* work, long work_bytes, hipStream_t s);
 // GGUF blocks -> f32 (nvals = whole blocks' values)
 hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hipStream_t s);
 // MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)

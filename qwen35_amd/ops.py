@@ -101,6 +101,25 @@ def quantize_mul_mat_vec(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int
     return out
 
 
+def split_work(rows: int, cols: int, device) -> torch.Tensor:
+    """Zeroed workspace for quantize_mul_mat_vec_split (its counters must start at zero)."""
+    n = load().qhip_quantize_mul_mat_vec_work_bytes(rows, cols)
+    return torch.zeros(max(n, 16), dtype=torch.uint8, device=device)
+
+
+def quantize_mul_mat_vec_split(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
+                               work: torch.Tensor, slice_values: int = 0, lanes_per_row: int = 0,
+                               rows_per_lane: int = 0, xq_out: torch.Tensor | None = None,
+                               out: torch.Tensor | None = None) -> torch.Tensor:
+    """One launch, split over K: each workgroup quantizes and multiplies one slice of x."""
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=w.device)
+    check("quantize_mul_mat_vec_split", load().qhip_launch_quantize_mul_mat_vec_split(
+        _p(w), _p(x), _p(xq_out) if xq_out is not None else None, _p(out), rows, cols, ttype, slice_values,
+        lanes_per_row, rows_per_lane, _p(work), work.numel(), _stream()))
+    return out
+
+
 def gemv_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
                lanes_per_row: int, tokens_per_pass: int, rows_per_lane: int = 1,
                out: torch.Tensor | None = None) -> torch.Tensor:

@@ -244,6 +244,71 @@ def test_fused_declines(gpu):
     assert rc not in (0, qwen35_amd.DECLINE)
 
 
+# ---- split-K quantize + GEMV ---------------------------------------------------------
+
+SPLIT = [(po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 37, 9728), (po.TT_Q4_K, 300, 5120), (po.TT_Q5_K, 100, 4352),
+         (po.TT_Q3_K, 60, 2304), (po.TT_Q2_K, 70, 2560), (po.TT_IQ4_XS, 80, 2560), (po.TT_IQ3_XXS, 90, 2560),
+         (po.TT_IQ3_S, 16, 2304), (po.TT_Q8_0, 300, 2048), (po.TT_IQ4_NL, 200, 1024), (po.TT_Q4_0, 50, 2560),
+         (po.TT_Q4_1, 70, 1536)]
+# (slice values, lanes per row, rows per lane); 0 picks.  768 leaves a short
+# last slice on most widths; 64 lanes on a 256-value slice idle most lanes.
+SPLIT_SHAPES = [(0, 0, 0), (256, 4, 1), (512, 8, 2), (768, 32, 2), (1024, 16, 4), (256, 64, 1), (2048, 64, 4)]
+
+
+@pytest.mark.parametrize("tt,rows,cols", SPLIT, ids=[case_id(*c) for c in SPLIT])
+def test_split_quantize_gemv(gpu, oracle, tt, rows, cols):
+    w = synth.make_weight(tt, rows, cols, seed=13, tag=tt)
+    x = synth.make_act(cols, 1, seed=13)
+    want = oracle.matvec(tt, w, x)[0]
+    xq_want = oracle.quantize_act(tt, x)[0]
+    wd, xd = to_dev(w, gpu), to_dev(x[0], gpu)
+    work = ops.split_work(rows, cols, gpu)
+    first = None
+    for sl, lpr, nr in SPLIT_SHAPES:
+        xq = torch.zeros(xq_want.shape[-1], dtype=torch.uint8, device=gpu)
+        got = ops.quantize_mul_mat_vec_split(tt, wd, xd, rows, cols, work, sl, lpr, nr, xq_out=xq).cpu().numpy()
+        assert np.array_equal(xq.cpu().numpy(), xq_want), (sl, lpr, nr)
+        assert rel_l2(got, want) < TOL, (sl, lpr, nr, rel_l2(got, want))
+        if (sl, lpr, nr) == (0, 0, 0):
+            first = got
+    # the counters are back at zero: a repeat gives the same bits, and so does
+    # a smaller matrix (fewer row tiles) on the same workspace
+    again = ops.quantize_mul_mat_vec_split(tt, wd, xd, rows, cols, work).cpu().numpy()
+    assert np.array_equal(again, first)
+    small = max(4, rows // 12 * 4)  # a multiple of 4 rows keeps the weight 4-byte aligned
+    got = ops.quantize_mul_mat_vec_split(tt, wd[:small], xd, small,
+                                         cols, work).cpu().numpy()
+    assert rel_l2(got, want[:small]) < TOL
+    assert np.array_equal(work[: 4 * 8192].cpu().numpy(), np.zeros(4 * 8192, np.uint8))
+
+
+def test_split_declines(gpu):
+    from qwen35_amd import _lib
+    L = _lib.load()
+    tt, rows, cols = po.TT_Q6_K, 8, 1024
+    w = torch.zeros(rows * cols // 256 * 210, dtype=torch.uint8, device=gpu)
+    xbuf = torch.zeros(cols + 4, device=gpu)
+    out = torch.empty(rows, device=gpu)
+    work = ops.split_work(rows, cols, gpu)
+    n = work.numel()
+    # activation not 16-byte aligned: decline
+    assert L.qhip_launch_quantize_mul_mat_vec_split(w.data_ptr(), xbuf[1:].data_ptr(), None, out.data_ptr(), rows,
+                                                    cols, tt, 0, 0, 0, work.data_ptr(), n, None) == qwen35_amd.DECLINE
+    # width not a multiple of 256 (Q8_0 rows of 1056 values): decline
+    w8 = torch.zeros(rows * 1056 // 32 * 34, dtype=torch.uint8, device=gpu)
+    x8 = torch.zeros(1056, device=gpu)
+    work8 = ops.split_work(rows, 1056, gpu)
+    assert L.qhip_launch_quantize_mul_mat_vec_split(w8.data_ptr(), x8.data_ptr(), None, out.data_ptr(), rows, 1056,
+                                                    po.TT_Q8_0, 0, 0, 0, work8.data_ptr(), work8.numel(),
+                                                    None) == qwen35_amd.DECLINE
+    # a workspace too small, a bad slice or shape: errors
+    for args in [(0, 0, 0, n - 4), (300, 0, 0, n), (0, 12, 0, n), (0, 2, 0, n), (0, 0, 3, n)]:
+        sl, lpr, nr, nb = args
+        rc = L.qhip_launch_quantize_mul_mat_vec_split(w.data_ptr(), xbuf.data_ptr(), None, out.data_ptr(), rows, cols,
+                                                      tt, sl, lpr, nr, work.data_ptr(), nb, None)
+        assert rc not in (0, qwen35_amd.DECLINE), args
+
+
 @pytest.mark.parametrize("tt", TYPES)
 def test_multiwave_team_shapes(gpu, oracle, tt):
     """Teams of two / four whole waves (one token), rows not a multiple of the
