@@ -77,19 +77,20 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
 // Measured on MI355X at the BASELINE shapes with split-K MMQ for small token
 // counts: Q4_K [17408, 5120] GEMV 23.6 us / MMQ 31.2 us at 4 tokens, 39.2 /
 // 30.3 us at 8; Q6_K [5120, 17408] 44.5 / 42.4 us at 8; Q8_0 [3584, 1024]
-// 5.3 / 7.9 us at 8, 8.1 / 8.0 us at 16.
+// 5.3 / 7.9 us at 8, 8.1 / 8.0 us at 16; Q3_K / Q2_K [17408, 5120] 48.6 /
+// 29.6 and 38.6 / 26.8 us at 8 (Q2_K 23.3 / 26.5 at 4).
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
-    case TT_Q4_K: case TT_Q5_K: case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: return 8;
+    case TT_Q4_K: case TT_Q5_K: case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: case TT_Q3_K:
+    case TT_Q2_K: return 8;
     default: return 16;
   }
 }
 
-// Formats with an MMQ kernel; the others (Q3_K, Q2_K) multiply many tokens
-// with the GEMV, which shares each weight load across up to 8 tokens per pass.
+// Formats with an MMQ kernel: all of them.
 static bool mmq_supported(int ttype) {
   return act32(ttype) || iq3(ttype) || ttype == TT_Q4_K || ttype == TT_Q6_K || ttype == TT_Q5_K ||
-         ttype == TT_IQ4_XS;
+         ttype == TT_IQ4_XS || ttype == TT_Q3_K || ttype == TT_Q2_K;
 }
 
 // The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image

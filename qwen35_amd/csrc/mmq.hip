@@ -36,6 +36,11 @@
 //                 ls - 32, no mins  (iq_kernels.c:967-1001)
 //   IQ3_XXS/IQ3_S the same on the signed grid values with the odd scale
 //                 2 ls + 1  (iq_kernels.c:612-643, :1728-1772)
+//   Q3_K          as Q6_K on q3 in [-4, 3] with the signed 6-bit group
+//                 scales sc - 32  (kernels256.c:349-369)
+//   Q2_K          as Q6_K on q2 in [0, 3] with the 4-bit group scales; the
+//                 mins term sum_g bsum[g]*min[g] as Q4_K's f16 MFMA
+//                 (kernels256.c:232-257)
 // and the float scaling follows per block / super-block.  For the 32-value
 // formats the accumulator input is the bit pattern of 1.5*2^23, so the MFMA
 // result read as a float is 1.5*2^23 + sumi exactly (|sumi| <= 2^19); one
@@ -117,6 +122,23 @@ struct alignas(16) MmqSmem<TT_Q6_K, BT, BR, false> {
   float ady[BT];
   float wd[BR];
   uint32_t wsc[BR][4];  // sixteen int8 group scales
+};
+
+// Q3_K: sixteen signed group scales (sc - 32) and d, like Q6_K
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_Q3_K, BT, BR, false> : MmqSmem<TT_Q6_K, BT, BR, false> {};
+
+// Q2_K: sixteen 4-bit group scales and mins, d and dmin; the mins term is the
+// f16 MFMA of Q4_K over the activation's 16-value sums
+template <int BT, int BR>
+struct alignas(16) MmqSmem<TT_Q2_K, BT, BR, false> {
+  uint8_t aq[BT * kQS];
+  uint8_t bq[BR * kQS];
+  _Float16 abs[BT][16];
+  _Float16 wmn[BR][16];
+  uint32_t wsc[BR][4];
+  float ady[BT];
+  float wd[BR], wdmin[BR];
 };
 
 __device__ __forceinline__ void st16(uint8_t* p, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -289,6 +311,49 @@ __device__ __forceinline__ void emit_w(MmqSmem<TT, BT, BR>& sm, const typename U
       sp[1] = (uint8_t)(2 * (w.sc >> 4) + 1);
       if (u4 == 0) sm.wd[row] = h2f(w.d);
     }
+  } else if constexpr (TT == TT_Q3_K) {
+    // unit c = values 64c..64c+63: half jj of it is shift g = 2(c&1) + jj of
+    // qs[32h..] with h = c >> 1; value = q2 - 4 unless its hmask bit 4h+g is
+    // set (kernels256.c:162-177): q2 | 0xFC per byte where the bit is clear
+    const int h = u4 >> 1;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int g = 2 * (u4 & 1) + jj;
+      uint32_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t q2 = (w.q[i] >> (2 * g)) & 0x03030303u;
+        const uint32_t hb = (w.hm[i] >> (4 * h + g)) & 0x01010101u;
+        v[i] = q2 | ((hb ^ 0x01010101u) * 0xFCu);
+      }
+      st16(dst + 32 * jj, v[0], v[1], v[2], v[3]);
+      st16(dst + 32 * jj + 16, v[4], v[5], v[6], v[7]);
+    }
+    // group scales 4c..4c+3: the unpacked 6-bit values (kernels256.c:129-151) - 32
+    const uint32_t base = (u4 & 1) ? w.s1 : w.s0;
+    const uint32_t scw = ((u4 >= 2 ? (base >> 4) : base) & 0x0F0F0F0Fu) | (((w.s2 >> (2 * u4)) & 0x03030303u) << 4);
+    sm.wsc[row][u4] = q6_minus32(scw);
+    if (u4 == 0) sm.wd[row] = h2f(w.d);
+  } else if constexpr (TT == TT_Q2_K) {
+    // unit c = values 64c..64c+63: half jj is shift j = 2(c&1) + jj of
+    // qs[32k..] with k = c >> 1 (kernels256.c:153-160)
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int j = 2 * (u4 & 1) + jj;
+      uint32_t v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = (w.q[i] >> (2 * j)) & 0x03030303u;
+      st16(dst + 32 * jj, v[0], v[1], v[2], v[3]);
+      st16(dst + 32 * jj + 16, v[4], v[5], v[6], v[7]);
+    }
+    // groups 4c..4c+3: scale = low nibble, min = high nibble
+    sm.wsc[row][u4] = w.sc & 0x0F0F0F0Fu;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sm.wmn[row][4 * u4 + k] = (_Float16)(float)((w.sc >> (8 * k + 4)) & 15u);
+    if (u4 == 0) {
+      sm.wd[row] = h2f(w.dd & 0xFFFFu);
+      sm.wdmin[row] = h2f(w.dd >> 16);
+    }
   } else {  // Q6_K: unit (h, lh) holds values 128h + 32q + 16lh + (0..15), q = 0..3
     const int h = (u4 >> 1) & 1, lh = u4 & 1;
     uint32_t v[4][4];
@@ -346,7 +411,7 @@ __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) st16(dst + 16 * i, a.y[4 * i], a.y[4 * i + 1], a.y[4 * i + 2], a.y[4 * i + 3]);
-    if constexpr (TT == TT_Q4_K || TT == TT_Q5_K) {
+    if constexpr (TT == TT_Q4_K || TT == TT_Q5_K || TT == TT_Q2_K) {
       _Float16* bp = &sm.abs[tok][4 * u4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) bp[i] = (_Float16)(float)a.bs[i];
@@ -724,13 +789,40 @@ __global__ __launch_bounds__(NT) void k_mmq(const uint8_t* __restrict__ W, const
         for (int q = 0; q < 4; ++q) dy[a][q] = *(const f32x4*)&sm.ady[tb0 + 32 * a + 8 * q + 4 * lh];
 #pragma unroll
       for (int b = 0; b < NB; ++b) d[b] = sm.wd[rb0 + 32 * b + li];
+      if constexpr (TT == TT_Q2_K) {
+        // mins: summs[t][r] = sum_g bsum[t][g] * min[r][g], exact in the f16
+        // MFMA (|bsum| <= 2032, min <= 15, 16 groups: < 2^24)
+        // (kernels256.c:232-257: dall * isum - dmin * summs)
+        f16x8 am[NA], bm[NB];
+        float ndm[NB];
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
+        for (int a = 0; a < NA; ++a) am[a] = *(const f16x8*)&sm.abs[tb0 + 32 * a + li][8 * lh];
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int b = 0; b < NB; ++b) {
+          bm[b] = *(const f16x8*)&sm.wmn[rb0 + 32 * b + li][8 * lh];
+          ndm[b] = -sm.wdmin[rb0 + 32 * b + li];
+        }
+        const f32x16 fz = {};
 #pragma unroll
-          for (int e = 0; e < 16; ++e)
-            acc[a][b][e] = __builtin_fmaf(d[b] * dy[a][e >> 2][e & 3], (float)isum[a][b][e], acc[a][b][e]);
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b) {
+            const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am[a], bm[b], fz, 0, 0, 0);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+              const float inner = __builtin_fmaf(d[b], (float)isum[a][b][e], ndm[b] * cm[e]);
+              acc[a][b][e] = __builtin_fmaf(dy[a][e >> 2][e & 3], inner, acc[a][b][e]);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+              acc[a][b][e] = __builtin_fmaf(d[b] * dy[a][e >> 2][e & 3], (float)isum[a][b][e], acc[a][b][e]);
+      }
     }
   }
 
@@ -1374,6 +1466,8 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
     case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, ksplit, s);
     case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, ksplit, s);
     case TT_IQ4_XS: return launch_mmq_type<TT_IQ4_XS>(g, bt, br, ksplit, s);
+    case TT_Q3_K: return launch_mmq_type<TT_Q3_K>(g, bt, br, ksplit, s);
+    case TT_Q2_K: return launch_mmq_type<TT_Q2_K>(g, bt, br, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }

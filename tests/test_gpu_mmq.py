@@ -58,6 +58,10 @@ CASES = [
     (po.TT_Q4_0, 200, 1280, 75),     # an odd chunk count
     (po.TT_Q8_0, 70, 2048, 66),
     (po.TT_Q4_1, 64, 1024, 128),
+    (po.TT_Q3_K, 150, 512, 65),
+    (po.TT_Q3_K, 72, 2304, 129),
+    (po.TT_Q2_K, 100, 768, 40),
+    (po.TT_Q2_K, 64, 2560, 16),
 ]
 IDS = [f"{po.NAMES[c[0]]}-{c[1]}x{c[2]}-t{c[3]}" for c in CASES]
 
@@ -90,6 +94,11 @@ def unit_scale_weight(tt, rows, cols, seed):
     elif tt in (po.TT_Q4_K, po.TT_Q5_K, po.TT_Q4_1):  # d = 1 and dmin (Q4_1: m) = 1
         blk[:, :, 0:2] = F16_ONE
         blk[:, :, 2:4] = F16_ONE
+    elif tt == po.TT_Q3_K:
+        blk[:, :, 108:110] = F16_ONE
+    elif tt == po.TT_Q2_K:  # d = 1 and dmin = 1
+        blk[:, :, 80:82] = F16_ONE
+        blk[:, :, 82:84] = F16_ONE
     else:
         blk[:, :, 208:210] = F16_ONE
     return w
@@ -105,7 +114,7 @@ def unit_scale_act(cols, tokens, seed):
 
 
 @pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_IQ4_NL, po.TT_Q4_K, po.TT_Q6_K, po.TT_Q5_K, po.TT_IQ4_XS,
-                                po.TT_Q4_0, po.TT_Q4_1, po.TT_IQ3_XXS, po.TT_IQ3_S])
+                                po.TT_Q4_0, po.TT_Q4_1, po.TT_IQ3_XXS, po.TT_IQ3_S, po.TT_Q3_K, po.TT_Q2_K])
 def test_mmq_block_integers_exact(gpu, oracle, tt):
     # IQ4_XS / IQ3: the super-block sums carry the scales (up to 31), so a
     # narrower width keeps every result below 2^24; IQ3_XXS's 1/4 leaves
@@ -116,7 +125,7 @@ def test_mmq_block_integers_exact(gpu, oracle, tt):
     x = unit_scale_act(cols, tokens, seed=5)
     act = oracle.quantize_act(tt, x)
     ints = oracle.block_ints(tt, w, act, cols).astype(np.int64)  # [tokens][rows][nints]
-    if tt in (po.TT_Q4_K, po.TT_Q5_K):
+    if tt in (po.TT_Q4_K, po.TT_Q5_K, po.TT_Q2_K):
         want = ints[:, :, 0::2].sum(-1) - ints[:, :, 1::2].sum(-1)  # isum - summs
     elif tt == po.TT_Q4_1:
         want = ints[:, :, 0::2].sum(-1) + ints[:, :, 1::2].sum(-1)  # sumi + sumy
@@ -343,9 +352,9 @@ def ctypes_byref(x):
 
 
 @pytest.mark.parametrize("tt", [po.TT_Q3_K, po.TT_Q2_K])
-def test_formats_without_mmq_decline_and_auto_uses_gemv(gpu, oracle, tt):
-    """Q3_K / Q2_K have no MMQ kernel: the explicit MMQ entry points decline,
-    the automatic path serves any token count with the GEMV."""
+def test_q3_k_q2_k_mmq_entry_points(gpu, oracle, tt):
+    """Q3_K / Q2_K: the reference-named tile entry point and the automatic
+    path take the MMQ; there is no weight image for them."""
     rows, cols, tokens = 72, 1024, 70
     w = synth.make_weight(tt, rows, cols, seed=12, tag=tt)
     x = synth.make_act(cols, tokens, seed=12)
@@ -353,10 +362,10 @@ def test_formats_without_mmq_decline_and_auto_uses_gemv(gpu, oracle, tt):
     xq = ops.quantize_act(tt, to_dev(x, gpu))
     out = torch.empty((tokens, rows), device=gpu)
     L = _lib.load()
-    assert L.qhip_launch_mmq_tuned(wd.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt,
-                                   64, 64, None) == qwen35_amd.DECLINE
+    want = oracle.matvec(tt, w, x)
     assert L.qhip_launch_mul_mat_vec_tile(wd.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt,
-                                          None) == qwen35_amd.DECLINE
+                                          None) == 0
+    assert rel_l2(out.cpu().numpy(), want) < TOL
     assert L.qhip_mmq_image_bytes(tt, rows, cols) == -1
     got = ops.mul_mat(tt, wd, xq, rows, cols, tokens).cpu().numpy()
     assert rel_l2(got, oracle.matvec(tt, w, x)) < TOL
