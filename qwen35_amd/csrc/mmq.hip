@@ -860,16 +860,6 @@ static int mmq_ksplit_for(const GemvArgs& g, int bt, int br, int nchunks, int mi
   return (int)(want < cap ? want : cap);
 }
 
-__global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ y, long n) {
-  for (long i = (long)blockIdx.x * 256 + threadIdx.x; i < n; i += (long)gridDim.x * 256) y[i] = 0.0f;
-}
-
-// a kernel, not a memset node, so the launch sequence stays capture-safe
-static void launch_fill_zero(float* y, long n, hipStream_t s) {
-  const long blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
-  hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)blocks), dim3(256), 0, s, y, n);
-}
-
 // ---- MMQ on a prepared weight image (Q4_K, Q6_K) -----------------------------------------
 // The K-quants' integer sub-scales are folded into the quantized values once,
 // at weight-load time: p = sc * q (Q4_K, 0..945) or p = sc * (q6 - 32) (Q6_K,
@@ -1189,7 +1179,11 @@ static hipError_t launch_mmq_img_t(const GemvArgs& g, int ksplit, hipStream_t s)
   ksplit = (nsb + cps - 1) / cps;
   const long G = ntr * ntt * ksplit;
   if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
-  if (ksplit > 1) launch_fill_zero(g.out, (long)g.tokens * g.rows, s);
+  if (ksplit > 1) {
+    // the slices add into y: zero it with a kernel (capture-safe, no memset node)
+    const hipError_t ez = launch_fill_zero(g.out, 4L * g.tokens * g.rows, s);
+    if (ez != hipSuccess) return ez;
+  }
   hipLaunchKernelGGL((k_mmq_img<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.tokens, nsb, g.act_bytes, (int)ntt, ksplit, cps);
   return hipGetLastError();
@@ -1409,7 +1403,11 @@ static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
   ksplit = (nchunks + cps - 1) / cps;  // no empty slices
   const long G = ntr * ntt * ksplit;
   if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
-  if (ksplit > 1) launch_fill_zero(g.out, (long)g.tokens * g.rows, s);
+  if (ksplit > 1) {
+    // the slices add into y: zero it with a kernel (capture-safe, no memset node)
+    const hipError_t ez = launch_fill_zero(g.out, 4L * g.tokens * g.rows, s);
+    if (ez != hipSuccess) return ez;
+  }
   hipLaunchKernelGGL((k_mmq<TT, BT, BR, NT>), dim3((unsigned)G), dim3(NT), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
                      ksplit, cps);
