@@ -889,8 +889,9 @@ static hipError_t launch_gemv_qsk_t(const GemvArgs& g, const float* x, void* xq_
   const int upr = g.cols / 64;
   const long rpw = (long)(WGS / 64) * (64 / team) * NR;
   const long tiles = (g.rows + rpw - 1) / rpw;
-  if (tiles > kSkMaxTiles || tiles > 65535) return hipErrorInvalidValue;
+  if (tiles > kSkMaxTiles) return hipErrorInvalidValue;
   const int ns = (upr + su - 1) / su;
+  if (ns > 65535) return hipErrorInvalidValue;  // grid y limit
   const long swb = g.row_bytes * su / upr;  // exact: su * 64 values are whole blocks
   const size_t lds = (size_t)fused_lds_bytes(TT, 64 * su);
   unsigned* cnt = (unsigned*)work;
