@@ -277,7 +277,10 @@ int qhip_backend_matvec_batch_k(qhip_backend *be, float *d_out, const qhip_linea
  * (the embedding lookup). */
 int qhip_backend_dequant_row(qhip_backend *be, float *d_dst, const qhip_linear *w, int row);
 /* Stream for subsequent calls (NULL = default stream) and a host wait.
- * Changing the stream forgets the memoized activation (below). */
+ * Changing the stream forgets the memoized activation (below) and, unless
+ * the old stream is being captured, waits for the old stream's work: the
+ * backend's activation scratch and split-K workspace are single buffers, so
+ * launches on two streams must not overlap. */
 int qhip_backend_set_stream(qhip_backend *be, void *stream);
 int qhip_backend_sync(qhip_backend *be);
 

@@ -352,7 +352,17 @@ int qhip_backend_dequant_row(qhip_backend* be, float* d_dst, const qhip_linear* 
 
 int qhip_backend_set_stream(qhip_backend* be, void* stream) {
   if (!be) return (int)hipErrorInvalidValue;
-  if (be->stream != (hipStream_t)stream) memo_clear(be);
+  if (be->stream != (hipStream_t)stream) {
+    memo_clear(be);
+    // the scratch and the split-K workspace are single buffers: the old
+    // stream's launches finish before another stream may write them (a
+    // stream under capture has nothing in flight to wait for)
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(be->stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+      const hipError_t e = hipStreamSynchronize(be->stream);
+      if (e != hipSuccess) return report("set_stream", e);
+    }
+  }
   be->stream = (hipStream_t)stream;
   return 0;
 }
