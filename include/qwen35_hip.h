@@ -130,6 +130,17 @@ int qhip_launch_mul_mat(const void *d_w, const void *d_xq, float *d_out, int row
 int qhip_launch_quantize_mul_mat_vec(const void *d_w, const float *d_x, void *d_xq_out, float *d_out,
                                      int rows, int cols, int ttype, void *stream);
 
+/* The one-launch quantize + GEMV with an explicit shape: `lanes_per_row`
+ * (1..64) lanes share `rows_per_lane` (1, 2 or 4) rows; `workgroup_threads`
+ * 256, 512 or 1024 (512 / 1024 with at most two rows per lane) quantize the
+ * activation once per workgroup; 0 picks for any of them.  Replaces nothing
+ * in the reference (its launch shapes are env knobs,
+ * src/kernels/cuda/mmvq.cu:685-772).  Declines as
+ * qhip_launch_quantize_mul_mat_vec. */
+int qhip_launch_quantize_mul_mat_vec_tuned(const void *d_w, const float *d_x, void *d_xq_out, float *d_out,
+                                           int rows, int cols, int ttype, int lanes_per_row, int rows_per_lane,
+                                           int workgroup_threads, void *stream);
+
 /* The same product for long rows, split over K: each workgroup quantizes and
  * multiplies one slice of `slice_values` values (a multiple of 256; 0 picks)
  * of a tile of rows, writes its partial sums into d_work, and the last

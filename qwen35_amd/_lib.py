@@ -48,6 +48,8 @@ SIGNATURES = {
                                       c_int, c_void_p]),
     "qhip_launch_quantize_mul_mat_vec": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
                                                  c_void_p]),
+    "qhip_launch_quantize_mul_mat_vec_tuned": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                                       c_int, c_int, c_int, c_int, c_void_p]),
     "qhip_quantize_mul_mat_vec_work_bytes": (c_long, [c_int, c_int]),
     "qhip_launch_quantize_mul_mat_vec_split": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                                        c_int, c_int, c_int, c_int, c_void_p, c_long,

@@ -308,7 +308,23 @@ int qhip_launch_quantize_mul_mat_vec(const void* d_w, const float* d_x, void* d_
   if (rows == 0) return 0;
   // float4 activation reads: x 16-byte aligned
   if (!fast_ok(g) || ((uintptr_t)d_x & 15u) || !gemv_fused_fits(ttype, cols)) return QHIP_DECLINE;
-  return (int)launch_gemv_fused(g, d_x, d_xq_out, 0, 0, S(stream));
+  return (int)launch_gemv_fused(g, d_x, d_xq_out, 0, 0, 0, S(stream));
+}
+
+int qhip_launch_quantize_mul_mat_vec_tuned(const void* d_w, const float* d_x, void* d_xq_out, float* d_out, int rows,
+                                           int cols, int ttype, int lanes_per_row, int rows_per_lane,
+                                           int workgroup_threads, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_x, d_out, rows, cols, 1, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (d_xq_out && !aligned4(d_xq_out)) return (int)hipErrorInvalidValue;
+  const int wgs = workgroup_threads, nr = rows_per_lane;
+  if (lanes_per_row < 0 || lanes_per_row > 64 || nr < 0 || nr > 4 || nr == 3 ||
+      (wgs != 0 && wgs != 256 && wgs != 512 && wgs != 1024) || (wgs > 256 && nr > 2))
+    return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!fast_ok(g) || ((uintptr_t)d_x & 15u) || !gemv_fused_fits(ttype, cols)) return QHIP_DECLINE;
+  return (int)launch_gemv_fused(g, d_x, d_xq_out, lanes_per_row, nr, wgs, S(stream));
 }
 
 long qhip_quantize_mul_mat_vec_work_bytes(int rows, int cols) {

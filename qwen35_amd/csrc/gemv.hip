@@ -784,6 +784,9 @@ template <int TT>
 static hipError_t launch_gemv_q_type(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int wgs,
                                      hipStream_t s) {
   if (wgs == 1024 && nr == 1) return launch_gemv_q_t<TT, 1, 1024>(g, x, xq_out, team, s);
+  if (wgs == 1024 && nr == 2) return launch_gemv_q_t<TT, 2, 1024>(g, x, xq_out, team, s);
+  if (wgs == 512 && nr == 1) return launch_gemv_q_t<TT, 1, 512>(g, x, xq_out, team, s);
+  if (wgs == 512 && nr == 2) return launch_gemv_q_t<TT, 2, 512>(g, x, xq_out, team, s);
   if (wgs != 256) return hipErrorInvalidValue;
   switch (nr) {
     case 1: return launch_gemv_q_t<TT, 1, 256>(g, x, xq_out, team, s);
@@ -849,15 +852,15 @@ bool gemv_fused_preferred(const GemvArgs& g) {
   return true;
 }
 
-hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
+hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int wgs,
                              hipStream_t s) {
   if (g.rows <= 0) return hipSuccess;
   if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols)) return hipErrorInvalidValue;
-  int wgs = 256;
-  if (team <= 0 && nr <= 0) {
+  if (team <= 0 && nr <= 0 && wgs <= 0) {
     fused_default_shape(g, team, nr, wgs);
   } else {
     if (nr <= 0) nr = 1;
+    if (wgs <= 0) wgs = 256;
     if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);
   }
   return dispatch_type(g.ttype, [&](auto tt) {

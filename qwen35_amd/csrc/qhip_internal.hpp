@@ -37,7 +37,8 @@ constexpr long kFusedMaxLds = 64 * 1024;
 bool gemv_fused_fits(int ttype, int cols);
 // whether the fused launch beats quantize + GEMV for this shape (measured rule)
 bool gemv_fused_preferred(const GemvArgs& g);
-hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr,
+// team / nr / wgs (workgroup threads: 256, or 512 / 1024 with nr <= 2) 0 = pick
+hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int wgs,
                              hipStream_t s);
 // Split-K quantize + GEMV for one token on long rows: slices of `slice`
 // values (a multiple of 256) per workgroup, partial sums in `work`

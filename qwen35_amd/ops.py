@@ -101,6 +101,18 @@ def quantize_mul_mat_vec(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int
     return out
 
 
+def quantize_mul_mat_vec_tuned(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
+                               lanes_per_row: int = 0, rows_per_lane: int = 0, workgroup_threads: int = 0,
+                               xq_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """The one-launch quantize + GEMV with an explicit shape (0 = pick)."""
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=w.device)
+    check("quantize_mul_mat_vec_tuned", load().qhip_launch_quantize_mul_mat_vec_tuned(
+        _p(w), _p(x), _p(xq_out) if xq_out is not None else None, _p(out), rows, cols, ttype, lanes_per_row,
+        rows_per_lane, workgroup_threads, _stream()))
+    return out
+
+
 def split_work(rows: int, cols: int, device) -> torch.Tensor:
     """Zeroed workspace for quantize_mul_mat_vec_split (its counters must start at zero)."""
     n = load().qhip_quantize_mul_mat_vec_work_bytes(rows, cols)

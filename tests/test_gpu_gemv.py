@@ -207,6 +207,29 @@ def test_fused_quantize_gemv(gpu, oracle, tt, rows, cols):
     assert rel_l2(got, two) < 1e-6
 
 
+FUSED_SHAPES = [(20, 1, 1024), (16, 2, 1024), (40, 2, 512), (8, 1, 512), (64, 4, 256), (12, 2, 256), (0, 0, 0)]
+
+
+@pytest.mark.parametrize("tt,rows,cols", [(po.TT_Q4_K, 1000, 2560), (po.TT_Q8_0, 333, 1024),
+                                          (po.TT_Q6_K, 70, 2304), (po.TT_IQ4_NL, 129, 2560)])
+def test_fused_explicit_shapes(gpu, oracle, tt, rows, cols):
+    """Explicit lanes / rows per lane / workgroup sizes, rows not a multiple
+    of any workgroup's rows."""
+    w = synth.make_weight(tt, rows, cols, seed=19, tag=tt)
+    x = synth.make_act(cols, 1, seed=19)
+    want = oracle.matvec(tt, w, x)[0]
+    xq_want = oracle.quantize_act(tt, x)[0]
+    wd, xd = to_dev(w, gpu), to_dev(x[0], gpu)
+    for lpr, nr, wgs in FUSED_SHAPES:
+        xq = torch.zeros(xq_want.shape[-1], dtype=torch.uint8, device=gpu)
+        got = ops.quantize_mul_mat_vec_tuned(tt, wd, xd, rows, cols, lpr, nr, wgs, xq_out=xq).cpu().numpy()
+        assert np.array_equal(xq.cpu().numpy(), xq_want), (lpr, nr, wgs)
+        assert rel_l2(got, want) < TOL, (lpr, nr, wgs, rel_l2(got, want))
+    for bad in [(8, 4, 512), (8, 1, 384), (65, 1, 256), (8, 3, 256)]:
+        with pytest.raises(qwen35_amd.QhipError):
+            ops.quantize_mul_mat_vec_tuned(tt, wd, xd, rows, cols, *bad)
+
+
 @pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K])
 def test_fused_quantize_special_values(gpu, oracle, tt):
     rows, cols = 40, 2048
