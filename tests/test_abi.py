@@ -100,9 +100,26 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert lib.qhip_launch_quantize_ragged(8, None, p, 2, 10, 256, p, None) == INVALID
     # parity export
     assert lib.qhip_launch_block_ints(p, p, p, 16, 96, 1, 8, None) == INVALID
+    # one-launch quantize + GEMV: bad shapes, and the split-K workspace checks
+    assert lib.qhip_launch_quantize_mul_mat_vec_tuned(p, p, None, p, 16, 256, 12, 65, 1, 256, None) == INVALID
+    assert lib.qhip_launch_quantize_mul_mat_vec_tuned(p, p, None, p, 16, 256, 12, 8, 4, 1024, None) == INVALID
+    need = lib.qhip_quantize_mul_mat_vec_work_bytes(16, 9728)
+    assert lib.qhip_launch_quantize_mul_mat_vec_split(p, p, None, p, 16, 9728, 14, 0, 0, 0, None, need,
+                                                      None) == INVALID
+    assert lib.qhip_launch_quantize_mul_mat_vec_split(p, p, None, p, 16, 9728, 14, 0, 0, 0, p, need - 4,
+                                                      None) == INVALID
+    assert lib.qhip_launch_quantize_mul_mat_vec_split(p, p, None, p, 16, 9728, 14, 300, 0, 0, p, need,
+                                                      None) == INVALID
     # backend with bad handle
     assert lib.qhip_backend_matvec(None, p, None, p) == INVALID
     assert lib.qhip_backend_alloc_scratch(None, 1024) == INVALID
+
+
+def test_split_workspace_size(lib):
+    # 32 KiB of row-tile counters, then one f32 partial per row and 256-value slice
+    for rows, cols in [(2560, 9728), (1, 256), (5120, 17408), (7, 300)]:
+        assert lib.qhip_quantize_mul_mat_vec_work_bytes(rows, cols) == 32768 + 4 * rows * ((cols + 255) // 256)
+    assert lib.qhip_quantize_mul_mat_vec_work_bytes(-1, 256) == 0
 
 
 def test_zero_sized_requests_are_no_ops(lib):
