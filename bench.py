@@ -128,7 +128,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the quantized matvec path has no "
-              "multi-GPU component; see DESIGN.md for how it would shard). Run with --gpus 1.",
+              "multi-GPU component; it would shard by output rows). Run with --gpus 1.",
               file=sys.stderr)
         return 2
 
