@@ -121,7 +121,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--profile-kernel", choices=["down", "gate_up", "fused_gate_up", "split_down", "step",
                                                  "step_unfused",
-                                                 "mmq_cfg5_q4k",
+                                                 "mmq_cfg5_q4k", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
                                                  "mmq_cfg4"],
                     help="run only this kernel (for rocprofv3) and exit")
     ap.add_argument("--copy-calib", action="store_true")
@@ -383,7 +383,8 @@ def main() -> int:
 
 def profile_mmq(torch, lib, ops, synth, dev, stream, which, launches):
     """Only the MMQ kernel of one configuration, for rocprofv3."""
-    tt, rows, cols, T = (12, 17408, 5120, 512) if which == "mmq_cfg5_q4k" else (8, 3584, 1024, 512)
+    tt, rows, cols, T = {"mmq_cfg5_q4k": (12, 17408, 5120, 512), "mmq_cfg5_q3k": (11, 17408, 5120, 512),
+                         "mmq_cfg5_q2k": (10, 17408, 5120, 512)}.get(which, (8, 3584, 1024, 512))
     w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
     aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
     y = torch.empty((T, rows), device=dev)
