@@ -160,6 +160,23 @@ int qhip_launch_quantize_mul_mat_vec_split(const void *d_w, const float *d_x, vo
                                            int lanes_per_row, int rows_per_lane, void *d_work,
                                            long work_bytes, void *stream);
 
+/* The split-K quantize + GEMV above WITHOUT a workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  Same kernels, arguments and results as
+ * qhip_launch_quantize_mul_mat_vec_split; the workspace is a 4 MiB array the
+ * library holds on each device it runs on until the process ends, so
+ * rows * ceil(cols / 256) may be at most 1,040,384 (larger shapes return
+ * hipErrorInvalidValue before anything is launched).  It calls no
+ * hipMalloc / hipFree.  Every call on one device shares that device's array:
+ * calls that overlap on one GPU (two streams or two host threads) race and
+ * must be serialized by the caller.  qhip_init sets the array up for its
+ * device; on a device qhip_init was not called for, the first call does. */
+int qhip_launch_quantize_mul_mat_vec_split_noalloc(const void *d_w, const float *d_x, void *d_xq_out,
+                                                   float *d_out, int rows, int cols, int ttype,
+                                                   int slice_values, int lanes_per_row, int rows_per_lane,
+                                                   void *stream);
+
 /* The GEMV with explicit launch shape: `lanes_per_row` (1..64, or 128 / 256
  * = two / four whole waves, one token only) lanes share `rows_per_lane` (1, 2
  * or 4) weight rows, walking their 64-value units in turn, and fold their

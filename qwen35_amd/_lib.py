@@ -54,6 +54,8 @@ SIGNATURES = {
     "qhip_launch_quantize_mul_mat_vec_split": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                                        c_int, c_int, c_int, c_int, c_void_p, c_long,
                                                        c_void_p]),
+    "qhip_launch_quantize_mul_mat_vec_split_noalloc": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+                                                               c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "qhip_mmq_image_bytes": (c_long, [c_int, c_int, c_int]),
     "qhip_launch_mmq_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "qhip_launch_mul_mat_image": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,

@@ -217,7 +217,7 @@ int qhip_init(int device) {
             device, g_name);
     return (int)hipErrorInvalidDevice;
   }
-  return 0;
+  return (int)scratch_init_current_device();
 }
 
 int qhip_gpu_arch(void) { probe(); return g_arch; }

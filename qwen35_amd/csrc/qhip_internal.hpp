@@ -52,6 +52,9 @@ hipError_t launch_fill_zero(void* p, long bytes, hipStream_t s);
 bool gemv_splitk_preferred(const GemvArgs& g);
 hipError_t launch_gemv_splitk(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int slice,
                               void* work, long work_bytes, hipStream_t s);
+// resolve (and clear) the no-allocation entry point's device array on the
+// current device; qhip_init calls it
+hipError_t scratch_init_current_device();
 // GGUF blocks -> f32 (nvals = whole blocks' values)
 hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hipStream_t s);
 // MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)

@@ -132,6 +132,19 @@ def quantize_mul_mat_vec_split(ttype: int, w: torch.Tensor, x: torch.Tensor, row
     return out
 
 
+def quantize_mul_mat_vec_split_noalloc(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
+                                       slice_values: int = 0, lanes_per_row: int = 0, rows_per_lane: int = 0,
+                                       xq_out: torch.Tensor | None = None,
+                                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """The split-K launch with the library's own per-device workspace (no allocation in the call)."""
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=w.device)
+    check("quantize_mul_mat_vec_split_noalloc", load().qhip_launch_quantize_mul_mat_vec_split_noalloc(
+        _p(w), _p(x), _p(xq_out) if xq_out is not None else None, _p(out), rows, cols, ttype, slice_values,
+        lanes_per_row, rows_per_lane, _stream()))
+    return out
+
+
 def gemv_tuned(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
                lanes_per_row: int, tokens_per_pass: int, rows_per_lane: int = 1,
                out: torch.Tensor | None = None) -> torch.Tensor:

@@ -1,0 +1,81 @@
+"""GPU parity of the no-allocation split-K quantize + GEMV
+(qhip_launch_quantize_mul_mat_vec_split_noalloc) against the workspace entry
+point it mirrors (qhip_launch_quantize_mul_mat_vec_split), through the C ABI.
+
+Both run the same kernels with the same launch shape and add the slices'
+partial sums in slice order, so their outputs and quantized activations must
+agree bit for bit; the float output is also held to the oracle within the
+1e-5 relative L2 tolerance.  Two calls in a row, the second on a smaller input,
+show that the shared device array carries nothing wrong from one call into the
+next (its row-tile counters return to zero after every launch)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from qwen35_amd import _lib, ops, synth
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+INVALID = 1  # hipErrorInvalidValue
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
+
+
+def _run_pair(gpu, oracle, tt, rows, cols, seed):
+    w = synth.make_weight(tt, rows, cols, seed=seed, tag=tt)
+    x = synth.make_act(cols, 1, seed=seed, tag=900 + tt)
+    wd = torch.from_numpy(w).to(gpu)
+    xd = torch.from_numpy(x[0]).to(gpu)
+    ab = ops.act_row_bytes(tt, cols)
+    xq_a = torch.zeros(ab, dtype=torch.uint8, device=gpu)
+    xq_b = torch.zeros(ab, dtype=torch.uint8, device=gpu)
+    print(f"no-alloc split-K {po.NAMES[tt]} [{rows}x{cols}] seed {seed}", flush=True)
+    got = ops.quantize_mul_mat_vec_split_noalloc(tt, wd, xd, rows, cols, xq_out=xq_a).cpu().numpy()
+    work = ops.split_work(rows, cols, gpu)
+    want = ops.quantize_mul_mat_vec_split(tt, wd, xd, rows, cols, work, xq_out=xq_b).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), "differs from the workspace entry point"
+    assert torch.equal(xq_a, xq_b)
+    assert np.array_equal(xq_a.cpu().numpy(), oracle.quantize_act(tt, x)[0])
+    ref = oracle.matvec(tt, w, x)[0]
+    assert rel_l2(got, ref) < TOL
+    return got
+
+
+def test_noalloc_matches_split_entry_twice(gpu, oracle):
+    # the config-2 down projection, then a smaller matrix of another format
+    _run_pair(gpu, oracle, po.TT_Q6_K, 2560, 9728, seed=0)
+    _run_pair(gpu, oracle, po.TT_Q4_K, 700, 8192, seed=1)
+    # and the first shape again: nothing left over from the smaller call
+    _run_pair(gpu, oracle, po.TT_Q6_K, 2560, 9728, seed=2)
+
+
+def test_noalloc_explicit_shape(gpu, oracle):
+    tt, rows, cols = po.TT_Q8_0, 333, 4096
+    w = synth.make_weight(tt, rows, cols, seed=3, tag=tt)
+    x = synth.make_act(cols, 1, seed=3, tag=77)
+    wd, xd = torch.from_numpy(w).to(gpu), torch.from_numpy(x[0]).to(gpu)
+    work = ops.split_work(rows, cols, gpu)
+    for sl, lpr, nr in ((256, 4, 1), (1024, 16, 2), (2048, 64, 4)):
+        print(f"no-alloc split-K Q8_0 [{rows}x{cols}] slice {sl} lanes {lpr} rows/lane {nr}", flush=True)
+        got = ops.quantize_mul_mat_vec_split_noalloc(tt, wd, xd, rows, cols, sl, lpr, nr).cpu().numpy()
+        want = ops.quantize_mul_mat_vec_split(tt, wd, xd, rows, cols, work, sl, lpr, nr).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_noalloc_rejects_shapes_beyond_its_array(gpu):
+    L = _lib.load()
+    p = ctypes.c_void_p(0x1000)  # never dereferenced: the size check fails first
+    # rows * ceil(cols / 256) = 65536 * 68 > 1,040,384
+    assert L.qhip_launch_quantize_mul_mat_vec_split_noalloc(p, p, None, p, 65536, 17408, po.TT_Q6_K, 0, 0, 0,
+                                                            None) == INVALID
+    # at the limit shape class it is accepted by the size check (then argument
+    # validation applies as in the workspace entry point: a NULL weight)
+    assert L.qhip_launch_quantize_mul_mat_vec_split_noalloc(None, p, None, p, 5120, 17408, po.TT_Q6_K, 0, 0, 0,
+                                                            None) == INVALID
