@@ -466,13 +466,16 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
             it = 100 if T <= 64 else 30
             s_g = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
                                                         PATH_GEMV, stream), it)
-            s_t = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
-                                                        PATH_MMQ, stream), it)
+            # the split-K workspace the Exec mirror passes (small grids split K)
+            work = ops.mul_mat_work(rows, cols, T, tt, dev)
+            wp, wn = (work.data_ptr(), work.numel()) if work is not None else (None, 0)
+            s_t = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
+                                                             tt, PATH_MMQ, wp, wn, stream), it)
             pt = {"T": T, "gemv_us": round(s_g * 1e6, 2), "mmq_tile_us": round(s_t * 1e6, 2)}
             s_m = s_t
             if img is not None:
                 s_i = timed(lambda: lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows,
-                                                                  cols, T, tt, 0, 0, stream), it)
+                                                                  cols, T, tt, 0, 0, wp, wn, stream), it)
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
             tops, fr = frac(rows, cols, T, s_m)

@@ -116,6 +116,22 @@ int qhip_launch_mul_mat_vec_q8_0(const void *d_w, const void *d_xq, float *d_out
  * with an argument. */
 int qhip_launch_mul_mat(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
                         int tokens, int ttype, int path, void *stream);
+/* The same with a workspace the MMQ may split K into.  The launches above
+ * never split K (each output tile is one workgroup's sum over all of K).
+ * With few output tiles (a few dozen tokens) one workgroup per tile leaves
+ * most of the GPU idle; given d_work of qhip_mul_mat_work_bytes(rows, cols,
+ * tokens, ttype) bytes (16-byte aligned, its first 32 KiB zero before the
+ * first launch -- hipMemset once at allocation -- and zero again after every
+ * launch), the default MMQ cuts K into slices, and the last workgroup of each
+ * tile adds the slices' partial tiles in slice order: results are the same on
+ * every run (no float atomics).  With a smaller or NULL d_work, K is not
+ * split.  Launches that share a d_work must not overlap (one stream).
+ * qhip_mul_mat_work_bytes is 0 when no split would be made.  No reference
+ * counterpart (the reference's MMQ never splits K, src/kernels/cuda/mmq.cu:
+ * 1197-1202). */
+long qhip_mul_mat_work_bytes(int rows, int cols, int tokens, int ttype);
+int qhip_launch_mul_mat_work(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
+                             int tokens, int ttype, int path, void *d_work, long work_bytes, void *stream);
 
 /* Quantize-and-multiply for one token in ONE launch: d_x is the f32
  * activation (16-byte aligned); every workgroup quantizes it with the
@@ -216,11 +232,14 @@ int qhip_launch_mmq_tuned(const void *d_w, const void *d_xq, float *d_out, int r
  *   qhip_launch_mmq_prepare  build it from GGUF bytes (d_image 16-byte aligned)
  *   qhip_launch_mul_mat_image  the product from the image: same contract and
  *     results as qhip_launch_mul_mat_vec_tile; tile 64x64 / 64x128 / 128x64
- *     tokens x rows, 0 x 0 = default */
+ *     tokens x rows, 0 x 0 = default; d_work (nullable) as for
+ *     qhip_launch_mul_mat_work (qhip_mul_mat_work_bytes covers the image
+ *     launch too) */
 long qhip_mmq_image_bytes(int ttype, int rows, int cols);
 int qhip_launch_mmq_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
 int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
-                              int tokens, int ttype, int tile_tokens, int tile_rows, void *stream);
+                              int tokens, int ttype, int tile_tokens, int tile_rows, void *d_work,
+                              long work_bytes, void *stream);
 
 /* ---- ragged prefill (no reference counterpart: the reference prefills one
  * sequence per chunk, src/engine.zig:1371) -------------------------------------
@@ -282,10 +301,28 @@ const char *qhip_backend_name(const qhip_backend *be);
  * (the condition matvecPair fuses on, backend_cuda.zig:3743-3794). */
 int qhip_backend_load_linear(qhip_backend *be, int ttype, int rows, int cols,
                              const void *host_data, qhip_linear *out);
-/* Adopt weights already resident on this device (no copy, not freed). */
+/* Adopt weights already resident on this device (no copy, not freed).  Call
+ * qhip_backend_free_linear before the caller releases or reuses that memory:
+ * it drops what the backend derived from the bytes (the MMQ image). */
 int qhip_backend_wrap_linear(qhip_backend *be, int ttype, int rows, int cols, const void *d_data,
                              qhip_linear *out);
 void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
+/* Build what the prefill of this weight uses beyond its GGUF bytes now, at
+ * load time, instead of inside the first matvec_batch_k: the MMQ image of a
+ * Q6_K weight (qhip_launch_mmq_prepare, 2.5x the GGUF bytes).  0 = built or
+ * nothing to build; QHIP_DECLINE = not built (images off, or past the memory
+ * budget): the prefill then runs the tile MMQ on the GGUF bytes.  No
+ * reference counterpart (its CUDA MMQ decodes GGUF blocks in every launch). */
+int qhip_backend_prepare_linear(qhip_backend *be, const qhip_linear *w);
+/* MMQ images on (default) or off; off, matvec_batch_k never builds one. */
+int qhip_backend_set_mmq_images(qhip_backend *be, int on);
+/* Cap on the device bytes this backend places (uploaded weights, MMQ images,
+ * scratch, workspaces, allocBuf regions); 0 = no cap (the default).
+ * QWEN35_CUDA_MAX_DEV_MIB of src/backend_cuda.zig:1754-1760 as an argument:
+ * a load or buffer past it fails with hipErrorOutOfMemory and a message; an
+ * MMQ image past it is simply not built.  mem_placed: bytes counted so far. */
+int qhip_backend_set_mem_budget(qhip_backend *be, size_t bytes);
+size_t qhip_backend_mem_placed(const qhip_backend *be);
 int qhip_backend_alloc_scratch(qhip_backend *be, int max_cols);
 int qhip_backend_alloc_scratch_k(qhip_backend *be, int max_cols, int k);
 void qhip_backend_free_scratch(qhip_backend *be);
@@ -331,9 +368,12 @@ int qhip_backend_act_stats(const qhip_backend *be, unsigned long long *hits,
                            unsigned long long *misses);
 /* Decode-step boundary (src/backend.zig:470-491 stepBegin/stepEnd).  A device
  * backend may ignore the hint; this one clears the activation memo at
- * step_begin (as backend_cuda.zig:7049-7053 does) and captures nothing: the
- * library's launches are capture-safe, so an engine can wrap a step in its own
- * HIP graph. */
+ * step_begin (as backend_cuda.zig:7049-7053 does) and captures nothing.  An
+ * engine can wrap a step in its own HIP graph: under capture the backend
+ * allocates nothing -- it builds no MMQ image (the tile MMQ runs instead) and
+ * grows no workspace (an MMQ that would need more runs unsplit) -- but the
+ * activation scratch must already be large enough, so run the step once
+ * eagerly (or call alloc_scratch_k and prepare_linear) before capturing. */
 void qhip_backend_step_begin(qhip_backend *be, unsigned pos);
 void qhip_backend_step_end(qhip_backend *be);
 

@@ -103,20 +103,34 @@ bool mmq_image_preferred(const GemvArgs& g) {
   return g.ttype == TT_Q6_K && g.tokens >= 8 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
-hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s) {
+// `work` (nullable): the split-K workspace of the MMQ (mmq_work_bytes)
+hipError_t dispatch_mul_mat(const GemvArgs& g, int path, void* work, long work_bytes, hipStream_t s) {
   if (g.rows == 0 || g.tokens == 0) return hipSuccess;
   const bool fast = fast_ok(g);
   switch (path) {
     case QHIP_PATH_GENERIC: return launch_gemv_generic(g, s);
     case QHIP_PATH_GEMV: return fast ? launch_gemv(g, 0, 0, 0, s) : launch_gemv_generic(g, s);
     case QHIP_PATH_MMQ:
-      return fast && mmq_supported(g.ttype) ? launch_mmq(g, 0, 0, s) : (hipError_t)QHIP_DECLINE;
+      return fast && mmq_supported(g.ttype) ? launch_mmq(g, 0, 0, work, work_bytes, s) : (hipError_t)QHIP_DECLINE;
     case QHIP_PATH_AUTO:
       if (!fast) return launch_gemv_generic(g, s);
-      if (mmq_supported(g.ttype) && g.tokens >= mmq_min_tokens(g.ttype)) return launch_mmq(g, 0, 0, s);
+      if (mmq_supported(g.ttype) && g.tokens >= mmq_min_tokens(g.ttype)) return launch_mmq(g, 0, 0, work, work_bytes, s);
       return launch_gemv(g, 0, 0, 0, s);
     default: return hipErrorInvalidValue;
   }
+}
+
+// Workspace the MMQ of this product may split K into: the tile MMQ's and, for
+// the formats with a weight image, the image MMQ's (the larger of the two);
+// 0 when neither splits.
+long mul_mat_work_bytes(const GemvArgs& g) {
+  if (!fast_ok(g) || !mmq_supported(g.ttype)) return 0;
+  long n = mmq_work_bytes(g);
+  if (mmq_image_bytes(g.ttype, g.rows, g.cols) > 0) {
+    const long m = mmq_image_work_bytes(g);
+    if (m > n) n = m;
+  }
+  return n;
 }
 
 // ---- ragged packer: one launch quantizes every sequence into the packed buffer
@@ -286,7 +300,24 @@ int qhip_launch_mul_mat(const void* d_w, const void* d_xq, float* d_out, int row
   GemvArgs g;
   hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
-  return (int)dispatch_mul_mat(g, path, S(stream));
+  return (int)dispatch_mul_mat(g, path, nullptr, 0, S(stream));
+}
+
+long qhip_mul_mat_work_bytes(int rows, int cols, int tokens, int ttype) {
+  static const uint8_t dummy[4] = {0, 0, 0, 0};  // aligned stand-ins: only the shape matters
+  GemvArgs g;
+  if (rows <= 0 || tokens <= 0 || make_args(dummy, dummy, (float*)dummy, rows, cols, tokens, ttype, g) != hipSuccess)
+    return 0;
+  return mul_mat_work_bytes(g);
+}
+
+int qhip_launch_mul_mat_work(const void* d_w, const void* d_xq, float* d_out, int rows, int cols, int tokens,
+                             int ttype, int path, void* d_work, long work_bytes, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_w, d_xq, d_out, rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
+  return (int)dispatch_mul_mat(g, path, d_work, d_work ? work_bytes : 0, S(stream));
 }
 
 int qhip_launch_mul_mat_vec(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
@@ -378,7 +409,7 @@ int qhip_launch_mmq_tuned(const void* d_w, const void* d_xq, float* d_out, int r
   const bool br_ok = tile_rows == 0 || tile_rows == 64 || tile_rows == 128;
   if (!bt_ok || !br_ok) return (int)hipErrorInvalidValue;
   if (!fast_ok(g) || !mmq_supported(ttype)) return QHIP_DECLINE;
-  return (int)launch_mmq(g, tile_tokens, tile_rows, S(stream));
+  return (int)launch_mmq(g, tile_tokens, tile_rows, nullptr, 0, S(stream));
 }
 
 long qhip_mmq_image_bytes(int ttype, int rows, int cols) { return mmq_image_bytes(ttype, rows, cols); }
@@ -392,7 +423,8 @@ int qhip_launch_mmq_prepare(int ttype, const void* d_w, int rows, int cols, void
 }
 
 int qhip_launch_mul_mat_image(const void* d_image, const void* d_xq, float* d_out, int rows, int cols,
-                              int tokens, int ttype, int tile_tokens, int tile_rows, void* stream) {
+                              int tokens, int ttype, int tile_tokens, int tile_rows, void* d_work,
+                              long work_bytes, void* stream) {
   GemvArgs g;
   hipError_t e = make_args(d_image, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
@@ -400,7 +432,8 @@ int qhip_launch_mul_mat_image(const void* d_image, const void* d_xq, float* d_ou
   const bool tile_ok = (tile_tokens == 0 && tile_rows == 0) || (tile_tokens == 64 && tile_rows == 64) ||
                        (tile_tokens == 64 && tile_rows == 128) || (tile_tokens == 128 && tile_rows == 64);
   if (!tile_ok || ((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
-  return (int)launch_mmq_image(g, tile_tokens, tile_rows, S(stream));
+  if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
+  return (int)launch_mmq_image(g, tile_tokens, tile_rows, d_work, d_work ? work_bytes : 0, S(stream));
 }
 
 int qhip_launch_mul_mat_vec_tile(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
@@ -450,7 +483,7 @@ int qhip_launch_mul_mat_ragged(const void* d_w, const void* d_xq_packed, float* 
   GemvArgs g;
   hipError_t e = make_args(d_w, d_xq_packed, d_out, rows, cols, total_tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
-  return (int)dispatch_mul_mat(g, QHIP_PATH_AUTO, S(stream));
+  return (int)dispatch_mul_mat(g, QHIP_PATH_AUTO, nullptr, 0, S(stream));
 }
 
 int qhip_launch_block_ints(const void* d_w, const void* d_xq, int32_t* d_ints, int rows, int cols,

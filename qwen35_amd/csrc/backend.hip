@@ -17,7 +17,8 @@
 #include <vector>
 
 namespace qhip {
-hipError_t dispatch_mul_mat(const GemvArgs& g, int path, hipStream_t s);
+hipError_t dispatch_mul_mat(const GemvArgs& g, int path, void* work, long work_bytes, hipStream_t s);
+long mul_mat_work_bytes(const GemvArgs& g);
 bool mmq_image_preferred(const GemvArgs& g);
 }
 
@@ -30,16 +31,41 @@ struct qhip_backend {
   // so consecutive loads are contiguous on the device.
   struct Chunk { uint8_t* base; size_t size, used; };
   std::vector<Chunk> arena;
-  std::vector<void*> bufs;       // allocBuf regions (freed by free_scratch)
+  std::vector<std::pair<void*, size_t>> bufs;  // allocBuf regions (freed by free_scratch)
   uint8_t* act = nullptr;        // quantized-activation scratch
   size_t act_cap = 0;
-  // split-K partials and row-tile counters (counters zero between launches)
+  // split-K partials and tile counters of the GEMV and MMQ launches
+  // (counters zero between launches)
   uint8_t* skwork = nullptr;
   size_t skwork_cap = 0;
-  // MMQ images of K-quant weights, built on first use with many tokens and
-  // kept until free_linear / destroy; keyed by (weight bytes, rows) because a
-  // fused matvecPair multiplies two adjacent weights as one.
-  std::map<std::pair<const void*, int>, void*> images;
+  // MMQ images of Q6_K weights (qhip_launch_mmq_prepare), built by
+  // prepare_linear or by the first prefill outside a graph capture, kept
+  // until free_linear / destroy.  Keyed by the whole linear (device bytes,
+  // type, rows, cols): a different weight wrapped at a reused address never
+  // meets a stale image.
+  struct ImageKey {
+    const void* dev;
+    int ttype, rows, cols;
+    bool operator<(const ImageKey& o) const {
+      if (dev != o.dev) return dev < o.dev;
+      if (ttype != o.ttype) return ttype < o.ttype;
+      if (rows != o.rows) return rows < o.rows;
+      return cols < o.cols;
+    }
+  };
+  struct Image {
+    void* p;
+    size_t bytes;
+  };
+  std::map<ImageKey, Image> images;
+  bool images_on = true;
+  // Device-memory budget (QWEN35_CUDA_MAX_DEV_MIB, backend_cuda.zig:1754-1760,
+  // as an argument): bytes this backend places on the device -- uploaded
+  // weights, MMQ images, scratch, workspaces, allocBuf regions.  0 = no cap.
+  // A load past the budget fails; an image past it is not built (the prefill
+  // then runs the tile MMQ on the GGUF bytes).
+  size_t budget = 0;
+  size_t placed = 0;  // bytes counted against the budget
   // What `act` holds (backend_cuda.zig:3425-3448 actQValid/actQMark): the
   // source pointer, width, token count and activation family of the last
   // quantization, so a second matvec of the same x skips its quantize.
@@ -61,28 +87,44 @@ static void memo_clear(qhip_backend* be) {
 static constexpr size_t kArenaChunk = size_t(1) << 30;  // 1 GiB
 static constexpr size_t kAlign = 256;
 
+static bool over_budget(const qhip_backend* be, size_t more) { return be->budget && be->placed + more > be->budget; }
+
+static hipError_t budget_error(const qhip_backend* be, const char* what, size_t more) {
+  fprintf(stderr,
+          "qwen35_hip: %s needs %zu MiB more; this backend has placed %zu MiB of its %zu MiB device budget\n",
+          what, more >> 20, be->placed >> 20, be->budget >> 20);
+  return hipErrorOutOfMemory;
+}
+
 static hipError_t arena_alloc(qhip_backend* be, size_t bytes, uint8_t** out) {
   bytes = (bytes + kAlign - 1) / kAlign * kAlign;
+  if (over_budget(be, bytes)) return budget_error(be, "weight upload", bytes);
   if (!be->arena.empty()) {
     auto& c = be->arena.back();
     if (c.size - c.used >= bytes) {
       *out = c.base + c.used;
       c.used += bytes;
+      be->placed += bytes;
       return hipSuccess;
     }
   }
-  const size_t sz = bytes > kArenaChunk ? bytes : kArenaChunk;
+  // a chunk of 1 GiB, or what is left of the budget if that is less
+  size_t sz = bytes > kArenaChunk ? bytes : kArenaChunk;
+  if (be->budget && sz > be->budget - be->placed) sz = bytes > be->budget - be->placed ? bytes : be->budget - be->placed;
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, sz);
   if (e != hipSuccess) return e;
   be->arena.push_back({(uint8_t*)p, sz, bytes});
+  be->placed += bytes;
   *out = (uint8_t*)p;
   return hipSuccess;
 }
 
 static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
   if (be->act_cap >= bytes) return hipSuccess;
+  if (over_budget(be, bytes - be->act_cap)) return budget_error(be, "activation scratch", bytes - be->act_cap);
   if (be->act) (void)hipFree(be->act);
+  be->placed -= be->act_cap;
   be->act = nullptr;
   be->act_cap = 0;
   memo_clear(be);
@@ -91,12 +133,20 @@ static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
   if (e != hipSuccess) return e;
   be->act = (uint8_t*)p;
   be->act_cap = bytes;
+  be->placed += bytes;
   return hipSuccess;
+}
+
+static bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
 }
 
 static hipError_t ensure_skwork(qhip_backend* be, size_t bytes) {
   if (be->skwork_cap >= bytes) return hipSuccess;
+  if (over_budget(be, bytes - be->skwork_cap)) return budget_error(be, "split-K workspace", bytes - be->skwork_cap);
   if (be->skwork) (void)hipFree(be->skwork);
+  be->placed -= be->skwork_cap;
   be->skwork = nullptr;
   be->skwork_cap = 0;
   void* p = nullptr;
@@ -111,7 +161,36 @@ static hipError_t ensure_skwork(qhip_backend* be, size_t bytes) {
   }
   be->skwork = (uint8_t*)p;
   be->skwork_cap = bytes;
+  be->placed += bytes;
   return hipSuccess;
+}
+
+// The MMQ image of a Q6_K weight: looked up, or built now when images are on,
+// the budget allows it and the stream is not being captured (building
+// allocates).  nullptr = run the tile MMQ on the GGUF bytes instead.
+static void* image_for(qhip_backend* be, const void* wdev, int ttype, int rows, int cols, hipError_t* err) {
+  *err = hipSuccess;
+  const qhip_backend::ImageKey key{wdev, ttype, rows, cols};
+  auto it = be->images.find(key);
+  if (it != be->images.end()) return it->second.p;
+  if (!be->images_on || capturing(be->stream)) return nullptr;
+  const long n = qhip_mmq_image_bytes(ttype, rows, cols);
+  if (n <= 0 || over_budget(be, (size_t)n)) return nullptr;
+  void* img = nullptr;
+  hipError_t e = hipMalloc(&img, (size_t)n);
+  if (e != hipSuccess) {
+    *err = e;
+    return nullptr;
+  }
+  const int rc = qhip_launch_mmq_prepare(ttype, wdev, rows, cols, img, be->stream);
+  if (rc) {
+    (void)hipFree(img);
+    *err = (hipError_t)rc;
+    return nullptr;
+  }
+  be->images.emplace(key, qhip_backend::Image{img, (size_t)n});
+  be->placed += (size_t)n;
+  return img;
 }
 
 // Bytes per value of the widest activation family (Q8_K: 292/256), so one
@@ -194,26 +273,24 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
     }
   }
   GemvArgs g{ttype, wdev, be->act, out, rows, cols, k, row_bytes, qhip_act_row_bytes(ttype, cols)};
-  if (mmq_image_preferred(g)) {
-    // prefill of a K-quant weight: MMQ from its image
-    auto key = std::make_pair(wdev, rows);
-    auto it = be->images.find(key);
-    if (it == be->images.end()) {
-      const long n = qhip_mmq_image_bytes(ttype, rows, cols);
-      void* img = nullptr;
-      e = hipMalloc(&img, (size_t)n);
-      if (e != hipSuccess) return report("MMQ image", e);
-      rc = qhip_launch_mmq_prepare(ttype, wdev, rows, cols, img, be->stream);
-      if (rc) {
-        (void)hipFree(img);
-        return report("MMQ image", (hipError_t)rc);
-      }
-      it = be->images.emplace(key, img).first;
-    }
-    return report("matvec", (hipError_t)qhip_launch_mul_mat_image(it->second, be->act, out, rows, cols, k, ttype,
-                                                                   0, 0, be->stream));
+  // the MMQ's split-K workspace for small grids, grown outside a capture
+  // only (under capture a launch that does not fit runs unsplit)
+  const long need = mul_mat_work_bytes(g);
+  if (need > 0 && (size_t)need > be->skwork_cap && !capturing(be->stream)) {
+    e = ensure_skwork(be, (size_t)need);
+    if (e != hipSuccess && e != hipErrorOutOfMemory) return report("split-K workspace", e);
   }
-  return report("matvec", dispatch_mul_mat(g, QHIP_PATH_AUTO, be->stream));
+  void* work = be->skwork;
+  const long work_bytes = (long)be->skwork_cap;
+  if (mmq_image_preferred(g)) {
+    // prefill of a Q6_K weight: MMQ from its image when there is one
+    void* img = image_for(be, wdev, ttype, rows, cols, &e);
+    if (e != hipSuccess) return report("MMQ image", e);
+    if (img)
+      return report("matvec", (hipError_t)qhip_launch_mul_mat_image(img, be->act, out, rows, cols, k, ttype, 0, 0,
+                                                                     work, work_bytes, be->stream));
+  }
+  return report("matvec", dispatch_mul_mat(g, QHIP_PATH_AUTO, work, work_bytes, be->stream));
 }
 
 extern "C" {
@@ -237,7 +314,7 @@ void qhip_backend_destroy(qhip_backend* be) {
   (void)hipSetDevice(be->device);
   (void)hipDeviceSynchronize();
   qhip_backend_free_scratch(be);
-  for (auto& kv : be->images) (void)hipFree(kv.second);
+  for (auto& kv : be->images) (void)hipFree(kv.second.p);
   for (auto& c : be->arena) (void)hipFree(c.base);
   delete be;
 }
@@ -267,16 +344,15 @@ int qhip_backend_wrap_linear(qhip_backend* be, int ttype, int rows, int cols, co
 }
 
 void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
-  // Arena memory is returned at destroy; MMQ images built from this weight are
-  // freed now; the handle is cleared so a stale use fails validation.
+  // Arena memory is returned at destroy; MMQ images built from this weight's
+  // bytes are freed now; the handle is cleared so a stale use fails
+  // validation.
   if (be && w && w->dev) {
     (void)hipStreamSynchronize(be->stream);
     for (auto it = be->images.begin(); it != be->images.end();) {
-      const uint8_t* p = (const uint8_t*)it->first.first;
-      const uint8_t* lo = (const uint8_t*)w->dev;
-      // images of this weight, alone or as the first half of a pair
-      if (p == lo) {
-        (void)hipFree(it->second);
+      if (it->first.dev == w->dev) {
+        (void)hipFree(it->second.p);
+        be->placed -= it->second.bytes;
         it = be->images.erase(it);
       } else {
         ++it;
@@ -285,6 +361,32 @@ void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
   }
   if (w) *w = qhip_linear{nullptr, 0, 0, 0, 0};
 }
+
+int qhip_backend_prepare_linear(qhip_backend* be, const qhip_linear* w) {
+  if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
+  const GemvArgs g{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 8, w->row_bytes,
+                   qhip_act_row_bytes(w->ttype, w->cols)};
+  if (!mmq_image_preferred(g)) return 0;  // no image serves this weight
+  if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;
+  hipError_t e;
+  void* img = image_for(be, w->dev, w->ttype, w->rows, w->cols, &e);
+  if (e != hipSuccess) return report("MMQ image", e);
+  return img ? 0 : QHIP_DECLINE;
+}
+
+int qhip_backend_set_mmq_images(qhip_backend* be, int on) {
+  if (!be) return (int)hipErrorInvalidValue;
+  be->images_on = on != 0;
+  return 0;
+}
+
+int qhip_backend_set_mem_budget(qhip_backend* be, size_t bytes) {
+  if (!be) return (int)hipErrorInvalidValue;
+  be->budget = bytes;
+  return 0;
+}
+
+size_t qhip_backend_mem_placed(const qhip_backend* be) { return be ? be->placed : 0; }
 
 int qhip_backend_alloc_scratch(qhip_backend* be, int max_cols) {
   return qhip_backend_alloc_scratch_k(be, max_cols, 1);
@@ -299,22 +401,30 @@ void qhip_backend_free_scratch(qhip_backend* be) {
   if (!be) return;
   (void)hipDeviceSynchronize();
   if (be->act) (void)hipFree(be->act);
+  be->placed -= be->act_cap;
   be->act = nullptr;
   be->act_cap = 0;
   memo_clear(be);
   if (be->skwork) (void)hipFree(be->skwork);
+  be->placed -= be->skwork_cap;
   be->skwork = nullptr;
   be->skwork_cap = 0;
-  for (void* p : be->bufs) (void)hipFree(p);
+  for (auto& b : be->bufs) {
+    (void)hipFree(b.first);
+    be->placed -= b.second;
+  }
   be->bufs.clear();
 }
 
 int qhip_backend_alloc_buf(qhip_backend* be, size_t len, float** d_out) {
   if (!be || !d_out) return (int)hipErrorInvalidValue;
+  const size_t bytes = len ? len * sizeof(float) : sizeof(float);
+  if (over_budget(be, bytes)) return (int)budget_error(be, "allocBuf", bytes);
   void* p = nullptr;
-  hipError_t e = hipMalloc(&p, len ? len * sizeof(float) : sizeof(float));
+  hipError_t e = hipMalloc(&p, bytes);
   if (e != hipSuccess) return report("allocBuf", e);
-  be->bufs.push_back(p);
+  be->bufs.emplace_back(p, bytes);
+  be->placed += bytes;
   *d_out = (float*)p;
   return 0;
 }

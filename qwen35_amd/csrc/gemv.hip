@@ -324,26 +324,16 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
         if (row0 + k < rows) Y[row0 + k] = acc[k];
     }
   } else {
-    // The partials and the counter are device-scope atomic accesses, coherent
-    // across the XCDs' L2s by themselves; a full device fence would instead
-    // write back and invalidate the whole L2 of every workgroup's XCD.
+    // deterministic hand-off (sk_* in qhip_device.hpp): partials in
+    // part[slice][row], the last workgroup of the row tile adds them in
+    // slice order
     float* pp = part + (long)blockIdx.y * rows;
     if (active && j == 0) {
 #pragma unroll
       for (int k = 0; k < NR; ++k)
-        if (row0 + k < rows) __hip_atomic_store(pp + row0 + k, acc[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (row0 + k < rows) sk_store(pp + row0 + k, acc[k]);
     }
-    // every partial store performed before the slice is counted in
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    __shared__ unsigned last;
-    if (threadIdx.x == 0)
-      last = __hip_atomic_fetch_add(cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                     gridDim.y - 1
-                 ? 1u
-                 : 0u;
-    __syncthreads();
-    if (last) {
+    if (sk_arrive(cnt + blockIdx.x, gridDim.y)) {
       const int rpw = (WGS / 64) * tpw * NR;
       const int ns = (int)gridDim.y;
       for (int i = threadIdx.x; i < rpw; i += WGS) {
@@ -354,16 +344,15 @@ __global__ __launch_bounds__(WGS) void k_gemv_q(const uint8_t* __restrict__ W, c
           for (; q + 8 <= ns; q += 8) {
             float t[8];
 #pragma unroll
-            for (int c = 0; c < 8; ++c)
-              t[c] = __hip_atomic_load(part + (long)(q + c) * rows + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int c = 0; c < 8; ++c) t[c] = sk_load(part + (long)(q + c) * rows + rr);
 #pragma unroll
             for (int c = 0; c < 8; ++c) v += t[c];
           }
-          for (; q < ns; ++q) v += __hip_atomic_load(part + (long)q * rows + rr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (; q < ns; ++q) v += sk_load(part + (long)q * rows + rr);
           Y[rr] = v;
         }
       }
-      if (threadIdx.x == 0) __hip_atomic_store(cnt + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sk_reset(cnt + blockIdx.x);
     }
   }
 }

@@ -420,11 +420,62 @@ __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int
   }
 }
 
+// ---- tile output -----------------------------------------------------------------------
+// Lanes 0..31 of a wave write 32 consecutive rows of one token per element.
+// Split over K (ksplit > 1): each slice's workgroup stores its partial tile in
+// part[(tile * ksplit + slice) * tile_elems + i] (i: the thread's element in
+// accumulator order, so the stores are coalesced) and the last workgroup of
+// the tile adds the slices in slice order (sk_* hand-off, qhip_device.hpp):
+// the output does not depend on which slice finished last.
+template <int NA, int NB, int NW>
+__device__ __forceinline__ void mmq_write_tile(f32x16 (&acc)[NA][NB], float* __restrict__ Y, int rows, int tokens,
+                                               int r0, int t0, int rb0, int tb0, int tile, int ksplit, int ks,
+                                               float* __restrict__ part, unsigned* __restrict__ cnt) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int li = lane & 31, lh = lane >> 5;
+  if (ksplit > 1) {
+    constexpr long TS = (long)NW * NA * NB * 1024;  // elements per tile
+    const long mine = (long)wv * NA * NB * 1024 + lane;
+    float* pp = part + ((long)tile * ksplit + ks) * TS + mine;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sk_store(pp + ((a * NB + b) * 16 + e) * 64, acc[a][b][e]);
+    if (!sk_arrive(cnt + tile, (unsigned)ksplit)) return;
+    const float* base = part + (long)tile * ksplit * TS + mine;
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float v = 0.0f;
+          for (int q = 0; q < ksplit; ++q) v += sk_load(base + q * TS + ((a * NB + b) * 16 + e) * 64);
+          acc[a][b][e] = v;
+        }
+    sk_reset(cnt + tile);
+  }
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int row = r0 + rb0 + 32 * b + li;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
+        if (row < rows && tok < tokens) Y[(long)tok * rows + row] = acc[a][b][e];
+      }
+    }
+}
+
 // ---- the kernel -------------------------------------------------------------------------
 template <int TT, int BT, int BR, int NT = 256>
 __global__ __launch_bounds__(NT) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                               float* __restrict__ Y, int rows, int tokens, long row_bytes,
-                                              long act_bytes, int upr, int ntile_t, int ksplit, int cps) {
+                                              long act_bytes, int upr, int ntile_t, int ksplit, int cps,
+                                              float* __restrict__ part, unsigned* __restrict__ cnt) {
   grid_prologue<TT>();
   constexpr bool K32 = act32(TT);
   // waves: 2 x 2 over (tokens, rows), or stacked along rows for a 32-token
@@ -826,31 +877,17 @@ __global__ __launch_bounds__(NT) void k_mmq(const uint8_t* __restrict__ W, const
     }
   }
 
-  // lanes 0..31 of a wave write 32 consecutive rows of one token per element
-#pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int row = r0 + rb0 + 32 * b + li;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
-        if (row < rows && tok < tokens) {
-          float* y = Y + (long)tok * rows + row;
-          if (ksplit > 1) unsafeAtomicAdd(y, acc[a][b][e]);
-          else *y = acc[a][b][e];
-        }
-      }
-    }
+  mmq_write_tile<NA, NB, NW>(acc, Y, rows, tokens, r0, t0, rb0, tb0, g, ksplit, ks, part, cnt);
 }
 
 // ---- split-K for small grids ----------------------------------------------------------
 // With fewer than two tile workgroups per CU the K loop of each tile is one
 // long dependent chain and the GPU idles.  For at most two token tiles (where
 // the output is small) K is cut into slices of at least `min_chunks` chunks,
-// aiming at about four workgroups per CU, and the slices' partial tiles are
-// added into the zero-filled output with float atomics (the summation order
-// of the slices is not fixed; every per-block integer stays exact).
+// aiming at about four workgroups per CU.  The slices' partial tiles go to a
+// caller workspace and the last workgroup of each tile adds them in slice
+// order (mmq_write_tile), so the output is the same on every run.  Without a
+// workspace large enough for the partials, K is not split.
 static int mmq_ksplit_for(const GemvArgs& g, int bt, int br, int nchunks, int min_chunks) {
   const long ntt = (g.tokens + bt - 1) / bt;
   const long tiles = (long)((g.rows + br - 1) / br) * ntt;
@@ -858,6 +895,21 @@ static int mmq_ksplit_for(const GemvArgs& g, int bt, int br, int nchunks, int mi
   const long want = (1024 + tiles - 1) / tiles;
   const int cap = nchunks / min_chunks;
   return (int)(want < cap ? want : cap);
+}
+
+// Slices actually launched for a requested ksplit (no empty slice).
+static int mmq_slices(int nchunks, int ksplit) {
+  if (ksplit < 1) ksplit = 1;
+  if (ksplit > nchunks) ksplit = nchunks;
+  const int cps = (nchunks + ksplit - 1) / ksplit;
+  return (nchunks + cps - 1) / cps;
+}
+
+// Workspace of a split launch: the tile counters, then the partial tiles.
+static long mmq_split_bytes(const GemvArgs& g, int bt, int br, int slices) {
+  if (slices <= 1) return 0;
+  const long tiles = (long)((g.rows + br - 1) / br) * ((g.tokens + bt - 1) / bt);
+  return kSkCountBytes + 4L * slices * tiles * bt * br;
 }
 
 // ---- MMQ on a prepared weight image (Q4_K, Q6_K) -----------------------------------------
@@ -965,7 +1017,8 @@ struct alignas(16) ImgSmem {
 template <int TT, int BT, int BR>
 __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG, const uint8_t* __restrict__ XQ,
                                                   float* __restrict__ Y, int rows, int tokens, int nsb,
-                                                  long act_bytes, int ntile_t, int ksplit, int cps) {
+                                                  long act_bytes, int ntile_t, int ksplit, int cps,
+                                                  float* __restrict__ part, unsigned* __restrict__ cnt) {
   constexpr int HB = img_hdr_bytes<TT>(), NH = HB / 16;
   constexpr int S = img_shift(TT);
   constexpr int NA = BT / 64, NB = BR / 64;
@@ -1131,21 +1184,7 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
     }
   }
 
-#pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int row = r0 + rb0 + 32 * b + li;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int tok = t0 + tb0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
-        if (row < rows && tok < tokens) {
-          float* y = Y + (long)tok * rows + row;
-          if (ksplit > 1) unsafeAtomicAdd(y, acc[a][b][e]);
-          else *y = acc[a][b][e];
-        }
-      }
-    }
+  mmq_write_tile<NA, NB, 4>(acc, Y, rows, tokens, r0, t0, rb0, tb0, g, ksplit, ks, part, cnt);
 }
 
 long mmq_image_bytes(int ttype, int rows, int cols) {
@@ -1169,47 +1208,50 @@ hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows
   return hipGetLastError();
 }
 
+// `ksplit` is already the launched slice count (mmq_slices); work holds
+// mmq_split_bytes when it is above 1
 template <int TT, int BT, int BR>
-static hipError_t launch_mmq_img_t(const GemvArgs& g, int ksplit, hipStream_t s) {
+static hipError_t launch_mmq_img_t(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
   const int nsb = g.cols / 256;
   const long ntr = (g.rows + BR - 1) / BR, ntt = (g.tokens + BT - 1) / BT;
-  if (ksplit < 1) ksplit = 1;
-  if (ksplit > nsb) ksplit = nsb;
   const int cps = (nsb + ksplit - 1) / ksplit;
-  ksplit = (nsb + cps - 1) / cps;
   const long G = ntr * ntt * ksplit;
-  if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
-  if (ksplit > 1) {
-    // the slices add into y: zero it with a kernel (capture-safe, no memset node)
-    const hipError_t ez = launch_fill_zero(g.out, 4L * g.tokens * g.rows, s);
-    if (ez != hipSuccess) return ez;
-  }
+  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr * ntt > kSkMaxTiles)) return hipErrorInvalidValue;
+  unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
+  float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
   hipLaunchKernelGGL((k_mmq_img<TT, BT, BR>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
-                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, nsb, g.act_bytes, (int)ntt, ksplit, cps);
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, nsb, g.act_bytes, (int)ntt, ksplit, cps, part,
+                     cnt);
   return hipGetLastError();
 }
 
 template <int TT>
-static hipError_t launch_mmq_img_type(const GemvArgs& g, int bt, int br, int ksplit, hipStream_t s) {
-  if (bt == 64 && br == 64) return launch_mmq_img_t<TT, 64, 64>(g, ksplit, s);
-  if (bt == 64 && br == 128) return launch_mmq_img_t<TT, 64, 128>(g, ksplit, s);
-  if (bt == 128 && br == 64) return launch_mmq_img_t<TT, 128, 64>(g, ksplit, s);
+static hipError_t launch_mmq_img_type(const GemvArgs& g, int bt, int br, int ksplit, void* work, hipStream_t s) {
+  if (bt == 64 && br == 64) return launch_mmq_img_t<TT, 64, 64>(g, ksplit, work, s);
+  if (bt == 64 && br == 128) return launch_mmq_img_t<TT, 64, 128>(g, ksplit, work, s);
+  if (bt == 128 && br == 64) return launch_mmq_img_t<TT, 128, 64>(g, ksplit, work, s);
   return hipErrorInvalidValue;
 }
 
+// Slices of the default image launch (small grids: split K over super-blocks,
+// k_mmq's rule with one chunk = one super-block).
+static int mmq_image_slices(const GemvArgs& g) { return mmq_slices(g.cols / 256, mmq_ksplit_for(g, 64, 64, g.cols / 256, 1)); }
+
+long mmq_image_work_bytes(const GemvArgs& g) { return mmq_split_bytes(g, 64, 64, mmq_image_slices(g)); }
+
 // g.w is the image
-hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, hipStream_t s) {
+hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   int ksplit = 1;
   if (bt <= 0 || br <= 0) {
     bt = 64;
     br = 64;
-    // small grids: split K over super-blocks (k_mmq's rule, one chunk = one super-block)
-    ksplit = mmq_ksplit_for(g, bt, br, g.cols / 256, 1);
+    ksplit = mmq_image_slices(g);
+    if (!work || work_bytes < mmq_split_bytes(g, bt, br, ksplit)) ksplit = 1;
   }
   switch (g.ttype) {
-    case TT_Q4_K: return launch_mmq_img_type<TT_Q4_K>(g, bt, br, ksplit, s);
-    case TT_Q6_K: return launch_mmq_img_type<TT_Q6_K>(g, bt, br, ksplit, s);
+    case TT_Q4_K: return launch_mmq_img_type<TT_Q4_K>(g, bt, br, ksplit, work, s);
+    case TT_Q6_K: return launch_mmq_img_type<TT_Q6_K>(g, bt, br, ksplit, work, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -1392,39 +1434,35 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, hipStream_t s) {
 }
 
 // ---- launchers --------------------------------------------------------------------------
+// `ksplit` is already the launched slice count (mmq_slices); work holds
+// mmq_split_bytes when it is above 1
 template <int TT, int BT, int BR, int NT = 256>
-static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, hipStream_t s) {
+static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
   const int upr = g.cols / 64;
   const int nchunks = (upr + 3) / 4;
   const long ntr = (g.rows + BR - 1) / BR, ntt = (g.tokens + BT - 1) / BT;
-  if (ksplit < 1) ksplit = 1;
-  if (ksplit > nchunks) ksplit = nchunks;
   const int cps = (nchunks + ksplit - 1) / ksplit;
-  ksplit = (nchunks + cps - 1) / cps;  // no empty slices
   const long G = ntr * ntt * ksplit;
-  if (G > 0x7FFFFFFFL) return hipErrorInvalidValue;
-  if (ksplit > 1) {
-    // the slices add into y: zero it with a kernel (capture-safe, no memset node)
-    const hipError_t ez = launch_fill_zero(g.out, 4L * g.tokens * g.rows, s);
-    if (ez != hipSuccess) return ez;
-  }
+  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr * ntt > kSkMaxTiles)) return hipErrorInvalidValue;
+  unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
+  float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
   hipLaunchKernelGGL((k_mmq<TT, BT, BR, NT>), dim3((unsigned)G), dim3(NT), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
-                     ksplit, cps);
+                     ksplit, cps, part, cnt);
   return hipGetLastError();
 }
 
 template <int TT>
-static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit, hipStream_t s) {
+static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit, void* work, hipStream_t s) {
   // Q4_K's 64 x 128 tile is the weights-direct kernel (never split)
   if constexpr (TT == TT_Q4_K)
     if (bt == 64 && br == 128) return launch_mmq_wd(g, s);
-  if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, s);
-  if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, s);
-  if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, s);
-  if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, ksplit, s);
-  if (bt == 128 && br == 64) return launch_mmq_t<TT, 128, 64>(g, ksplit, s);
-  if (bt == 128 && br == 128) return launch_mmq_t<TT, 128, 128>(g, ksplit, s);
+  if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, work, s);
+  if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, work, s);
+  if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, work, s);
+  if (bt == 64 && br == 128) return launch_mmq_t<TT, 64, 128>(g, ksplit, work, s);
+  if (bt == 128 && br == 64) return launch_mmq_t<TT, 128, 64>(g, ksplit, work, s);
+  if (bt == 128 && br == 128) return launch_mmq_t<TT, 128, 128>(g, ksplit, work, s);
   return hipErrorInvalidValue;
 }
 
@@ -1446,26 +1484,41 @@ static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
 }
 
 
-hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s) {
+// Slices of the default tile launch (0 when it is the weights-direct kernel,
+// which never splits).
+static int mmq_default_slices(const GemvArgs& g, int bt, int br) {
+  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return 1;
+  const int nchunks = (g.cols / 64 + 3) / 4;
+  return mmq_slices(nchunks, mmq_ksplit_for(g, bt, br, nchunks, 2));
+}
+
+long mmq_work_bytes(const GemvArgs& g) {
+  int bt = 0, br = 0;
+  mmq_default_tile(g, bt, br);
+  return mmq_split_bytes(g, bt, br, mmq_default_slices(g, bt, br));
+}
+
+hipError_t launch_mmq(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   int ksplit = 1;
   if (bt <= 0 || br <= 0) {
     mmq_default_tile(g, bt, br);
-    ksplit = mmq_ksplit_for(g, bt, br, (g.cols / 64 + 3) / 4, 2);
+    ksplit = mmq_default_slices(g, bt, br);
+    if (!work || work_bytes < mmq_split_bytes(g, bt, br, ksplit)) ksplit = 1;
   }
   switch (g.ttype) {
-    case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, ksplit, s);
-    case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, ksplit, s);
-    case TT_Q4_0: return launch_mmq_type<TT_Q4_0>(g, bt, br, ksplit, s);
-    case TT_Q4_1: return launch_mmq_type<TT_Q4_1>(g, bt, br, ksplit, s);
-    case TT_IQ3_XXS: return launch_mmq_type<TT_IQ3_XXS>(g, bt, br, ksplit, s);
-    case TT_IQ3_S: return launch_mmq_type<TT_IQ3_S>(g, bt, br, ksplit, s);
-    case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, ksplit, s);
-    case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, ksplit, s);
-    case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, ksplit, s);
-    case TT_IQ4_XS: return launch_mmq_type<TT_IQ4_XS>(g, bt, br, ksplit, s);
-    case TT_Q3_K: return launch_mmq_type<TT_Q3_K>(g, bt, br, ksplit, s);
-    case TT_Q2_K: return launch_mmq_type<TT_Q2_K>(g, bt, br, ksplit, s);
+    case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, ksplit, work, s);
+    case TT_IQ4_NL: return launch_mmq_type<TT_IQ4_NL>(g, bt, br, ksplit, work, s);
+    case TT_Q4_0: return launch_mmq_type<TT_Q4_0>(g, bt, br, ksplit, work, s);
+    case TT_Q4_1: return launch_mmq_type<TT_Q4_1>(g, bt, br, ksplit, work, s);
+    case TT_IQ3_XXS: return launch_mmq_type<TT_IQ3_XXS>(g, bt, br, ksplit, work, s);
+    case TT_IQ3_S: return launch_mmq_type<TT_IQ3_S>(g, bt, br, ksplit, work, s);
+    case TT_Q4_K: return launch_mmq_type<TT_Q4_K>(g, bt, br, ksplit, work, s);
+    case TT_Q6_K: return launch_mmq_type<TT_Q6_K>(g, bt, br, ksplit, work, s);
+    case TT_Q5_K: return launch_mmq_type<TT_Q5_K>(g, bt, br, ksplit, work, s);
+    case TT_IQ4_XS: return launch_mmq_type<TT_IQ4_XS>(g, bt, br, ksplit, work, s);
+    case TT_Q3_K: return launch_mmq_type<TT_Q3_K>(g, bt, br, ksplit, work, s);
+    case TT_Q2_K: return launch_mmq_type<TT_Q2_K>(g, bt, br, ksplit, work, s);
     default: return hipErrorInvalidValue;
   }
 }

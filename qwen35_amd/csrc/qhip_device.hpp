@@ -209,6 +209,56 @@ __device__ __forceinline__ uint32_t sign_bytes4(uint32_t s) {
   return (t << 8) - t;
 }
 
+// ---- split-K hand-off between workgroups (deterministic) -----------------------
+// The workgroups of one output tile each own a slice of K.  Each stores its
+// partial sums with sk_store, then calls sk_arrive; the last workgroup of the
+// tile to arrive (whichever it is) reads every slice's partials with sk_load,
+// adds them in slice order -- so the result does not depend on which
+// workgroup finished last -- and puts the tile's counter back to zero with
+// sk_reset.  No workgroup waits for another.
+//
+// The guarantee this relies on, on gfx950 (LLVM AMDGPUUsage, memory model of
+// the GFX942 family, which gfx950 follows):
+//  * agent-scope atomic loads, stores and read-modify-writes are issued with
+//    the sc1 cache-policy bit: stores are written through every XCD-private
+//    cache to the agent coherence point, loads and RMWs are served from it,
+//    never from a stale line of this XCD's L2 or the CU's L1;
+//  * a store counts in vmcnt until the memory system acknowledges it, so after
+//    `s_waitcnt vmcnt(0)` this wave's sc1 stores are performed at the
+//    coherence point (an agent-scope release is `buffer_wbl2 sc1` followed by
+//    exactly this wait; the write-back only matters for stores not already
+//    written through, and every store the hand-off needs is an sc1 store);
+//  * the workgroup barrier orders each wave's wait before thread 0's counter
+//    RMW, and the last workgroup issues its sk_loads after the RMW that saw
+//    the final count has returned (barrier again).
+// So every partial is at the coherence point before the last workgroup's
+// counter RMW can return the final count, and its sk_loads read them there.
+// A release/acquire pair through __threadfence() gives the same order in
+// terms of the HIP memory model, but writes back and invalidates the whole L2
+// per workgroup: 25-490 us instead of about 10 us for the config-2 down
+// projection (measured on MI355X).
+__device__ __forceinline__ void sk_store(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float sk_load(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Every thread of the workgroup calls it after its sk_stores; true in every
+// thread of the workgroup that brings the tile's count to `slices`.
+__device__ __forceinline__ bool sk_arrive(unsigned* cnt, unsigned slices) {
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partials are performed
+  __syncthreads();
+  __shared__ unsigned last;
+  if (threadIdx.x == 0)
+    last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == slices - 1 ? 1u : 0u;
+  __syncthreads();
+  return last != 0;
+}
+// the last workgroup, once: the counter is zero again for the next launch
+__device__ __forceinline__ void sk_reset(unsigned* cnt) {
+  if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Every thread of the workgroup must call it before any early exit.
 template <int TT>
 __device__ __forceinline__ void grid_prologue() {

@@ -57,13 +57,18 @@ hipError_t launch_gemv_splitk(const GemvArgs& g, const float* x, void* xq_out, i
 hipError_t scratch_init_current_device();
 // GGUF blocks -> f32 (nvals = whole blocks' values)
 hipError_t launch_dequant(int ttype, const void* src, float* dst, long nvals, hipStream_t s);
-// MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick)
-hipError_t launch_mmq(const GemvArgs& g, int bt, int br, hipStream_t s);
+// MMQ tile: bt tokens x br rows per workgroup, each 64 or 128 (0 = pick).
+// With the default tile, small grids split K when `work` holds
+// mmq_work_bytes(g) bytes (its first kSkCountBytes zero, as for the split-K
+// GEMV); otherwise, and with an explicit tile, K is not split.
+hipError_t launch_mmq(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s);
+long mmq_work_bytes(const GemvArgs& g);
 // MMQ weight image of a K-quant weight (sub-scales folded into two int8 planes)
 long mmq_image_bytes(int ttype, int rows, int cols);
 hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
                               hipStream_t s);
-// g.w = the image; bt x br tile (0 = default)
-hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, hipStream_t s);
+// g.w = the image; bt x br tile (0 = default; splits K as launch_mmq)
+hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s);
+long mmq_image_work_bytes(const GemvArgs& g);
 
 }  // namespace qhip

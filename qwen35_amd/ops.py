@@ -91,6 +91,23 @@ def mul_mat(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
     return out
 
 
+def mul_mat_work(rows: int, cols: int, tokens: int, ttype: int, device) -> torch.Tensor | None:
+    """Zeroed split-K workspace for mul_mat_split / mul_mat_image (None when no split would be made)."""
+    n = load().qhip_mul_mat_work_bytes(rows, cols, tokens, ttype)
+    return torch.zeros(n, dtype=torch.uint8, device=device) if n > 0 else None
+
+
+def mul_mat_split(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
+                  work: torch.Tensor | None, path: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """mul_mat with a workspace: the MMQ of small grids splits K (deterministic slice order)."""
+    if out is None:
+        out = torch.empty((tokens, rows), dtype=torch.float32, device=w.device)
+    check("mul_mat_work", load().qhip_launch_mul_mat_work(
+        _p(w), _p(xq), _p(out), rows, cols, tokens, ttype, path, _p(work) if work is not None else None,
+        work.numel() if work is not None else 0, _stream()))
+    return out
+
+
 def quantize_mul_mat_vec(ttype: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
                          xq_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """One launch: quantize f32 x (one token) inside the GEMV and multiply."""
@@ -177,10 +194,11 @@ def mmq_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor
 
 
 def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
-                  tile_tokens: int = 0, tile_rows: int = 0) -> torch.Tensor:
+                  tile_tokens: int = 0, tile_rows: int = 0, work: torch.Tensor | None = None) -> torch.Tensor:
     out = torch.empty((tokens, rows), dtype=torch.float32, device=img.device)
-    check("mul_mat_image", load().qhip_launch_mul_mat_image(_p(img), _p(xq), _p(out), rows, cols, tokens, ttype,
-                                                            tile_tokens, tile_rows, _stream()))
+    check("mul_mat_image", load().qhip_launch_mul_mat_image(
+        _p(img), _p(xq), _p(out), rows, cols, tokens, ttype, tile_tokens, tile_rows,
+        _p(work) if work is not None else None, work.numel() if work is not None else 0, _stream()))
     return out
 
 
@@ -266,6 +284,25 @@ class Backend:
         check("wrap_linear", self.lib.qhip_backend_wrap_linear(self._h, ttype, rows, cols, _p(dev),
                                                                ctypes.byref(lin)))
         return lin
+
+    def free_linear(self, w: QhipLinear) -> None:
+        self.lib.qhip_backend_free_linear(self._h, ctypes.byref(w))
+
+    def prepare_linear(self, w: QhipLinear) -> int:
+        """Build the weight's MMQ image now: 0 built / nothing to build, -1 not built."""
+        rc = self.lib.qhip_backend_prepare_linear(self._h, ctypes.byref(w))
+        if rc not in (0, -1):
+            check("prepare_linear", rc)
+        return rc
+
+    def set_mmq_images(self, on: bool) -> None:
+        check("set_mmq_images", self.lib.qhip_backend_set_mmq_images(self._h, int(bool(on))))
+
+    def set_mem_budget(self, nbytes: int) -> None:
+        check("set_mem_budget", self.lib.qhip_backend_set_mem_budget(self._h, nbytes))
+
+    def mem_placed(self) -> int:
+        return int(self.lib.qhip_backend_mem_placed(self._h))
 
     def matvec(self, out: torch.Tensor, w: QhipLinear, x: torch.Tensor) -> None:
         check("matvec", self.lib.qhip_backend_matvec(self._h, _p(out), ctypes.byref(w), _p(x)))

@@ -122,6 +122,23 @@ def test_split_workspace_size(lib):
     assert lib.qhip_quantize_mul_mat_vec_work_bytes(-1, 256) == 0
 
 
+def test_mmq_split_workspace_size(lib):
+    # cfg5 at 16 tokens splits K (a few hundred row tiles); 512 tokens does not
+    # (enough tiles), nor does a GEMV-only or unknown type
+    n = lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 12)
+    assert n > 32768 and n % 4 == 0
+    assert lib.qhip_mul_mat_work_bytes(5120, 17408, 16, 14) > 32768
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 0
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 99) == 0
+    assert lib.qhip_mul_mat_work_bytes(0, 5120, 16, 12) == 0
+    p = ctypes.c_void_p(0x1000)
+    # a misaligned workspace or a negative size is rejected before any launch
+    assert lib.qhip_launch_mul_mat_work(p, p, p, 16, 256, 8, 12, 0, ctypes.c_void_p(0x1004), n, None) == INVALID
+    assert lib.qhip_launch_mul_mat_work(p, p, p, 16, 256, 8, 12, 0, p, -1, None) == INVALID
+    assert lib.qhip_launch_mul_mat_image(p, p, p, 16, 256, 8, 12, 0, 0, ctypes.c_void_p(0x1004), n,
+                                         None) == INVALID
+
+
 def test_zero_sized_requests_are_no_ops(lib):
     p = ctypes.c_void_p(0x1000)
     assert lib.qhip_launch_mul_mat_vec(p, p, p, 0, 256, 1, 8, None) == 0

@@ -83,6 +83,12 @@ def test_mmq_matches_oracle_every_tile(gpu, oracle, tt, rows, cols, tokens):
     assert rc == 0
     assert rel_l2(out.cpu().numpy(), want) < TOL
     assert rel_l2(ops.mul_mat(tt, wd, xq, rows, cols, tokens).cpu().numpy(), want) < TOL
+    # with the split-K workspace (small grids cut K; deterministic slice order)
+    work = ops.mul_mat_work(rows, cols, tokens, tt, gpu)
+    a = ops.mul_mat_split(tt, wd, xq, rows, cols, tokens, work, 2).cpu().numpy()
+    b = ops.mul_mat_split(tt, wd, xq, rows, cols, tokens, work, 2).cpu().numpy()
+    assert rel_l2(a, want) < TOL
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
 def unit_scale_weight(tt, rows, cols, seed):
@@ -297,6 +303,9 @@ def test_mmq_image_matches_oracle(gpu, oracle, tt, rows, cols, tokens):
     for bt, br in [(64, 64), (64, 128), (128, 64), (0, 0)]:
         got = ops.mul_mat_image(tt, img, xq, rows, cols, tokens, bt, br).cpu().numpy()
         assert rel_l2(got, want) < TOL, (bt, br, rel_l2(got, want))
+    work = ops.mul_mat_work(rows, cols, tokens, tt, gpu)
+    got = ops.mul_mat_image(tt, img, xq, rows, cols, tokens, work=work).cpu().numpy()
+    assert rel_l2(got, want) < TOL
 
 
 @pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
