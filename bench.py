@@ -1,30 +1,31 @@
 #!/usr/bin/env python3
 """bench.py -- quantized GEMV / MMQ throughput on one MI355X.
 
-Headline workload: one decode FFN step at batch 1
-through the Exec mirror (the slots the engine calls): matvecPair over the Q4_K
-gate/up weights [9728,2560] x2 (adjacent in the weight arena: one launch) from
-f32 x[2560], then matvec over the Q6_K down weight [2560,9728] from f32
-h[9728].  The mirror quantizes x (Q8_K) inside the gate/up GEMV (one launch)
-and h inside the down GEMV, split over K: each workgroup quantizes and
-multiplies one 1024-value slice of h, the last one of a row tile to finish
-adds the partial sums (one launch).
-`value` = algorithmic bytes of the step's GEMVs (packed weights + f32 x + f32 y
-per GEMV) / step time, inputs resident in HBM.  Weight sets rotate over enough
-device copies (> 512 MB per pass) that every step streams from HBM, not from
-the 256 MB Infinity Cache.
+Headline (BASELINE.json metric "quant GEMV GB/s (% of HBM peak) at bs=1", on
+its largest single-GPU configuration, configs[2]): the IQ4_NL output-head
+GEMV [248320, 2560] at batch 1, as the engine calls it -- the Exec mirror's
+matvec from f32 x (Q8_0 quantization of x on the device, then the GEMV).  The
+357 MB weight is larger than the 256 MB Infinity Cache, so every launch
+streams it from HBM.  `value` = algorithmic bytes (packed weights + f32 x +
+f32 y = 358,584,320 B) / step time, inputs resident in HBM.  `roofline` is the
+GEMV kernel alone (the step's dominant kernel), timed with HIP events on its
+launch stream.
 
-Also reported: the other configurations' GEMV bandwidth, the dominant
-kernel's roofline fraction (HIP events around back-to-back launches of that
-kernel alone), and the reference's CPU path timed on this host's cores.
+Also reported: the config-2 decode FFN step (gate/up + down through the Exec
+mirror) and its kernels, the GEMV bandwidth of configs 1 and 5 and of the
+further formats, the MMQ (config 4 ragged and dense, the config-5 token sweep
+and its GEMV->MMQ crossover), and the CPU baseline: this repository's C
+restatement of the reference's CPU path at the host's ISA tier (oracle/,
+AVX2 / AVX-512 VNNI as the reference dispatches them) on every configuration.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --profile-kernel down --steps 200   (one kernel only, for rocprofv3)
+       python bench.py --profile-kernel cfg3_gemv --steps 200   (one kernel only, for rocprofv3)
        python bench.py --copy-calib       (a plain copy of known size, for counter scaling)
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -39,6 +40,14 @@ HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, vendor figure
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA (POP/s x 1e3)
 ROTATE_BYTES = 512 << 20  # per-pass footprint that defeats the MALL
 METRIC = "quant GEMV GB/s (% of HBM peak) at bs=1; MMQ prefill tokens/s"
+TQ8, TQ4, TQ6, TIQ = 8, 12, 14, 20
+PATH_AUTO, PATH_GEMV, PATH_MMQ = 0, 1, 2
+H2, F2 = 2560, 9728          # config 2 (4B-class FFN)
+R3, C3 = 248320, 2560        # config 3 (output head)
+
+PROFILE_KERNELS = ["cfg3_gemv", "cfg3_step", "cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv",
+                   "down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused",
+                   "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k"]
 
 
 def log(*a):
@@ -73,7 +82,8 @@ WARM_SECONDS = 0.1  # GPU clocks ramp down while the host prepares inputs
 
 
 def time_loop(torch, fn, iters: int, warmup: int) -> float:
-    """Average seconds per call of fn(i), HIP events on the current stream.
+    """Average seconds per call of fn(i), HIP events on the current stream (the
+    stream every launch here goes to).
 
     Warm-up is at least `warmup` calls and at least WARM_SECONDS of back-to-back
     calls: after host-side setup the GPU's clocks have dropped, and the first
@@ -111,297 +121,236 @@ def single_latency(torch, fn, reps: int = 20) -> float:
     return statistics.median(ts)
 
 
-def main() -> int:
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--profile-kernel", choices=["down", "gate_up", "fused_gate_up", "split_down", "step",
-                                                 "step_unfused",
-                                                 "mmq_cfg5_q4k", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
-                                                 "mmq_cfg4"],
-                    help="run only this kernel (for rocprofv3) and exit")
-    ap.add_argument("--copy-calib", action="store_true")
-    args = ap.parse_args()
-    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one GPU only (the quantized matvec path has no "
-              "multi-GPU component; it would shard by output rows). Run with --gpus 1.",
-              file=sys.stderr)
-        return 2
-
-    import numpy as np
-    import torch
-
-    import qwen35_amd
-    from qwen35_amd import _lib, ops, synth
-
-    lib = _lib.load()
-    qwen35_amd.check("qhip_init", lib.qhip_init(0))
-    dev = torch.device("cuda:0")
-    stream = torch.cuda.current_stream().cuda_stream
-    TQ4, TQ6, TQ8, TIQ = 12, 14, 8, 20
-
-    if args.copy_calib:
-        n = 256 << 20
-        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n, "launches": 5}))
-        return 0
-
-    # ---- headline workload: cfg2 FFN step through the Exec mirror --------------
-    # matvecPair(gate, up, x) + matvec(down, h) (src/backend.zig:153-176 slots):
-    # the mirror quantizes x and h on the device and runs one GEMV per slot
-    # (adjacent gate/up weights are one launch): x inside the gate/up GEMV
-    # (width 2560), h inside the split-K down launch (width 9728).
-    import ctypes
-    H, F = 2560, 9728
-    t0 = time.time()
-    wg = synth.make_weight(TQ4, F, H, seed=0, tag=1)
-    wu = synth.make_weight(TQ4, F, H, seed=0, tag=2)
-    wd = synth.make_weight(TQ6, H, F, seed=0, tag=3)
-    x = synth.make_act(H, 1, seed=0, tag=100)
-    hvec = synth.make_act(F, 1, seed=0, tag=101)
-    gu_bytes, d_bytes = wg.nbytes + wu.nbytes, wd.nbytes
-    set_bytes = gu_bytes + d_bytes
-    copies = max(1, -(-ROTATE_BYTES // set_bytes))
-    be = ops.Backend(0)
-    lins = []
-    for _ in range(copies):
-        lg = be.load_linear(TQ4, F, H, wg)
-        lu = be.load_linear(TQ4, F, H, wu)
-        ld = be.load_linear(TQ6, H, F, wd)
-        assert lu.dev == lg.dev + F * lg.row_bytes  # adjacent: matvecPair is one launch
-        lins.append((ctypes.byref(lg), ctypes.byref(lu), ctypes.byref(ld), lg))
-    sha = synth.sha256(np.concatenate([wg.reshape(-1), wu.reshape(-1), wd.reshape(-1)]))
-    log(f"cfg2 weights {set_bytes / 1e6:.1f} MB x {copies} copies in the backend arena "
-        f"(gen+upload {time.time() - t0:.1f}s), sha256 {sha[:16]}")
-    xd = torch.from_numpy(x[0]).to(dev)
-    hd = torch.from_numpy(hvec[0]).to(dev)
-    y_gu = torch.empty(2 * F, device=dev)
-    y_d = torch.empty(H, device=dev)
-    bh = be._h
-    p_x, p_h, p_ygu, p_yd = (ctypes.c_void_p(t.data_ptr()) for t in (xd, hd, y_gu, y_d))
-
-    def gate_up(i):
-        g_, u_, _, _ = lins[i % copies]
-        rc = lib.qhip_backend_matvec_pair(bh, p_ygu, g_, u_, p_x)
-        assert rc == 0, rc
-
-    def down(i):
-        rc = lib.qhip_backend_matvec(bh, p_yd, lins[i % copies][2], p_h)
-        assert rc == 0, rc
-
-    def step(i):
-        gate_up(i)
-        down(i)
-
-    # the same step on the C ABI's separate quantize + matvec launches (4 launches)
-    xq = torch.empty(lib.qhip_act_row_bytes(TQ4, H), dtype=torch.uint8, device=dev)
-    hq = torch.empty(lib.qhip_act_row_bytes(TQ6, F), dtype=torch.uint8, device=dev)
-
-    # the step's two GEMV kernels alone, on activations quantized beforehand
-    assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
-    assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
-
-    def gemv_gate_up(i):
-        rc = lib.qhip_launch_mul_mat_vec(lins[i % copies][3].dev, xq.data_ptr(), y_gu.data_ptr(), 2 * F, H, 1, TQ4,
-                                         stream)
-        assert rc == 0, rc
-
-    def gemv_down(i):
-        rc = lib.qhip_launch_mul_mat_vec(lins[i % copies][3].dev + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1,
-                                         TQ6, stream)
-        assert rc == 0, rc
-
-    # the launches the mirror issues in the step: quantize + GEMV in one launch
-    # for gate/up (width 2560) and, split over K, for down (9728)
-    skwork = ops.split_work(H, F, dev)
-
-    def split_down(i):
-        rc = lib.qhip_launch_quantize_mul_mat_vec_split(lins[i % copies][3].dev + gu_bytes, hd.data_ptr(), None,
-                                                        y_d.data_ptr(), H, F, TQ6, 0, 0, 0, skwork.data_ptr(),
-                                                        skwork.numel(), stream)
-        assert rc == 0, rc
-
-    def fused_gate_up(i):
-        rc = lib.qhip_launch_quantize_mul_mat_vec(lins[i % copies][3].dev, xd.data_ptr(), None, y_gu.data_ptr(),
-                                                  2 * F, H, TQ4, stream)
-        assert rc == 0, rc
-
-    def quantize_h(i):
-        assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
-
-    def step_unfused(i):
-        lg = lins[i % copies][3]
-        assert lib.qhip_launch_quantize_act(TQ4, xd.data_ptr(), xq.data_ptr(), H, 1, stream) == 0
-        assert lib.qhip_launch_mul_mat_vec(lg.dev, xq.data_ptr(), y_gu.data_ptr(), 2 * F, H, 1, TQ4, stream) == 0
-        assert lib.qhip_launch_quantize_act(TQ6, hd.data_ptr(), hq.data_ptr(), F, 1, stream) == 0
-        assert lib.qhip_launch_mul_mat_vec(lg.dev + gu_bytes, hq.data_ptr(), y_d.data_ptr(), H, F, 1, TQ6,
-                                           stream) == 0
-
-    if args.profile_kernel in ("down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused"):
-        for i in range(3):
-            step(i)
-        fn = {"down": gemv_down, "gate_up": gemv_gate_up, "fused_gate_up": fused_gate_up,
-              "split_down": split_down, "step": step,
-              "step_unfused": step_unfused}[args.profile_kernel]
-        for i in range(args.steps):
-            fn(i)
-        torch.cuda.synchronize()
-        print(json.dumps({"profiled": args.profile_kernel, "launches": args.steps, "copies": copies}))
-        return 0
-    if args.profile_kernel:
-        profile_mmq(torch, lib, ops, synth, dev, stream, args.profile_kernel, args.steps)
-        return 0
-
-    step_bytes = gemv_bytes(2 * F, H, gu_bytes) + gemv_bytes(H, F, d_bytes)
-    sec = time_loop(torch, step, args.steps, args.warmup)
-    value = step_bytes / sec / 1e9
-    log(f"cfg2 step: {sec * 1e6:.2f} us, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% HBM)")
-    sec_unfused = time_loop(torch, step_unfused, args.steps, args.warmup)
-    log(f"cfg2 step, separate quantize launches: {sec_unfused * 1e6:.2f} us")
-
-    # each launch of the step alone, back to back; the roofline's kernel is the
-    # longest of them.  The GEMVs on pre-quantized activations are reported too.
-    n_k = max(200, args.steps)
-    gu_alg = gemv_bytes(2 * F, H, gu_bytes)
-    d_alg = gemv_bytes(H, F, d_bytes)
-    q_alg = 4 * F + lib.qhip_act_row_bytes(TQ6, F)
-    fgu_sec = time_loop(torch, fused_gate_up, n_k, 20)
-    sd_sec = time_loop(torch, split_down, n_k, 20)
-    d_sec = time_loop(torch, gemv_down, n_k, 20)
-    qh_sec = time_loop(torch, quantize_h, n_k, 20)
-    gu_sec = time_loop(torch, gemv_gate_up, n_k, 20)
-
-    def entry(alg, sec):
-        return {"alg_bytes": alg, "avg_us": sec * 1e6, "gbs": alg / sec / 1e9}
-
-    kernels = {
-        "fused_q4_k_gate_up_19456x2560": entry(gu_alg, fgu_sec),
-        "split_q6_k_down_2560x9728": entry(d_alg, sd_sec),
-    }
-    # the separate launches the split-K down replaces, and the gate/up GEMV on
-    # a pre-quantized activation
-    off_step = {"gemv_q4_k_gate_up_19456x2560_prequantized": entry(gu_alg, gu_sec),
-                "gemv_q6_k_down_2560x9728_prequantized": entry(d_alg, d_sec),
-                "quantize_q8_k_9728": entry(q_alg, qh_sec)}
-    dom = max(kernels, key=lambda k: kernels[k]["avg_us"])
-    achieved = kernels[dom]["gbs"]
-    traffic = None
+def traffic_for(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (FETCH_SIZE and WRITE_SIZE, scaled by a plain copy's readings)."""
     tpath = ROOT / "profiles" / "traffic.json"
-    if tpath.exists():
-        try:
-            traffic = json.loads(tpath.read_text()).get(dom, {}).get("hbm_bytes_per_launch")
-        except (ValueError, AttributeError):
-            traffic = None
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": dom,
-                "alg_bytes_per_launch": kernels[dom]["alg_bytes"],
-                "avg_launch_us": round(kernels[dom]["avg_us"], 3)}
-    latency = {"gate_up_single_launch_us": round(single_latency(torch, fused_gate_up) * 1e6, 2),
-               "down_single_launch_us": round(single_latency(torch, split_down) * 1e6, 2),
-               "step_single_us": round(single_latency(torch, step) * 1e6, 2)}
+    try:
+        return json.loads(tpath.read_text()).get(kernel, {}).get("hbm_bytes_per_launch")
+    except (OSError, ValueError, AttributeError):
+        return None
 
-    # ---- other configurations (GEMV bandwidth per launch, back-to-back) ------
+
+class Ctx:
+    def __init__(self, torch, np, lib, ops, synth, dev, stream):
+        self.torch, self.np, self.lib, self.ops, self.synth = torch, np, lib, ops, synth
+        self.dev, self.stream = dev, stream
+
+
+# ---- config 3: the headline ------------------------------------------------------------
+
+class Cfg3:
+    """The IQ4_NL output head through the Exec mirror (resident weight) and its
+    GEMV kernel alone on a pre-quantized activation."""
+
+    def __init__(self, c: Ctx):
+        self.c = c
+        torch, ops, synth, lib = c.torch, c.ops, c.synth, c.lib
+        t0 = time.time()
+        w = synth.make_weight(TIQ, R3, C3, seed=0, tag=TIQ)
+        self.x = synth.make_act(C3, 1, seed=0, tag=103)
+        self.sha = synth.sha256(w)
+        self.be = ops.Backend(0)
+        self.lin = self.be.load_linear(TIQ, R3, C3, w)
+        self.wbytes = w.nbytes
+        self.w_host = w
+        self.xd = torch.from_numpy(self.x[0]).to(c.dev)
+        self.y = torch.empty(R3, device=c.dev)
+        self.xq = ops.quantize_act(TIQ, self.xd)
+        self.alg = gemv_bytes(R3, C3, self.wbytes)
+        self._p = [ctypes.c_void_p(t.data_ptr()) for t in (self.y, self.xd)]
+        self._lin = ctypes.byref(self.lin)
+        log(f"cfg3 IQ4_NL [{R3}x{C3}] {self.wbytes / 1e6:.1f} MB resident (gen+upload {time.time() - t0:.1f}s), "
+            f"sha256 {self.sha[:16]}")
+
+    def step(self, i=0):
+        rc = self.c.lib.qhip_backend_matvec(self.be._h, self._p[0], self._lin, self._p[1])
+        assert rc == 0, rc
+
+    def gemv(self, i=0):
+        rc = self.c.lib.qhip_launch_mul_mat_vec(self.lin.dev, self.xq.data_ptr(), self.y.data_ptr(), R3, C3, 1, TIQ,
+                                                self.c.stream)
+        assert rc == 0, rc
+
+    def quantize(self, i=0):
+        rc = self.c.lib.qhip_launch_quantize_act(TIQ, self.xd.data_ptr(), self.xq.data_ptr(), C3, 1, self.c.stream)
+        assert rc == 0, rc
+
+
+# ---- config 2: decode FFN step through the Exec mirror ----------------------------------
+
+class Cfg2:
+    """matvecPair(gate, up, x) + matvec(down, h) (src/backend.zig:153-176 slots):
+    the mirror quantizes x and h on the device and runs one launch per slot --
+    x inside the fused gate/up GEMV (width 2560), h inside the split-K down GEMV
+    (width 9728).  Weight sets rotate over enough copies (> 512 MB per pass)
+    that every step streams from HBM."""
+
+    def __init__(self, c: Ctx):
+        self.c = c
+        torch, np, ops, synth, lib = c.torch, c.np, c.ops, c.synth, c.lib
+        t0 = time.time()
+        self.wg = synth.make_weight(TQ4, F2, H2, seed=0, tag=1)
+        self.wu = synth.make_weight(TQ4, F2, H2, seed=0, tag=2)
+        self.wd = synth.make_weight(TQ6, H2, F2, seed=0, tag=3)
+        self.x = synth.make_act(H2, 1, seed=0, tag=100)
+        self.h = synth.make_act(F2, 1, seed=0, tag=101)
+        self.gu_bytes, self.d_bytes = self.wg.nbytes + self.wu.nbytes, self.wd.nbytes
+        set_bytes = self.gu_bytes + self.d_bytes
+        self.copies = max(1, -(-ROTATE_BYTES // set_bytes))
+        self.be = ops.Backend(0)
+        self.lins = []
+        for _ in range(self.copies):
+            lg = self.be.load_linear(TQ4, F2, H2, self.wg)
+            lu = self.be.load_linear(TQ4, F2, H2, self.wu)
+            ld = self.be.load_linear(TQ6, H2, F2, self.wd)
+            assert lu.dev == lg.dev + F2 * lg.row_bytes  # adjacent: matvecPair is one launch
+            self.lins.append((ctypes.byref(lg), ctypes.byref(lu), ctypes.byref(ld), lg))
+        log(f"cfg2 weights {set_bytes / 1e6:.1f} MB x {self.copies} copies in the backend arena "
+            f"(gen+upload {time.time() - t0:.1f}s)")
+        self.xd = torch.from_numpy(self.x[0]).to(c.dev)
+        self.hd = torch.from_numpy(self.h[0]).to(c.dev)
+        self.y_gu = torch.empty(2 * F2, device=c.dev)
+        self.y_d = torch.empty(H2, device=c.dev)
+        self._p = [ctypes.c_void_p(t.data_ptr()) for t in (self.xd, self.hd, self.y_gu, self.y_d)]
+        self.xq = torch.empty(lib.qhip_act_row_bytes(TQ4, H2), dtype=torch.uint8, device=c.dev)
+        self.hq = torch.empty(lib.qhip_act_row_bytes(TQ6, F2), dtype=torch.uint8, device=c.dev)
+        assert lib.qhip_launch_quantize_act(TQ4, self.xd.data_ptr(), self.xq.data_ptr(), H2, 1, c.stream) == 0
+        assert lib.qhip_launch_quantize_act(TQ6, self.hd.data_ptr(), self.hq.data_ptr(), F2, 1, c.stream) == 0
+        self.skwork = ops.split_work(H2, F2, c.dev)
+        self.step_bytes = gemv_bytes(2 * F2, H2, self.gu_bytes) + gemv_bytes(H2, F2, self.d_bytes)
+
+    def gate_up(self, i):
+        g_, u_, _, _ = self.lins[i % self.copies]
+        assert self.c.lib.qhip_backend_matvec_pair(self.be._h, self._p[2], g_, u_, self._p[0]) == 0
+
+    def down(self, i):
+        assert self.c.lib.qhip_backend_matvec(self.be._h, self._p[3], self.lins[i % self.copies][2], self._p[1]) == 0
+
+    def step(self, i):
+        self.gate_up(i)
+        self.down(i)
+
+    def base(self, i):
+        return self.lins[i % self.copies][3].dev
+
+    def gemv_gate_up(self, i):
+        assert self.c.lib.qhip_launch_mul_mat_vec(self.base(i), self.xq.data_ptr(), self.y_gu.data_ptr(), 2 * F2, H2,
+                                                  1, TQ4, self.c.stream) == 0
+
+    def gemv_down(self, i):
+        assert self.c.lib.qhip_launch_mul_mat_vec(self.base(i) + self.gu_bytes, self.hq.data_ptr(),
+                                                  self.y_d.data_ptr(), H2, F2, 1, TQ6, self.c.stream) == 0
+
+    def split_down(self, i):
+        assert self.c.lib.qhip_launch_quantize_mul_mat_vec_split(
+            self.base(i) + self.gu_bytes, self.hd.data_ptr(), None, self.y_d.data_ptr(), H2, F2, TQ6, 0, 0, 0,
+            self.skwork.data_ptr(), self.skwork.numel(), self.c.stream) == 0
+
+    def fused_gate_up(self, i):
+        assert self.c.lib.qhip_launch_quantize_mul_mat_vec(self.base(i), self.xd.data_ptr(), None,
+                                                           self.y_gu.data_ptr(), 2 * F2, H2, TQ4, self.c.stream) == 0
+
+    def quantize_h(self, i):
+        assert self.c.lib.qhip_launch_quantize_act(TQ6, self.hd.data_ptr(), self.hq.data_ptr(), F2, 1,
+                                                   self.c.stream) == 0
+
+    def step_unfused(self, i):
+        L, s = self.c.lib, self.c.stream
+        assert L.qhip_launch_quantize_act(TQ4, self.xd.data_ptr(), self.xq.data_ptr(), H2, 1, s) == 0
+        self.gemv_gate_up(i)
+        self.quantize_h(i)
+        self.gemv_down(i)
+
+    def run(self, steps, warmup):
+        torch = self.c.torch
+        sec = time_loop(torch, self.step, steps, warmup)
+        sec_unfused = time_loop(torch, self.step_unfused, steps, warmup)
+        n_k = max(200, steps)
+        gu_alg = gemv_bytes(2 * F2, H2, self.gu_bytes)
+        d_alg = gemv_bytes(H2, F2, self.d_bytes)
+
+        def entry(alg, s):
+            return {"alg_bytes": alg, "avg_us": round(s * 1e6, 3), "gbs": round(alg / s / 1e9, 1),
+                    "hbm_frac": round(alg / s / 1e9 / HBM_PEAK_GBS, 4)}
+
+        res = {"workload": "matvecPair Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down "
+                           "[2560,9728] from f32 h[9728] through the Exec mirror",
+               "step_alg_bytes": self.step_bytes, "us_per_step": round(sec * 1e6, 3),
+               "gbs": round(self.step_bytes / sec / 1e9, 1),
+               "hbm_frac": round(self.step_bytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+               "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2),
+               "weight_copies_rotated": self.copies,
+               "kernels": {"fused_q4_k_gate_up_19456x2560": entry(gu_alg, time_loop(torch, self.fused_gate_up, n_k, 20)),
+                           "split_q6_k_down_2560x9728": entry(d_alg, time_loop(torch, self.split_down, n_k, 20))},
+               "kernels_off_step": {
+                   "gemv_q4_k_gate_up_19456x2560_prequantized": entry(gu_alg, time_loop(torch, self.gemv_gate_up, n_k, 20)),
+                   "gemv_q6_k_down_2560x9728_prequantized": entry(d_alg, time_loop(torch, self.gemv_down, n_k, 20)),
+                   "quantize_q8_k_9728": entry(4 * F2 + self.c.lib.qhip_act_row_bytes(TQ6, F2),
+                                               time_loop(torch, self.quantize_h, n_k, 20))},
+               "step_single_launch_us": round(single_latency(torch, self.step) * 1e6, 2)}
+        log(f"cfg2 step: {res['us_per_step']} us, {res['gbs']} GB/s ({100 * res['hbm_frac']:.1f}% HBM); "
+            f"separate quantize launches {res['us_per_step_separate_quantize_launches']} us")
+        return res
+
+
+# ---- other GEMV configurations -----------------------------------------------------------
+
+GEMV_CONFIGS = (("cfg1_q8_0_6144x1024", TQ8, 6144, 1024),
+                ("cfg5_q4_k_17408x5120", TQ4, 17408, 5120),
+                ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408),
+                # further formats at the config-5 gate/up shape
+                ("q5_k_17408x5120", 13, 17408, 5120),
+                ("q3_k_17408x5120", 11, 17408, 5120),
+                ("q2_k_17408x5120", 10, 17408, 5120),
+                ("iq4_xs_17408x5120", 23, 17408, 5120),
+                ("q4_0_17408x5120", 2, 17408, 5120),
+                ("q4_1_17408x5120", 3, 17408, 5120),
+                ("iq3_xxs_17408x5120", 18, 17408, 5120),
+                ("iq3_s_17408x5120", 21, 17408, 5120))
+
+
+def gemv_stream(c: Ctx, tt, rows, cols):
+    w = c.synth.make_weight(tt, rows, cols, seed=0, tag=tt)
+    st = Stream(c.torch, w.reshape(-1), c.dev)
+    xv = c.torch.from_numpy(c.synth.make_act(cols, 1, seed=0)).to(c.dev)
+    aq = c.ops.quantize_act(tt, xv)
+    yo = c.torch.empty(rows, device=c.dev)
+
+    def one(i):
+        rc = c.lib.qhip_launch_mul_mat_vec(st.ptr(i), aq.data_ptr(), yo.data_ptr(), rows, cols, 1, tt, c.stream)
+        assert rc == 0, rc
+    return st, one, (aq, yo)
+
+
+def bench_gemv_configs(c: Ctx):
     extra = {}
-    if not args.no_extra:
-        for name, tt, rows, cols in (("cfg1_q8_0_6144x1024", TQ8, 6144, 1024),
-                                     ("cfg3_iq4_nl_248320x2560", TIQ, 248320, 2560),
-                                     ("cfg5_q4_k_17408x5120", TQ4, 17408, 5120),
-                                     ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408),
-                                     # further formats at the config-5 gate/up shape
-                                     ("q5_k_17408x5120", 13, 17408, 5120),
-                                     ("q3_k_17408x5120", 11, 17408, 5120),
-                                     ("q2_k_17408x5120", 10, 17408, 5120),
-                                     ("iq4_xs_17408x5120", 23, 17408, 5120),
-                                     ("q4_0_17408x5120", 2, 17408, 5120),
-                                     ("q4_1_17408x5120", 3, 17408, 5120),
-                                     ("iq3_xxs_17408x5120", 18, 17408, 5120),
-                                     ("iq3_s_17408x5120", 21, 17408, 5120)):
-            t1 = time.time()
-            w = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
-            st = Stream(torch, w.reshape(-1), dev)
-            del w
-            xv = torch.from_numpy(synth.make_act(cols, 1, seed=0)).to(dev)
-            aq = ops.quantize_act(tt, xv)
-            yo = torch.empty(rows, device=dev)
-
-            def one(i, st=st, tt=tt, rows=rows, cols=cols, aq=aq, yo=yo):
-                rc = lib.qhip_launch_mul_mat_vec(st.ptr(i), aq.data_ptr(), yo.data_ptr(), rows, cols, 1,
-                                                 tt, stream)
-                assert rc == 0, rc
-
-            s = time_loop(torch, one, max(50, min(2000, int(2e9 // st.n))), 10)
-            alg = gemv_bytes(rows, cols, st.n)
-            extra[name] = {"gbs": round(alg / s / 1e9, 1), "hbm_frac": round(alg / s / 1e9 / HBM_PEAK_GBS, 4),
-                           "avg_us": round(s * 1e6, 3), "alg_bytes": alg, "copies": st.copies,
-                           "single_launch_us": round(single_latency(torch, one) * 1e6, 2)}
-            log(f"{name}: {extra[name]['gbs']} GB/s, {extra[name]['avg_us']} us/launch "
-                f"({st.copies} copies, {time.time() - t1:.1f}s)")
-            del st
-            torch.cuda.empty_cache()
-
-    # ---- MMQ prefill: config 4 (ragged + dense 512) and config 5 crossover ------
-    mmq = None
-    if not args.no_extra:
-        mmq = bench_mmq(torch, np, lib, ops, synth, dev, stream)
-
-    # ---- CPU baseline: the reference's own kernels on this host ---------------
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(np, synth, wg, wu, wd, x, hvec, step_bytes, args.cpu_seconds)
-
-    out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-        "data": "synthetic (SplitMix64 seed 0, BASELINE.json config rules)",
-        "config": {"workload": "cfg2 decode FFN step, batch 1, through the Exec mirror: matvecPair "
-                               "Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down [2560,9728] "
-                               "from f32 h[9728] (Q8_K quantization on the device: of x inside the gate/up "
-                               "GEMV launch, of h inside the split-K down GEMV launch)",
-                   "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": step_bytes,
-                   "weight_copies_rotated": copies, "parallelism": "single GPU",
-                   "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2)},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "kernels": kernels,
-        "kernels_off_step": off_step,
-        "latency": latency,
-        "configs": extra,
-        "mmq": mmq,
-    }
-    print(json.dumps(out), flush=True)
-    return 0
+    for name, tt, rows, cols in GEMV_CONFIGS:
+        t1 = time.time()
+        st, one, keep = gemv_stream(c, tt, rows, cols)
+        s = time_loop(c.torch, one, max(50, min(2000, int(2e9 // st.n))), 10)
+        alg = gemv_bytes(rows, cols, st.n)
+        extra[name] = {"gbs": round(alg / s / 1e9, 1), "hbm_frac": round(alg / s / 1e9 / HBM_PEAK_GBS, 4),
+                       "avg_us": round(s * 1e6, 3), "alg_bytes": alg, "copies": st.copies,
+                       "single_launch_us": round(single_latency(c.torch, one) * 1e6, 2)}
+        log(f"{name}: {extra[name]['gbs']} GB/s, {extra[name]['avg_us']} us/launch "
+            f"({st.copies} copies, {time.time() - t1:.1f}s)")
+        del st, keep
+        c.torch.cuda.empty_cache()
+    return extra
 
 
-def profile_mmq(torch, lib, ops, synth, dev, stream, which, launches):
-    """Only the MMQ kernel of one configuration, for rocprofv3."""
-    tt, rows, cols, T = {"mmq_cfg5_q4k": (12, 17408, 5120, 512), "mmq_cfg5_q3k": (11, 17408, 5120, 512),
-                         "mmq_cfg5_q2k": (10, 17408, 5120, 512)}.get(which, (8, 3584, 1024, 512))
-    w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
-    aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
-    y = torch.empty((T, rows), device=dev)
-    for _ in range(launches):
-        assert lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt, 2, stream) == 0
-    torch.cuda.synchronize()
-    print(json.dumps({"profiled": which, "launches": launches}))
+# ---- MMQ ------------------------------------------------------------------------------------
 
-
-def bench_mmq(torch, np, lib, ops, synth, dev, stream):
+def bench_mmq(c: Ctx):
     """Config 4: Q8_0 [3584,1024] with eight ragged sequences (lengths uniform on
     [16,256], packed by the ragged quantizer, one launch) and a dense 512-token
     sequence.  Config 5: Q4_K gate [17408,5120] and Q6_K down [5120,17408] at
-    T = 1, 4, 16, 64, 512 on the GEMV and on the MMQ, and the crossover.
-    Throughput: tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak.
-    `mmq_us` is the faster of the tile MMQ and (Q6_K) the image MMQ."""
-    PATH_GEMV, PATH_MMQ = 1, 2
+    T = 1, 4, 16, 64, 512 on the GEMV and on the MMQ (with the split-K
+    workspace the Exec mirror passes), and the crossover.  Throughput:
+    tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak.  `mmq_us`
+    is the faster of the tile MMQ and (Q6_K) the image MMQ."""
+    torch, lib, ops, synth, dev, stream = c.torch, c.lib, c.ops, c.synth, c.dev, c.stream
     res = {}
 
     def timed(fn, iters):
@@ -411,8 +360,7 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
         tops = 2.0 * rows * cols * T / sec / 1e12
         return round(tops, 1), round(tops / INT8_PEAK_TOPS, 4)
 
-    # config 4
-    tt, rows, cols = 8, 3584, 1024
+    tt, rows, cols = TQ8, 3584, 1024
     w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
     lens = [int(v) for v in synth.ragged_lengths(8, 16, 256, seed=0)]
     seqs = [torch.from_numpy(synth.make_act(cols, n, seed=0, tag=300 + i)).to(dev) for i, n in enumerate(lens)]
@@ -445,18 +393,19 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
     s_d = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), xq5.data_ptr(), y5.data_ptr(), rows, cols, T, tt,
                                                 PATH_MMQ, stream), 200)
     tops, fr = frac(rows, cols, T, s_d)
+    mem = 3899392 + 4 * cols * T + 4 * rows * T
     res["cfg4_dense512_q8_0_3584x1024"] = {"tokens": T, "tokens_per_s": round(T / s_d, 1),
-                                           "us_mmq": round(s_d * 1e6, 2), "int8_tops": tops, "int8_mfma_frac": fr}
-    log(f"mmq cfg4: ragged {total} tokens {s_mm * 1e6:.1f} us ({res['cfg4_ragged_q8_0_3584x1024']['int8_mfma_frac']:.3f} "
-        f"of int8 peak); dense 512 {s_d * 1e6:.1f} us")
+                                           "us_mmq": round(s_d * 1e6, 2), "int8_tops": tops, "int8_mfma_frac": fr,
+                                           "alg_bytes": mem, "hbm_frac": round(mem / s_d / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"mmq cfg4: ragged {total} tokens {s_mm * 1e6:.1f} us "
+        f"({res['cfg4_ragged_q8_0_3584x1024']['int8_mfma_frac']:.3f} of int8 peak); dense 512 {s_d * 1e6:.1f} us")
     del w, xq, yo, seqs
 
-    # config 5 sweep
     sweep = {}
-    for name, tt, rows, cols in (("q4_k_17408x5120", 12, 17408, 5120), ("q6_k_5120x17408", 14, 5120, 17408)):
+    for name, tt, rows, cols in (("q4_k_17408x5120", TQ4, 17408, 5120), ("q6_k_5120x17408", TQ6, 5120, 17408)):
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
         # the prepared MMQ weight image the Exec mirror uses for Q6_K prefill
-        img = ops.mmq_image(tt, w, rows, cols) if tt == 14 else None
+        img = ops.mmq_image(tt, w, rows, cols) if tt == TQ6 else None
         rows_out = []
         cross = None
         for T in (1, 4, 16, 64, 512):
@@ -464,11 +413,11 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
             aq = ops.quantize_act(tt, x)
             y = torch.empty((T, rows), device=dev)
             it = 100 if T <= 64 else 30
-            s_g = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
-                                                        PATH_GEMV, stream), it)
             # the split-K workspace the Exec mirror passes (small grids split K)
             work = ops.mul_mat_work(rows, cols, T, tt, dev)
             wp, wn = (work.data_ptr(), work.numel()) if work is not None else (None, 0)
+            s_g = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+                                                        PATH_GEMV, stream), it)
             s_t = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
                                                              tt, PATH_MMQ, wp, wn, stream), it)
             pt = {"T": T, "gemv_us": round(s_g * 1e6, 2), "mmq_tile_us": round(s_t * 1e6, 2)}
@@ -493,57 +442,251 @@ def bench_mmq(torch, np, lib, ops, synth, dev, stream):
     return res
 
 
-def cpu_baseline(np, synth, wg, wu, wd, x, hvec, step_bytes, budget_s):
-    """The reference's x86 kernels (oracle/_ref, compiled from its sources) on
-    this host's cores: Q8_K quantize + row dots with the reference pool's chunk
-    rule, rotating weight copies (>512 MB) like the GPU does."""
+# ---- CPU baseline ----------------------------------------------------------------------------
+
+def cpu_time(fn, budget_s, min_reps=5, max_reps=200):
+    """Median seconds of fn() after one warm-up call, within a time budget."""
+    fn(0)
+    ts, i = [], 1
+    deadline = time.time() + budget_s
+    while len(ts) < max_reps:
+        t = time.perf_counter()
+        fn(i)
+        ts.append(time.perf_counter() - t)
+        i += 1
+        if len(ts) >= min_reps and time.time() > deadline:
+            break
+    return statistics.median(ts), len(ts)
+
+
+def cpu_baseline(c: Ctx, cfg3: Cfg3, cfg2: Cfg2 | None, budget_s: float, all_configs: bool):
+    """This repository's C restatement of the reference CPU path (oracle/): the
+    activation quantized once per token, then one row dot per (token, row) at
+    the host's ISA tier (IQ4_NL / Q4_K / Q6_K AVX2, Q8_0 AVX-512 VNNI, as the
+    reference dispatches), row-parallel with the reference pool's chunk rule
+    (src/pool.zig:489-494) over the host cores this process may use."""
+    np, synth = c.np, c.synth
     sys.path.insert(0, str(ROOT / "oracle"))
     import pyoracle
     orc = pyoracle.Oracle()
-    ref = pyoracle.load_ref()
-    kind = "reference" if ref is not None else "port"
     threads = pyoracle.host_threads()
-    H, F = x.shape[1], hvec.shape[1]
-    gu = np.concatenate([wg, wu])
-    one = gu.nbytes + wd.nbytes
-    copies = max(1, -(-ROTATE_BYTES // one))
-    gus = [gu.copy() for _ in range(copies)]
-    wds = [wd.copy() for _ in range(copies)]
-    quant = (ref or orc).quantize_act
-    dot4 = ref.dot_fn_addr(12) if ref else orc.dot_fn_addr(12)
-    dot6 = ref.dot_fn_addr(14) if ref else orc.dot_fn_addr(14)
-    y1 = np.empty((1, 2 * F), np.float32)
-    y2 = np.empty((1, H), np.float32)
+    nproc = os.cpu_count()
 
-    def step(i, nt):
-        xq = quant(12, x)
-        orc.matvec_q_fn(dot4, 12, gus[i % copies], xq, H, y1, nt)
-        hq = quant(14, hvec)
-        orc.matvec_q_fn(dot6, 14, wds[i % copies], hq, F, y2, nt)
+    def gemv_case(tt, W, x, rows, cols, copies=1):
+        """quantize x once, then the row dots; weight copies rotated."""
+        dot = orc.simd_dot_fn_addr(tt)
+        Ws = [W] + [W.copy() for _ in range(copies - 1)]
+        y = np.empty((x.shape[0], rows), np.float32)
 
-    res = {}
-    for nt in (threads, 1):
-        for i in range(2):
-            step(i, nt)
-        ts, i = [], 0
-        deadline = time.time() + (budget_s if nt == threads else budget_s / 3)
-        while len(ts) < 200:
-            t = time.perf_counter()
-            step(i, nt)
-            ts.append(time.perf_counter() - t)
-            i += 1
-            if len(ts) >= 5 and time.time() > deadline:
-                break
-        res[nt] = (statistics.median(ts), len(ts))
-    med, n = res[threads]
-    tier = ref.tier() if ref else "scalar port"
-    log(f"cpu baseline ({kind}, {threads} threads, {tier}): {med * 1e3:.2f} ms/step, "
-        f"{step_bytes / med / 1e9:.2f} GB/s; 1 thread {res[1][0] * 1e3:.2f} ms")
-    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "sample": f"cfg2 FFN step (Q8_K quantize + Q4_K 2x[9728,2560] + Q6_K [2560,9728] row dots), "
-                      f"median of {n} steps over {copies} rotating weight copies, tier {tier}",
-            "ms_per_step": round(med * 1e3, 3),
-            "one_thread_gbs": round(step_bytes / res[1][0] / 1e9, 3)}
+        def run(i, nt):
+            act = orc.quantize_act(tt, x)
+            orc.matvec_q_fn(dot, tt, Ws[i % copies], act, cols, y, nt)
+        return run
+
+    res = {"kind": "port", "cores": threads, "host_nproc": nproc, "configs": {}}
+
+    def record(name, run, alg, unit_den, budget, unit="GB/s", extra=None):
+        med, n = cpu_time(lambda i: run(i, threads), budget)
+        med1, n1 = cpu_time(lambda i: run(i, 1), budget / 3, min_reps=3)
+        if unit == "GB/s":
+            v, v1 = alg / med / 1e9, alg / med1 / 1e9
+        else:
+            v, v1 = unit_den / med, unit_den / med1
+        ent = {"value": round(v, 3), "unit": unit, "threads": threads, "ms": round(med * 1e3, 3), "reps": n,
+               "one_thread_value": round(v1, 3), "one_thread_ms": round(med1 * 1e3, 3)}
+        if extra:
+            ent.update(extra)
+        res["configs"][name] = ent
+        log(f"cpu {name}: {v:.2f} {unit} on {threads} threads ({med * 1e3:.2f} ms), 1 thread {v1:.2f}")
+        return ent
+
+    # config 3 (the headline workload), the whole GEMV
+    r3 = gemv_case(TIQ, cfg3.w_host, cfg3.x, R3, C3)
+    head = record("cfg3_iq4_nl_248320x2560", r3, cfg3.alg, None, budget_s * 0.4,
+                  extra={"tier": orc.simd_tier(TIQ)})
+    res.update({"value": head["value"], "unit": "GB/s", "tier": orc.simd_tier(TIQ),
+                "sample": f"the whole config-3 GEMV (Q8_0 quantize of x[2560] + 248320 IQ4_NL row dots, AVX2 "
+                          f"codebook shuffle), median of {head['reps']} runs on {threads} threads "
+                          f"(host nproc {nproc}); 1 thread {head['one_thread_value']} GB/s"})
+    if not all_configs:
+        return res
+    budget = budget_s * 0.6 / 6
+    # config 1: Q8_0 [6144, 1024], copies rotated past 512 MB like the GPU
+    w1 = synth.make_weight(TQ8, 6144, 1024, seed=0, tag=TQ8)
+    x1 = synth.make_act(1024, 1, seed=0)
+    record("cfg1_q8_0_6144x1024", gemv_case(TQ8, w1, x1, 6144, 1024, copies=max(1, ROTATE_BYTES // w1.nbytes)),
+           gemv_bytes(6144, 1024, w1.nbytes), None, budget, extra={"tier": orc.simd_tier(TQ8)})
+    del w1
+    # config 2: the decode FFN step (quantize x, gate/up dots, quantize h, down dots)
+    if cfg2 is not None:
+        gu = np.concatenate([cfg2.wg, cfg2.wu])
+        r_gu = gemv_case(TQ4, gu, cfg2.x, 2 * F2, H2, copies=cfg2.copies)
+        r_d = gemv_case(TQ6, cfg2.wd, cfg2.h, H2, F2, copies=cfg2.copies)
+
+        def step(i, nt):
+            r_gu(i, nt)
+            r_d(i, nt)
+        record("cfg2_ffn_step", step, cfg2.step_bytes, None, budget, extra={"tier": orc.simd_tier(TQ4)})
+        del gu
+    # config 4: dense 512 tokens and the ragged batch (tokens/s)
+    w4 = synth.make_weight(TQ8, 3584, 1024, seed=0, tag=TQ8)
+    x4 = synth.make_act(1024, 512, seed=0, tag=400)
+    record("cfg4_dense512_q8_0_3584x1024", gemv_case(TQ8, w4, x4, 3584, 1024), None, 512, budget,
+           unit="tokens/s")
+    lens = [int(v) for v in synth.ragged_lengths(8, 16, 256, seed=0)]
+    xr = np.concatenate([synth.make_act(1024, n, seed=0, tag=300 + i) for i, n in enumerate(lens)])
+    record("cfg4_ragged_q8_0_3584x1024", gemv_case(TQ8, w4, xr, 3584, 1024), None, sum(lens), budget,
+           unit="tokens/s", extra={"tokens": sum(lens)})
+    del w4, x4, xr
+    # config 5: one and 64 tokens on both matrices
+    for name, tt, rows, cols in (("cfg5_q4_k_17408x5120", TQ4, 17408, 5120), ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408)):
+        w5 = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
+        for T in (1, 64):
+            x5 = synth.make_act(cols, T, seed=0, tag=500 + T)
+            record(f"{name}_t{T}", gemv_case(tt, w5, x5, rows, cols), gemv_bytes(rows, cols, w5.nbytes, T), T,
+                   budget / 2, unit="GB/s" if T == 1 else "tokens/s", extra={"tier": orc.simd_tier(tt)})
+        del w5
+    return res
+
+
+# ---- profiling entry: one kernel only ---------------------------------------------------
+
+def profile(c: Ctx, which: str, launches: int):
+    torch, lib, ops, synth, dev, stream = c.torch, c.lib, c.ops, c.synth, c.dev, c.stream
+    fn = None
+    keep = []
+    if which in ("cfg3_gemv", "cfg3_step"):
+        c3 = Cfg3(c)
+        keep.append(c3)
+        fn = c3.gemv if which == "cfg3_gemv" else c3.step
+    elif which in ("cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv"):
+        tt, rows, cols = {"cfg1_gemv": (TQ8, 6144, 1024), "cfg5_q4k_gemv": (TQ4, 17408, 5120),
+                          "cfg5_q6k_gemv": (TQ6, 5120, 17408)}[which]
+        st, fn, k = gemv_stream(c, tt, rows, cols)
+        keep += [st, k]
+    elif which in ("down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused"):
+        c2 = Cfg2(c)
+        keep.append(c2)
+        fn = {"down": c2.gemv_down, "gate_up": c2.gemv_gate_up, "fused_gate_up": c2.fused_gate_up,
+              "split_down": c2.split_down, "step": c2.step, "step_unfused": c2.step_unfused}[which]
+    else:
+        tt, rows, cols, T = {"mmq_cfg5_q4k": (TQ4, 17408, 5120, 512), "mmq_cfg5_q3k": (11, 17408, 5120, 512),
+                             "mmq_cfg5_q2k": (10, 17408, 5120, 512), "mmq_cfg5_q6k_image": (TQ6, 5120, 17408, 512),
+                             "mmq_cfg4": (TQ8, 3584, 1024, 512)}[which]
+        w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
+        aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
+        y = torch.empty((T, rows), device=dev)
+        keep += [w, aq, y]
+        if which == "mmq_cfg5_q6k_image":
+            img = ops.mmq_image(tt, w, rows, cols)
+            keep.append(img)
+
+            def fn(i):
+                assert lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+                                                     0, 0, None, 0, stream) == 0
+        else:
+            def fn(i):
+                assert lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+                                               PATH_MMQ, stream) == 0
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    for i in range(launches):
+        fn(i)
+    torch.cuda.synchronize()
+    print(json.dumps({"profiled": which, "launches": launches}))
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline workload")
+    ap.add_argument("--cpu-seconds", type=float, default=30.0, help="CPU baseline budget over all configs")
+    ap.add_argument("--profile-kernel", choices=PROFILE_KERNELS, help="run only this kernel (for rocprofv3) and exit")
+    ap.add_argument("--copy-calib", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the quantized matvec path has no "
+              "multi-GPU component; it would shard by output rows). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import qwen35_amd
+    from qwen35_amd import _lib, ops, synth
+
+    lib = _lib.load()
+    qwen35_amd.check("qhip_init", lib.qhip_init(0))
+    dev = torch.device("cuda:0")
+    c = Ctx(torch, np, lib, ops, synth, dev, torch.cuda.current_stream().cuda_stream)
+
+    if args.copy_calib:
+        n = 256 << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes_read": n, "copy_calib_bytes_written": n, "launches": 5}))
+        return 0
+    if args.profile_kernel:
+        profile(c, args.profile_kernel, args.steps)
+        return 0
+
+    # ---- headline: config 3 through the Exec mirror ------------------------------------
+    c3 = Cfg3(c)
+    sec = time_loop(torch, c3.step, args.steps, args.warmup)
+    value = c3.alg / sec / 1e9
+    log(f"cfg3 step (quantize + GEMV): {sec * 1e6:.2f} us, {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% HBM)")
+    n_k = max(200, args.steps)
+    g_sec = time_loop(torch, c3.gemv, n_k, 20)
+    q_sec = time_loop(torch, c3.quantize, n_k, 20)
+    achieved = c3.alg / g_sec / 1e9
+    kname = "gemv_iq4_nl_248320x2560"
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic_for(kname), "kernel": kname,
+                "alg_bytes_per_launch": c3.alg, "avg_launch_us": round(g_sec * 1e6, 3)}
+    log(f"cfg3 GEMV kernel alone: {g_sec * 1e6:.2f} us = {achieved:.1f} GB/s ({100 * achieved / HBM_PEAK_GBS:.1f}% "
+        f"of 8 TB/s); quantize launch {q_sec * 1e6:.2f} us")
+    latency = {"cfg3_step_single_us": round(single_latency(torch, c3.step) * 1e6, 2),
+               "cfg3_gemv_single_launch_us": round(single_latency(torch, c3.gemv) * 1e6, 2)}
+
+    cfg2 = extra = mmq = None
+    c2 = None
+    if not args.no_extra:
+        c2 = Cfg2(c)
+        cfg2 = c2.run(args.steps, args.warmup)
+        extra = bench_gemv_configs(c)
+        mmq = bench_mmq(c)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(c, c3, c2, args.cpu_seconds, not args.no_extra)
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic (SplitMix64 seed 0, BASELINE.json config rules)",
+        "config": {"workload": "cfg3: IQ4_NL output-head GEMV [248320,2560], batch 1, through the Exec mirror's "
+                               "matvec from f32 x[2560] (Q8_0 quantization of x on the device, then the GEMV); "
+                               "357 MB of weights resident in HBM, larger than the Infinity Cache",
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4), "step_alg_bytes": c3.alg,
+                   "weight_sha256": c3.sha, "parallelism": "single GPU",
+                   "gemv_kernel_us": round(g_sec * 1e6, 3), "quantize_launch_us": round(q_sec * 1e6, 3)},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "latency": latency,
+        "cfg2_step": cfg2,
+        "configs": extra,
+        "mmq": mmq,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
 
 
 if __name__ == "__main__":

@@ -124,6 +124,13 @@ int orc_dequant_row(int ttype, int cols, const void *w, float *out);
 orc_dot_fn   orc_dot_fn_for(int ttype);
 orc_quant_fn orc_quant_fn_for(int ttype);
 
+/* oracle_simd.c: the host-ISA tier of the row dot (IQ4_NL / Q4_K / Q6_K AVX2,
+ * Q8_0 AVX-512 VNNI or AVX2; other types and hosts without AVX2: the scalar
+ * restatement), the tier's name, and the Q8_0 AVX2 form on its own. */
+orc_dot_fn   orc_simd_dot_fn_for(int ttype);
+const char  *orc_simd_tier(int ttype);
+orc_dot_fn   orc_simd_dot_q8_0_avx2(void);
+
 #ifdef __cplusplus
 }
 #endif

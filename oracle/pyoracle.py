@@ -93,6 +93,12 @@ class Oracle:
         L.orc_dequant_row.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, _c_f32p]
         L.orc_dot_fn_for.restype = ctypes.c_void_p
         L.orc_dot_fn_for.argtypes = [ctypes.c_int]
+        L.orc_simd_dot_fn_for.restype = ctypes.c_void_p
+        L.orc_simd_dot_fn_for.argtypes = [ctypes.c_int]
+        L.orc_simd_tier.restype = ctypes.c_char_p
+        L.orc_simd_tier.argtypes = [ctypes.c_int]
+        L.orc_simd_dot_q8_0_avx2.restype = ctypes.c_void_p
+        L.orc_simd_dot_q8_0_avx2.argtypes = []
         L.orc_quant_fn_for.restype = ctypes.c_void_p
         L.orc_quant_fn_for.argtypes = [ctypes.c_int]
         for name in ("orc_iq3xxs_grid", "orc_iq3s_grid"):
@@ -165,6 +171,27 @@ class Oracle:
 
     def dot_fn_addr(self, ttype: int) -> int:
         return self.lib.orc_dot_fn_for(ttype)
+
+    def simd_dot_fn_addr(self, ttype: int) -> int:
+        """The row dot at this host's ISA tier (oracle_simd.c)."""
+        return self.lib.orc_simd_dot_fn_for(ttype)
+
+    def simd_tier(self, ttype: int) -> str:
+        return self.lib.orc_simd_tier(ttype).decode()
+
+    def simd_q8_0_avx2_addr(self) -> int:
+        return self.lib.orc_simd_dot_q8_0_avx2() or 0
+
+    def matvec_dot(self, dot_fn_addr: int, ttype: int, W: np.ndarray, x: np.ndarray,
+                   nthreads: int = 1) -> np.ndarray:
+        """matvec with a chosen row-dot function (quantize with the oracle, then dot)."""
+        x2 = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, x.shape[-1])
+        cols = x2.shape[1]
+        act = self.quantize_act(ttype, x2)
+        W = np.ascontiguousarray(W).reshape(-1, row_bytes(ttype, cols))
+        out = np.zeros((x2.shape[0], W.shape[0]), np.float32)
+        self.matvec_q_fn(dot_fn_addr, ttype, W, act, cols, out, nthreads)
+        return out
 
     def iq3_grid(self, ttype: int) -> np.ndarray:
         """The oracle's IQ3_XXS (256) or IQ3_S (512) grid as u32 entries."""

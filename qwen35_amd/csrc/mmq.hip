@@ -445,16 +445,30 @@ __device__ __forceinline__ void mmq_write_tile(f32x16 (&acc)[NA][NB], float* __r
         for (int e = 0; e < 16; ++e) sk_store(pp + ((a * NB + b) * 16 + e) * 64, acc[a][b][e]);
     if (!sk_arrive(cnt + tile, (unsigned)ksplit)) return;
     const float* base = part + (long)tile * ksplit * TS + mine;
+    // slice by slice, in slice order: one slice's loads are independent and
+    // go out together (one memory latency per slice, not per element)
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          float v = 0.0f;
-          for (int q = 0; q < ksplit; ++q) v += sk_load(base + q * TS + ((a * NB + b) * 16 + e) * 64);
-          acc[a][b][e] = v;
-        }
+        for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
+    for (int q = 0; q < ksplit; ++q) {
+      const float* pq = base + q * TS;
+      f32x16 t[NA][NB];
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) t[a][b][e] = sk_load(pq + ((a * NB + b) * 16 + e) * 64);
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[a][b][e] += t[a][b][e];
+    }
     sk_reset(cnt + tile);
   }
 #pragma unroll

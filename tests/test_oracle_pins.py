@@ -430,3 +430,41 @@ def test_iq3_dot_equals_scaled_dequant(oracle, tt):
         got = oracle.matvec(tt, w[r:r + 1], x)[:, 0]
         want = ints[:, r, :].astype(np.float64) @ scale
         assert np.allclose(got, want, rtol=2e-6, atol=0)
+
+
+# ---- the host-ISA tiers of the restatement (oracle_simd.c, the CPU baseline) --
+
+SIMD_CASES = [(po.TT_IQ4_NL, 2560), (po.TT_Q8_0, 1024), (po.TT_Q4_K, 2560), (po.TT_Q6_K, 9728)]
+
+
+@pytest.mark.parametrize("tt,cols", SIMD_CASES, ids=[po.NAMES[c[0]] for c in SIMD_CASES])
+def test_simd_tier_matches_scalar(oracle, tt, cols):
+    """Same integers on every tier; IQ4_NL (AVX2) and Q8_0 (VNNI) fold the
+    blocks sequentially like the scalar restatement, so they must agree bit
+    for bit; the 8-lane FMA folds (Q4_K, Q6_K, Q8_0 AVX2) within 1e-6."""
+    from qwen35_amd import synth
+    w = synth.make_weight(tt, 48, cols, seed=21, tag=tt)
+    x = synth.make_act(cols, 3, seed=22)
+    want = oracle.matvec(tt, w, x)
+    got = oracle.matvec_dot(oracle.simd_dot_fn_addr(tt), tt, w, x)
+    tier = oracle.simd_tier(tt)
+    if tt == po.TT_IQ4_NL or tier in ("avx512vnni", "scalar"):
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), tier
+    else:
+        assert np.linalg.norm(got - want) / np.linalg.norm(want) < 1e-6
+    if tt == po.TT_Q8_0 and oracle.simd_q8_0_avx2_addr():
+        g2 = oracle.matvec_dot(oracle.simd_q8_0_avx2_addr(), tt, w, x)
+        assert np.linalg.norm(g2 - want) / np.linalg.norm(want) < 1e-6
+
+
+@pytest.mark.parametrize("tt", [po.TT_Q8_0, po.TT_Q4_K, po.TT_Q6_K], ids=["Q8_0", "Q4_K", "Q6_K"])
+def test_simd_tier_matches_reference_build(oracle, ref, tt):
+    """The restated tiers against the reference's own compiled kernels, which
+    dispatch to the same tier on this host: bit-identical floats."""
+    from qwen35_amd import synth
+    cols = {po.TT_Q8_0: 2048, po.TT_Q4_K: 5120, po.TT_Q6_K: 9728}[tt]
+    w = synth.make_weight(tt, 40, cols, seed=23, tag=tt)
+    x = synth.make_act(cols, 2, seed=24)
+    got = oracle.matvec_dot(oracle.simd_dot_fn_addr(tt), tt, w, x)
+    want = oracle.matvec_dot(ref.dot_fn_addr(tt), tt, w, x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
