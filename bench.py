@@ -408,7 +408,7 @@ def bench_mmq(c: Ctx):
         img = ops.mmq_image(tt, w, rows, cols) if tt == TQ6 else None
         rows_out = []
         cross = None
-        for T in (1, 4, 16, 64, 512):
+        for T in (1, 4, 8, 16, 64, 512):
             x = torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev)
             aq = ops.quantize_act(tt, x)
             y = torch.empty((T, rows), device=dev)
@@ -427,6 +427,13 @@ def bench_mmq(c: Ctx):
                                                                   cols, T, tt, 0, 0, wp, wn, stream), it)
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
+            # the automatic path (what the Exec mirror's matvecBatchK takes)
+            s_a = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
+                                                             tt, PATH_AUTO, wp, wn, stream), it)
+            pt["auto_us"] = round(s_a * 1e6, 2)
+            if s_a > 1.1 * min(s_g, s_t):
+                pt["auto_warning"] = "the automatic GEMV/MMQ choice is more than 10% slower than the faster path"
+                log(f"WARNING: {name} T={T}: auto {s_a * 1e6:.2f} us vs GEMV {s_g * 1e6:.2f} / MMQ {s_t * 1e6:.2f} us")
             tops, fr = frac(rows, cols, T, s_m)
             pt.update({"mmq_us": round(s_m * 1e6, 2), "gemv_tokens_per_s": round(T / s_g, 1),
                        "mmq_tokens_per_s": round(T / s_m, 1), "mmq_int8_tops": tops, "mmq_int8_mfma_frac": fr})

@@ -73,17 +73,19 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
   return hipSuccess;
 }
 
-// Token count from which the MMQ tiles beat the weight-streaming GEMV.
-// Measured on MI355X at the BASELINE shapes with split-K MMQ for small token
-// counts: Q4_K [17408, 5120] GEMV 23.6 us / MMQ 31.2 us at 4 tokens, 39.2 /
-// 30.3 us at 8; Q6_K [5120, 17408] 44.5 / 42.4 us at 8; Q8_0 [3584, 1024]
-// 5.3 / 7.9 us at 8, 8.1 / 8.0 us at 16; Q3_K / Q2_K [17408, 5120] 48.6 /
-// 29.6 and 38.6 / 26.8 us at 8 (Q2_K 23.3 / 26.5 at 4).
+// Token count from which the MMQ tiles beat the weight-streaming GEMV, both
+// at their defaults (the MMQ with the split-K workspace the Exec mirror
+// passes).  Measured on MI355X: Q4_K [17408, 5120] GEMV 22.6 / MMQ 24.0 us at
+// 5 tokens, 25.1 / 24.0 at 6; Q6_K [5120, 17408] 35.1 / 40.0 at 6, 42.5 /
+// 40.2 at 8; IQ4_NL [17408, 5120] 30.8 / 34.7 at 8, 46.4 / 34.7 at 12;
+// Q8_0 [3584, 1024] 7.8 / 8.7 at 16; Q3_K / Q2_K [17408, 5120] 48.6 / 29.6
+// and 38.6 / 26.8 us at 8 (Q2_K 23.3 / 26.5 at 4).
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
-    case TT_Q4_K: case TT_Q5_K: case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: case TT_Q3_K:
-    case TT_Q2_K: return 8;
-    default: return 16;
+    case TT_Q4_K: case TT_Q5_K: return 6;
+    case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: case TT_Q3_K: case TT_Q2_K: return 8;
+    case TT_IQ4_NL: case TT_Q4_0: case TT_Q4_1: return 10;
+    default: return 24;
   }
 }
 
@@ -99,8 +101,11 @@ static bool mmq_supported(int ttype) {
 // -- the tile path's per-16-value integer scaling dominates it.  For Q4_K the
 // image's 3.9x larger weight bytes cost more than the scaling they save (43 /
 // 30 us at 16 tokens, 201 / 172 us at 512), so Q4_K stays on the tile path.
+// With the deterministic split-K both run for few tokens, the tile path is
+// ahead up to 64 tokens ([5120, 17408]: 40.3 / 43.0 us image at 16 tokens,
+// 45.6 / 46.4 at 64), so the image is taken from 96 tokens.
 bool mmq_image_preferred(const GemvArgs& g) {
-  return g.ttype == TT_Q6_K && g.tokens >= 8 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+  return g.ttype == TT_Q6_K && g.tokens >= 96 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
 // `work` (nullable): the split-K workspace of the MMQ (mmq_work_bytes)

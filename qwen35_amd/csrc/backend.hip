@@ -364,7 +364,8 @@ void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
 
 int qhip_backend_prepare_linear(qhip_backend* be, const qhip_linear* w) {
   if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
-  const GemvArgs g{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 8, w->row_bytes,
+  // a long prefill: whether any token count would use an image for this weight
+  const GemvArgs g{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 4096, w->row_bytes,
                    qhip_act_row_bytes(w->ttype, w->cols)};
   if (!mmq_image_preferred(g)) return 0;  // no image serves this weight
   if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;

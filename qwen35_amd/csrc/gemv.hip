@@ -53,12 +53,22 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
       typename U::W w[NR];
 #pragma unroll
       for (int k = 0; k < NR; ++k) w[k] = U::load_w(wrow[k], u);
+      if constexpr (NT == 1) {
+        const typename U::A a = U::load_a(XQ + (long)t0 * act_bytes, u);
 #pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        if (NT == 1 || t0 + t < tokens) {
-          const typename U::A a = U::load_a(XQ + (long)(t0 + t) * act_bytes, u);
+        for (int k = 0; k < NR; ++k) acc[0][k] += U::dot(w[k], a);
+      } else {
+        // decode each weight unit once, multiply it by every token of the pass
+        typename Prep<TT>::P p[NR];
 #pragma unroll
-          for (int k = 0; k < NR; ++k) acc[t][k] += U::dot(w[k], a);
+        for (int k = 0; k < NR; ++k) p[k] = Prep<TT>::prep(w[k]);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          if (t0 + t < tokens) {
+            const typename U::A a = U::load_a(XQ + (long)(t0 + t) * act_bytes, u);
+#pragma unroll
+            for (int k = 0; k < NR; ++k) acc[t][k] += Prep<TT>::dotp(p[k], a);
+          }
         }
       }
     }
@@ -593,7 +603,11 @@ int gemv_pick_team(int rows, int cols, int target_waves) {
   return best;
 }
 
-int gemv_pick_nt(int tokens) { return tokens >= 8 ? 8 : tokens >= 4 ? 4 : tokens >= 2 ? 2 : 1; }
+// Tokens per pass: the smallest power of two covering the tokens (at most 8);
+// the pass masks the tokens past the end.  Swept on MI355X at the config-5
+// shapes: three tokens in one 4-token pass cost 15.8 us against 19.0 us for a
+// 2-token and a 1-token pass (Q4_K [17408, 5120]).
+int gemv_pick_nt(int tokens) { return tokens > 4 ? 8 : tokens > 2 ? 4 : tokens > 1 ? 2 : 1; }
 
 template <int TT, int NT, int NR>
 static hipError_t launch_gemv_t(const GemvArgs& g, int team, hipStream_t s) {
@@ -707,11 +721,16 @@ hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t 
   if (team <= 0 && nr <= 0 && g.tokens == 1) {
     default_shape(g, team, nr);
   } else if (team <= 0 && nr <= 0 && nt <= 0) {
-    // several tokens: two rows per lane halve the activation loads per weight
-    // load (swept at T = 2..32 on [17408, 5120] Q4_K and [5120, 17408] Q6_K:
-    // 1.6-1.8x over one row per lane; Q8_0 is launch-bound either way)
-    nr = g.ttype == TT_Q8_0 ? 1 : 2;
-    team = g.ttype == TT_Q6_K ? 64 : g.ttype == TT_Q8_0 ? 32 : 16;
+    // several tokens: each weight unit is decoded once (Prep<TT>) and
+    // multiplied by every token of the pass; two rows per lane halve the
+    // activation loads per weight load.  Swept on MI355X over 8..64 lanes,
+    // 1..4 rows and 2..8 tokens per pass at T = 2..16: Q4_K [17408, 5120]
+    // 20 lanes x 2 rows (T = 4: 18.9 us against 22.0 with 16 lanes), four
+    // rows from 6 tokens (T = 8: 29.7 vs 31.4 us); Q6_K [5120, 17408] 64
+    // lanes x 2 rows; IQ4_NL [17408, 5120] 20 x 2; Q8_0 [3584, 1024] one row
+    // (launch-bound either way).
+    nr = g.ttype == TT_Q8_0 ? 1 : (g.ttype == TT_Q4_K && g.tokens >= 6) ? 4 : 2;
+    team = g.ttype == TT_Q6_K ? 64 : g.ttype == TT_Q8_0 ? 32 : g.ttype == TT_Q4_K || g.ttype == TT_IQ4_NL ? 20 : 16;
   } else {
     if (nr <= 0) nr = 1;
     if (team <= 0) team = gemv_pick_team((g.rows + nr - 1) / nr, g.cols, kGemvTargetWaves);

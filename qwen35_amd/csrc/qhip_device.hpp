@@ -1037,4 +1037,117 @@ __host__ inline auto dispatch_type(int ttype, F&& f) -> decltype(f(std::integral
   }
 }
 
+
+// ---- a weight unit decoded once, multiplied by several tokens --------------------
+// The multi-token GEMV multiplies every weight unit it loads by up to eight
+// tokens.  Prep<TT>::prep(w) does the unit's token-independent decode once
+// (nibble and bit-plane unpacking, codebook lookups, scale unpacking, f16
+// scale conversion) and Prep<TT>::dotp(p, a) is what is left per token: the
+// dot4 products and the scaling, with the integers and the float expression of
+// Unit<TT>::dot unchanged (same results bit for bit).  The default keeps the
+// unit as loaded.
+template <int TT>
+struct Prep {
+  using P = typename Unit<TT>::W;
+  static __device__ __forceinline__ P prep(const typename Unit<TT>::W& w) { return w; }
+  static __device__ __forceinline__ float dotp(const P& p, const typename Unit<TT>::A& a) { return Unit<TT>::dot(p, a); }
+};
+
+template <>
+struct Prep<TT_Q4_K> {
+  struct P { uint32_t lo[8], hi[8]; int sc0, sc1, m0, m1; float d, dmin; };
+  static __device__ __forceinline__ P prep(const Unit<TT_Q4_K>::W& w) {
+    P p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p.lo[i] = w.q[i] & 0x0F0F0F0Fu;
+      p.hi[i] = (w.q[i] >> 4) & 0x0F0F0F0Fu;
+    }
+    const uint32_t S0 = w.hdr[1], S1 = w.hdr[2], S2 = w.hdr[3];
+    const bool upper = w.c >= 2;
+    const uint32_t scw = upper ? ((S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u)) : (S0 & 0x3F3F3F3Fu);
+    const uint32_t mnw = upper ? (((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u)) : (S1 & 0x3F3F3F3Fu);
+    const uint32_t sh = 16u * (uint32_t)(w.c & 1);
+    p.sc0 = (int)((scw >> sh) & 0xFFu);
+    p.sc1 = (int)((scw >> (sh + 8)) & 0xFFu);
+    p.m0 = (int)((mnw >> sh) & 0xFFu);
+    p.m1 = (int)((mnw >> (sh + 8)) & 0xFFu);
+    p.d = h2f(w.hdr[0]);
+    p.dmin = h2f(w.hdr[0] >> 16);
+    return p;
+  }
+  static __device__ __forceinline__ float dotp(const P& p, const ActQ8K& a) {
+    int lo = 0, hi = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo = dot4(p.lo[i], a.y[i], lo);
+      hi = dot4(p.hi[i], a.y[8 + i], hi);
+    }
+    const int isum = p.sc0 * lo + p.sc1 * hi;
+    const int summs = p.m0 * (a.bs[0] + a.bs[1]) + p.m1 * (a.bs[2] + a.bs[3]);
+    const float d = a.d * p.d;
+    const float dmin = a.d * p.dmin;
+    return d * (float)isum - dmin * (float)summs;
+  }
+};
+
+template <>
+struct Prep<TT_Q6_K> {
+  struct P { uint32_t v[16]; int sc[4]; float d; };  // v[4q + i]: 0..63 values of group q
+  static __device__ __forceinline__ P prep(const Unit<TT_Q6_K>::W& w) {
+    P p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t la = w.la[i], lb = w.lb[i], qh = w.qh[i];
+      p.v[i] = (la & 0x0F0F0F0Fu) | ((qh & 0x03030303u) << 4);
+      p.v[4 + i] = (lb & 0x0F0F0F0Fu) | ((qh << 2) & 0x30303030u);
+      p.v[8 + i] = ((la >> 4) & 0x0F0F0F0Fu) | (qh & 0x30303030u);
+      p.v[12 + i] = ((lb >> 4) & 0x0F0F0F0Fu) | ((qh >> 2) & 0x30303030u);
+    }
+    p.sc[0] = sext8(w.sc01);
+    p.sc[1] = sext8(w.sc01 >> 16);
+    p.sc[2] = sext8(w.sc23);
+    p.sc[3] = sext8(w.sc23 >> 16);
+    p.d = h2f(w.d);
+    return p;
+  }
+  static __device__ __forceinline__ float dotp(const P& p, const ActQ8K& a) {
+    int s[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s[q] = dot4(p.v[4 * q + i], a.y[4 * q + i], s[q]);
+    const int isum = p.sc[0] * (s[0] - 32 * a.bs[0]) + p.sc[1] * (s[1] - 32 * a.bs[1]) +
+                     p.sc[2] * (s[2] - 32 * a.bs[2]) + p.sc[3] * (s[3] - 32 * a.bs[3]);
+    return (p.d * a.d) * (float)isum;
+  }
+};
+
+template <>
+struct Prep<TT_IQ4_NL> {
+  struct P { uint32_t lo[8], hi[8]; float d0, d1; };  // [0..3] block 0, [4..7] block 1
+  static __device__ __forceinline__ P prep(const Unit<TT_IQ4_NL>::W& w) {
+    P p;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p.lo[i] = iq4_lo(w.q[i]);
+      p.hi[i] = iq4_hi(w.q[i]);
+    }
+    p.d0 = h2f(w.d0);
+    p.d1 = h2f(w.d1);
+    return p;
+  }
+  static __device__ __forceinline__ float dotp(const P& p, const ActPair& a) {
+    int s0 = 0, s1 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s0 = dot4(p.lo[i], a.q[i], s0);
+      s0 = dot4(p.hi[i], a.q[4 + i], s0);
+      s1 = dot4(p.lo[4 + i], a.q[8 + i], s1);
+      s1 = dot4(p.hi[4 + i], a.q[12 + i], s1);
+    }
+    return (p.d0 * a.d0) * (float)s0 + (p.d1 * a.d1) * (float)s1;
+  }
+};
+
 }  // namespace qhip

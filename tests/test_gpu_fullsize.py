@@ -204,7 +204,7 @@ def test_backend_image_budget_and_opt_out(gpu, oracle):
     """A backend whose device budget cannot hold the Q6_K image, or with
     images off, runs the tile MMQ on the GGUF bytes: same parity, no image
     placed; prepare_linear builds the image at load time when it fits."""
-    tt, rows, cols, T = po.TT_Q6_K, 4096, 4608, 40
+    tt, rows, cols, T = po.TT_Q6_K, 4096, 4608, 128  # a prefill long enough for the image path
     w = synth.make_weight(tt, rows, cols, seed=3, tag=tt)
     x = synth.make_act(cols, T, seed=3)
     want = oracle.matvec(tt, w, x, nthreads=THREADS)
@@ -242,7 +242,7 @@ def test_backend_wrapped_memory_reused_after_free(gpu, oracle):
     """wrap_linear + free_linear, then another weight of the same shape in the
     same device memory: the second prefill must not meet the first weight's
     image."""
-    tt, rows, cols, T = po.TT_Q6_K, 256, 2304, 24
+    tt, rows, cols, T = po.TT_Q6_K, 256, 2304, 128  # long enough for the image path
     wa = synth.make_weight(tt, rows, cols, seed=11, tag=tt)
     wb = synth.make_weight(tt, rows, cols, seed=12, tag=tt)
     x = synth.make_act(cols, T, seed=11)

@@ -338,7 +338,7 @@ def test_mmq_image_rejects_other_types(gpu):
 def test_backend_prefill_batch(gpu, oracle, tt):
     """matvecBatchK above the crossover: the MMQ image for Q6_K, the tile MMQ
     for Q4_K; the second call reuses the cached image."""
-    rows, cols, k = 130, 2560 if tt == po.TT_Q4_K else 2304, 80
+    rows, cols, k = 130, 2560 if tt == po.TT_Q4_K else 2304, 80 if tt == po.TT_Q4_K else 130
     w = synth.make_weight(tt, rows, cols, seed=31, tag=tt)
     x = synth.make_act(cols, k, seed=31)
     be = ops.Backend(0)
