@@ -13,7 +13,9 @@ from pathlib import Path
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-ORACLE_SO = HERE / "liboracle.so"
+# QWEN35_ORACLE_SO names another build of the same restatement (the sanitized
+# one, oracle/_san/liboracle.so)
+ORACLE_SO = Path(os.environ.get("QWEN35_ORACLE_SO") or HERE / "liboracle.so")
 REF_SO = HERE / "_ref" / "libqref.so"
 
 TT_Q8_0, TT_Q4_K, TT_Q6_K, TT_IQ4_NL = 8, 12, 14, 20

@@ -432,6 +432,38 @@ def test_iq3_dot_equals_scaled_dequant(oracle, tt):
         assert np.allclose(got, want, rtol=2e-6, atol=0)
 
 
+def test_q2_k_dequant_equals_block_ints(oracle):
+    """Ties the Q2_K dequant (quant_dequant.zig:892-919) to the block integers
+    pinned bit for bit against the reference build (kernels256.c:232-257):
+    each value dequantizes to d * (scales[g] & 15) * q - dmin * (scales[g] >> 4),
+    so with d = 1, dmin = 0 the dequantized row dotted with integer activations
+    (Q8_K scale exactly 1) is isum, and with d = 0, dmin = 1 it is -summs.  A
+    value read from the wrong byte, shift or 16-value group, a scale nibble
+    swapped, or the mins term's sign flipped moves one of the two sums; with
+    d = 2^-3, dmin = 2^-5 both terms come back exactly."""
+    rng = np.random.default_rng(11)
+    cols, nrows = 1024, 6
+    nb = cols // 256
+    w = rng.integers(0, 256, (nrows, nb, 84), dtype=np.uint8)
+    x = rng.integers(-127, 128, (3, cols)).astype(np.float32)
+    x[:, ::256] = 127.0
+    act = oracle.quantize_act(po.TT_Q2_K, x)
+    for b in range(nb):
+        assert act[0, 292 * b:292 * b + 4].view(np.float32)[0] == 1.0
+    h = {v: np.array([v], np.float16).view(np.uint8) for v in (0.0, 1.0, 0.125, 0.03125)}
+    for d, dmin in ((1.0, 0.0), (0.0, 1.0), (0.125, 0.03125)):
+        w[:, :, 80:82] = h[d]
+        w[:, :, 82:84] = h[dmin]
+        rows = w.reshape(nrows, -1)
+        ints = oracle.block_ints(po.TT_Q2_K, rows, act, cols).reshape(3, nrows, nb, 2).astype(np.float64)
+        for r in range(nrows):
+            deq = oracle.dequant_row(po.TT_Q2_K, rows[r], cols).astype(np.float64).reshape(nb, 256)
+            for t in range(3):
+                got = (deq * x[t].reshape(nb, 256)).sum(1)
+                want = d * ints[t, r, :, 0] - dmin * ints[t, r, :, 1]
+                assert np.array_equal(got, want), (d, dmin, r, t)
+
+
 # ---- the host-ISA tiers of the restatement (oracle_simd.c, the CPU baseline) --
 
 SIMD_CASES = [(po.TT_IQ4_NL, 2560), (po.TT_Q8_0, 1024), (po.TT_Q4_K, 2560), (po.TT_Q6_K, 9728)]
