@@ -241,6 +241,36 @@ int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_ou
                               int tokens, int ttype, int tile_tokens, int tile_rows, void *d_work,
                               long work_bytes, void *stream);
 
+/* GEMV weight image (no reference counterpart; the reference's CUDA GEMV reads
+ * the GGUF blocks as they are, mmvq.cu).  For the 32-value 4-bit formats
+ * (IQ4_NL, Q4_0), whose 18-byte blocks leave every 16-byte piece of a row
+ * misaligned: the same bytes per row (36 per 64 values), reordered so that
+ * each 16-byte load of the GEMV is aligned and the lanes of a team read one
+ * contiguous span -- 16 quant bytes per block in the order the team walks
+ * the row, then the f16 scales, each lane's adjacent.  The order depends on
+ * the row width only (the team width and pass count the library takes for
+ * it); widths 1024, 1280, 2048, 2560, 3072, 3840, 4096, 5120, 6144 and 8192
+ * have one.  The activation of the image GEMV is quantized
+ * into the matching split layout (the same Q8_0 values and scales as
+ * qhip_launch_quantize_act; scales stored as f32): 72 bytes per 64 values.
+ *   qhip_gemv_image_bytes      image size (rows x GGUF row bytes); -1 for
+ *                              other types or widths
+ *   qhip_gemv_image_act_bytes  bytes of `tokens` split activation rows, or -1
+ *   qhip_launch_gemv_prepare   build it from GGUF bytes (d_w 4-byte aligned,
+ *                              d_image 16-byte aligned, not d_w)
+ *   qhip_launch_quantize_act_image  f32 x[tokens][cols] -> split activation
+ *                              (d_xa 16-byte aligned)
+ *   qhip_launch_mul_mat_vec_image   out[r] = W[r] . x for one token from the
+ *     image and the split activation: the integers of the GGUF-layout GEMV,
+ *     floats within its tolerance.  rows_per_lane 1 or 2 (0 = the library's
+ *     choice). */
+long qhip_gemv_image_bytes(int ttype, int rows, int cols);
+long qhip_gemv_image_act_bytes(int ttype, int cols, int tokens);
+int qhip_launch_gemv_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
+int qhip_launch_quantize_act_image(int ttype, const float *d_x, void *d_xa, int cols, int tokens, void *stream);
+int qhip_launch_mul_mat_vec_image(const void *d_image, const void *d_xa, float *d_out, int rows, int cols,
+                                  int ttype, int rows_per_lane, void *stream);
+
 /* ---- ragged prefill (no reference counterpart: the reference prefills one
  * sequence per chunk, src/engine.zig:1371) -------------------------------------
  * Sequence i owns packed tokens [offsets[i], offsets[i+1]); offsets has
@@ -303,19 +333,26 @@ int qhip_backend_load_linear(qhip_backend *be, int ttype, int rows, int cols,
                              const void *host_data, qhip_linear *out);
 /* Adopt weights already resident on this device (no copy, not freed).  Call
  * qhip_backend_free_linear before the caller releases or reuses that memory:
- * it drops what the backend derived from the bytes (the MMQ image). */
+ * it drops what the backend derived from the bytes (the MMQ and GEMV
+ * images). */
 int qhip_backend_wrap_linear(qhip_backend *be, int ttype, int rows, int cols, const void *d_data,
                              qhip_linear *out);
 void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
-/* Build what the prefill of this weight uses beyond its GGUF bytes now, at
- * load time, instead of inside the first matvec_batch_k: the MMQ image of a
- * Q6_K weight (qhip_launch_mmq_prepare, 2.5x the GGUF bytes).  0 = built or
- * nothing to build; QHIP_DECLINE = not built (images off, or past the memory
- * budget): the prefill then runs the tile MMQ on the GGUF bytes.  No
- * reference counterpart (its CUDA MMQ decodes GGUF blocks in every launch). */
+/* Build what this weight's products use beyond its GGUF bytes now, at load
+ * time, instead of inside the first matvec: the GEMV image of an IQ4_NL /
+ * Q4_0 weight large enough for the decode matvec to read it
+ * (qhip_launch_gemv_prepare, the GGUF bytes once more; built in load order,
+ * so adjacent weights get adjacent images and matvecPair stays one launch),
+ * and the MMQ image of a Q6_K weight (qhip_launch_mmq_prepare, 2.5x the GGUF
+ * bytes).  0 = built or nothing to build; QHIP_DECLINE = not built (images
+ * off, or past the memory budget): the products then read the GGUF bytes.
+ * No reference counterpart (its CUDA kernels decode the GGUF blocks in every
+ * launch). */
 int qhip_backend_prepare_linear(qhip_backend *be, const qhip_linear *w);
 /* MMQ images on (default) or off; off, matvec_batch_k never builds one. */
 int qhip_backend_set_mmq_images(qhip_backend *be, int on);
+/* GEMV images on (default) or off; off, matvec never builds or reads one. */
+int qhip_backend_set_gemv_images(qhip_backend *be, int on);
 /* Cap on the device bytes this backend places (uploaded weights, MMQ images,
  * scratch, workspaces, allocBuf regions); 0 = no cap (the default).
  * QWEN35_CUDA_MAX_DEV_MIB of src/backend_cuda.zig:1754-1760 as an argument:

@@ -60,6 +60,11 @@ SIGNATURES = {
     "qhip_launch_mmq_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "qhip_launch_mul_mat_image": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                           c_int, c_void_p, c_long, c_void_p]),
+    "qhip_gemv_image_bytes": (c_long, [c_int, c_int, c_int]),
+    "qhip_gemv_image_act_bytes": (c_long, [c_int, c_int, c_int]),
+    "qhip_launch_gemv_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "qhip_launch_quantize_act_image": (c_int, [c_int, c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "qhip_launch_mul_mat_vec_image": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "qhip_mul_mat_work_bytes": (c_long, [c_int, c_int, c_int, c_int]),
     "qhip_launch_mul_mat_work": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                          c_void_p, c_long, c_void_p]),
@@ -82,6 +87,7 @@ SIGNATURES = {
     "qhip_backend_free_linear": (None, [c_void_p, ctypes.POINTER(QhipLinear)]),
     "qhip_backend_prepare_linear": (c_int, [c_void_p, ctypes.POINTER(QhipLinear)]),
     "qhip_backend_set_mmq_images": (c_int, [c_void_p, c_int]),
+    "qhip_backend_set_gemv_images": (c_int, [c_void_p, c_int]),
     "qhip_backend_set_mem_budget": (c_int, [c_void_p, c_size_t]),
     "qhip_backend_mem_placed": (c_size_t, [c_void_p]),
     "qhip_backend_alloc_scratch": (c_int, [c_void_p, c_int]),

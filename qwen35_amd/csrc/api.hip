@@ -441,6 +441,46 @@ int qhip_launch_mul_mat_image(const void* d_image, const void* d_xq, float* d_ou
   return (int)launch_mmq_image(g, tile_tokens, tile_rows, d_work, d_work ? work_bytes : 0, S(stream));
 }
 
+long qhip_gemv_image_bytes(int ttype, int rows, int cols) {
+  const long rb = weight_row_bytes(ttype, cols);
+  if (rb < 0 || rows < 0 || !gemv_image_format(ttype) || !gemv_image_width(cols)) return -1;
+  return (long)rows * rb;
+}
+
+long qhip_gemv_image_act_bytes(int ttype, int cols, int tokens) {
+  if (weight_row_bytes(ttype, cols) < 0 || !gemv_image_format(ttype) || !gemv_image_width(cols) || tokens < 0)
+    return -1;
+  return gemv_image_act_bytes(cols, tokens);
+}
+
+int qhip_launch_gemv_prepare(int ttype, const void* d_w, int rows, int cols, void* d_image, void* stream) {
+  const long rb = weight_row_bytes(ttype, cols);
+  if (qhip_gemv_image_bytes(ttype, rows, cols) < 0) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!d_w || !d_image || !aligned4(d_w) || ((uintptr_t)d_image & 15u) || d_image == d_w)
+    return (int)hipErrorInvalidValue;
+  return (int)launch_gemv_image_prepare(d_w, rb, rows, cols, d_image, S(stream));
+}
+
+int qhip_launch_quantize_act_image(int ttype, const float* d_x, void* d_xa, int cols, int tokens, void* stream) {
+  if (qhip_gemv_image_act_bytes(ttype, cols, tokens) < 0 || tokens > 65535) return (int)hipErrorInvalidValue;
+  if (tokens == 0) return 0;
+  if (!d_x || !d_xa || !aligned4(d_x) || ((uintptr_t)d_xa & 15u)) return (int)hipErrorInvalidValue;
+  return (int)launch_quantize_act_image(d_x, d_xa, cols, tokens, cols, S(stream));
+}
+
+int qhip_launch_mul_mat_vec_image(const void* d_image, const void* d_xa, float* d_out, int rows, int cols,
+                                  int ttype, int rows_per_lane, void* stream) {
+  const long rb = weight_row_bytes(ttype, cols);
+  if (qhip_gemv_image_bytes(ttype, rows, cols) < 0) return (int)hipErrorInvalidValue;
+  if (rows_per_lane < 0 || rows_per_lane > 2) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!d_image || !d_xa || !d_out || ((uintptr_t)d_image & 15u) || ((uintptr_t)d_xa & 15u))
+    return (int)hipErrorInvalidValue;
+  const GemvArgs g{ttype, d_image, d_xa, d_out, rows, cols, 1, rb, gemv_image_act_bytes(cols, 1)};
+  return (int)launch_gemv_image(g, rows_per_lane, S(stream));
+}
+
 int qhip_launch_mul_mat_vec_tile(const void* d_w, const void* d_xq, float* d_out, int rows, int cols,
                                  int tokens, int ttype, void* stream) {
   return qhip_launch_mul_mat(d_w, d_xq, d_out, rows, cols, tokens, ttype, QHIP_PATH_MMQ, stream);

@@ -59,6 +59,21 @@ struct qhip_backend {
   };
   std::map<ImageKey, Image> images;
   bool images_on = true;
+  // GEMV images of the 32-value 4-bit formats (gemv_image.hip), keyed by the
+  // device address of the first GGUF row they mirror.  Their bytes come from
+  // a bump arena of their own, so images built in load order are adjacent
+  // exactly when their weights are, and an adjacent matvecPair stays one
+  // launch.  free_linear drops the entries over the weight's rows; the arena
+  // memory is returned at destroy, as the weights' is.
+  struct GImage {
+    uint8_t* img;
+    int ttype, rows, cols;
+    long row_bytes;
+  };
+  std::map<const uint8_t*, GImage> gimages;
+  struct Chunk2 { uint8_t* base; size_t size, used; };
+  std::vector<Chunk2> img_arena;
+  bool gemv_images_on = true;
   // Device-memory budget (QWEN35_CUDA_MAX_DEV_MIB, backend_cuda.zig:1754-1760,
   // as an argument): bytes this backend places on the device -- uploaded
   // weights, MMQ images, scratch, workspaces, allocBuf regions.  0 = no cap.
@@ -200,6 +215,86 @@ static size_t act_bytes_for(int cols, int k) {
   return c / 256 * 292 * (size_t)k + 256;
 }
 
+// memo family of the split activation the GEMV image reads (the others are
+// the activation block sizes, 32 and 256)
+static constexpr int kFamSplit = 1 << 16;
+
+static hipError_t img_arena_alloc(qhip_backend* be, size_t bytes, uint8_t** out) {
+  bytes = (bytes + kAlign - 1) / kAlign * kAlign;
+  if (over_budget(be, bytes)) return hipErrorOutOfMemory;
+  if (!be->img_arena.empty()) {
+    auto& c = be->img_arena.back();
+    if (c.size - c.used >= bytes) {
+      *out = c.base + c.used;
+      c.used += bytes;
+      be->placed += bytes;
+      return hipSuccess;
+    }
+  }
+  size_t sz = bytes > kArenaChunk ? bytes : kArenaChunk;
+  if (be->budget && sz > be->budget - be->placed) sz = bytes;
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, sz);
+  if (e != hipSuccess) return e;
+  be->img_arena.push_back({(uint8_t*)p, sz, bytes});
+  be->placed += bytes;
+  *out = (uint8_t*)p;
+  return hipSuccess;
+}
+
+// The image bytes of GGUF rows [wdev, wdev + rows * row_bytes), when images
+// cover them contiguously (one image, or adjacent images of adjacent
+// weights); nullptr otherwise.
+static uint8_t* gimage_lookup(const qhip_backend* be, const void* wdev, int ttype, int rows, int cols,
+                              long row_bytes) {
+  const uint8_t* p = (const uint8_t*)wdev;
+  long need = rows;
+  uint8_t* first = nullptr;
+  uint8_t* expect = nullptr;
+  while (need > 0) {
+    auto it = be->gimages.upper_bound(p);
+    if (it == be->gimages.begin()) return nullptr;
+    --it;
+    const qhip_backend::GImage& g = it->second;
+    if (g.ttype != ttype || g.cols != cols || g.row_bytes != row_bytes) return nullptr;
+    const long off = (long)(p - it->first);
+    if (off % row_bytes || off / row_bytes >= g.rows) return nullptr;
+    uint8_t* ip = g.img + off;
+    if (first == nullptr) first = ip;
+    else if (ip != expect) return nullptr;
+    const long take = need < g.rows - off / row_bytes ? need : g.rows - off / row_bytes;
+    need -= take;
+    p += take * row_bytes;
+    expect = ip + take * row_bytes;
+  }
+  return first;
+}
+
+// Build the image of rows [wdev, wdev + rows * row_bytes) when images are on,
+// the budget allows it and the stream is not being captured (building
+// allocates); nullptr = run the GGUF-layout path.
+static uint8_t* gimage_for(qhip_backend* be, const void* wdev, int ttype, int rows, int cols, long row_bytes,
+                           hipError_t* err) {
+  *err = hipSuccess;
+  if (uint8_t* hit = gimage_lookup(be, wdev, ttype, rows, cols, row_bytes)) return hit;
+  if (!be->gemv_images_on || capturing(be->stream)) return nullptr;
+  const long n = qhip_gemv_image_bytes(ttype, rows, cols);
+  if (n <= 0 || over_budget(be, (size_t)n)) return nullptr;
+  uint8_t* img = nullptr;
+  hipError_t e = img_arena_alloc(be, (size_t)n, &img);
+  if (e != hipSuccess) {
+    if (e != hipErrorOutOfMemory) *err = e;
+    return nullptr;
+  }
+  const int rc = qhip_launch_gemv_prepare(ttype, wdev, rows, cols, img, be->stream);
+  if (rc) {
+    *err = (hipError_t)rc;
+    return nullptr;
+  }
+  be->gimages[(const uint8_t*)wdev] = qhip_backend::GImage{img, ttype, rows, cols, row_bytes};
+  return img;
+}
+
 static int report(const char* what, hipError_t e) {
   if (e != hipSuccess && (int)e != QHIP_DECLINE)
     fprintf(stderr, "qwen35_hip: %s failed: %s\n", what, hipGetErrorString(e));
@@ -218,6 +313,36 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   // the activation family: Q8_0 rows for 32-value weight blocks, Q8_K for
   // 256-value super-blocks (backend_cpu.zig:42-50 actFamily)
   const int fam = qhip_quant_act_block_elems(ttype);
+  if (k == 1 && be->gemv_images_on) {
+    // the 32-value 4-bit formats on larger matrices: split quantize + GEMV
+    // from the weight's GEMV image
+    const GemvArgs g1{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
+    if (gemv_image_preferred(g1)) {
+      hipError_t ei;
+      uint8_t* img = gimage_for(be, wdev, ttype, rows, cols, row_bytes, &ei);
+      if (ei != hipSuccess) return report("GEMV image", ei);
+      if (img) {
+        const bool hs = be->memo_on && be->memo_src == x && be->memo_cols == cols && be->memo_k == 1 &&
+                        be->memo_fam == kFamSplit && be->act;
+        if (be->memo_on) (hs ? be->memo_hits : be->memo_misses)++;
+        if (!hs) {
+          const hipError_t ea = ensure_act(be, act_bytes_for(cols, 1));
+          if (ea != hipSuccess) return report("activation scratch", ea);
+          memo_clear(be);
+          const int rq = qhip_launch_quantize_act_image(ttype, x, be->act, cols, 1, be->stream);
+          if (rq) return report("quantize", (hipError_t)rq);
+          if (be->memo_on) {
+            be->memo_src = x;
+            be->memo_cols = cols;
+            be->memo_k = 1;
+            be->memo_fam = kFamSplit;
+          }
+        }
+        return report("matvec", (hipError_t)qhip_launch_mul_mat_vec_image(img, be->act, out, rows, cols, ttype, 0,
+                                                                           be->stream));
+      }
+    }
+  }
   const bool hit = be->memo_on && be->memo_src == x && be->memo_cols == cols && be->memo_k == k &&
                    be->memo_fam == fam && be->act;
   if (be->memo_on) (hit ? be->memo_hits : be->memo_misses)++;
@@ -316,6 +441,7 @@ void qhip_backend_destroy(qhip_backend* be) {
   qhip_backend_free_scratch(be);
   for (auto& kv : be->images) (void)hipFree(kv.second.p);
   for (auto& c : be->arena) (void)hipFree(c.base);
+  for (auto& c : be->img_arena) (void)hipFree(c.base);
   delete be;
 }
 
@@ -358,6 +484,14 @@ void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
         ++it;
       }
     }
+    const uint8_t* lo = (const uint8_t*)w->dev;
+    const uint8_t* hi = lo + (size_t)w->rows * (size_t)w->row_bytes;
+    for (auto it = be->gimages.begin(); it != be->gimages.end();) {
+      const uint8_t* a = it->first;
+      const uint8_t* b = a + (size_t)it->second.rows * (size_t)it->second.row_bytes;
+      if (a < hi && lo < b) it = be->gimages.erase(it);
+      else ++it;
+    }
   }
   if (w) *w = qhip_linear{nullptr, 0, 0, 0, 0};
 }
@@ -365,9 +499,19 @@ void qhip_backend_free_linear(qhip_backend* be, qhip_linear* w) {
 int qhip_backend_prepare_linear(qhip_backend* be, const qhip_linear* w) {
   if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
   // a long prefill: whether any token count would use an image for this weight
+  const GemvArgs g1{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 1, w->row_bytes,
+                    qhip_act_row_bytes(w->ttype, w->cols)};
+  if (be->gemv_images_on && gemv_image_preferred(g1)) {
+    // a decode matvec: the GEMV image
+    if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;
+    hipError_t e;
+    const uint8_t* img = gimage_for(be, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, &e);
+    if (e != hipSuccess) return report("GEMV image", e);
+    if (!img) return QHIP_DECLINE;
+  }
   const GemvArgs g{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 4096, w->row_bytes,
                    qhip_act_row_bytes(w->ttype, w->cols)};
-  if (!mmq_image_preferred(g)) return 0;  // no image serves this weight
+  if (!mmq_image_preferred(g)) return 0;  // no MMQ image serves this weight
   if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;
   hipError_t e;
   void* img = image_for(be, w->dev, w->ttype, w->rows, w->cols, &e);
@@ -378,6 +522,13 @@ int qhip_backend_prepare_linear(qhip_backend* be, const qhip_linear* w) {
 int qhip_backend_set_mmq_images(qhip_backend* be, int on) {
   if (!be) return (int)hipErrorInvalidValue;
   be->images_on = on != 0;
+  return 0;
+}
+
+int qhip_backend_set_gemv_images(qhip_backend* be, int on) {
+  if (!be) return (int)hipErrorInvalidValue;
+  be->gemv_images_on = on != 0;
+  memo_clear(be);
   return 0;
 }
 

@@ -70,5 +70,17 @@ hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows
 // g.w = the image; bt x br tile (0 = default; splits K as launch_mmq)
 hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s);
 long mmq_image_work_bytes(const GemvArgs& g);
+// GEMV weight image of the 32-value 4-bit formats (gemv_image.hip): the same
+// bytes per row, quant bytes 16-byte aligned in unit order, scales apart
+bool gemv_image_format(int ttype);
+bool gemv_image_width(int cols);  // a team width and pass count exist for this row width
+long gemv_image_act_bytes(int cols, int tokens);
+hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s);
+hipError_t launch_quantize_act_image(const float* x, void* out, int cols, int tokens, long x_stride, hipStream_t s);
+// g.w = the image, g.xq = one token's split activation; nr rows per team (1,
+// 2; 0 = pick)
+hipError_t launch_gemv_image(const GemvArgs& g, int nr, hipStream_t s);
+// whether quantize + image GEMV beats the GGUF-layout launches (measured rule)
+bool gemv_image_preferred(const GemvArgs& g);
 
 }  // namespace qhip

@@ -202,6 +202,38 @@ def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, co
     return out
 
 
+def gemv_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """The GEMV weight image of an IQ4_NL / Q4_0 weight (same bytes per row, quant bytes 16-byte aligned)."""
+    n = load().qhip_gemv_image_bytes(ttype, rows, cols)
+    if n < 0:
+        raise ValueError(f"no GEMV image for type {ttype} at cols={cols}")
+    img = torch.empty(max(n, 16), dtype=torch.uint8, device=w.device)
+    check("gemv_prepare", load().qhip_launch_gemv_prepare(ttype, _p(w), rows, cols, _p(img), _stream()))
+    return img
+
+
+def quantize_act_image(ttype: int, x: torch.Tensor) -> torch.Tensor:
+    """f32 [tokens, cols] -> the split Q8_0 activation the GEMV image reads."""
+    x = x.contiguous()
+    cols = x.shape[-1]
+    tokens = x.numel() // cols
+    n = load().qhip_gemv_image_act_bytes(ttype, cols, tokens)
+    if n < 0:
+        raise ValueError(f"no split activation for type {ttype} at cols={cols}")
+    out = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device)
+    check("quantize_act_image", load().qhip_launch_quantize_act_image(ttype, _p(x), _p(out), cols, tokens,
+                                                                      _stream()))
+    return out
+
+
+def mul_mat_vec_image(ttype: int, img: torch.Tensor, xa: torch.Tensor, rows: int, cols: int,
+                      rows_per_lane: int = 0) -> torch.Tensor:
+    out = torch.empty(rows, dtype=torch.float32, device=img.device)
+    check("mul_mat_vec_image", load().qhip_launch_mul_mat_vec_image(
+        _p(img), _p(xa), _p(out), rows, cols, ttype, rows_per_lane, _stream()))
+    return out
+
+
 def block_ints(ttype: int, w: torch.Tensor, xq: torch.Tensor, rows: int, cols: int,
                tokens: int) -> torch.Tensor:
     be = _GEOM[ttype][0]
@@ -289,7 +321,7 @@ class Backend:
         self.lib.qhip_backend_free_linear(self._h, ctypes.byref(w))
 
     def prepare_linear(self, w: QhipLinear) -> int:
-        """Build the weight's MMQ image now: 0 built / nothing to build, -1 not built."""
+        """Build the weight's GEMV / MMQ image now: 0 built / nothing to build, -1 not built."""
         rc = self.lib.qhip_backend_prepare_linear(self._h, ctypes.byref(w))
         if rc not in (0, -1):
             check("prepare_linear", rc)
@@ -297,6 +329,9 @@ class Backend:
 
     def set_mmq_images(self, on: bool) -> None:
         check("set_mmq_images", self.lib.qhip_backend_set_mmq_images(self._h, int(bool(on))))
+
+    def set_gemv_images(self, on: bool) -> None:
+        check("set_gemv_images", self.lib.qhip_backend_set_gemv_images(self._h, int(bool(on))))
 
     def set_mem_budget(self, nbytes: int) -> None:
         check("set_mem_budget", self.lib.qhip_backend_set_mem_budget(self._h, nbytes))

@@ -110,7 +110,25 @@ def test_invalid_arguments_rejected_before_launch(lib):
                                                       None) == INVALID
     assert lib.qhip_launch_quantize_mul_mat_vec_split(p, p, None, p, 16, 9728, 14, 300, 0, 0, p, need,
                                                       None) == INVALID
+    # GEMV image: formats without one, widths not a multiple of 64, alignment
+    assert lib.qhip_gemv_image_bytes(12, 16, 2560) == -1
+    assert lib.qhip_gemv_image_bytes(20, 16, 96) == -1
+    assert lib.qhip_gemv_image_bytes(20, 16, 2560) == 16 * 1440
+    assert lib.qhip_gemv_image_act_bytes(20, 2560, 2) == 2 * 72 * 40
+    assert lib.qhip_gemv_image_act_bytes(8, 2560, 1) == -1
+    assert lib.qhip_launch_gemv_prepare(12, p, 16, 2560, p, None) == INVALID
+    assert lib.qhip_launch_gemv_prepare(20, p, 16, 2560, ctypes.c_void_p(0x1008), None) == INVALID
+    assert lib.qhip_launch_gemv_prepare(20, p, 16, 2560, p, None) == INVALID  # in place
+    assert lib.qhip_launch_quantize_act_image(20, p, ctypes.c_void_p(0x1004), 2560, 1, None) == INVALID
+    assert lib.qhip_launch_quantize_act_image(20, p, p, 96, 1, None) == INVALID
+    assert lib.qhip_gemv_image_bytes(20, 16, 64) == -1      # no team width for one unit
+    assert lib.qhip_gemv_image_bytes(20, 16, 9728) == -1    # long rows: the GGUF-layout kernels
+    assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 2560, 20, 3, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec_image(p, p, None, 16, 2560, 20, 0, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 2560, 14, 0, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 9728, 20, 0, None) == INVALID
     # backend with bad handle
+    assert lib.qhip_backend_set_gemv_images(None, 1) == INVALID
     assert lib.qhip_backend_matvec(None, p, None, p) == INVALID
     assert lib.qhip_backend_alloc_scratch(None, 1024) == INVALID
 
