@@ -75,14 +75,15 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
 
 // Token count from which the MMQ tiles beat the weight-streaming GEMV, both
 // at their defaults (the MMQ with the split-K workspace the Exec mirror
-// passes).  Measured on MI355X: Q4_K [17408, 5120] GEMV 22.6 / MMQ 24.0 us at
-// 5 tokens, 25.1 / 24.0 at 6; Q6_K [5120, 17408] 35.1 / 40.0 at 6, 42.5 /
+// passes).  Measured on MI355X: Q4_K [17408, 5120] (the weights-direct MMQ)
+// GEMV 18.7 / MMQ 19.7 us at 4 tokens, 22.5 / 19.7 at 5; Q6_K [5120, 17408] 35.1 / 40.0 at 6, 42.5 /
 // 40.2 at 8; IQ4_NL [17408, 5120] 30.8 / 34.7 at 8, 46.4 / 34.7 at 12;
 // Q8_0 [3584, 1024] 7.8 / 8.7 at 16; Q3_K / Q2_K [17408, 5120] 48.6 / 29.6
 // and 38.6 / 26.8 us at 8 (Q2_K 23.3 / 26.5 at 4).
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
-    case TT_Q4_K: case TT_Q5_K: return 6;
+    case TT_Q4_K: return 5;
+    case TT_Q5_K: return 6;
     case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: case TT_Q3_K: case TT_Q2_K: return 8;
     case TT_IQ4_NL: case TT_Q4_0: case TT_Q4_1: return 10;
     default: return 24;

@@ -1270,49 +1270,55 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
   }
 }
 
-// ---- weights-direct MMQ (Q4_K, 64 tokens x 128 rows) --------------------------------------
+// ---- weights-direct MMQ (Q4_K, 32 or 64 tokens x 128 rows) -----------------------------------
 // Each wave owns 32 weight rows and reads their Q4_K bytes from global memory
 // straight into MFMA B fragments, with no LDS image of the weights: lane l
 // holds row l%32, and each 16-byte qs piece gives it values 16*(l/32)..+15 of
 // two sub-blocks (low / high nibbles), scaled by the split sub-block scale as
-// in k_mmq.  The workgroup's 64 tokens of Q8_K activation are copied into LDS
-// by global_load_lds (DMA, no registers), double-buffered: chunk c+1 (one
-// super-block) lands while chunk c is multiplied.  LDS token row: qs[256] |
-// bsums[16] | d, 304 bytes, so 16-byte fragment reads of 32 consecutive
-// tokens fall 12 banks apart (conflict-free).  Measured on MI355X, config 5
-// Q4_K [17408, 5120]: T = 512 146-150 us against 184 us for the 64 x 64 tile
-// kernel in the same harness, T = 128 56 against 62 us; it loses below 128
-// tokens (no split-K), where the tile kernel stays the default.
-constexpr int kWdRow = 304, kWdPieces = 19, kWdBT = 64, kWdBR = 128;
-constexpr int kWdStage = kWdBT * kWdRow;
-constexpr int kWdDma = (kWdBT * kWdPieces + 255) / 256;  // DMA pieces per thread
+// in k_mmq.  The workgroup's BT = 32 NA tokens of Q8_K activation are copied
+// into LDS by global_load_lds (DMA, no registers), double-buffered: chunk c+1
+// (one super-block) lands while chunk c is multiplied.  LDS token row: qs[256]
+// | bsums[16] | d, 304 bytes, so 16-byte fragment reads of 32 consecutive
+// tokens fall 12 banks apart (conflict-free).  K may be cut into ksplit slices
+// of cps super-blocks (small grids: few tokens), the partial tiles added in
+// slice order by the tile's last workgroup (mmq_write_tile).  Measured on
+// MI355X, config 5 Q4_K [17408, 5120]: T = 512 146-150 us against 184 us for
+// the 64 x 64 tile kernel in the same harness, T = 128 56 against 62 us;
+// with the split, T = 8 / 16 / 32 / 64 20.3 / 20.8 / 21.6 / 32.3 us against
+// 24.1 / 24.1 / 24.2 / 32.5 for the tile kernel's split launch.
+constexpr int kWdRow = 304, kWdPieces = 19, kWdBR = 128;
 
 __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
   return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
 }
 
+template <int NA>
 __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                      float* __restrict__ Y, int rows, int tokens, long row_bytes,
-                                                     long act_bytes, int nsb, int ntile_t) {
-  constexpr int NA = 2;
-  __shared__ __attribute__((aligned(16))) uint8_t act[2][kWdStage];
+                                                     long act_bytes, int nsb, int ntile_t, int ksplit, int cps,
+                                                     float* __restrict__ part, unsigned* __restrict__ cnt) {
+  constexpr int BT = 32 * NA, STAGE = BT * kWdRow, NDMA = (BT * kWdPieces + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint8_t act[2][STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
   const int G = gridDim.x;
   int g = blockIdx.x;
   if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
-  const int r0 = (g / ntile_t) * kWdBR, t0 = (g % ntile_t) * kWdBT;
+  const int ks = g % ksplit;
+  g /= ksplit;
+  const int r0 = (g / ntile_t) * kWdBR, t0 = (g % ntile_t) * BT;
   const int row = r0 + 32 * wv + li;
   const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
 
   // DMA piece p = 64*(4i + wave) + lane of the stage: token p/19, 16-byte
   // slot p%19 (16 qs slots, two bsum slots, one slot holding d); tokens past
   // the end re-read the last one
-  long goff[kWdDma];
-  bool gon[kWdDma];
+  long goff[NDMA];
+  bool gon[NDMA];
 #pragma unroll
-  for (int i = 0; i < kWdDma; ++i) {
+  for (int i = 0; i < NDMA; ++i) {
     const int p = 64 * (4 * i + wv) + lane;
-    gon[i] = p < kWdBT * kWdPieces;
+    gon[i] = p < BT * kWdPieces;
     const int tp = p / kWdPieces, j = p - tp * kWdPieces;
     int tok = t0 + tp;
     tok = tok < tokens ? tok : tokens - 1;
@@ -1320,8 +1326,8 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
   }
   auto issue_act = [&](int sb, int buf) {
 #pragma unroll
-    for (int i = 0; i < kWdDma; ++i) {
-      if (4 * i + wv < (kWdBT * kWdPieces + 63) / 64 && gon[i])
+    for (int i = 0; i < NDMA; ++i) {
+      if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
         __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
                                          (__attribute__((address_space(3))) void*)(&act[buf][0] + 1024 * (4 * i + wv)),
                                          16, 0, 0);
@@ -1335,22 +1341,22 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
     for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
   };
 
-  f32x16 acc[NA];
+  f32x16 acc[NA][1];
 #pragma unroll
   for (int a = 0; a < NA; ++a)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
+    for (int e = 0; e < 16; ++e) acc[a][0][e] = 0.0f;
   const i32x16 zero = {};
   const f32x16 fz = {};
 
-  issue_act(0, 0);
-  issue_w(0, wh, wq);
+  issue_act(sb0, 0);
+  issue_w(sb0, wh, wq);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  for (int sb = 0; sb < nsb; ++sb) {
-    const int cur = sb & 1;
+  for (int sb = sb0; sb < sb1; ++sb) {
+    const int cur = (sb - sb0) & 1;
     u32x4 nh, nq[4];
-    if (sb + 1 < nsb) {
+    if (sb + 1 < sb1) {
       issue_act(sb + 1, cur ^ 1);
       issue_w(sb + 1, nh, nq);
     }
@@ -1417,33 +1423,49 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
         const int ci = chi[a][e], cl = clo[a][e];  // (scalar copies: see k_mmq)
         const int isum = 8 * ci + cl;
         const float inner = __builtin_fmaf(d, (float)isum, ndm * cm[e]);
-        acc[a][e] = __builtin_fmaf(dy, inner, acc[a][e]);
+        acc[a][0][e] = __builtin_fmaf(dy, inner, acc[a][0][e]);
       }
     }
     __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
     __syncthreads();
-    if (sb + 1 < nsb) {
+    if (sb + 1 < sb1) {
       wh = nh;
 #pragma unroll
       for (int c = 0; c < 4; ++c) wq[c] = nq[c];
     }
   }
-  if (row < rows) {
-#pragma unroll
-    for (int a = 0; a < NA; ++a)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = t0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
-        if (t < tokens) Y[(long)t * rows + row] = acc[a][e];
-      }
-  }
+  mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, g, ksplit, ks, part, cnt);
 }
 
-static hipError_t launch_mmq_wd(const GemvArgs& g, hipStream_t s) {
-  const long ntt = (g.tokens + kWdBT - 1) / kWdBT, ntr = (g.rows + kWdBR - 1) / kWdBR;
-  if (ntt * ntr > 0x7FFFFFFFL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_mmq_wd_q4k, dim3((unsigned)(ntt * ntr)), dim3(256), 0, s, (const uint8_t*)g.w,
-                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, g.cols / 256, (int)ntt);
+// Tokens per weights-direct tile: 32 up to 32 tokens (a 64-token tile would
+// spend half its MFMA and epilogue work on padding), else 64.
+static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
+
+// Slices of a weights-direct launch: K split when the grid has fewer than two
+// workgroups per CU, aiming at four, at least two super-blocks per slice (a
+// split aiming at eight workgroups per CU, or one super-block per slice, is
+// slower: the partial tiles' traffic grows with the slices).
+static int wd_slices(const GemvArgs& g) {
+  const int nsb = g.cols / 256;
+  return mmq_slices(nsb, mmq_ksplit_for(g, wd_bt(g), kWdBR, nsb, 2));
+}
+
+static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
+  const int bt = wd_bt(g), nsb = g.cols / 256;
+  const long ntt = (g.tokens + bt - 1) / bt, ntr = (g.rows + kWdBR - 1) / kWdBR;
+  const int cps = (nsb + ksplit - 1) / ksplit;
+  const long G = ntt * ntr * ksplit;
+  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntt * ntr > kSkMaxTiles)) return hipErrorInvalidValue;
+  unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
+  float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
+  if (bt == 32)
+    hipLaunchKernelGGL(k_mmq_wd_q4k<1>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
+                       ksplit, cps, part, cnt);
+  else
+    hipLaunchKernelGGL(k_mmq_wd_q4k<2>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
+                       ksplit, cps, part, cnt);
   return hipGetLastError();
 }
 
@@ -1468,9 +1490,10 @@ static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, void* work, hipStr
 
 template <int TT>
 static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit, void* work, hipStream_t s) {
-  // Q4_K's 64 x 128 tile is the weights-direct kernel (never split)
+  // Q4_K's 64 x 128 tile is the weights-direct kernel (never split when
+  // asked for explicitly)
   if constexpr (TT == TT_Q4_K)
-    if (bt == 64 && br == 128) return launch_mmq_wd(g, s);
+    if (bt == 64 && br == 128) return launch_mmq_wd(g, ksplit, work, s);
   if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, work, s);
   if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, work, s);
   if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, work, s);
@@ -1494,14 +1517,16 @@ static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
   const bool small = g.tokens <= 32 && !act32(g.ttype);
   bt = small ? 32 : 64;
   br = small ? 128 : 64;
-  if (g.ttype == TT_Q4_K && g.tokens >= 128) br = 128;  // the weights-direct kernel
+  if (g.ttype == TT_Q4_K) {  // the weights-direct kernel
+    bt = 64;
+    br = 128;
+  }
 }
 
 
-// Slices of the default tile launch (0 when it is the weights-direct kernel,
-// which never splits).
+// Slices of the default tile launch.
 static int mmq_default_slices(const GemvArgs& g, int bt, int br) {
-  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return 1;
+  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return wd_slices(g);
   const int nchunks = (g.cols / 64 + 3) / 4;
   return mmq_slices(nchunks, mmq_ksplit_for(g, bt, br, nchunks, 2));
 }
@@ -1509,6 +1534,7 @@ static int mmq_default_slices(const GemvArgs& g, int bt, int br) {
 long mmq_work_bytes(const GemvArgs& g) {
   int bt = 0, br = 0;
   mmq_default_tile(g, bt, br);
+  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return mmq_split_bytes(g, wd_bt(g), kWdBR, wd_slices(g));
   return mmq_split_bytes(g, bt, br, mmq_default_slices(g, bt, br));
 }
 
@@ -1518,7 +1544,8 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, void* work, long work_b
   if (bt <= 0 || br <= 0) {
     mmq_default_tile(g, bt, br);
     ksplit = mmq_default_slices(g, bt, br);
-    if (!work || work_bytes < mmq_split_bytes(g, bt, br, ksplit)) ksplit = 1;
+    const bool wd = g.ttype == TT_Q4_K && bt == 64 && br == 128;
+    if (!work || work_bytes < mmq_split_bytes(g, wd ? wd_bt(g) : bt, br, ksplit)) ksplit = 1;
   }
   switch (g.ttype) {
     case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, ksplit, work, s);
