@@ -911,6 +911,38 @@ static int mmq_ksplit_for(const GemvArgs& g, int bt, int br, int nchunks, int mi
   return (int)(want < cap ? want : cap);
 }
 
+// Slices for a launch of `tiles` tiles of a kernel that holds two workgroups
+// per CU (the weights-direct and image MMQs: their registers allow two waves
+// per SIMD): the smallest count of 1..4 whose grid fills its rounds of
+// resident workgroups at least 80%, else the fullest.  A grid of 1.25 rounds
+// spends a whole round at a quarter of the GPU; cutting K evens the rounds at
+// the price of the partial tiles.  Measured on MI355X (config 5, Q6_K image /
+// Q4_K weights-direct, us at 1 / 2 / 3 / 4 slices): T = 128 106 / 66 / 49 / 66
+// and 57 / 54 / 46 / 50; T = 256 121 / 115 / 92 / 101 and 92 / 84 / 78 / 84;
+// T = 384 128 / 131 / 136 / 141 and 110 / 114 / 113 / 120; T = 512 210 / 176
+// / 180 / 188 and 144 / 147 / 152 / 162; T = 1024 334 / 349 / 372 / 385 and
+// 256 / 294 / 310 / 346 -- the rule picks the best count at all but Q4_K
+// T = 512 (147 against 144 us).
+extern "C" int qhip_gpu_cu_count(void);
+static int mmq_round_slices(long tiles, int nchunks, int min_chunks) {
+  if (tiles > kSkMaxTiles) return 1;
+  const int cus = qhip_gpu_cu_count();
+  const long cap = 2L * (cus > 0 ? cus : 256);
+  int best = 1;
+  double best_u = 0.0;
+  for (int ks = 1; ks <= 4; ++ks) {
+    if (ks > 1 && nchunks / ks < min_chunks) break;
+    const long w = tiles * ks, rounds = (w + cap - 1) / cap;
+    const double u = (double)w / (double)(rounds * cap);
+    if (u >= 0.8) return ks;
+    if (u > best_u) {
+      best_u = u;
+      best = ks;
+    }
+  }
+  return best;
+}
+
 // Slices actually launched for a requested ksplit (no empty slice).
 static int mmq_slices(int nchunks, int ksplit) {
   if (ksplit < 1) ksplit = 1;
@@ -1249,7 +1281,13 @@ static hipError_t launch_mmq_img_type(const GemvArgs& g, int bt, int br, int ksp
 
 // Slices of the default image launch (small grids: split K over super-blocks,
 // k_mmq's rule with one chunk = one super-block).
-static int mmq_image_slices(const GemvArgs& g) { return mmq_slices(g.cols / 256, mmq_ksplit_for(g, 64, 64, g.cols / 256, 1)); }
+// One token tile: the small-grid rule (mmq_ksplit_for); several: whole rounds.
+static int mmq_image_slices(const GemvArgs& g) {
+  const int nsb = g.cols / 256;
+  const long ntt = (g.tokens + 63) / 64;
+  if (ntt >= 2) return mmq_slices(nsb, mmq_round_slices(ntt * ((g.rows + 63) / 64), nsb, 1));
+  return mmq_slices(nsb, mmq_ksplit_for(g, 64, 64, nsb, 1));
+}
 
 long mmq_image_work_bytes(const GemvArgs& g) { return mmq_split_bytes(g, 64, 64, mmq_image_slices(g)); }
 
@@ -1441,12 +1479,15 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
 // spend half its MFMA and epilogue work on padding), else 64.
 static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
 
-// Slices of a weights-direct launch: K split when the grid has fewer than two
-// workgroups per CU, aiming at four, at least two super-blocks per slice (a
-// split aiming at eight workgroups per CU, or one super-block per slice, is
-// slower: the partial tiles' traffic grows with the slices).
+// Slices of a weights-direct launch: with one token tile, K split when the
+// grid has fewer than two workgroups per CU, aiming at four, at least two
+// super-blocks per slice (a split aiming at eight workgroups per CU, or one
+// super-block per slice, is slower: the partial tiles' traffic grows with the
+// slices); with several, the round-filling count (mmq_round_slices).
 static int wd_slices(const GemvArgs& g) {
   const int nsb = g.cols / 256;
+  const long ntt = (g.tokens + wd_bt(g) - 1) / wd_bt(g);
+  if (ntt >= 2) return mmq_slices(nsb, mmq_round_slices(ntt * ((g.rows + kWdBR - 1) / kWdBR), nsb, 2));
   return mmq_slices(nsb, mmq_ksplit_for(g, wd_bt(g), kWdBR, nsb, 2));
 }
 
