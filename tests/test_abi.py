@@ -141,12 +141,15 @@ def test_split_workspace_size(lib):
 
 
 def test_mmq_split_workspace_size(lib):
-    # cfg5 at 16 tokens splits K (a few hundred row tiles); 512 tokens does not
-    # (enough tiles), nor does a GEMV-only or unknown type
+    # cfg5 at 16 tokens splits K (a few hundred row tiles); at 512 tokens the
+    # 1088 weights-direct tiles fill 2.1 rounds of 512 resident workgroups, so
+    # K is cut in two (2176 over 5 rounds: 85% full); 1024 tokens (2176 tiles)
+    # is not split; a GEMV-only or unknown type has no workspace
     n = lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 12)
     assert n > 32768 and n % 4 == 0
     assert lib.qhip_mul_mat_work_bytes(5120, 17408, 16, 14) > 32768
-    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 0
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 32768 + 4 * 2 * 1088 * 64 * 128
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 1024, 12) == 0
     assert lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 99) == 0
     assert lib.qhip_mul_mat_work_bytes(0, 5120, 16, 12) == 0
     p = ctypes.c_void_p(0x1000)
