@@ -1475,6 +1475,135 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
   mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, g, ksplit, ks, part, cnt);
 }
 
+// Few tokens (T <= 8 NG, NG < 4; one 32-token tile): the same staging, one
+// MFMA per sub-block on the raw nibbles, and the sub-block scale applied to
+// the integer result by an integer multiply-add (isum = sum_j sc_j S_j,
+// kernels256.c:474-498) -- but only on the accumulator elements of real
+// tokens: lane element e holds token 8 (e / 4) + 4 (lane / 32) + e % 4, so the
+// first 4 NG elements cover tokens 0 .. 8 NG - 1.  The split-scale planes of
+// k_mmq_wd_q4k cost two products per weight value and two MFMAs whatever the
+// token count; here the per-weight work is the nibble extraction alone.
+template <int NG>
+__global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                      float* __restrict__ Y, int rows, int tokens, long row_bytes,
+                                                      long act_bytes, int nsb, int ksplit, int cps,
+                                                      float* __restrict__ part, unsigned* __restrict__ cnt) {
+  constexpr int BT = 32, STAGE = BT * kWdRow, NDMA = (BT * kWdPieces + 255) / 256, NE = 4 * NG;
+  __shared__ __attribute__((aligned(16))) uint8_t act[2][STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
+  const int ks = g % ksplit;
+  g /= ksplit;
+  const int r0 = g * kWdBR;
+  const int row = r0 + 32 * wv + li;
+  const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
+
+  long goff[NDMA];
+  bool gon[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int p = 64 * (4 * i + wv) + lane;
+    gon[i] = p < BT * kWdPieces;
+    const int tp = p / kWdPieces, j = p - tp * kWdPieces;
+    const int tok = tp < tokens ? tp : tokens - 1;
+    goff[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
+  }
+  auto issue_act = [&](int sb, int buf) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
+        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
+                                         (__attribute__((address_space(3))) void*)(&act[buf][0] + 1024 * (4 * i + wv)),
+                                         16, 0, 0);
+    }
+  };
+  u32x4 wh, wq[4];
+  auto issue_w = [&](int sb, u32x4& h, u32x4 (&q)[4]) {
+    const uint8_t* b = wrow + 144L * sb;
+    h = *(const u32x4*)b;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
+  };
+
+  f32x16 acc[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[0][0][e] = 0.0f;
+  const i32x16 zero = {};
+  const f32x16 fz = {};
+
+  issue_act(sb0, 0);
+  issue_w(sb0, wh, wq);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int sb = sb0; sb < sb1; ++sb) {
+    const int cur = (sb - sb0) & 1;
+    u32x4 nh, nq[4];
+    if (sb + 1 < sb1) {
+      issue_act(sb + 1, cur ^ 1);
+      issue_w(sb + 1, nh, nq);
+    }
+    const uint8_t* A = &act[cur][0];
+    const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
+    const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
+    const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
+    const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+    int isum[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) isum[e] = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t q0 = wq[c].x, q1 = wq[c].y, q2 = wq[c].z, q3 = wq[c].w;
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi) {
+        const int s = 2 * c + hi;
+        const i32x4 bq = {(int)((hi ? q0 >> 4 : q0) & 0x0F0F0F0Fu), (int)((hi ? q1 >> 4 : q1) & 0x0F0F0F0Fu),
+                          (int)((hi ? q2 >> 4 : q2) & 0x0F0F0F0Fu), (int)((hi ? q3 >> 4 : q3) & 0x0F0F0F0Fu)};
+        const int sc = (int)(((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 63u);
+        const i32x4 af = *(const i32x4*)(A + li * kWdRow + 32 * s + 16 * lh);
+        const i32x16 S = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bq, zero, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < NE; ++e) isum[e] += sc * S[e];
+      }
+    }
+    // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
+    const uint32_t mn = lh ? mn_hi : mn_lo;
+    f16x8 bm;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const _Float16 m = (_Float16)(float)((mn >> (8 * k)) & 255u);
+      bm[2 * k] = m;
+      bm[2 * k + 1] = m;
+    }
+    const float d = h2f(wh.x), ndm = -h2f(wh.x >> 16);
+    const i16x8 bs = *(const i16x8*)(A + li * kWdRow + 256 + 16 * lh);
+    f16x8 am;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const short v = bs[k];
+      am[k] = (_Float16)v;
+    }
+    const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, fz, 0, 0, 0);
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const int t = 8 * (e >> 2) + 4 * lh + (e & 3);
+      const float dy = *(const float*)(A + t * kWdRow + 288);
+      const float inner = __builtin_fmaf(d, (float)isum[e], ndm * cm[e]);
+      acc[0][0][e] = __builtin_fmaf(dy, inner, acc[0][0][e]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
+    __syncthreads();
+    if (sb + 1 < sb1) {
+      wh = nh;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) wq[c] = nq[c];
+    }
+  }
+  mmq_write_tile<1, 1, 4>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+}
+
 // Tokens per weights-direct tile: 32 up to 32 tokens (a 64-token tile would
 // spend half its MFMA and epilogue work on padding), else 64.
 static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
@@ -1499,7 +1628,17 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipSt
   if (G > 0x7FFFFFFFL || (ksplit > 1 && ntt * ntr > kSkMaxTiles)) return hipErrorInvalidValue;
   unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
   float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
-  if (bt == 32)
+  if (bt == 32 && g.tokens <= 24) {
+    // few tokens: the raw-nibble form on the real tokens' elements
+    const int ng = (g.tokens + 7) / 8;
+#define QHIP_WDS(N)                                                                                          \
+  if (ng == N)                                                                                               \
+    hipLaunchKernelGGL(k_mmq_wds_q4k<N>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,            \
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, ksplit, cps, \
+                       part, cnt);
+    QHIP_WDS(1) QHIP_WDS(2) QHIP_WDS(3)
+#undef QHIP_WDS
+  } else if (bt == 32)
     hipLaunchKernelGGL(k_mmq_wd_q4k<1>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
                        ksplit, cps, part, cnt);
