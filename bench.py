@@ -443,13 +443,18 @@ def bench_mmq(c: Ctx):
                                                                   cols, T, tt, 0, 0, wp, wn, stream), it)
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
-            # the automatic path (what the Exec mirror's matvecBatchK takes)
+            # the C ABI's automatic path (GEMV or tile MMQ by the measured
+            # crossover), and what the Exec mirror's matvecBatchK launches: the
+            # same, except the Q6_K MMQ image from 96 tokens
             s_a = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
                                                              tt, PATH_AUTO, wp, wn, stream), it)
             pt["auto_us"] = round(s_a * 1e6, 2)
-            if s_a > 1.1 * min(s_g, s_t):
-                pt["auto_warning"] = "the automatic GEMV/MMQ choice is more than 10% slower than the faster path"
-                log(f"WARNING: {name} T={T}: auto {s_a * 1e6:.2f} us vs GEMV {s_g * 1e6:.2f} / MMQ {s_t * 1e6:.2f} us")
+            s_mirror = s_i if img is not None and T >= 96 else s_a
+            pt["mirror_us"] = round(s_mirror * 1e6, 2)
+            if s_mirror > 1.1 * min(s_g, s_m):
+                pt["mirror_warning"] = "the Exec mirror's choice is more than 10% slower than the fastest path"
+                log(f"WARNING: {name} T={T}: mirror {s_mirror * 1e6:.2f} us vs GEMV {s_g * 1e6:.2f} / "
+                    f"MMQ {s_m * 1e6:.2f} us")
             tops, fr = frac(rows, cols, T, s_m)
             pt.update({"mmq_us": round(s_m * 1e6, 2), "gemv_tokens_per_s": round(T / s_g, 1),
                        "mmq_tokens_per_s": round(T / s_m, 1), "mmq_int8_tops": tops, "mmq_int8_mfma_frac": fr})
@@ -599,18 +604,21 @@ def profile(c: Ctx, which: str, launches: int):
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
         aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
         y = torch.empty((T, rows), device=dev)
-        keep += [w, aq, y]
+        # the split-K workspace the Exec mirror passes
+        wk = ops.mul_mat_work(rows, cols, T, tt, dev)
+        wp, wn = (wk.data_ptr(), wk.numel()) if wk is not None else (None, 0)
+        keep += [w, aq, y, wk]
         if which == "mmq_cfg5_q6k_image":
             img = ops.mmq_image(tt, w, rows, cols)
             keep.append(img)
 
             def fn(i):
                 assert lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
-                                                     0, 0, None, 0, stream) == 0
+                                                     0, 0, wp, wn, stream) == 0
         else:
             def fn(i):
-                assert lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
-                                               PATH_MMQ, stream) == 0
+                assert lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
+                                                    PATH_MMQ, wp, wn, stream) == 0
     # the same warm-up and HIP-event timing as the measured run, so that a
     # trace of this process shows the launches bench.py reports: the last
     # `launches` launches of the kernel in the trace are the timed ones
