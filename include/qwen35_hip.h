@@ -241,6 +241,29 @@ int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_ou
                               int tokens, int ttype, int tile_tokens, int tile_rows, void *d_work,
                               long work_bytes, void *stream);
 
+/* Q6_K fragment image (no reference counterpart; the reference's CUDA MMQ
+ * decodes the GGUF blocks in every launch, mmq.cu:499-659).  The GGUF bytes
+ * permuted -- the same 210 bytes per row and 256 values -- so that the
+ * few-token MMQ loads each matrix-core fragment as one aligned, contiguous
+ * 1 KB per wave instruction (a GGUF row's 210-byte blocks leave most of its
+ * 8-byte pieces misaligned).  Rows in groups of 32, the last padded with zero
+ * rows; group r, super-block b is a 6720-byte tile at (r * cols/256 + b) *
+ * 6720: [0, 6144) lane L = i + 32k (row i, value half k) holds 24 dwords,
+ * dwords 4c..4c+3 at 1024c + 16L; dwords 6j..6j+5 (j = 2h + m) are the 8
+ * bytes of ql at 64h + 16m + 8k, of ql at 64h + 32 + 16m + 8k and of qh at
+ * 128 + 32h + 16m + 8k; [6144, 6656) row i's 16 scales at 16i; [6656, 6720)
+ * row i's f16 d at 2i.
+ *   qhip_wd_image_bytes    image size, -1 unless ttype is Q6_K and cols % 256 == 0
+ *   qhip_launch_wd_prepare build it from GGUF bytes (d_image 16-byte aligned)
+ *   qhip_launch_mul_mat_wd_image  d_out [tokens, rows] from the image, 1..32
+ *     tokens (Q8_K activations as for qhip_launch_mul_mat); d_work (nullable)
+ *     as for qhip_launch_mul_mat_work, qhip_mul_mat_work_bytes covers it; the
+ *     same block integers as the reference, float sums within its rounding */
+long qhip_wd_image_bytes(int ttype, int rows, int cols);
+int qhip_launch_wd_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
+int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
+                                 int tokens, int ttype, void *d_work, long work_bytes, void *stream);
+
 /* GEMV weight image (no reference counterpart; the reference's CUDA GEMV reads
  * the GGUF blocks as they are, mmvq.cu).  For the 32-value 4-bit formats
  * (IQ4_NL, Q4_0), whose 18-byte blocks leave every 16-byte piece of a row

@@ -60,6 +60,10 @@ SIGNATURES = {
     "qhip_launch_mmq_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
     "qhip_launch_mul_mat_image": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int,
                                           c_int, c_void_p, c_long, c_void_p]),
+    "qhip_wd_image_bytes": (c_long, [c_int, c_int, c_int]),
+    "qhip_launch_wd_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "qhip_launch_mul_mat_wd_image": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
+                                             c_long, c_void_p]),
     "qhip_gemv_image_bytes": (c_long, [c_int, c_int, c_int]),
     "qhip_gemv_image_act_bytes": (c_long, [c_int, c_int, c_int]),
     "qhip_launch_gemv_prepare": (c_int, [c_int, c_void_p, c_int, c_int, c_void_p, c_void_p]),

@@ -76,15 +76,16 @@ static hipError_t make_args(const void* w, const void* xq, float* out, int rows,
 // Token count from which the MMQ tiles beat the weight-streaming GEMV, both
 // at their defaults (the MMQ with the split-K workspace the Exec mirror
 // passes).  Measured on MI355X: Q4_K [17408, 5120] (the weights-direct MMQ)
-// GEMV 18.7 / MMQ 19.7 us at 4 tokens, 22.5 / 19.7 at 5; Q6_K [5120, 17408] 35.1 / 40.0 at 6, 42.5 /
-// 40.2 at 8; IQ4_NL [17408, 5120] 30.8 / 34.7 at 8, 46.4 / 34.7 at 12;
+// GEMV 18.7 / MMQ 19.7 us at 4 tokens, 22.5 / 19.7 at 5; Q6_K [5120, 17408] (the few-token
+// weights-direct MMQ on the GGUF rows) 27.2 / 31.5 at 4, 37.1 / 31.5 at 6; IQ4_NL [17408, 5120] 30.8 /
+// 34.7 at 8, 46.4 / 34.7 at 12;
 // Q8_0 [3584, 1024] 7.8 / 8.7 at 16; Q3_K / Q2_K [17408, 5120] 48.6 / 29.6
 // and 38.6 / 26.8 us at 8 (Q2_K 23.3 / 26.5 at 4).
 static int mmq_min_tokens(int ttype) {
   switch (ttype) {
     case TT_Q4_K: return 5;
-    case TT_Q5_K: return 6;
-    case TT_IQ4_XS: case TT_Q6_K: case TT_IQ3_XXS: case TT_IQ3_S: case TT_Q3_K: case TT_Q2_K: return 8;
+    case TT_Q5_K: case TT_Q6_K: return 6;
+    case TT_IQ4_XS: case TT_IQ3_XXS: case TT_IQ3_S: case TT_Q3_K: case TT_Q2_K: return 8;
     case TT_IQ4_NL: case TT_Q4_0: case TT_Q4_1: return 10;
     default: return 24;
   }
@@ -440,6 +441,28 @@ int qhip_launch_mul_mat_image(const void* d_image, const void* d_xq, float* d_ou
   if (!tile_ok || ((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
   if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
   return (int)launch_mmq_image(g, tile_tokens, tile_rows, d_work, d_work ? work_bytes : 0, S(stream));
+}
+
+long qhip_wd_image_bytes(int ttype, int rows, int cols) { return wd_image_bytes(ttype, rows, cols); }
+
+int qhip_launch_wd_prepare(int ttype, const void* d_w, int rows, int cols, void* d_image, void* stream) {
+  const long rb = weight_row_bytes(ttype, cols);
+  if (rb < 0 || wd_image_bytes(ttype, rows, cols) < 0) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  if (!d_w || !d_image || ((uintptr_t)d_image & 15u)) return (int)hipErrorInvalidValue;
+  return (int)launch_wd_prepare(ttype, d_w, rb, rows, cols, d_image, S(stream));
+}
+
+int qhip_launch_mul_mat_wd_image(const void* d_image, const void* d_xq, float* d_out, int rows, int cols,
+                                 int tokens, int ttype, void* d_work, long work_bytes, void* stream) {
+  GemvArgs g;
+  hipError_t e = make_args(d_image, d_xq, d_out, rows, cols, tokens, ttype, g);
+  if (e != hipSuccess) return (int)e;
+  if (wd_image_bytes(ttype, rows, cols) < 0 || tokens > 32) return (int)hipErrorInvalidValue;
+  if (((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
+  if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
+  if (rows == 0 || tokens == 0) return 0;
+  return (int)launch_mmq_wd_image(g, d_work, d_work ? work_bytes : 0, S(stream));
 }
 
 long qhip_gemv_image_bytes(int ttype, int rows, int cols) {

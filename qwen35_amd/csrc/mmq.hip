@@ -426,8 +426,13 @@ __device__ __forceinline__ void emit_a(SM& sm, const MmqAct<TT>& a, int tok, int
 // part[(tile * ksplit + slice) * tile_elems + i] (i: the thread's element in
 // accumulator order, so the stores are coalesced) and the last workgroup of
 // the tile adds the slices in slice order (sk_* hand-off, qhip_device.hpp):
-// the output does not depend on which slice finished last.
-template <int NA, int NB, int NW>
+// the output does not depend on which slice finished last.  The last
+// workgroup's loads of several slices go out together (up to 64 values per
+// lane in flight): each batch costs one memory latency, and a grid cut into
+// 20-30 slices would otherwise wait one latency per slice.  NEL < 16: only the
+// first NEL accumulator elements hold real tokens (the few-token kernels);
+// the rest are neither handed off nor written.
+template <int NA, int NB, int NW, int NEL = 16>
 __device__ __forceinline__ void mmq_write_tile(f32x16 (&acc)[NA][NB], float* __restrict__ Y, int rows, int tokens,
                                                int r0, int t0, int rb0, int tb0, int tile, int ksplit, int ks,
                                                float* __restrict__ part, unsigned* __restrict__ cnt) {
@@ -442,32 +447,39 @@ __device__ __forceinline__ void mmq_write_tile(f32x16 (&acc)[NA][NB], float* __r
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) sk_store(pp + ((a * NB + b) * 16 + e) * 64, acc[a][b][e]);
+        for (int e = 0; e < NEL; ++e) sk_store(pp + ((a * NB + b) * 16 + e) * 64, acc[a][b][e]);
     if (!sk_arrive(cnt + tile, (unsigned)ksplit)) return;
     const float* base = part + (long)tile * ksplit * TS + mine;
-    // slice by slice, in slice order: one slice's loads are independent and
-    // go out together (one memory latency per slice, not per element)
+    // in slice order, U slices' loads at a time (a batch past the last slice
+    // re-reads the last one and drops it)
+    constexpr int PER = NA * NB * NEL, U = PER >= 64 ? 1 : 64 / PER;
 #pragma unroll
     for (int a = 0; a < NA; ++a)
 #pragma unroll
       for (int b = 0; b < NB; ++b)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.0f;
-    for (int q = 0; q < ksplit; ++q) {
-      const float* pq = base + q * TS;
-      f32x16 t[NA][NB];
+    for (int q0 = 0; q0 < ksplit; q0 += U) {
+      float t[U][NA][NB][NEL];
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
+      for (int u = 0; u < U; ++u) {
+        const float* pq = base + (q0 + u < ksplit ? q0 + u : ksplit - 1) * TS;
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+        for (int a = 0; a < NA; ++a)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) t[a][b][e] = sk_load(pq + ((a * NB + b) * 16 + e) * 64);
+          for (int b = 0; b < NB; ++b)
 #pragma unroll
-      for (int a = 0; a < NA; ++a)
+            for (int e = 0; e < NEL; ++e) t[u][a][b][e] = sk_load(pq + ((a * NB + b) * 16 + e) * 64);
+      }
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
+      for (int u = 0; u < U; ++u)
+        if (q0 + u < ksplit)
 #pragma unroll
-          for (int e = 0; e < 16; ++e) acc[a][b][e] += t[a][b][e];
+          for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+              for (int e = 0; e < NEL; ++e) acc[a][b][e] += t[u][a][b][e];
     }
     sk_reset(cnt + tile);
   }
@@ -1326,6 +1338,16 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
 // 24.1 / 24.1 / 24.2 / 32.5 for the tile kernel's split launch.
 constexpr int kWdRow = 304, kWdPieces = 19, kWdBR = 128;
 
+// Makes the loaded registers complete here: the compiler may otherwise sink
+// the prologue's weight loads past the barrier into the loop, where the wait
+// for them then stalls every iteration on the loads in flight for the next.
+template <class T>
+__device__ __forceinline__ T wd_pinned(T v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+#define wd_pin(x) ((x) = wd_pinned(x))
+
 __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
   return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
 }
@@ -1362,12 +1384,12 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
     tok = tok < tokens ? tok : tokens - 1;
     goff[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
   }
-  auto issue_act = [&](int sb, int buf) {
+  auto issue_act = [&](int sb, uint8_t* buf) {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
         __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
-                                         (__attribute__((address_space(3))) void*)(&act[buf][0] + 1024 * (4 * i + wv)),
+                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
                                          16, 0, 0);
     }
   };
@@ -1387,18 +1409,23 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
   const i32x16 zero = {};
   const f32x16 fz = {};
 
-  issue_act(sb0, 0);
+  issue_act(sb0, &act[0][0]);
   issue_w(sb0, wh, wq);
+  wd_pin(wh);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) wd_pin(wq[c]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // one super-block: compute from A while super-block sb + 1 lands in nxt
   for (int sb = sb0; sb < sb1; ++sb) {
     const int cur = (sb - sb0) & 1;
+    const uint8_t* A = &act[cur][0];
+    uint8_t* nxt = &act[cur ^ 1][0];
     u32x4 nh, nq[4];
     if (sb + 1 < sb1) {
-      issue_act(sb + 1, cur ^ 1);
+      issue_act(sb + 1, nxt);
       issue_w(sb + 1, nh, nq);
     }
-    const uint8_t* A = &act[cur][0];
     __builtin_amdgcn_iglp_opt(0);
     // 6-bit scales and mins of this lane's row (kernels256.c:105-125)
     const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
@@ -1511,12 +1538,12 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
     const int tok = tp < tokens ? tp : tokens - 1;
     goff[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
   }
-  auto issue_act = [&](int sb, int buf) {
+  auto issue_act = [&](int sb, uint8_t* buf) {
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
         __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
-                                         (__attribute__((address_space(3))) void*)(&act[buf][0] + 1024 * (4 * i + wv)),
+                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
                                          16, 0, 0);
     }
   };
@@ -1534,18 +1561,23 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
   const i32x16 zero = {};
   const f32x16 fz = {};
 
-  issue_act(sb0, 0);
+  issue_act(sb0, &act[0][0]);
   issue_w(sb0, wh, wq);
+  wd_pin(wh);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) wd_pin(wq[c]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  // one super-block: compute from A while super-block sb + 1 lands in nxt
   for (int sb = sb0; sb < sb1; ++sb) {
     const int cur = (sb - sb0) & 1;
+    const uint8_t* A = &act[cur][0];
+    uint8_t* nxt = &act[cur ^ 1][0];
     u32x4 nh, nq[4];
     if (sb + 1 < sb1) {
-      issue_act(sb + 1, cur ^ 1);
+      issue_act(sb + 1, nxt);
       issue_w(sb + 1, nh, nq);
     }
-    const uint8_t* A = &act[cur][0];
     const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
     const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
     const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
@@ -1601,7 +1633,344 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
       for (int c = 0; c < 4; ++c) wq[c] = nq[c];
     }
   }
-  mmq_write_tile<1, 1, 4>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+}
+
+// Q6_K, few tokens (T <= 8 NG; one 32-token tile): the weights-direct
+// structure of k_mmq_wds_q4k on the Q6_K bytes.  Lane l of a wave holds row
+// l%32 and, for 16-value group g = 8h + m + 2q (kernels256.c:720-738, values
+// 128h + 32q + 16m + 0..15), its values 8(l/32)..+7: bytes of ql at 64h +
+// 32(q&1) + 16m + 8(l/32) (low nibble for q < 2, high for q >= 2) and the
+// 2-bit field 2q of qh at 32h + 16m + 8(l/32), decoded as the unsigned 6-bit
+// value u = q6.  One v_mfma_i32_32x32x16_i8 per group gives S_g = sum u*q8;
+// the reference's integer isum = sum_g sc_g sum (u - 32) q8 = sum_g sc_g S_g
+// - 32 sum_g sc_g bsum_g, the last sum by an exact f16 MFMA (bsums below 2048,
+// scales int8, every partial sum below 2^24).  Scaling and epilogue only on
+// the accumulator elements of real tokens.
+//
+// IMG = false reads the GGUF rows (NG < 4): 14 loads per lane and super-block,
+// most of them misaligned (210-byte blocks) and each spanning 32 rows -- the
+// texture path, not HBM, bounds it.  IMG = true reads the fragment image
+// below: 8 loads per lane, each wave instruction one aligned, contiguous 1 KB.
+//
+// Q6_K fragment image: the GGUF bytes permuted, the same 210 bytes per row and
+// super-block.  Rows in groups of 32 (the last group padded with zero rows);
+// group r, super-block sb is a 6720-byte tile at (r * nsb + sb) * 6720:
+//   [0, 6144)     lane L = i + 32 k (row i of the group, value half k) holds 24
+//                 dwords, piece c = dwords 4c..4c+3 at 1024 c + 16 L; dwords
+//                 6j..6j+5 for j = 2h + m are the 8 bytes of ql at 64h + 16m +
+//                 8k, of ql at 64h + 32 + 16m + 8k, and of qh at 128 + 32h +
+//                 16m + 8k
+//   [6144, 6656)  row i's 16 int8 scales at 6144 + 16 i
+//   [6656, 6720)  row i's f16 d at 6656 + 2 i
+constexpr int kWdiTile = 6720;
+
+template <bool IMG>
+struct Q6Regs;
+template <>
+struct Q6Regs<false> {
+  u32x2 la[4], lb[4], qh[4];
+  u32x4 sc;
+  uint32_t d;
+  __device__ __forceinline__ uint32_t ql(int j, int odd, int k) const { return odd ? lb[j][k] : la[j][k]; }
+  __device__ __forceinline__ uint32_t qhi(int j, int k) const { return qh[j][k]; }
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      wd_pin(la[j]);
+      wd_pin(lb[j]);
+      wd_pin(qh[j]);
+    }
+    wd_pin(sc);
+    wd_pin(d);
+  }
+};
+template <>
+struct Q6Regs<true> {
+  u32x4 p[6];
+  u32x4 sc;
+  uint32_t d;
+  __device__ __forceinline__ uint32_t at(int i) const { return p[i >> 2][i & 3]; }
+  __device__ __forceinline__ uint32_t ql(int j, int odd, int k) const { return at(6 * j + 2 * odd + k); }
+  __device__ __forceinline__ uint32_t qhi(int j, int k) const { return at(6 * j + 4 + k); }
+  __device__ __forceinline__ void pin() {
+#pragma unroll
+    for (int c = 0; c < 6; ++c) wd_pin(p[c]);
+    wd_pin(sc);
+    wd_pin(d);
+  }
+};
+
+// One super-block of k_mmq_wds_q6k / k_mmq_wdp_q6k: the 16 group MFMAs on
+// this lane's decoded 6-bit values (B, from the Q6Regs `wc`) against the
+// staged activation row `arow` of `A`, the integer scaling and the -32
+// offset on the NE kept elements, then acc[0][0] += dy * d * isum.  A macro,
+// not a function: the same code behind a call boundary (even forced inline)
+// is scheduled with 13-93 more VGPRs by this compiler.
+#define QHIP_Q6K_SUPERBLOCK(wc, A, arow)                                                               \
+  do {                                                                                                 \
+    const i32x16 zero_ = {};                                                                           \
+    const f32x16 fz_ = {};                                                                             \
+    const uint32_t scw[4] = {(wc).sc.x, (wc).sc.y, (wc).sc.z, (wc).sc.w};                              \
+    int isum[NE];                                                                                      \
+    _Pragma("unroll") for (int e = 0; e < NE; ++e) isum[e] = 0;                                        \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                    \
+      const int h = j >> 1, m = j & 1;                                                                 \
+      _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                                  \
+        const int grp = 8 * h + m + 2 * q;                                                             \
+        uint32_t v[2];                                                                                 \
+        _Pragma("unroll") for (int k = 0; k < 2; ++k) {                                                \
+          const uint32_t l = (wc).ql(j, q & 1, k), x = (wc).qhi(j, k);                                 \
+          const uint32_t nib = (q >= 2 ? l >> 4 : l) & 0x0F0F0F0Fu;                                    \
+          const uint32_t hi = q == 0 ? (x << 4) & 0x30303030u                                          \
+                              : q == 1 ? (x << 2) & 0x30303030u                                        \
+                              : q == 2 ? x & 0x30303030u                                               \
+                                       : (x >> 2) & 0x30303030u;                                       \
+          v[k] = nib | hi;                                                                             \
+        }                                                                                              \
+        const long bq = (long)(((unsigned long)v[1] << 32) | v[0]);                                    \
+        const long af = *(const long*)((A) + (arow) * kWdRow + 16 * grp + 8 * lh);                     \
+        const i32x16 S = __builtin_amdgcn_mfma_i32_32x32x16_i8(af, bq, zero_, 0, 0, 0);                \
+        const int sc = (int)(int8_t)(scw[grp >> 2] >> (8 * (grp & 3)));                                \
+        _Pragma("unroll") for (int e = 0; e < NE; ++e) isum[e] += sc * S[e];                           \
+      }                                                                                                \
+    }                                                                                                  \
+    /* sum_g sc_g bsum_g[t], exact in the f16 MFMA: A = the token's 8 bsums of                         \
+       groups 8(l/32)..+7, B = the row's scales of the same groups */                                  \
+    const i16x8 bs = *(const i16x8*)((A) + (arow) * kWdRow + 256 + 16 * lh);                           \
+    f16x8 am, bm;                                                                                      \
+    _Pragma("unroll") for (int k = 0; k < 8; ++k) {                                                    \
+      const short bv = bs[k];                                                                          \
+      am[k] = (_Float16)bv;                                                                            \
+      bm[k] = (_Float16)(float)(int)(int8_t)(scw[2 * lh + (k >> 2)] >> (8 * (k & 3)));                 \
+    }                                                                                                  \
+    const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, fz_, 0, 0, 0);                    \
+    const float dw = h2f((wc).d);                                                                      \
+    /* the reference's integer (kernels256.c:720-738) */                                               \
+    _Pragma("unroll") for (int e = 0; e < NE; ++e) {                                                   \
+      const int t = 8 * (e >> 2) + 4 * lh + (e & 3);                                                   \
+      const float dy = *(const float*)((A) + t * kWdRow + 288);                                        \
+      const int tot = isum[e] - 32 * (int)cm[e];                                                       \
+      acc[0][0][e] = __builtin_fmaf(dy, dw * (float)tot, acc[0][0][e]);                                \
+    }                                                                                                  \
+  } while (0)
+
+// DMA offsets of the activation pieces a lane moves: piece P = 64 (4i + wave)
+// + lane of a run of stages of TR token rows: stage P / (19 TR), token row
+// (P % (19 TR)) / 19, 16-byte slot (P % (19 TR)) % 19 (16 qs slots, two bsum
+// slots, one holding d); rows past the last token re-read it.  st[i] = the
+// piece's stage, or nst when the piece is past the run.
+template <int NDMA, int TR>
+__device__ __forceinline__ void wd_dma_plan(int wv, int lane, int tokens, long act_bytes, int nst, long (&off)[NDMA],
+                                            int (&st)[NDMA]) {
+  constexpr int NPC = TR * kWdPieces;
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int P = 64 * (4 * i + wv) + lane;
+    const int sg = P / NPC, p = P - sg * NPC;
+    const int tp = p / kWdPieces, j = p - tp * kWdPieces;
+    const int tok = tp < tokens ? tp : tokens - 1;
+    st[i] = P < nst * NPC ? sg : nst;
+    off[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
+  }
+}
+
+// GGUF rows, T <= 8 NG (NG < 4), two stages double-buffered: super-block sb + 1
+// is loaded while sb is multiplied.  Only the 8 NG token rows the kept
+// elements read are staged (lanes of later rows read row 0: their MFMA
+// columns are never kept).
+template <int NG>
+__global__ __launch_bounds__(256) void k_mmq_wds_q6k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                      float* __restrict__ Y, int rows, int tokens, long row_bytes,
+                                                      long act_bytes, int nsb, int ksplit, int cps,
+                                                      float* __restrict__ part, unsigned* __restrict__ cnt) {
+  constexpr int TR = 8 * NG, NE = 4 * NG, STAGE = TR * kWdRow, NPC = TR * kWdPieces, NDMA = (NPC + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint8_t act[2][STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
+  const int ks = g % ksplit;
+  g /= ksplit;
+  const int r0 = g * kWdBR;
+  const int row = r0 + 32 * wv + li;
+  const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
+  const int arow = li < TR ? li : 0;
+
+  long goff[NDMA];
+  int gst[NDMA];
+  wd_dma_plan<NDMA, TR>(wv, lane, tokens, act_bytes, 1, goff, gst);
+  auto issue_act = [&](int sb, uint8_t* buf) {
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      if (4 * i + wv < (NPC + 63) / 64 && gst[i] == 0)
+        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
+                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
+                                         16, 0, 0);
+    }
+  };
+  auto issue_w = [&](int sb, Q6Regs<false>& q) {
+    const uint8_t* b = wrow + 210L * sb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int h = j >> 1, m = j & 1;
+      q.la[j] = *(const u32x2_u*)(b + 64 * h + 16 * m + 8 * lh);
+      q.lb[j] = *(const u32x2_u*)(b + 64 * h + 32 + 16 * m + 8 * lh);
+      q.qh[j] = *(const u32x2_u*)(b + 128 + 32 * h + 16 * m + 8 * lh);
+    }
+    q.sc = *(const u32x4_u*)(b + 192);
+    q.d = *(const uint16_t*)(b + 208);
+  };
+
+  f32x16 acc[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[0][0][e] = 0.0f;
+
+  Q6Regs<false> wc, wn;
+  issue_act(sb0, &act[0][0]);
+  issue_w(sb0, wc);
+  wc.pin();
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int sb = sb0; sb < sb1; ++sb) {
+    const int cur = (sb - sb0) & 1;
+    if (sb + 1 < sb1) {
+      issue_act(sb + 1, &act[cur ^ 1][0]);
+      issue_w(sb + 1, wn);
+    }
+    QHIP_Q6K_SUPERBLOCK(wc, &act[cur][0], arow);
+    __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
+    __syncthreads();
+    if (sb + 1 < sb1) wc = wn;
+  }
+  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+}
+
+// The fragment image, T <= 8 NG: the workgroup's K slice in groups of CPS
+// super-blocks, each group's weight loads (8 per lane and super-block, every
+// wave instruction one aligned 1 KB) and activation DMA all issued before any
+// of it is used.  Measured on MI355X, config 5 Q6_K [5120, 17408], 1 / 8 / 16
+// / 24 tokens: 21.1 / 21.4 / 24.1 / 28.0 us with CPS = 2, against 22.1 / 22.2
+// / 24.4 / 28.2 double-buffered one super-block at a time and 22.5 / 22.7 /
+// 25.9 / 30.4 with CPS = 3 (more registers, fewer resident workgroups).
+template <int NG, int CPS>
+__global__ __launch_bounds__(256) void k_mmq_wdp_q6k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                      float* __restrict__ Y, int rows, int tokens, long act_bytes,
+                                                      int nsb, int ksplit, int cps, float* __restrict__ part,
+                                                      unsigned* __restrict__ cnt) {
+  constexpr int TR = 8 * NG, NE = 4 * NG;
+  constexpr int STAGE = TR * kWdRow, NPC = TR * kWdPieces, NDMA = (CPS * NPC + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint8_t act[CPS * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
+  const int ks = g % ksplit;
+  g /= ksplit;
+  const int r0 = g * kWdBR;
+  // this wave's group of 32 rows (a group past the end re-reads the last)
+  const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
+  const uint8_t* wbase = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile;
+  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
+  const int arow = li < TR ? li : 0;
+
+  long goff[NDMA];
+  int gst[NDMA];
+  wd_dma_plan<NDMA, TR>(wv, lane, tokens, act_bytes, CPS, goff, gst);
+
+  f32x16 acc[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[0][0][e] = 0.0f;
+
+  for (int base = sb0; base < sb1; base += CPS) {
+    const int n = sb1 - base < CPS ? sb1 - base : CPS;
+    Q6Regs<true> wr[CPS];
+#pragma unroll
+    for (int s = 0; s < CPS; ++s) {
+      if (s < n) {
+        const uint8_t* b = wbase + (long)kWdiTile * (base + s);
+#pragma unroll
+        for (int c = 0; c < 6; ++c) wr[s].p[c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+        wr[s].sc = *(const u32x4*)(b + 6144 + 16 * li);
+        wr[s].d = *(const uint16_t*)(b + 6656 + 2 * li);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      if (4 * i + wv < (CPS * NPC + 63) / 64 && gst[i] < n)
+        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * (base + gst[i])),
+                                         (__attribute__((address_space(3))) void*)(act + 1024 * (4 * i + wv)), 16,
+                                         0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every weight register and DMA piece of the group
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < CPS; ++s)
+      if (s < n) QHIP_Q6K_SUPERBLOCK(wr[s], act + s * STAGE, arow);
+    __syncthreads();  // the next group's DMA overwrites the stages
+  }
+  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+}
+
+// One thread per (tile, lane L) of the Q6_K fragment image: lane L's 96 quant
+// bytes; lanes L < 32 also the row's scales and d.  Rows past the end: zeros.
+__device__ __forceinline__ uint32_t ld32_bytes(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+__global__ __launch_bounds__(256) void k_wd_prepare_q6k(const uint8_t* __restrict__ W, uint8_t* __restrict__ IMG,
+                                                         int rows, long row_bytes, int nsb, long nthreads) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= nthreads) return;
+  const int L = (int)(gid & 63), i = L & 31, k = L >> 5;
+  const long tile = gid >> 6;  // group * nsb + sb
+  const long grp = tile / nsb;
+  const int sb = (int)(tile - grp * nsb);
+  const long row = grp * 32 + i;
+  uint8_t* t = IMG + tile * kWdiTile;
+  uint32_t q[24];
+  uint32_t sc[4] = {0, 0, 0, 0}, d = 0;
+  if (row < rows) {
+    const uint8_t* b = W + row * row_bytes + 210L * sb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int h = j >> 1, m = j & 1;
+#pragma unroll
+      for (int w = 0; w < 2; ++w) {
+        q[6 * j + w] = ld32_bytes(b + 64 * h + 16 * m + 8 * k + 4 * w);
+        q[6 * j + 2 + w] = ld32_bytes(b + 64 * h + 32 + 16 * m + 8 * k + 4 * w);
+        q[6 * j + 4 + w] = ld32_bytes(b + 128 + 32 * h + 16 * m + 8 * k + 4 * w);
+      }
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) sc[w] = ld32_bytes(b + 192 + 4 * w);
+    d = (uint32_t)b[208] | ((uint32_t)b[209] << 8);
+  } else {
+#pragma unroll
+    for (int w = 0; w < 24; ++w) q[w] = 0;
+  }
+#pragma unroll
+  for (int c = 0; c < 6; ++c) *(uint4*)(t + 1024 * c + 16 * L) = make_uint4(q[4 * c], q[4 * c + 1], q[4 * c + 2], q[4 * c + 3]);
+  if (k == 0) {
+    *(uint4*)(t + 6144 + 16 * i) = make_uint4(sc[0], sc[1], sc[2], sc[3]);
+    *(uint16_t*)(t + 6656 + 2 * i) = (uint16_t)d;
+  }
+}
+
+long wd_image_bytes(int ttype, int rows, int cols) {
+  if (ttype != TT_Q6_K || rows < 0 || cols <= 0 || cols % 256) return -1;
+  return (long)((rows + 31) / 32) * (cols / 256) * kWdiTile;
+}
+
+hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
+                             hipStream_t s) {
+  if (wd_image_bytes(ttype, rows, cols) < 0) return hipErrorInvalidValue;
+  const int nsb = cols / 256;
+  const long n = (long)((rows + 31) / 32) * nsb * 64;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_wd_prepare_q6k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
+                     (uint8_t*)img, rows, row_bytes, nsb, n);
+  return hipGetLastError();
 }
 
 // Tokens per weights-direct tile: 32 up to 32 tokens (a 64-token tile would
@@ -1646,6 +2015,58 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipSt
     hipLaunchKernelGGL(k_mmq_wd_q4k<2>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
                        ksplit, cps, part, cnt);
+  return hipGetLastError();
+}
+
+// Q6_K at up to 24 tokens on the default path: the few-token weights-direct
+// kernel (one 32-token tile, 128 rows per workgroup, K split like the Q4_K one).
+static bool wds_q6k(const GemvArgs& g) { return g.ttype == TT_Q6_K && g.tokens <= 24; }
+
+static int wds_q6k_slices(const GemvArgs& g) {
+  const int nsb = g.cols / 256;
+  return mmq_slices(nsb, mmq_ksplit_for(g, 32, kWdBR, nsb, 2));
+}
+
+static hipError_t launch_mmq_wds_q6k(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
+  const int nsb = g.cols / 256;
+  const long ntr = (g.rows + kWdBR - 1) / kWdBR;
+  const int cps = (nsb + ksplit - 1) / ksplit;
+  const long G = ntr * ksplit;
+  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr > kSkMaxTiles)) return hipErrorInvalidValue;
+  unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
+  float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
+  const int ng = (g.tokens + 7) / 8;
+#define QHIP_WDS6(N)                                                                                          \
+  if (ng == N)                                                                                                \
+    hipLaunchKernelGGL(k_mmq_wds_q6k<N>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,             \
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, ksplit, cps, \
+                       part, cnt);
+  QHIP_WDS6(1) QHIP_WDS6(2) QHIP_WDS6(3)
+#undef QHIP_WDS6
+  return hipGetLastError();
+}
+
+// Q6_K from the fragment image, 1..32 tokens; work as for launch_mmq (the
+// same slices as the GGUF-row launch, so mmq_work_bytes covers it).
+hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s) {
+  if (g.ttype != TT_Q6_K || g.tokens < 1 || g.tokens > 32) return hipErrorInvalidValue;
+  if (g.rows <= 0) return hipSuccess;
+  int ksplit = wds_q6k_slices(g);
+  if (!work || work_bytes < mmq_split_bytes(g, 32, kWdBR, ksplit)) ksplit = 1;
+  const int nsb = g.cols / 256;
+  const long ntr = (g.rows + kWdBR - 1) / kWdBR;
+  const int cps = (nsb + ksplit - 1) / ksplit;
+  const long G = ntr * ksplit;
+  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr > kSkMaxTiles)) return hipErrorInvalidValue;
+  unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
+  float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
+  const int ng = (g.tokens + 7) / 8;
+#define QHIP_WDP(N)                                                                                           \
+  if (ng == N)                                                                                                \
+    hipLaunchKernelGGL((k_mmq_wdp_q6k<N, 2>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,         \
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, nsb, ksplit, cps, part, cnt);
+  QHIP_WDP(1) QHIP_WDP(2) QHIP_WDP(3) QHIP_WDP(4)
+#undef QHIP_WDP
   return hipGetLastError();
 }
 
@@ -1707,6 +2128,7 @@ static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
 // Slices of the default tile launch.
 static int mmq_default_slices(const GemvArgs& g, int bt, int br) {
   if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return wd_slices(g);
+  if (wds_q6k(g)) return wds_q6k_slices(g);
   const int nchunks = (g.cols / 64 + 3) / 4;
   return mmq_slices(nchunks, mmq_ksplit_for(g, bt, br, nchunks, 2));
 }
@@ -1726,6 +2148,7 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, void* work, long work_b
     ksplit = mmq_default_slices(g, bt, br);
     const bool wd = g.ttype == TT_Q4_K && bt == 64 && br == 128;
     if (!work || work_bytes < mmq_split_bytes(g, wd ? wd_bt(g) : bt, br, ksplit)) ksplit = 1;
+    if (wds_q6k(g)) return launch_mmq_wds_q6k(g, ksplit, work, s);
   }
   switch (g.ttype) {
     case TT_Q8_0: return launch_mmq_type<TT_Q8_0>(g, bt, br, ksplit, work, s);

@@ -69,6 +69,11 @@ hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows
                               hipStream_t s);
 // g.w = the image; bt x br tile (0 = default; splits K as launch_mmq)
 hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s);
+// Q6_K fragment image (the GGUF bytes permuted for the few-token MMQ)
+long wd_image_bytes(int ttype, int rows, int cols);
+hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
+                             hipStream_t s);
+hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s);
 long mmq_image_work_bytes(const GemvArgs& g);
 // GEMV weight image of the 32-value 4-bit formats (gemv_image.hip): the same
 // bytes per row, quant bytes 16-byte aligned in unit order, scales apart

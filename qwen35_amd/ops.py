@@ -202,6 +202,26 @@ def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, co
     return out
 
 
+def wd_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    """The fragment image of a Q6_K weight (the GGUF bytes permuted for the few-token MMQ)."""
+    n = load().qhip_wd_image_bytes(ttype, rows, cols)
+    if n < 0:
+        raise ValueError(f"no fragment image for type {ttype} at cols={cols}")
+    img = torch.empty(max(n, 16), dtype=torch.uint8, device=w.device)
+    check("wd_prepare", load().qhip_launch_wd_prepare(ttype, _p(w), rows, cols, _p(img), _stream()))
+    return img
+
+
+def mul_mat_wd_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
+                     work: torch.Tensor | None = None) -> torch.Tensor:
+    """out [tokens, rows] from the fragment image (1..32 tokens)."""
+    out = torch.empty((tokens, rows), dtype=torch.float32, device=img.device)
+    check("mul_mat_wd_image", load().qhip_launch_mul_mat_wd_image(
+        _p(img), _p(xq), _p(out), rows, cols, tokens, ttype,
+        _p(work) if work is not None else None, work.numel() if work is not None else 0, _stream()))
+    return out
+
+
 def gemv_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
     """The GEMV weight image of an IQ4_NL / Q4_0 weight (same bytes per row, quant bytes 16-byte aligned)."""
     n = load().qhip_gemv_image_bytes(ttype, rows, cols)

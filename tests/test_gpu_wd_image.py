@@ -1,0 +1,118 @@
+"""GPU: the Q6_K fragment image -- its layout restated on the host from the
+GGUF bytes, the few-token MMQ read from it against the oracle at every token
+count either side of each kernel variant (1..32) and row counts off the
+32-row groups, the same bits as the GGUF-row few-token kernel, exact block
+integers at unit scales, extreme 6-bit values and scales, bit-equal reruns."""
+import numpy as np
+import pytest
+import torch
+
+import pyoracle as po
+from qwen35_amd import ops, synth
+from test_gpu_mmq import rel_l2, to_dev, unit_scale_act, unit_scale_weight
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-5
+PATH_MMQ = 2
+TQ6 = po.TT_Q6_K
+
+
+def wd_image_of(w, rows, cols):
+    """The documented fragment-image layout, from the GGUF bytes."""
+    nsb = cols // 256
+    ngrp = (rows + 31) // 32
+    pad = np.zeros((ngrp * 32, nsb, 210), np.uint8)
+    pad[:rows] = w.reshape(rows, nsb, 210)
+    img = np.zeros((ngrp, nsb, 6720), np.uint8)
+    for k in range(2):
+        pieces = []
+        for j in range(4):
+            h, m = j >> 1, j & 1
+            for off in (64 * h + 16 * m + 8 * k, 64 * h + 32 + 16 * m + 8 * k, 128 + 32 * h + 16 * m + 8 * k):
+                pieces.append(pad[:, :, off:off + 8])
+        lane = np.concatenate(pieces, axis=-1).reshape(ngrp, 32, nsb, 96)
+        for c in range(6):
+            img[:, :, 1024 * c + 512 * k:1024 * c + 512 * (k + 1)] = \
+                lane[:, :, :, 16 * c:16 * c + 16].transpose(0, 2, 1, 3).reshape(ngrp, nsb, 512)
+    img[:, :, 6144:6656] = pad[:, :, 192:208].reshape(ngrp, 32, nsb, 16).transpose(0, 2, 1, 3).reshape(ngrp, nsb, 512)
+    img[:, :, 6656:6720] = pad[:, :, 208:210].reshape(ngrp, 32, nsb, 2).transpose(0, 2, 1, 3).reshape(ngrp, nsb, 64)
+    return img.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (31, 512), (32, 2304), (33, 256), (70, 1024)])
+def test_wd_image_layout(gpu, rows, cols):
+    w = synth.make_weight(TQ6, rows, cols, seed=40, tag=rows)
+    n = ops.load().qhip_wd_image_bytes(TQ6, rows, cols)
+    assert n == (rows + 31) // 32 * (cols // 256) * 6720
+    img = ops.wd_image(TQ6, to_dev(w, gpu), rows, cols).cpu().numpy()
+    assert np.array_equal(img[:n], wd_image_of(w, rows, cols))
+
+
+@pytest.fixture(scope="module")
+def q6(gpu):
+    rows, cols = 333, 4608
+    w = synth.make_weight(TQ6, rows, cols, seed=41, tag=TQ6)
+    wd = to_dev(w, gpu)
+    return rows, cols, w, wd, ops.wd_image(TQ6, wd, rows, cols)
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 7, 8, 9, 16, 17, 24, 25, 31, 32])
+def test_wd_image_mmq_vs_oracle(gpu, oracle, q6, tokens):
+    rows, cols, w, wd, img = q6
+    x = synth.make_act(cols, tokens, seed=42, tag=tokens)
+    xq = ops.quantize_act(TQ6, to_dev(x, gpu))
+    work = ops.mul_mat_work(rows, cols, tokens, TQ6, gpu)
+    got = ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens, work)
+    assert rel_l2(got.cpu().numpy(), oracle.matvec(TQ6, w, x)) < TOL
+    assert torch.equal(got, ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens, work))
+    # without a workspace: not split, the same integers
+    plain = ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens)
+    assert rel_l2(plain.cpu().numpy(), got.cpu().numpy()) < 1e-6
+    if tokens <= 24:
+        # the GGUF-row few-token kernel: the same arithmetic in the same order
+        raw = ops.mul_mat_split(TQ6, wd, xq, rows, cols, tokens, work, PATH_MMQ)
+        assert torch.equal(got, raw)
+
+
+@pytest.mark.parametrize("tokens", [1, 6, 8, 19, 32])
+def test_wd_image_integers_exact(gpu, oracle, tokens):
+    rows, cols = 96, 1024
+    w = unit_scale_weight(TQ6, rows, cols, seed=43)
+    x = unit_scale_act(cols, tokens, seed=43)
+    act = oracle.quantize_act(TQ6, x)
+    want = oracle.block_ints(TQ6, w, act, cols).astype(np.int64).sum(-1)
+    assert np.abs(want).max() < 2 ** 24
+    img = ops.wd_image(TQ6, to_dev(w, gpu), rows, cols)
+    xq = ops.quantize_act(TQ6, to_dev(x, gpu))
+    work = ops.mul_mat_work(rows, cols, tokens, TQ6, gpu)
+    for wk in (work, None):
+        got = ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens, wk).cpu().numpy()
+        assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_wd_image_extreme_values(gpu, oracle):
+    rows, cols, tokens = 40, 2048, 12
+    w = unit_scale_weight(TQ6, rows, cols, seed=44).reshape(rows, -1, 210)
+    rng = np.random.default_rng(44)
+    w[:, :, 0:192] = np.where(rng.random((rows, w.shape[1], 192)) < 0.5, 0x00, 0xFF).astype(np.uint8)
+    w[:, :, 192:208] = np.where(rng.random((rows, w.shape[1], 16)) < 0.5, 0x80, 0x7F).astype(np.uint8)
+    w = w.reshape(rows, -1)
+    x = np.where(rng.random((tokens, cols)) < 0.5, -127.0, 127.0).astype(np.float32)
+    img = ops.wd_image(TQ6, to_dev(w, gpu), rows, cols)
+    xq = ops.quantize_act(TQ6, to_dev(x, gpu))
+    got = ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens, ops.mul_mat_work(rows, cols, tokens, TQ6, gpu))
+    assert rel_l2(got.cpu().numpy(), oracle.matvec(TQ6, w, x)) < TOL
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(5120, 17408, 8), (4096, 4096, 24), (130, 256, 1)])
+def test_wd_image_model_shapes(gpu, oracle, rows, cols, tokens):
+    """The config-5 down projection and other widths, through the split."""
+    w = synth.make_weight(TQ6, rows, cols, seed=45, tag=rows)
+    x = synth.make_act(cols, tokens, seed=45, tag=tokens)
+    wd = to_dev(w, gpu)
+    img = ops.wd_image(TQ6, wd, rows, cols)
+    xq = ops.quantize_act(TQ6, to_dev(x, gpu))
+    work = ops.mul_mat_work(rows, cols, tokens, TQ6, gpu)
+    got = ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens, work)
+    want = oracle.matvec(TQ6, w[: min(rows, 512)], x) if rows > 512 else oracle.matvec(TQ6, w, x)
+    assert rel_l2(got.cpu().numpy()[:, : want.shape[1]], want) < TOL
