@@ -420,11 +420,13 @@ def bench_mmq(c: Ctx):
     sweep = {}
     for name, tt, rows, cols in (("q4_k_17408x5120", TQ4, 17408, 5120), ("q6_k_5120x17408", TQ6, 5120, 17408)):
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
-        # the prepared MMQ weight image the Exec mirror uses for Q6_K prefill
+        # the prepared MMQ weight image the Exec mirror uses for Q6_K prefill,
+        # and the fragment image it uses for 3..32 tokens
         img = ops.mmq_image(tt, w, rows, cols) if tt == TQ6 else None
+        frag = ops.wd_image(tt, w, rows, cols) if tt == TQ6 else None
         rows_out = []
         cross = None
-        for T in (1, 4, 8, 16, 64, 512):
+        for T in (1, 2, 4, 8, 16, 32, 64, 512):
             x = torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev)
             aq = ops.quantize_act(tt, x)
             y = torch.empty((T, rows), device=dev)
@@ -443,13 +445,20 @@ def bench_mmq(c: Ctx):
                                                                   cols, T, tt, 0, 0, wp, wn, stream), it)
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
+            s_f = None
+            if frag is not None and T <= 32:
+                s_f = timed(lambda: lib.qhip_launch_mul_mat_wd_image(frag.data_ptr(), aq.data_ptr(), y.data_ptr(),
+                                                                     rows, cols, T, tt, wp, wn, stream), it)
+                pt["mmq_fragment_image_us"] = round(s_f * 1e6, 2)
+                s_m = min(s_m, s_f)
             # the C ABI's automatic path (GEMV or tile MMQ by the measured
             # crossover), and what the Exec mirror's matvecBatchK launches: the
-            # same, except the Q6_K MMQ image from 96 tokens
+            # same, except the Q6_K fragment image at 3..32 tokens and the
+            # MMQ image from 96
             s_a = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
                                                              tt, PATH_AUTO, wp, wn, stream), it)
             pt["auto_us"] = round(s_a * 1e6, 2)
-            s_mirror = s_i if img is not None and T >= 96 else s_a
+            s_mirror = s_i if img is not None and T >= 96 else s_f if s_f is not None and T >= 3 else s_a
             pt["mirror_us"] = round(s_mirror * 1e6, 2)
             if s_mirror > 1.1 * min(s_g, s_m):
                 pt["mirror_warning"] = "the Exec mirror's choice is more than 10% slower than the fastest path"
@@ -461,10 +470,14 @@ def bench_mmq(c: Ctx):
             rows_out.append(pt)
             if cross is None and s_m < s_g:
                 cross = T
-        sweep[name] = {"points": rows_out, "crossover_T": cross}
+        # small batches against one token: what the Exec mirror launches at
+        # 2..8 tokens over the batch-1 GEMV
+        t1 = next(p["gemv_us"] for p in rows_out if p["T"] == 1)
+        ratio = max(p["mirror_us"] for p in rows_out if 2 <= p["T"] <= 8) / t1
+        sweep[name] = {"points": rows_out, "crossover_T": cross, "mirror_2_8_over_gemv_1": round(ratio, 3)}
         log(f"mmq cfg5 {name}: " + ", ".join(f"T={p['T']} gemv {p['gemv_us']} / mmq {p['mmq_us']} us"
                                               for p in rows_out) + f"; crossover T={cross}")
-        del w, img
+        del w, img, frag
         torch.cuda.empty_cache()
     res["cfg5_sweep"] = sweep
     return res

@@ -110,6 +110,17 @@ bool mmq_image_preferred(const GemvArgs& g) {
   return g.ttype == TT_Q6_K && g.tokens >= 96 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
+// Few tokens of a large Q6_K weight: the Exec mirror multiplies them from the
+// weight's fragment image (the GGUF bytes once more, permuted).  Measured on
+// MI355X, [5120, 17408]: 21.0 / 21.3 / 24.0 / 28.0 / 34.1 us at 2 / 4 / 16 /
+// 24 / 32 tokens from the image, against GEMV 19.5 / 27.2 us at 2 / 4 and the
+// GGUF-row MMQ 31.4 / 31.5 / 34.2 / 37.0 / 37.6 us: the image from 3 tokens
+// (GEMV about 23 us there) up to its 32-token limit.
+bool wd_image_preferred(const GemvArgs& g) {
+  return g.ttype == TT_Q6_K && g.tokens >= 3 && g.tokens <= 32 && (long)g.rows * g.cols >= (1L << 23) &&
+         wd_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+}
+
 // `work` (nullable): the split-K workspace of the MMQ (mmq_work_bytes)
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, void* work, long work_bytes, hipStream_t s) {
   if (g.rows == 0 || g.tokens == 0) return hipSuccess;

@@ -20,6 +20,7 @@ namespace qhip {
 hipError_t dispatch_mul_mat(const GemvArgs& g, int path, void* work, long work_bytes, hipStream_t s);
 long mul_mat_work_bytes(const GemvArgs& g);
 bool mmq_image_preferred(const GemvArgs& g);
+bool wd_image_preferred(const GemvArgs& g);
 }
 
 using namespace qhip;
@@ -38,19 +39,22 @@ struct qhip_backend {
   // (counters zero between launches)
   uint8_t* skwork = nullptr;
   size_t skwork_cap = 0;
-  // MMQ images of Q6_K weights (qhip_launch_mmq_prepare), built by
-  // prepare_linear or by the first prefill outside a graph capture, kept
-  // until free_linear / destroy.  Keyed by the whole linear (device bytes,
-  // type, rows, cols): a different weight wrapped at a reused address never
-  // meets a stale image.
+  // MMQ images of Q6_K weights: the two-plane image of the prefill MMQ
+  // (qhip_launch_mmq_prepare, kind kImgMmq) and the fragment image of the
+  // few-token MMQ (qhip_launch_wd_prepare, kind kImgFrag), built by
+  // prepare_linear or by the first product that reads them outside a graph
+  // capture, kept until free_linear / destroy.  Keyed by the whole linear
+  // (device bytes, type, rows, cols) and the kind: a different weight wrapped
+  // at a reused address never meets a stale image.
   struct ImageKey {
     const void* dev;
-    int ttype, rows, cols;
+    int ttype, rows, cols, kind;
     bool operator<(const ImageKey& o) const {
       if (dev != o.dev) return dev < o.dev;
       if (ttype != o.ttype) return ttype < o.ttype;
       if (rows != o.rows) return rows < o.rows;
-      return cols < o.cols;
+      if (cols != o.cols) return cols < o.cols;
+      return kind < o.kind;
     }
   };
   struct Image {
@@ -180,16 +184,19 @@ static hipError_t ensure_skwork(qhip_backend* be, size_t bytes) {
   return hipSuccess;
 }
 
-// The MMQ image of a Q6_K weight: looked up, or built now when images are on,
+static constexpr int kImgMmq = 0, kImgFrag = 1;
+
+// An MMQ image of a Q6_K weight: looked up, or built now when images are on,
 // the budget allows it and the stream is not being captured (building
-// allocates).  nullptr = run the tile MMQ on the GGUF bytes instead.
-static void* image_for(qhip_backend* be, const void* wdev, int ttype, int rows, int cols, hipError_t* err) {
+// allocates).  nullptr = run the MMQ on the GGUF bytes instead.
+static void* image_for(qhip_backend* be, const void* wdev, int ttype, int rows, int cols, int kind,
+                       hipError_t* err) {
   *err = hipSuccess;
-  const qhip_backend::ImageKey key{wdev, ttype, rows, cols};
+  const qhip_backend::ImageKey key{wdev, ttype, rows, cols, kind};
   auto it = be->images.find(key);
   if (it != be->images.end()) return it->second.p;
   if (!be->images_on || capturing(be->stream)) return nullptr;
-  const long n = qhip_mmq_image_bytes(ttype, rows, cols);
+  const long n = kind == kImgFrag ? qhip_wd_image_bytes(ttype, rows, cols) : qhip_mmq_image_bytes(ttype, rows, cols);
   if (n <= 0 || over_budget(be, (size_t)n)) return nullptr;
   void* img = nullptr;
   hipError_t e = hipMalloc(&img, (size_t)n);
@@ -197,7 +204,8 @@ static void* image_for(qhip_backend* be, const void* wdev, int ttype, int rows, 
     *err = e;
     return nullptr;
   }
-  const int rc = qhip_launch_mmq_prepare(ttype, wdev, rows, cols, img, be->stream);
+  const int rc = kind == kImgFrag ? qhip_launch_wd_prepare(ttype, wdev, rows, cols, img, be->stream)
+                                  : qhip_launch_mmq_prepare(ttype, wdev, rows, cols, img, be->stream);
   if (rc) {
     (void)hipFree(img);
     *err = (hipError_t)rc;
@@ -407,9 +415,17 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   }
   void* work = be->skwork;
   const long work_bytes = (long)be->skwork_cap;
+  if (wd_image_preferred(g)) {
+    // a few tokens of a Q6_K weight: the MMQ from its fragment image
+    void* img = image_for(be, wdev, ttype, rows, cols, kImgFrag, &e);
+    if (e != hipSuccess) return report("fragment image", e);
+    if (img)
+      return report("matvec", (hipError_t)qhip_launch_mul_mat_wd_image(img, be->act, out, rows, cols, k, ttype, work,
+                                                                        work_bytes, be->stream));
+  }
   if (mmq_image_preferred(g)) {
     // prefill of a Q6_K weight: MMQ from its image when there is one
-    void* img = image_for(be, wdev, ttype, rows, cols, &e);
+    void* img = image_for(be, wdev, ttype, rows, cols, kImgMmq, &e);
     if (e != hipSuccess) return report("MMQ image", e);
     if (img)
       return report("matvec", (hipError_t)qhip_launch_mul_mat_image(img, be->act, out, rows, cols, k, ttype, 0, 0,
@@ -509,14 +525,19 @@ int qhip_backend_prepare_linear(qhip_backend* be, const qhip_linear* w) {
     if (e != hipSuccess) return report("GEMV image", e);
     if (!img) return QHIP_DECLINE;
   }
-  const GemvArgs g{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 4096, w->row_bytes,
-                   qhip_act_row_bytes(w->ttype, w->cols)};
-  if (!mmq_image_preferred(g)) return 0;  // no MMQ image serves this weight
-  if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;
-  hipError_t e;
-  void* img = image_for(be, w->dev, w->ttype, w->rows, w->cols, &e);
-  if (e != hipSuccess) return report("MMQ image", e);
-  return img ? 0 : QHIP_DECLINE;
+  // a few tokens (the fragment image) and a long prefill (the MMQ image)
+  int rc = 0;
+  for (const int kind : {kImgFrag, kImgMmq}) {
+    const GemvArgs g{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, kind == kImgFrag ? 8 : 4096,
+                     w->row_bytes, qhip_act_row_bytes(w->ttype, w->cols)};
+    if (!(kind == kImgFrag ? wd_image_preferred(g) : mmq_image_preferred(g))) continue;
+    if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;
+    hipError_t e;
+    void* img = image_for(be, w->dev, w->ttype, w->rows, w->cols, kind, &e);
+    if (e != hipSuccess) return report(kind == kImgFrag ? "fragment image" : "MMQ image", e);
+    if (!img) rc = QHIP_DECLINE;
+  }
+  return rc;
 }
 
 int qhip_backend_set_mmq_images(qhip_backend* be, int on) {

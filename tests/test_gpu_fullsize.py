@@ -209,6 +209,7 @@ def test_backend_image_budget_and_opt_out(gpu, oracle):
     x = synth.make_act(cols, T, seed=3)
     want = oracle.matvec(tt, w, x, nthreads=THREADS)
     img_bytes = rows * cols // 256 * 528
+    frag_bytes = rows * cols // 256 * 210  # the few-token fragment image, built with it
     xd = to_dev(x, gpu)
     for mode in ("capped", "off", "prepared"):
         be = ops.Backend(0)
@@ -221,7 +222,7 @@ def test_backend_image_budget_and_opt_out(gpu, oracle):
                 be.set_mmq_images(False)
             else:
                 assert be.prepare_linear(lin) == 0
-                assert be.mem_placed() == base + img_bytes
+                assert be.mem_placed() == base + img_bytes + frag_bytes
             out = torch.empty((T, rows), device=gpu)
             for rep in range(2):
                 be.matvec_batch_k(out, lin, xd, T)

@@ -116,3 +116,40 @@ def test_wd_image_model_shapes(gpu, oracle, rows, cols, tokens):
     got = ops.mul_mat_wd_image(TQ6, img, xq, rows, cols, tokens, work)
     want = oracle.matvec(TQ6, w[: min(rows, 512)], x) if rows > 512 else oracle.matvec(TQ6, w, x)
     assert rel_l2(got.cpu().numpy()[:, : want.shape[1]], want) < TOL
+
+
+@pytest.fixture()
+def backend(gpu):
+    be = ops.Backend(0)
+    yield be
+    be.close()
+
+
+@pytest.mark.parametrize("tokens", [2, 3, 5, 8, 24, 32, 33])
+def test_backend_few_tokens_from_fragment_image(gpu, oracle, backend, tokens):
+    """matvecBatchK of a large Q6_K weight: the fragment image from 3 to 32
+    tokens (built by prepare_linear), the same integers as the GGUF-row MMQ
+    the backend runs with images off; GEMV below 3 tokens, the tile MMQ above
+    32."""
+    rows, cols = 2048, 4608
+    w = synth.make_weight(TQ6, rows, cols, seed=46, tag=TQ6)
+    x = synth.make_act(cols, tokens, seed=46, tag=tokens)
+    lin = backend.load_linear(TQ6, rows, cols, w)
+    base = backend.mem_placed()
+    assert backend.prepare_linear(lin) == 0
+    assert backend.mem_placed() - base >= rows * cols // 256 * (210 + 528)  # fragment + MMQ images
+    xd = to_dev(x, gpu)
+    out = torch.empty((tokens, rows), device=gpu)
+    backend.matvec_batch_k(out, lin, xd, tokens)
+    backend.sync()
+    got = out.cpu().numpy()
+    assert rel_l2(got, oracle.matvec(TQ6, w, x)) < TOL
+    backend.set_mmq_images(False)
+    off = torch.empty((tokens, rows), device=gpu)
+    backend.matvec_batch_k(off, lin, xd, tokens)
+    backend.sync()
+    if 6 <= tokens <= 24:
+        assert np.array_equal(off.cpu().numpy(), got)  # the GGUF-row kernel, same order
+    else:
+        assert rel_l2(off.cpu().numpy(), got) < 1e-6
+    backend.set_mmq_images(True)
