@@ -366,13 +366,17 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
  * Q4_0 weight large enough for the decode matvec to read it
  * (qhip_launch_gemv_prepare, the GGUF bytes once more; built in load order,
  * so adjacent weights get adjacent images and matvecPair stays one launch),
- * and the MMQ image of a Q6_K weight (qhip_launch_mmq_prepare, 2.5x the GGUF
- * bytes).  0 = built or nothing to build; QHIP_DECLINE = not built (images
- * off, or past the memory budget): the products then read the GGUF bytes.
+ * and the two images of a Q6_K weight: the fragment image of the few-token
+ * MMQ (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads
+ * it at 3..32 tokens when rows * cols >= 2^23) and the MMQ image of the
+ * prefill (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 96 tokens).
+ * 0 = built or nothing to build; QHIP_DECLINE = not all built (images off, or
+ * past the memory budget): the products then read the GGUF bytes.
  * No reference counterpart (its CUDA kernels decode the GGUF blocks in every
  * launch). */
 int qhip_backend_prepare_linear(qhip_backend *be, const qhip_linear *w);
-/* MMQ images on (default) or off; off, matvec_batch_k never builds one. */
+/* MMQ images (the Q6_K fragment and MMQ images) on (default) or off; off,
+ * matvec_batch_k never builds or reads one. */
 int qhip_backend_set_mmq_images(qhip_backend *be, int on);
 /* GEMV images on (default) or off; off, matvec never builds or reads one. */
 int qhip_backend_set_gemv_images(qhip_backend *be, int on);
