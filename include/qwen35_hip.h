@@ -241,24 +241,29 @@ int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_ou
                               int tokens, int ttype, int tile_tokens, int tile_rows, void *d_work,
                               long work_bytes, void *stream);
 
-/* Q6_K fragment image (no reference counterpart; the reference's CUDA MMQ
- * decodes the GGUF blocks in every launch, mmq.cu:499-659).  The GGUF bytes
- * permuted -- the same 210 bytes per row and 256 values -- so that the
- * few-token MMQ loads each matrix-core fragment as one aligned, contiguous
- * 1 KB per wave instruction (a GGUF row's 210-byte blocks leave most of its
- * 8-byte pieces misaligned).  Rows in groups of 32, the last padded with zero
- * rows; group r, super-block b is a 6720-byte tile at (r * cols/256 + b) *
- * 6720: [0, 6144) lane L = i + 32k (row i, value half k) holds 24 dwords,
- * dwords 4c..4c+3 at 1024c + 16L; dwords 6j..6j+5 (j = 2h + m) are the 8
- * bytes of ql at 64h + 16m + 8k, of ql at 64h + 32 + 16m + 8k and of qh at
- * 128 + 32h + 16m + 8k; [6144, 6656) row i's 16 scales at 16i; [6656, 6720)
- * row i's f16 d at 2i.
- *   qhip_wd_image_bytes    image size, -1 unless ttype is Q6_K and cols % 256 == 0
+/* Fragment images of Q6_K and Q4_K weights (no reference counterpart; the
+ * reference's CUDA MMQ decodes the GGUF blocks in every launch,
+ * mmq.cu:499-659).  The GGUF bytes permuted -- the same bytes per row and 256
+ * values -- so that the weights-direct MMQ loads each matrix-core fragment as
+ * one aligned, contiguous 1 KB per wave instruction (a GGUF row's blocks
+ * otherwise give a wave instruction 32 rows' pieces, most of them misaligned
+ * for Q6_K's 210-byte blocks).  Rows in groups of 32, the last padded with
+ * zero rows; group r, super-block b is one tile at (r * cols/256 + b) * tile:
+ *   Q6_K, 6720-byte tiles: [0, 6144) lane L = i + 32k (row i, value half k)
+ *     holds 24 dwords, dwords 4c..4c+3 at 1024c + 16L; dwords 6j..6j+5
+ *     (j = 2h + m) are the 8 bytes of ql at 64h + 16m + 8k, of ql at
+ *     64h + 32 + 16m + 8k and of qh at 128 + 32h + 16m + 8k; [6144, 6656) row
+ *     i's 16 scales at 16i; [6656, 6720) row i's f16 d at 2i.
+ *   Q4_K, 4608-byte tiles: [0, 4096) lane L holds qs bytes 32c + 16k .. +15
+ *     of row i at 1024c + 16L (c < 4); [4096, 4608) row i's 16-byte header
+ *     (d, dmin, scales) at 16i.
+ *   qhip_wd_image_bytes    image size, -1 unless ttype is Q6_K / Q4_K and cols % 256 == 0
  *   qhip_launch_wd_prepare build it from GGUF bytes (d_image 16-byte aligned)
- *   qhip_launch_mul_mat_wd_image  d_out [tokens, rows] from the image, 1..32
- *     tokens (Q8_K activations as for qhip_launch_mul_mat); d_work (nullable)
- *     as for qhip_launch_mul_mat_work, qhip_mul_mat_work_bytes covers it; the
- *     same block integers as the reference, float sums within its rounding */
+ *   qhip_launch_mul_mat_wd_image  d_out [tokens, rows] from the image (Q6_K
+ *     1..32 tokens, Q4_K any count; Q8_K activations as for
+ *     qhip_launch_mul_mat); d_work (nullable) as for qhip_launch_mul_mat_work,
+ *     qhip_mul_mat_work_bytes covers it; the same bits as the MMQ on the GGUF
+ *     rows (QHIP_PATH_MMQ) with the same workspace */
 long qhip_wd_image_bytes(int ttype, int rows, int cols);
 int qhip_launch_wd_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
 int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
@@ -366,17 +371,17 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
  * Q4_0 weight large enough for the decode matvec to read it
  * (qhip_launch_gemv_prepare, the GGUF bytes once more; built in load order,
  * so adjacent weights get adjacent images and matvecPair stays one launch),
- * and the two images of a Q6_K weight: the fragment image of the few-token
- * MMQ (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads
- * it at 3..32 tokens when rows * cols >= 2^23) and the MMQ image of the
- * prefill (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 96 tokens).
+ * the fragment image of a Q6_K or Q4_K weight with rows * cols >= 2^23
+ * (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads it
+ * from 3 tokens, Q6_K up to 32) and the MMQ image of a Q6_K weight
+ * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 96 tokens).
  * 0 = built or nothing to build; QHIP_DECLINE = not all built (images off, or
  * past the memory budget): the products then read the GGUF bytes.
  * No reference counterpart (its CUDA kernels decode the GGUF blocks in every
  * launch). */
 int qhip_backend_prepare_linear(qhip_backend *be, const qhip_linear *w);
-/* MMQ images (the Q6_K fragment and MMQ images) on (default) or off; off,
- * matvec_batch_k never builds or reads one. */
+/* MMQ images (the fragment images and the Q6_K MMQ image) on (default) or
+ * off; off, matvec_batch_k never builds or reads one. */
 int qhip_backend_set_mmq_images(qhip_backend *be, int on);
 /* GEMV images on (default) or off; off, matvec never builds or reads one. */
 int qhip_backend_set_gemv_images(qhip_backend *be, int on);

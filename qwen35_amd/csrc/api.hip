@@ -110,15 +110,20 @@ bool mmq_image_preferred(const GemvArgs& g) {
   return g.ttype == TT_Q6_K && g.tokens >= 96 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
-// Few tokens of a large Q6_K weight: the Exec mirror multiplies them from the
-// weight's fragment image (the GGUF bytes once more, permuted).  Measured on
-// MI355X, [5120, 17408]: 21.0 / 21.3 / 24.0 / 28.0 / 34.1 us at 2 / 4 / 16 /
-// 24 / 32 tokens from the image, against GEMV 19.5 / 27.2 us at 2 / 4 and the
-// GGUF-row MMQ 31.4 / 31.5 / 34.2 / 37.0 / 37.6 us: the image from 3 tokens
-// (GEMV about 23 us there) up to its 32-token limit.
+// Batches of a large Q6_K or Q4_K weight: the Exec mirror multiplies them
+// from the weight's fragment image (the GGUF bytes once more, permuted).
+// Measured on MI355X: Q6_K [5120, 17408] 21.0 / 21.3 / 24.0 / 28.0 / 34.1 us
+// at 2 / 4 / 16 / 24 / 32 tokens from the image, against GEMV 19.5 / 27.2 us at
+// 2 / 4 and the GGUF-row MMQ 31.4 / 31.5 / 34.2 / 37.0 / 37.6 us; Q4_K
+// [17408, 5120] 14.5 / 14.5 / 15.8 / 19.8 / 29.9 / 43.4 / 132.6 us at 2 / 4 /
+// 16 / 32 / 64 / 128 / 512 tokens, against GEMV 12.6 / 18.6 us at 2 / 4 and
+// the GGUF-row MMQ 16.5 / 16.7 / 17.9 / 21.7 / 33.2 / 46.2 / 141.6 us.  The
+// image from 3 tokens (GEMV about 23 / 15.5 us there); Q6_K up to its 32-token
+// limit (the MMQ image from 96).
 bool wd_image_preferred(const GemvArgs& g) {
-  return g.ttype == TT_Q6_K && g.tokens >= 3 && g.tokens <= 32 && (long)g.rows * g.cols >= (1L << 23) &&
-         wd_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+  if (g.tokens < 3 || (long)g.rows * g.cols < (1L << 23) || !fast_ok(g)) return false;
+  if (g.ttype == TT_Q6_K) return g.tokens <= 32 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
+  return g.ttype == TT_Q4_K && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
 }
 
 // `work` (nullable): the split-K workspace of the MMQ (mmq_work_bytes)
@@ -469,7 +474,7 @@ int qhip_launch_mul_mat_wd_image(const void* d_image, const void* d_xq, float* d
   GemvArgs g;
   hipError_t e = make_args(d_image, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
-  if (wd_image_bytes(ttype, rows, cols) < 0 || tokens > 32) return (int)hipErrorInvalidValue;
+  if (wd_image_bytes(ttype, rows, cols) < 0 || (ttype == TT_Q6_K && tokens > 32)) return (int)hipErrorInvalidValue;
   if (((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
   if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
   if (rows == 0 || tokens == 0) return 0;

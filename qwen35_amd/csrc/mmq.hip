@@ -1338,6 +1338,17 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
 // 24.1 / 24.1 / 24.2 / 32.5 for the tile kernel's split launch.
 constexpr int kWdRow = 304, kWdPieces = 19, kWdBR = 128;
 
+// Q4_K fragment image: the GGUF bytes permuted, the same 144 bytes per row and
+// super-block.  Rows in groups of 32 (the last group padded with zero rows);
+// group r, super-block sb is a 4608-byte tile at (r * nsb + sb) * 4608:
+//   [0, 4096)     lane L = i + 32 k (row i of the group, half k) holds the qs
+//                 bytes 32c + 16k .. +15 of row i at 1024 c + 16 L (c < 4)
+//   [4096, 4608)  row i's 16-byte header (d, dmin, the 12 scale bytes) at
+//                 4096 + 16 i
+// so each wave instruction of the weights-direct kernels loads one aligned,
+// contiguous 1 KB (512 bytes for the headers) instead of 32 rows' pieces.
+constexpr int kWdiTile4 = 4608;
+
 // Makes the loaded registers complete here: the compiler may otherwise sink
 // the prologue's weight loads past the barrier into the loop, where the wait
 // for them then stalls every iteration on the loads in flight for the next.
@@ -1352,7 +1363,7 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
   return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
 }
 
-template <int NA>
+template <int NA, bool IMG>
 __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                      float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                                      long act_bytes, int nsb, int ntile_t, int ksplit, int cps,
@@ -1366,8 +1377,15 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
   const int ks = g % ksplit;
   g /= ksplit;
   const int r0 = (g / ntile_t) * kWdBR, t0 = (g % ntile_t) * BT;
-  const int row = r0 + 32 * wv + li;
-  const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  const uint8_t* wrow;
+  if constexpr (IMG) {
+    // this wave's group of 32 rows (a group past the end re-reads the last)
+    const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
+    wrow = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile4;
+  } else {
+    const int row = r0 + 32 * wv + li;
+    wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  }
   const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
 
   // DMA piece p = 64*(4i + wave) + lane of the stage: token p/19, 16-byte
@@ -1395,10 +1413,17 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
   };
   u32x4 wh, wq[4];
   auto issue_w = [&](int sb, u32x4& h, u32x4 (&q)[4]) {
-    const uint8_t* b = wrow + 144L * sb;
-    h = *(const u32x4*)b;
+    if constexpr (IMG) {
+      const uint8_t* b = wrow + (long)kWdiTile4 * sb;
+      h = *(const u32x4*)(b + 4096 + 16 * li);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
+      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+    } else {
+      const uint8_t* b = wrow + 144L * sb;
+      h = *(const u32x4*)b;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
+    }
   };
 
   f32x16 acc[NA][1];
@@ -1510,7 +1535,57 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
 // first 4 NG elements cover tokens 0 .. 8 NG - 1.  The split-scale planes of
 // k_mmq_wd_q4k cost two products per weight value and two MFMAs whatever the
 // token count; here the per-weight work is the nibble extraction alone.
-template <int NG>
+// One super-block of k_mmq_wds_q4k / k_mmq_wdp_q4k: one MFMA per 32-value
+// sub-block on the raw nibbles, the sub-block scale applied to the integer
+// result on the NE kept elements, the mins through an exact f16 MFMA, then
+// acc[0][0] += dy * (d * isum - dmin * summs).  A macro, as the Q6_K one.
+#define QHIP_Q4K_SUPERBLOCK(wh_, wq_, A, arow)                                                                       \
+  do {                                                                                                               \
+    const i32x16 zero_ = {};                                                                                         \
+    const f32x16 fz_ = {};                                                                                           \
+    const uint32_t S0_ = (wh_).y, S1_ = (wh_).z, S2_ = (wh_).w;                                                      \
+    const uint32_t sc_lo_ = S0_ & 0x3F3F3F3Fu, mn_lo_ = S1_ & 0x3F3F3F3Fu;                                           \
+    const uint32_t sc_hi_ = (S2_ & 0x0F0F0F0Fu) | ((S0_ >> 2) & 0x30303030u);                                        \
+    const uint32_t mn_hi_ = ((S2_ >> 4) & 0x0F0F0F0Fu) | ((S1_ >> 2) & 0x30303030u);                                 \
+    int isum_[NE];                                                                                                   \
+    _Pragma("unroll") for (int e_ = 0; e_ < NE; ++e_) isum_[e_] = 0;                                                 \
+    _Pragma("unroll") for (int c_ = 0; c_ < 4; ++c_) {                                                               \
+      const uint32_t q0_ = (wq_)[c_].x, q1_ = (wq_)[c_].y, q2_ = (wq_)[c_].z, q3_ = (wq_)[c_].w;                     \
+      _Pragma("unroll") for (int hi_ = 0; hi_ < 2; ++hi_) {                                                          \
+        const int s_ = 2 * c_ + hi_;                                                                                 \
+        const i32x4 bq_ = {(int)((hi_ ? q0_ >> 4 : q0_) & 0x0F0F0F0Fu), (int)((hi_ ? q1_ >> 4 : q1_) & 0x0F0F0F0Fu), \
+                          (int)((hi_ ? q2_ >> 4 : q2_) & 0x0F0F0F0Fu), (int)((hi_ ? q3_ >> 4 : q3_) & 0x0F0F0F0Fu)}; \
+        const int sc_ = (int)(((s_ < 4 ? sc_lo_ : sc_hi_) >> (8 * (s_ & 3))) & 63u);                                 \
+        const i32x4 af_ = *(const i32x4*)((A) + (arow) * kWdRow + 32 * s_ + 16 * lh);                                \
+        const i32x16 S_ = __builtin_amdgcn_mfma_i32_32x32x32_i8(af_, bq_, zero_, 0, 0, 0);                           \
+        _Pragma("unroll") for (int e_ = 0; e_ < NE; ++e_) isum_[e_] += sc_ * S_[e_];                                 \
+      }                                                                                                              \
+    }                                                                                                                \
+    /* mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA */                                  \
+    const uint32_t mn_ = lh ? mn_hi_ : mn_lo_;                                                                       \
+    f16x8 bm_;                                                                                                       \
+    _Pragma("unroll") for (int k_ = 0; k_ < 4; ++k_) {                                                               \
+      const _Float16 m_ = (_Float16)(float)((mn_ >> (8 * k_)) & 255u);                                               \
+      bm_[2 * k_] = m_;                                                                                              \
+      bm_[2 * k_ + 1] = m_;                                                                                          \
+    }                                                                                                                \
+    const float d_ = h2f((wh_).x), ndm_ = -h2f((wh_).x >> 16);                                                       \
+    const i16x8 bs_ = *(const i16x8*)((A) + (arow) * kWdRow + 256 + 16 * lh);                                        \
+    f16x8 am_;                                                                                                       \
+    _Pragma("unroll") for (int k_ = 0; k_ < 8; ++k_) {                                                               \
+      const short v_ = bs_[k_];                                                                                      \
+      am_[k_] = (_Float16)v_;                                                                                        \
+    }                                                                                                                \
+    const f32x16 cm_ = __builtin_amdgcn_mfma_f32_32x32x16_f16(am_, bm_, fz_, 0, 0, 0);                               \
+    _Pragma("unroll") for (int e_ = 0; e_ < NE; ++e_) {                                                              \
+      const int t_ = 8 * (e_ >> 2) + 4 * lh + (e_ & 3);                                                              \
+      const float dy_ = *(const float*)((A) + t_ * kWdRow + 288);                                                    \
+      const float inner_ = __builtin_fmaf(d_, (float)isum_[e_], ndm_ * cm_[e_]);                                     \
+      acc[0][0][e_] = __builtin_fmaf(dy_, inner_, acc[0][0][e_]);                                                    \
+    }                                                                                                                \
+  } while (0)
+
+template <int NG, bool IMG>
 __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                       float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                                       long act_bytes, int nsb, int ksplit, int cps,
@@ -1524,8 +1599,15 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
   const int ks = g % ksplit;
   g /= ksplit;
   const int r0 = g * kWdBR;
-  const int row = r0 + 32 * wv + li;
-  const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  const uint8_t* wrow;
+  if constexpr (IMG) {
+    // this wave's group of 32 rows (a group past the end re-reads the last)
+    const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
+    wrow = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile4;
+  } else {
+    const int row = r0 + 32 * wv + li;
+    wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
+  }
   const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
 
   long goff[NDMA];
@@ -1549,10 +1631,17 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
   };
   u32x4 wh, wq[4];
   auto issue_w = [&](int sb, u32x4& h, u32x4 (&q)[4]) {
-    const uint8_t* b = wrow + 144L * sb;
-    h = *(const u32x4*)b;
+    if constexpr (IMG) {
+      const uint8_t* b = wrow + (long)kWdiTile4 * sb;
+      h = *(const u32x4*)(b + 4096 + 16 * li);
 #pragma unroll
-    for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
+      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+    } else {
+      const uint8_t* b = wrow + 144L * sb;
+      h = *(const u32x4*)b;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
+    }
   };
 
   f32x16 acc[1][1];
@@ -1578,53 +1667,7 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
       issue_act(sb + 1, nxt);
       issue_w(sb + 1, nh, nq);
     }
-    const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
-    const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
-    const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-    const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-    int isum[NE];
-#pragma unroll
-    for (int e = 0; e < NE; ++e) isum[e] = 0;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t q0 = wq[c].x, q1 = wq[c].y, q2 = wq[c].z, q3 = wq[c].w;
-#pragma unroll
-      for (int hi = 0; hi < 2; ++hi) {
-        const int s = 2 * c + hi;
-        const i32x4 bq = {(int)((hi ? q0 >> 4 : q0) & 0x0F0F0F0Fu), (int)((hi ? q1 >> 4 : q1) & 0x0F0F0F0Fu),
-                          (int)((hi ? q2 >> 4 : q2) & 0x0F0F0F0Fu), (int)((hi ? q3 >> 4 : q3) & 0x0F0F0F0Fu)};
-        const int sc = (int)(((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 63u);
-        const i32x4 af = *(const i32x4*)(A + li * kWdRow + 32 * s + 16 * lh);
-        const i32x16 S = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bq, zero, 0, 0, 0);
-#pragma unroll
-        for (int e = 0; e < NE; ++e) isum[e] += sc * S[e];
-      }
-    }
-    // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
-    const uint32_t mn = lh ? mn_hi : mn_lo;
-    f16x8 bm;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const _Float16 m = (_Float16)(float)((mn >> (8 * k)) & 255u);
-      bm[2 * k] = m;
-      bm[2 * k + 1] = m;
-    }
-    const float d = h2f(wh.x), ndm = -h2f(wh.x >> 16);
-    const i16x8 bs = *(const i16x8*)(A + li * kWdRow + 256 + 16 * lh);
-    f16x8 am;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const short v = bs[k];
-      am[k] = (_Float16)v;
-    }
-    const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, fz, 0, 0, 0);
-#pragma unroll
-    for (int e = 0; e < NE; ++e) {
-      const int t = 8 * (e >> 2) + 4 * lh + (e & 3);
-      const float dy = *(const float*)(A + t * kWdRow + 288);
-      const float inner = __builtin_fmaf(d, (float)isum[e], ndm * cm[e]);
-      acc[0][0][e] = __builtin_fmaf(dy, inner, acc[0][0][e]);
-    }
+    QHIP_Q4K_SUPERBLOCK(wh, wq, A, li);
     __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
     __syncthreads();
     if (sb + 1 < sb1) {
@@ -1707,52 +1750,52 @@ struct Q6Regs<true> {
 // offset on the NE kept elements, then acc[0][0] += dy * d * isum.  A macro,
 // not a function: the same code behind a call boundary (even forced inline)
 // is scheduled with 13-93 more VGPRs by this compiler.
-#define QHIP_Q6K_SUPERBLOCK(wc, A, arow)                                                               \
-  do {                                                                                                 \
-    const i32x16 zero_ = {};                                                                           \
-    const f32x16 fz_ = {};                                                                             \
-    const uint32_t scw[4] = {(wc).sc.x, (wc).sc.y, (wc).sc.z, (wc).sc.w};                              \
-    int isum[NE];                                                                                      \
-    _Pragma("unroll") for (int e = 0; e < NE; ++e) isum[e] = 0;                                        \
-    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                                    \
-      const int h = j >> 1, m = j & 1;                                                                 \
-      _Pragma("unroll") for (int q = 0; q < 4; ++q) {                                                  \
-        const int grp = 8 * h + m + 2 * q;                                                             \
-        uint32_t v[2];                                                                                 \
-        _Pragma("unroll") for (int k = 0; k < 2; ++k) {                                                \
-          const uint32_t l = (wc).ql(j, q & 1, k), x = (wc).qhi(j, k);                                 \
-          const uint32_t nib = (q >= 2 ? l >> 4 : l) & 0x0F0F0F0Fu;                                    \
-          const uint32_t hi = q == 0 ? (x << 4) & 0x30303030u                                          \
-                              : q == 1 ? (x << 2) & 0x30303030u                                        \
-                              : q == 2 ? x & 0x30303030u                                               \
-                                       : (x >> 2) & 0x30303030u;                                       \
-          v[k] = nib | hi;                                                                             \
-        }                                                                                              \
-        const long bq = (long)(((unsigned long)v[1] << 32) | v[0]);                                    \
-        const long af = *(const long*)((A) + (arow) * kWdRow + 16 * grp + 8 * lh);                     \
-        const i32x16 S = __builtin_amdgcn_mfma_i32_32x32x16_i8(af, bq, zero_, 0, 0, 0);                \
-        const int sc = (int)(int8_t)(scw[grp >> 2] >> (8 * (grp & 3)));                                \
-        _Pragma("unroll") for (int e = 0; e < NE; ++e) isum[e] += sc * S[e];                           \
-      }                                                                                                \
-    }                                                                                                  \
-    /* sum_g sc_g bsum_g[t], exact in the f16 MFMA: A = the token's 8 bsums of                         \
-       groups 8(l/32)..+7, B = the row's scales of the same groups */                                  \
-    const i16x8 bs = *(const i16x8*)((A) + (arow) * kWdRow + 256 + 16 * lh);                           \
-    f16x8 am, bm;                                                                                      \
-    _Pragma("unroll") for (int k = 0; k < 8; ++k) {                                                    \
-      const short bv = bs[k];                                                                          \
-      am[k] = (_Float16)bv;                                                                            \
-      bm[k] = (_Float16)(float)(int)(int8_t)(scw[2 * lh + (k >> 2)] >> (8 * (k & 3)));                 \
-    }                                                                                                  \
-    const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, fz_, 0, 0, 0);                    \
-    const float dw = h2f((wc).d);                                                                      \
-    /* the reference's integer (kernels256.c:720-738) */                                               \
-    _Pragma("unroll") for (int e = 0; e < NE; ++e) {                                                   \
-      const int t = 8 * (e >> 2) + 4 * lh + (e & 3);                                                   \
-      const float dy = *(const float*)((A) + t * kWdRow + 288);                                        \
-      const int tot = isum[e] - 32 * (int)cm[e];                                                       \
-      acc[0][0][e] = __builtin_fmaf(dy, dw * (float)tot, acc[0][0][e]);                                \
-    }                                                                                                  \
+#define QHIP_Q6K_SUPERBLOCK(wc, A, arow)                                                   \
+  do {                                                                                     \
+    const i32x16 zero_ = {};                                                               \
+    const f32x16 fz_ = {};                                                                 \
+    const uint32_t scw_[4] = {(wc).sc.x, (wc).sc.y, (wc).sc.z, (wc).sc.w};                 \
+    int isum_[NE];                                                                         \
+    _Pragma("unroll") for (int e_ = 0; e_ < NE; ++e_) isum_[e_] = 0;                       \
+    _Pragma("unroll") for (int j_ = 0; j_ < 4; ++j_) {                                     \
+      const int h_ = j_ >> 1, m_ = j_ & 1;                                                 \
+      _Pragma("unroll") for (int q_ = 0; q_ < 4; ++q_) {                                   \
+        const int grp_ = 8 * h_ + m_ + 2 * q_;                                             \
+        uint32_t v_[2];                                                                    \
+        _Pragma("unroll") for (int k_ = 0; k_ < 2; ++k_) {                                 \
+          const uint32_t l_ = (wc).ql(j_, q_ & 1, k_), x_ = (wc).qhi(j_, k_);              \
+          const uint32_t nib_ = (q_ >= 2 ? l_ >> 4 : l_) & 0x0F0F0F0Fu;                    \
+          const uint32_t hi_ = q_ == 0 ? (x_ << 4) & 0x30303030u                           \
+                              : q_ == 1 ? (x_ << 2) & 0x30303030u                          \
+                              : q_ == 2 ? x_ & 0x30303030u                                 \
+                                       : (x_ >> 2) & 0x30303030u;                          \
+          v_[k_] = nib_ | hi_;                                                             \
+        }                                                                                  \
+        const long bq_ = (long)(((unsigned long)v_[1] << 32) | v_[0]);                     \
+        const long af_ = *(const long*)((A) + (arow) * kWdRow + 16 * grp_ + 8 * lh);       \
+        const i32x16 S_ = __builtin_amdgcn_mfma_i32_32x32x16_i8(af_, bq_, zero_, 0, 0, 0); \
+        const int sc_ = (int)(int8_t)(scw_[grp_ >> 2] >> (8 * (grp_ & 3)));                \
+        _Pragma("unroll") for (int e_ = 0; e_ < NE; ++e_) isum_[e_] += sc_ * S_[e_];       \
+      }                                                                                    \
+    }                                                                                      \
+    /* sum_g sc_g bsum_g[t], exact in the f16 MFMA: A = the token's 8 bsums of              \
+       groups 8(l/32)..+7, B = the row's scales of the same groups */                       \
+    const i16x8 bs_ = *(const i16x8*)((A) + (arow) * kWdRow + 256 + 16 * lh);              \
+    f16x8 am_, bm_;                                                                         \
+    _Pragma("unroll") for (int k_ = 0; k_ < 8; ++k_) {                                     \
+      const short bv_ = bs_[k_];                                                           \
+      am_[k_] = (_Float16)bv_;                                                             \
+      bm_[k_] = (_Float16)(float)(int)(int8_t)(scw_[2 * lh + (k_ >> 2)] >> (8 * (k_ & 3))); \
+    }                                                                                      \
+    const f32x16 cm_ = __builtin_amdgcn_mfma_f32_32x32x16_f16(am_, bm_, fz_, 0, 0, 0);      \
+    const float dw_ = h2f((wc).d);                                                         \
+    /* the reference's integer (kernels256.c:720-738) */                                   \
+    _Pragma("unroll") for (int e_ = 0; e_ < NE; ++e_) {                                    \
+      const int t_ = 8 * (e_ >> 2) + 4 * lh + (e_ & 3);                                    \
+      const float dy_ = *(const float*)((A) + t_ * kWdRow + 288);                          \
+      const int tot_ = isum_[e_] - 32 * (int)cm_[e_];                                      \
+      acc[0][0][e_] = __builtin_fmaf(dy_, dw_ * (float)tot_, acc[0][0][e_]);               \
+    }                                                                                      \
   } while (0)
 
 // DMA offsets of the activation pieces a lane moves: piece P = 64 (4i + wave)
@@ -1907,7 +1950,10 @@ __global__ __launch_bounds__(256) void k_mmq_wdp_q6k(const uint8_t* __restrict__
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < CPS; ++s)
-      if (s < n) QHIP_Q6K_SUPERBLOCK(wr[s], act + s * STAGE, arow);
+      if (s < n) {
+        const uint8_t* As = act + s * STAGE;
+        QHIP_Q6K_SUPERBLOCK(wr[s], As, arow);
+      }
     __syncthreads();  // the next group's DMA overwrites the stages
   }
   mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
@@ -1957,9 +2003,37 @@ __global__ __launch_bounds__(256) void k_wd_prepare_q6k(const uint8_t* __restric
   }
 }
 
+// One thread per (tile, lane L) of the Q4_K fragment image: lane L's four
+// 16-byte qs pieces; lanes L < 32 also the row's header.  Rows past the end:
+// zeros.  GGUF Q4_K rows are 144 bytes per super-block: every piece aligned.
+__global__ __launch_bounds__(256) void k_wd_prepare_q4k(const uint8_t* __restrict__ W, uint8_t* __restrict__ IMG,
+                                                         int rows, long row_bytes, int nsb, long nthreads) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= nthreads) return;
+  const int L = (int)(gid & 63), i = L & 31, k = L >> 5;
+  const long tile = gid >> 6;  // group * nsb + sb
+  const long grp = tile / nsb;
+  const int sb = (int)(tile - grp * nsb);
+  const long row = grp * 32 + i;
+  uint8_t* t = IMG + tile * kWdiTile4;
+  uint4 q[4], h = make_uint4(0u, 0u, 0u, 0u);
+  if (row < rows) {
+    const uint8_t* b = W + row * row_bytes + 144L * sb;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = *(const uint4*)(b + 16 + 32 * c + 16 * k);
+    h = *(const uint4*)b;
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) q[c] = make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) *(uint4*)(t + 1024 * c + 16 * L) = q[c];
+  if (k == 0) *(uint4*)(t + 4096 + 16 * i) = h;
+}
+
 long wd_image_bytes(int ttype, int rows, int cols) {
-  if (ttype != TT_Q6_K || rows < 0 || cols <= 0 || cols % 256) return -1;
-  return (long)((rows + 31) / 32) * (cols / 256) * kWdiTile;
+  if ((ttype != TT_Q6_K && ttype != TT_Q4_K) || rows < 0 || cols <= 0 || cols % 256) return -1;
+  return (long)((rows + 31) / 32) * (cols / 256) * (ttype == TT_Q6_K ? kWdiTile : kWdiTile4);
 }
 
 hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
@@ -1968,9 +2042,77 @@ hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows,
   const int nsb = cols / 256;
   const long n = (long)((rows + 31) / 32) * nsb * 64;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_wd_prepare_q6k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
-                     (uint8_t*)img, rows, row_bytes, nsb, n);
+  if (ttype == TT_Q6_K)
+    hipLaunchKernelGGL(k_wd_prepare_q6k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
+                       (uint8_t*)img, rows, row_bytes, nsb, n);
+  else
+    hipLaunchKernelGGL(k_wd_prepare_q4k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
+                       (uint8_t*)img, rows, row_bytes, nsb, n);
   return hipGetLastError();
+}
+
+// The Q4_K fragment image, T <= 8 NG (NG < 4): the structure of
+// k_mmq_wdp_q6k -- the workgroup's K slice in groups of CPS super-blocks, each
+// group's weight loads (5 per lane and super-block) and activation DMA of the
+// 8 NG kept token rows all issued before any of it is used.
+template <int NG, int CPS>
+__global__ __launch_bounds__(256) void k_mmq_wdp_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                      float* __restrict__ Y, int rows, int tokens, long act_bytes,
+                                                      int nsb, int ksplit, int cps, float* __restrict__ part,
+                                                      unsigned* __restrict__ cnt) {
+  constexpr int TR = 8 * NG, NE = 4 * NG;
+  constexpr int STAGE = TR * kWdRow, NPC = TR * kWdPieces, NDMA = (CPS * NPC + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint8_t act[CPS * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
+  const int ks = g % ksplit;
+  g /= ksplit;
+  const int r0 = g * kWdBR;
+  const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
+  const uint8_t* wbase = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile4;
+  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
+  const int arow = li < TR ? li : 0;
+
+  long goff[NDMA];
+  int gst[NDMA];
+  wd_dma_plan<NDMA, TR>(wv, lane, tokens, act_bytes, CPS, goff, gst);
+
+  f32x16 acc[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[0][0][e] = 0.0f;
+
+  for (int base = sb0; base < sb1; base += CPS) {
+    const int n = sb1 - base < CPS ? sb1 - base : CPS;
+    u32x4 wh[CPS], wq[CPS][4];
+#pragma unroll
+    for (int s = 0; s < CPS; ++s) {
+      if (s < n) {
+        const uint8_t* b = wbase + (long)kWdiTile4 * (base + s);
+        wh[s] = *(const u32x4*)(b + 4096 + 16 * li);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) wq[s][c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      if (4 * i + wv < (CPS * NPC + 63) / 64 && gst[i] < n)
+        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * (base + gst[i])),
+                                         (__attribute__((address_space(3))) void*)(act + 1024 * (4 * i + wv)), 16,
+                                         0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // every weight register and DMA piece of the group
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < CPS; ++s)
+      if (s < n) {
+        const uint8_t* As = act + s * STAGE;
+        QHIP_Q4K_SUPERBLOCK(wh[s], wq[s], As, arow);
+      }
+    __syncthreads();  // the next group's DMA overwrites the stages
+  }
+  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
 }
 
 // Tokens per weights-direct tile: 32 up to 32 tokens (a 64-token tile would
@@ -1989,6 +2131,7 @@ static int wd_slices(const GemvArgs& g) {
   return mmq_slices(nsb, mmq_ksplit_for(g, wd_bt(g), kWdBR, nsb, 2));
 }
 
+template <bool IMG>
 static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
   const int bt = wd_bt(g), nsb = g.cols / 256;
   const long ntt = (g.tokens + bt - 1) / bt, ntr = (g.rows + kWdBR - 1) / kWdBR;
@@ -2002,17 +2145,17 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipSt
     const int ng = (g.tokens + 7) / 8;
 #define QHIP_WDS(N)                                                                                          \
   if (ng == N)                                                                                               \
-    hipLaunchKernelGGL(k_mmq_wds_q4k<N>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,            \
+    hipLaunchKernelGGL((k_mmq_wds_q4k<N, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,            \
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, ksplit, cps, \
                        part, cnt);
     QHIP_WDS(1) QHIP_WDS(2) QHIP_WDS(3)
 #undef QHIP_WDS
   } else if (bt == 32)
-    hipLaunchKernelGGL(k_mmq_wd_q4k<1>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+    hipLaunchKernelGGL((k_mmq_wd_q4k<1, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
                        ksplit, cps, part, cnt);
   else
-    hipLaunchKernelGGL(k_mmq_wd_q4k<2>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+    hipLaunchKernelGGL((k_mmq_wd_q4k<2, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
                        ksplit, cps, part, cnt);
   return hipGetLastError();
@@ -2046,9 +2189,29 @@ static hipError_t launch_mmq_wds_q6k(const GemvArgs& g, int ksplit, void* work, 
   return hipGetLastError();
 }
 
-// Q6_K from the fragment image, 1..32 tokens; work as for launch_mmq (the
-// same slices as the GGUF-row launch, so mmq_work_bytes covers it).
+// From the fragment image: Q6_K 1..32 tokens, Q4_K any count; work as for
+// launch_mmq (the same slices as the GGUF-row launch, so mmq_work_bytes
+// covers it).
 hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s) {
+  if (g.ttype == TT_Q4_K) {
+    if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+    int ksplit = wd_slices(g);
+    if (!work || work_bytes < mmq_split_bytes(g, wd_bt(g), kWdBR, ksplit)) ksplit = 1;
+    // up to 8 tokens: the whole-group prefetch (14.4-14.6 us at config 5,
+    // against 15.0-15.2 double-buffered); beyond, the double-buffered kernels
+    // (15.8 / 19.8 us at 16 / 24 tokens, against 16.8 / 19.3)
+    if (g.tokens > 8) return launch_mmq_wd<true>(g, ksplit, work, s);
+    const int nsb = g.cols / 256;
+    const long ntr = (g.rows + kWdBR - 1) / kWdBR;
+    const int cps = (nsb + ksplit - 1) / ksplit;
+    const long G = ntr * ksplit;
+    if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr > kSkMaxTiles)) return hipErrorInvalidValue;
+    unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
+    float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
+    hipLaunchKernelGGL((k_mmq_wdp_q4k<1, 2>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, nsb, ksplit, cps, part, cnt);
+    return hipGetLastError();
+  }
   if (g.ttype != TT_Q6_K || g.tokens < 1 || g.tokens > 32) return hipErrorInvalidValue;
   if (g.rows <= 0) return hipSuccess;
   int ksplit = wds_q6k_slices(g);
@@ -2094,7 +2257,7 @@ static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit,
   // Q4_K's 64 x 128 tile is the weights-direct kernel (never split when
   // asked for explicitly)
   if constexpr (TT == TT_Q4_K)
-    if (bt == 64 && br == 128) return launch_mmq_wd(g, ksplit, work, s);
+    if (bt == 64 && br == 128) return launch_mmq_wd<false>(g, ksplit, work, s);
   if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, work, s);
   if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, work, s);
   if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, work, s);

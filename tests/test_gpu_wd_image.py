@@ -1,8 +1,9 @@
-"""GPU: the Q6_K fragment image -- its layout restated on the host from the
-GGUF bytes, the few-token MMQ read from it against the oracle at every token
-count either side of each kernel variant (1..32) and row counts off the
-32-row groups, the same bits as the GGUF-row few-token kernel, exact block
-integers at unit scales, extreme 6-bit values and scales, bit-equal reruns."""
+"""GPU: the Q6_K and Q4_K fragment images -- their layouts restated on the
+host from the GGUF bytes, the weights-direct MMQ read from them against the
+oracle at token counts either side of each kernel variant and row counts off
+the 32-row groups, the same bits as the GGUF-row kernels, exact block
+integers at unit scales, extreme 6-bit values and scales, bit-equal reruns,
+and the Exec mirror reading the Q6_K image."""
 import numpy as np
 import pytest
 import torch
@@ -15,6 +16,7 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-5
 PATH_MMQ = 2
 TQ6 = po.TT_Q6_K
+TQ4 = po.TT_Q4_K
 
 
 def wd_image_of(w, rows, cols):
@@ -125,31 +127,102 @@ def backend(gpu):
     be.close()
 
 
-@pytest.mark.parametrize("tokens", [2, 3, 5, 8, 24, 32, 33])
-def test_backend_few_tokens_from_fragment_image(gpu, oracle, backend, tokens):
-    """matvecBatchK of a large Q6_K weight: the fragment image from 3 to 32
-    tokens (built by prepare_linear), the same integers as the GGUF-row MMQ
-    the backend runs with images off; GEMV below 3 tokens, the tile MMQ above
-    32."""
+@pytest.mark.parametrize("tt,tokens", [(TQ6, 2), (TQ6, 3), (TQ6, 5), (TQ6, 8), (TQ6, 24), (TQ6, 32), (TQ6, 33),
+                                       (po.TT_Q4_K, 2), (po.TT_Q4_K, 3), (po.TT_Q4_K, 8), (po.TT_Q4_K, 40),
+                                       (po.TT_Q4_K, 130)])
+def test_backend_batches_from_fragment_image(gpu, oracle, backend, tt, tokens):
+    """matvecBatchK of a large Q6_K / Q4_K weight: the fragment image from 3
+    tokens (Q6_K up to 32), built by prepare_linear, the same bits as the
+    GGUF-row MMQ the backend runs with images off; GEMV below 3 tokens."""
     rows, cols = 2048, 4608
-    w = synth.make_weight(TQ6, rows, cols, seed=46, tag=TQ6)
+    w = synth.make_weight(tt, rows, cols, seed=46, tag=tt)
     x = synth.make_act(cols, tokens, seed=46, tag=tokens)
-    lin = backend.load_linear(TQ6, rows, cols, w)
+    lin = backend.load_linear(tt, rows, cols, w)
     base = backend.mem_placed()
     assert backend.prepare_linear(lin) == 0
-    assert backend.mem_placed() - base >= rows * cols // 256 * (210 + 528)  # fragment + MMQ images
+    img = rows * cols // 256 * (210 + 528 if tt == TQ6 else 144)  # fragment (+ Q6_K MMQ) image
+    assert backend.mem_placed() - base >= img
     xd = to_dev(x, gpu)
     out = torch.empty((tokens, rows), device=gpu)
     backend.matvec_batch_k(out, lin, xd, tokens)
     backend.sync()
     got = out.cpu().numpy()
-    assert rel_l2(got, oracle.matvec(TQ6, w, x)) < TOL
+    assert rel_l2(got, oracle.matvec(tt, w, x)) < TOL
     backend.set_mmq_images(False)
     off = torch.empty((tokens, rows), device=gpu)
     backend.matvec_batch_k(off, lin, xd, tokens)
     backend.sync()
-    if 6 <= tokens <= 24:
+    mmq_from = 6 if tt == TQ6 else 5  # the GGUF rows' GEMV / MMQ crossover
+    if mmq_from <= tokens and (tt != TQ6 or tokens <= 24):
         assert np.array_equal(off.cpu().numpy(), got)  # the GGUF-row kernel, same order
     else:
         assert rel_l2(off.cpu().numpy(), got) < 1e-6
     backend.set_mmq_images(True)
+
+
+
+
+def wd_image_q4k_of(w, rows, cols):
+    """The documented Q4_K fragment-image layout, from the GGUF bytes."""
+    nsb = cols // 256
+    ngrp = (rows + 31) // 32
+    pad = np.zeros((ngrp * 32, nsb, 144), np.uint8)
+    pad[:rows] = w.reshape(rows, nsb, 144)
+    img = np.zeros((ngrp, nsb, 4608), np.uint8)
+    g = pad.reshape(ngrp, 32, nsb, 144).transpose(0, 2, 1, 3)  # [group, sb, row, 144]
+    for c in range(4):
+        for k in range(2):
+            img[:, :, 1024 * c + 512 * k:1024 * c + 512 * (k + 1)] = \
+                g[:, :, :, 16 + 32 * c + 16 * k:32 + 32 * c + 16 * k].reshape(ngrp, nsb, 512)
+    img[:, :, 4096:4608] = g[:, :, :, 0:16].reshape(ngrp, nsb, 512)
+    return img.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (31, 512), (32, 2304), (33, 256), (70, 1024)])
+def test_wd_image_q4k_layout(gpu, rows, cols):
+    w = synth.make_weight(TQ4, rows, cols, seed=50, tag=rows)
+    n = ops.load().qhip_wd_image_bytes(TQ4, rows, cols)
+    assert n == (rows + 31) // 32 * (cols // 256) * 4608
+    img = ops.wd_image(TQ4, to_dev(w, gpu), rows, cols).cpu().numpy()
+    assert np.array_equal(img[:n], wd_image_q4k_of(w, rows, cols))
+
+
+@pytest.fixture(scope="module")
+def q4(gpu):
+    rows, cols = 333, 5120
+    w = synth.make_weight(TQ4, rows, cols, seed=51, tag=TQ4)
+    wd = to_dev(w, gpu)
+    return rows, cols, w, wd, ops.wd_image(TQ4, wd, rows, cols)
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 8, 9, 24, 25, 32, 33, 64, 65, 130, 257])
+def test_wd_image_q4k_vs_oracle(gpu, oracle, q4, tokens):
+    """Every weights-direct Q4_K variant from the image: the same bits as from
+    the GGUF rows (same slices, same order)."""
+    rows, cols, w, wd, img = q4
+    x = synth.make_act(cols, tokens, seed=52, tag=tokens)
+    xq = ops.quantize_act(TQ4, to_dev(x, gpu))
+    work = ops.mul_mat_work(rows, cols, tokens, TQ4, gpu)
+    got = ops.mul_mat_wd_image(TQ4, img, xq, rows, cols, tokens, work)
+    assert rel_l2(got.cpu().numpy(), oracle.matvec(TQ4, w, x)) < TOL
+    assert torch.equal(got, ops.mul_mat_wd_image(TQ4, img, xq, rows, cols, tokens, work))
+    raw = ops.mul_mat_split(TQ4, wd, xq, rows, cols, tokens, work, PATH_MMQ)
+    assert torch.equal(got, raw)
+    plain = ops.mul_mat_wd_image(TQ4, img, xq, rows, cols, tokens)
+    assert rel_l2(plain.cpu().numpy(), got.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("tokens", [3, 20, 40, 72])
+def test_wd_image_q4k_integers_exact(gpu, oracle, tokens):
+    rows, cols = 96, 1024
+    w = unit_scale_weight(TQ4, rows, cols, seed=53)
+    x = unit_scale_act(cols, tokens, seed=53)
+    act = oracle.quantize_act(TQ4, x)
+    ints = oracle.block_ints(TQ4, w, act, cols).astype(np.int64)
+    want = ints[:, :, 0::2].sum(-1) - ints[:, :, 1::2].sum(-1)
+    assert np.abs(want).max() < 2 ** 24
+    img = ops.wd_image(TQ4, to_dev(w, gpu), rows, cols)
+    xq = ops.quantize_act(TQ4, to_dev(x, gpu))
+    work = ops.mul_mat_work(rows, cols, tokens, TQ4, gpu)
+    got = ops.mul_mat_wd_image(TQ4, img, xq, rows, cols, tokens, work).cpu().numpy()
+    assert np.array_equal(got, want.astype(np.float32))
