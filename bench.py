@@ -49,7 +49,8 @@ R3, C3 = 248320, 2560        # config 3 (output head)
 
 PROFILE_KERNELS = ["cfg3_gemv", "cfg3_step", "cfg3_gemv_gguf", "cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv",
                    "down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused",
-                   "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k"]
+                   "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
+                   "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8"]
 
 
 def log(*a):
@@ -362,10 +363,11 @@ def bench_mmq(c: Ctx):
     """Config 4: Q8_0 [3584,1024] with eight ragged sequences (lengths uniform on
     [16,256], packed by the ragged quantizer, one launch) and a dense 512-token
     sequence.  Config 5: Q4_K gate [17408,5120] and Q6_K down [5120,17408] at
-    T = 1, 4, 16, 64, 512 on the GEMV and on the MMQ (with the split-K
-    workspace the Exec mirror passes), and the crossover.  Throughput:
+    T = 1, 2, 4, 8, 16, 32, 64, 512 on the GEMV and on the MMQ (with the
+    split-K workspace the Exec mirror passes), and the crossover.  Throughput:
     tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak.  `mmq_us`
-    is the faster of the tile MMQ and (Q6_K) the image MMQ."""
+    is the fastest of the MMQ on the GGUF rows, from the fragment image and
+    (Q6_K) from the MMQ image; `mirror_us` is what the Exec mirror launches."""
     torch, lib, ops, synth, dev, stream = c.torch, c.lib, c.ops, c.synth, c.dev, c.stream
     res = {}
 
@@ -423,7 +425,7 @@ def bench_mmq(c: Ctx):
         # the prepared MMQ weight image the Exec mirror uses for Q6_K prefill,
         # and the fragment image it uses for 3..32 tokens
         img = ops.mmq_image(tt, w, rows, cols) if tt == TQ6 else None
-        frag = ops.wd_image(tt, w, rows, cols) if tt == TQ6 else None
+        frag = ops.wd_image(tt, w, rows, cols)
         rows_out = []
         cross = None
         for T in (1, 2, 4, 8, 16, 32, 64, 512):
@@ -446,19 +448,21 @@ def bench_mmq(c: Ctx):
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
             s_f = None
-            if frag is not None and T <= 32:
+            if tt == TQ4 or T <= 32:
                 s_f = timed(lambda: lib.qhip_launch_mul_mat_wd_image(frag.data_ptr(), aq.data_ptr(), y.data_ptr(),
                                                                      rows, cols, T, tt, wp, wn, stream), it)
                 pt["mmq_fragment_image_us"] = round(s_f * 1e6, 2)
                 s_m = min(s_m, s_f)
             # the C ABI's automatic path (GEMV or tile MMQ by the measured
             # crossover), and what the Exec mirror's matvecBatchK launches: the
-            # same, except the Q6_K fragment image at 3..32 tokens and the
-            # MMQ image from 96
+            # same, except the fragment image from 2 tokens (Q6_K up to 32)
+            # and the Q6_K MMQ image from 96
             s_a = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
                                                              tt, PATH_AUTO, wp, wn, stream), it)
             pt["auto_us"] = round(s_a * 1e6, 2)
-            s_mirror = s_i if img is not None and T >= 96 else s_f if s_f is not None and T >= 3 else s_a
+            s_mirror = s_i if img is not None and T >= 96 else s_f if s_f is not None and T >= 2 else s_a
+            pt["mirror_path"] = ("mmq_image" if img is not None and T >= 96 else
+                                 "fragment_image" if s_f is not None and T >= 2 else "auto")
             pt["mirror_us"] = round(s_mirror * 1e6, 2)
             if s_mirror > 1.1 * min(s_g, s_m):
                 pt["mirror_warning"] = "the Exec mirror's choice is more than 10% slower than the fastest path"
@@ -613,7 +617,9 @@ def profile(c: Ctx, which: str, launches: int):
     else:
         tt, rows, cols, T = {"mmq_cfg5_q4k": (TQ4, 17408, 5120, 512), "mmq_cfg5_q3k": (11, 17408, 5120, 512),
                              "mmq_cfg5_q2k": (10, 17408, 5120, 512), "mmq_cfg5_q6k_image": (TQ6, 5120, 17408, 512),
-                             "mmq_cfg4": (TQ8, 3584, 1024, 512)}[which]
+                             "mmq_cfg4": (TQ8, 3584, 1024, 512), "mmq_cfg5_q4k_frag": (TQ4, 17408, 5120, 512),
+                             "mmq_cfg5_q4k_frag_t8": (TQ4, 17408, 5120, 8),
+                             "mmq_cfg5_q6k_frag_t8": (TQ6, 5120, 17408, 8)}[which]
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
         aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
         y = torch.empty((T, rows), device=dev)
@@ -628,6 +634,14 @@ def profile(c: Ctx, which: str, launches: int):
             def fn(i):
                 assert lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
                                                      0, 0, wp, wn, stream) == 0
+        elif "_frag" in which:
+            # the fragment image the Exec mirror reads
+            img = ops.wd_image(tt, w, rows, cols)
+            keep.append(img)
+
+            def fn(i):
+                assert lib.qhip_launch_mul_mat_wd_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
+                                                        tt, wp, wn, stream) == 0
         else:
             def fn(i):
                 assert lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,

@@ -373,7 +373,7 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
  * so adjacent weights get adjacent images and matvecPair stays one launch),
  * the fragment image of a Q6_K or Q4_K weight with rows * cols >= 2^23
  * (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads it
- * from 3 tokens, Q6_K up to 32) and the MMQ image of a Q6_K weight
+ * from 2 tokens, Q6_K up to 32) and the MMQ image of a Q6_K weight
  * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 96 tokens).
  * 0 = built or nothing to build; QHIP_DECLINE = not all built (images off, or
  * past the memory budget): the products then read the GGUF bytes.

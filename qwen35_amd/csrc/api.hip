@@ -112,16 +112,17 @@ bool mmq_image_preferred(const GemvArgs& g) {
 
 // Batches of a large Q6_K or Q4_K weight: the Exec mirror multiplies them
 // from the weight's fragment image (the GGUF bytes once more, permuted).
-// Measured on MI355X: Q6_K [5120, 17408] 21.0 / 21.3 / 24.0 / 28.0 / 34.1 us
-// at 2 / 4 / 16 / 24 / 32 tokens from the image, against GEMV 19.5 / 27.2 us at
-// 2 / 4 and the GGUF-row MMQ 31.4 / 31.5 / 34.2 / 37.0 / 37.6 us; Q4_K
-// [17408, 5120] 14.5 / 14.5 / 15.8 / 19.8 / 29.9 / 43.4 / 132.6 us at 2 / 4 /
-// 16 / 32 / 64 / 128 / 512 tokens, against GEMV 12.6 / 18.6 us at 2 / 4 and
-// the GGUF-row MMQ 16.5 / 16.7 / 17.9 / 21.7 / 33.2 / 46.2 / 141.6 us.  The
-// image from 3 tokens (GEMV about 23 / 15.5 us there); Q6_K up to its 32-token
-// limit (the MMQ image from 96).
+// Measured on MI355X: Q6_K [5120, 17408] 17.5 / 17.6 / 17.7 / 22.6 / 27.8 /
+// 34.1 us at 2 / 4 / 8 / 16 / 24 / 32 tokens from the image, against GEMV
+// 19.4 / 27.1 / 42.4 us at 2 / 4 / 8 and the GGUF-row MMQ 31.5 / 31.4 / 31.4 /
+// 34.2 / 36.9 / 37.7 us; Q4_K [17408, 5120] 11.0 / 11.3 / 11.4 / 13.3 / 20.0
+// / 30.3 / 137.8 us at 2 / 4 / 8 / 16 / 32 / 64 / 512 tokens, against GEMV
+// 12.5 / 18.5 / 29.5 us at 2 / 4 / 8 and the GGUF-row MMQ 16.5 / 16.7 / 16.8 /
+// 18.0 / 21.7 / 33.1 / 146.6 us.  The image from 2 tokens (at one the GEMV,
+// 10.3 / 14.9 us, is ahead); Q6_K up to its 32-token limit (the MMQ image
+// from 96).
 bool wd_image_preferred(const GemvArgs& g) {
-  if (g.tokens < 3 || (long)g.rows * g.cols < (1L << 23) || !fast_ok(g)) return false;
+  if (g.tokens < 2 || (long)g.rows * g.cols < (1L << 23) || !fast_ok(g)) return false;
   if (g.ttype == TT_Q6_K) return g.tokens <= 32 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
   return g.ttype == TT_Q4_K && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
 }

@@ -1535,7 +1535,7 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
 // first 4 NG elements cover tokens 0 .. 8 NG - 1.  The split-scale planes of
 // k_mmq_wd_q4k cost two products per weight value and two MFMAs whatever the
 // token count; here the per-weight work is the nibble extraction alone.
-// One super-block of k_mmq_wds_q4k / k_mmq_wdp_q4k: one MFMA per 32-value
+// One super-block of k_mmq_wds_q4k / k_mmq_rk: one MFMA per 32-value
 // sub-block on the raw nibbles, the sub-block scale applied to the integer
 // result on the NE kept elements, the mins through an exact f16 MFMA, then
 // acc[0][0] += dy * (d * isum - dmin * summs).  A macro, as the Q6_K one.
@@ -1585,7 +1585,7 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
     }                                                                                                                \
   } while (0)
 
-template <int NG, bool IMG>
+template <int NG>
 __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                       float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                                       long act_bytes, int nsb, int ksplit, int cps,
@@ -1599,15 +1599,8 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
   const int ks = g % ksplit;
   g /= ksplit;
   const int r0 = g * kWdBR;
-  const uint8_t* wrow;
-  if constexpr (IMG) {
-    // this wave's group of 32 rows (a group past the end re-reads the last)
-    const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
-    wrow = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile4;
-  } else {
-    const int row = r0 + 32 * wv + li;
-    wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
-  }
+  const int row = r0 + 32 * wv + li;
+  const uint8_t* wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
   const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
 
   long goff[NDMA];
@@ -1631,24 +1624,15 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
   };
   u32x4 wh, wq[4];
   auto issue_w = [&](int sb, u32x4& h, u32x4 (&q)[4]) {
-    if constexpr (IMG) {
-      const uint8_t* b = wrow + (long)kWdiTile4 * sb;
-      h = *(const u32x4*)(b + 4096 + 16 * li);
+    const uint8_t* b = wrow + 144L * sb;
+    h = *(const u32x4*)b;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
-    } else {
-      const uint8_t* b = wrow + 144L * sb;
-      h = *(const u32x4*)b;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
-    }
+    for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
   };
 
   f32x16 acc[1][1];
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[0][0][e] = 0.0f;
-  const i32x16 zero = {};
-  const f32x16 fz = {};
 
   issue_act(sb0, &act[0][0]);
   issue_w(sb0, wh, wq);
@@ -1744,7 +1728,7 @@ struct Q6Regs<true> {
   }
 };
 
-// One super-block of k_mmq_wds_q6k / k_mmq_wdp_q6k: the 16 group MFMAs on
+// One super-block of k_mmq_wds_q6k / k_mmq_wdp_q6k / k_mmq_rk: the 16 group MFMAs on
 // this lane's decoded 6-bit values (B, from the Q6Regs `wc`) against the
 // staged activation row `arow` of `A`, the integer scaling and the -32
 // offset on the NE kept elements, then acc[0][0] += dy * d * isum.  A macro,
@@ -2051,33 +2035,53 @@ hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows,
   return hipGetLastError();
 }
 
-// The Q4_K fragment image, T <= 8 NG (NG < 4): the structure of
-// k_mmq_wdp_q6k -- the workgroup's K slice in groups of CPS super-blocks, each
-// group's weight loads (5 per lane and super-block) and activation DMA of the
-// 8 NG kept token rows all issued before any of it is used.
-template <int NG, int CPS>
-__global__ __launch_bounds__(256) void k_mmq_wdp_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
-                                                      float* __restrict__ Y, int rows, int tokens, long act_bytes,
-                                                      int nsb, int ksplit, int cps, float* __restrict__ part,
-                                                      unsigned* __restrict__ cnt) {
+// ---- few tokens, K split inside the workgroup -------------------------------------------
+// T <= 8 NG from a fragment image with no split-K hand-off between
+// workgroups: a workgroup of NW waves owns one group of 32 rows; wave w takes
+// super-blocks [w cpw, (w+1) cpw) of the whole row (its own activation stages
+// in LDS, its weight loads and DMA for CPS super-blocks issued before any of
+// it is used), and the waves' partial sums are added through LDS in wave
+// order by wave 0, which writes the outputs.  The hand-off of the split
+// launches (partials written through to the coherence point, a counter
+// round trip, the last workgroup reading every slice back) costs 3.5-4 us at
+// config 5 whatever the token count; here the sum stays in the workgroup.
+// Measured on MI355X, config 5, 1 / 8 / 16 / 24 tokens: Q4_K [17408, 5120]
+// with 4 waves 10.6 / 11.4 / 13.1 / 17.1 us (2 / 3 / 5 / 6 / 8 waves: 13.4 /
+// 11.6 / 11.2 / 11.2 / 11.7 us at 1 token), against 14.5 / 14.7 / 15.8 / 20.0
+// for the split launches; Q6_K [5120, 17408] (160 groups) with 12 waves
+// 17.3 / 17.8 / 22.6 / 28.3 us (8 / 10 / 14 / 16 waves: 19.4 / 18.9 / 18.9 /
+// 18.8 at 1 token), against 20.9 / 21.2 / 24.0 / 27.8.  One super-block per
+// load round (CPS = 1) beats whole groups of 2-5 (Q4_K 11.6-15.4 us at 1
+// token): fewer registers, more waves resident.
+template <int TT, int NG, int NW, int CPS>
+__global__ __launch_bounds__(64 * NW) void k_mmq_rk(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                     float* __restrict__ Y, int rows, int tokens, long act_bytes,
+                                                     int nsb, int cpw) {
   constexpr int TR = 8 * NG, NE = 4 * NG;
-  constexpr int STAGE = TR * kWdRow, NPC = TR * kWdPieces, NDMA = (CPS * NPC + 255) / 256;
-  __shared__ __attribute__((aligned(16))) uint8_t act[CPS * STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
-  const int G = gridDim.x;
-  int g = blockIdx.x;
-  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
-  const int ks = g % ksplit;
-  g /= ksplit;
-  const int r0 = g * kWdBR;
-  const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
-  const uint8_t* wbase = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile4;
-  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
+  constexpr int STAGE = TR * kWdRow, NPC = TR * kWdPieces, NDW = (CPS * NPC + 63) / 64;
+  constexpr int TILE = TT == TT_Q6_K ? kWdiTile : kWdiTile4;
+  constexpr int LDSB = NW * CPS * STAGE > NW * NE * 256 ? NW * CPS * STAGE : NW * NE * 256;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDSB];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, li = lane & 31, lh = lane >> 5;
+  const int grp = blockIdx.x, ngrp = (rows + 31) >> 5;
+  const uint8_t* wbase = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * TILE;
+  const int sb0 = wv * cpw, sb1 = sb0 + cpw < nsb ? sb0 + cpw : nsb;
   const int arow = li < TR ? li : 0;
+  uint8_t* act = lds + wv * CPS * STAGE;  // this wave's stages
 
-  long goff[NDMA];
-  int gst[NDMA];
-  wd_dma_plan<NDMA, TR>(wv, lane, tokens, act_bytes, CPS, goff, gst);
+  // DMA piece P = 64 i + lane of this wave's run: stage P / (19 TR), token
+  // row (P % (19 TR)) / 19, slot (P % (19 TR)) % 19
+  long goff[NDW];
+  int gst[NDW];
+#pragma unroll
+  for (int i = 0; i < NDW; ++i) {
+    const int P = 64 * i + lane;
+    const int sg = P / NPC, p = P - sg * NPC;
+    const int tp = p / kWdPieces, j = p - tp * kWdPieces;
+    const int tok = tp < tokens ? tp : tokens - 1;
+    gst[i] = P < CPS * NPC ? sg : CPS;
+    goff[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
+  }
 
   f32x16 acc[1][1];
 #pragma unroll
@@ -2085,34 +2089,74 @@ __global__ __launch_bounds__(256) void k_mmq_wdp_q4k(const uint8_t* __restrict__
 
   for (int base = sb0; base < sb1; base += CPS) {
     const int n = sb1 - base < CPS ? sb1 - base : CPS;
-    u32x4 wh[CPS], wq[CPS][4];
+    if constexpr (TT == TT_Q6_K) {
+      Q6Regs<true> wr[CPS];
 #pragma unroll
-    for (int s = 0; s < CPS; ++s) {
-      if (s < n) {
-        const uint8_t* b = wbase + (long)kWdiTile4 * (base + s);
-        wh[s] = *(const u32x4*)(b + 4096 + 16 * li);
+      for (int s = 0; s < CPS; ++s) {
+        if (s < n) {
+          const uint8_t* b = wbase + (long)TILE * (base + s);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) wq[s][c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+          for (int c = 0; c < 6; ++c) wr[s].p[c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+          wr[s].sc = *(const u32x4*)(b + 6144 + 16 * li);
+          wr[s].d = *(const uint16_t*)(b + 6656 + 2 * li);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NDW; ++i)
+        if (gst[i] < n)
+          __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * (base + gst[i])),
+                                           (__attribute__((address_space(3))) void*)(act + 1024 * i), 16, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's weights and stages (no other wave reads them)
+#pragma unroll
+      for (int s = 0; s < CPS; ++s) {
+        if (s < n) {
+          const uint8_t* As = act + s * STAGE;
+          QHIP_Q6K_SUPERBLOCK(wr[s], As, arow);
+        }
+      }
+    } else {
+      u32x4 wh[CPS], wq[CPS][4];
+#pragma unroll
+      for (int s = 0; s < CPS; ++s) {
+        if (s < n) {
+          const uint8_t* b = wbase + (long)TILE * (base + s);
+          wh[s] = *(const u32x4*)(b + 4096 + 16 * li);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) wq[s][c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < NDW; ++i)
+        if (gst[i] < n)
+          __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * (base + gst[i])),
+                                           (__attribute__((address_space(3))) void*)(act + 1024 * i), 16, 0, 0);
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's weights and stages (no other wave reads them)
+#pragma unroll
+      for (int s = 0; s < CPS; ++s) {
+        if (s < n) {
+          const uint8_t* As = act + s * STAGE;
+          QHIP_Q4K_SUPERBLOCK(wh[s], wq[s], As, arow);
+        }
       }
     }
-#pragma unroll
-    for (int i = 0; i < NDMA; ++i) {
-      if (4 * i + wv < (CPS * NPC + 63) / 64 && gst[i] < n)
-        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * (base + gst[i])),
-                                         (__attribute__((address_space(3))) void*)(act + 1024 * (4 * i + wv)), 16,
-                                         0, 0);
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // every weight register and DMA piece of the group
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < CPS; ++s)
-      if (s < n) {
-        const uint8_t* As = act + s * STAGE;
-        QHIP_Q4K_SUPERBLOCK(wh[s], wq[s], As, arow);
-      }
-    __syncthreads();  // the next group's DMA overwrites the stages
   }
-  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+  // the waves' partials, added in wave order
+  __syncthreads();  // every wave is done with its stages
+  float* red = (float*)lds;
+#pragma unroll
+  for (int e = 0; e < NE; ++e) red[(wv * NE + e) * 64 + lane] = acc[0][0][e];
+  __syncthreads();
+  if (wv == 0) {
+    const int row = grp * 32 + li;
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      float v = red[e * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) v += red[(w * NE + e) * 64 + lane];
+      const int tok = 8 * (e >> 2) + 4 * lh + (e & 3);
+      if (row < rows && tok < tokens) Y[(long)tok * rows + row] = v;
+    }
+  }
 }
 
 // Tokens per weights-direct tile: 32 up to 32 tokens (a 64-token tile would
@@ -2140,17 +2184,22 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipSt
   if (G > 0x7FFFFFFFL || (ksplit > 1 && ntt * ntr > kSkMaxTiles)) return hipErrorInvalidValue;
   unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
   float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
-  if (bt == 32 && g.tokens <= 24) {
-    // few tokens: the raw-nibble form on the real tokens' elements
-    const int ng = (g.tokens + 7) / 8;
+  if constexpr (!IMG) {
+    if (bt == 32 && g.tokens <= 24) {
+      // few tokens: the raw-nibble form on the real tokens' elements (the
+      // fragment image's few-token launches are k_mmq_rk)
+      const int ng = (g.tokens + 7) / 8;
 #define QHIP_WDS(N)                                                                                          \
   if (ng == N)                                                                                               \
-    hipLaunchKernelGGL((k_mmq_wds_q4k<N, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,            \
+    hipLaunchKernelGGL(k_mmq_wds_q4k<N>, dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,            \
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, ksplit, cps, \
                        part, cnt);
-    QHIP_WDS(1) QHIP_WDS(2) QHIP_WDS(3)
+      QHIP_WDS(1) QHIP_WDS(2) QHIP_WDS(3)
 #undef QHIP_WDS
-  } else if (bt == 32)
+      return hipGetLastError();
+    }
+  }
+  if (bt == 32)
     hipLaunchKernelGGL((k_mmq_wd_q4k<1, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
                        ksplit, cps, part, cnt);
@@ -2192,28 +2241,34 @@ static hipError_t launch_mmq_wds_q6k(const GemvArgs& g, int ksplit, void* work, 
 // From the fragment image: Q6_K 1..32 tokens, Q4_K any count; work as for
 // launch_mmq (the same slices as the GGUF-row launch, so mmq_work_bytes
 // covers it).
+template <int TT, int NW>
+static hipError_t launch_mmq_rk(const GemvArgs& g, hipStream_t s) {
+  const int nsb = g.cols / 256, ngrp = (g.rows + 31) / 32;
+  const int cpw = (nsb + NW - 1) / NW;
+  const int ng = (g.tokens + 7) / 8;
+#define QHIP_RK(N)                                                                                               \
+  if (ng == N)                                                                                                   \
+    hipLaunchKernelGGL((k_mmq_rk<TT, N, NW, 1>), dim3((unsigned)ngrp), dim3(64 * NW), 0, s, (const uint8_t*)g.w, \
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, nsb, cpw);
+  QHIP_RK(1) QHIP_RK(2) QHIP_RK(3)
+#undef QHIP_RK
+  return hipGetLastError();
+}
+
 hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s) {
+  if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   if (g.ttype == TT_Q4_K) {
-    if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+    // up to 24 tokens the K split inside the workgroup; beyond, the 32- and
+    // 64-token weights-direct tiles (split over workgroups on small grids)
+    if (g.tokens <= 24) return launch_mmq_rk<TT_Q4_K, 4>(g, s);
     int ksplit = wd_slices(g);
     if (!work || work_bytes < mmq_split_bytes(g, wd_bt(g), kWdBR, ksplit)) ksplit = 1;
-    // up to 8 tokens: the whole-group prefetch (14.4-14.6 us at config 5,
-    // against 15.0-15.2 double-buffered); beyond, the double-buffered kernels
-    // (15.8 / 19.8 us at 16 / 24 tokens, against 16.8 / 19.3)
-    if (g.tokens > 8) return launch_mmq_wd<true>(g, ksplit, work, s);
-    const int nsb = g.cols / 256;
-    const long ntr = (g.rows + kWdBR - 1) / kWdBR;
-    const int cps = (nsb + ksplit - 1) / ksplit;
-    const long G = ntr * ksplit;
-    if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr > kSkMaxTiles)) return hipErrorInvalidValue;
-    unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
-    float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
-    hipLaunchKernelGGL((k_mmq_wdp_q4k<1, 2>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
-                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, nsb, ksplit, cps, part, cnt);
-    return hipGetLastError();
+    return launch_mmq_wd<true>(g, ksplit, work, s);
   }
-  if (g.ttype != TT_Q6_K || g.tokens < 1 || g.tokens > 32) return hipErrorInvalidValue;
-  if (g.rows <= 0) return hipSuccess;
+  if (g.ttype != TT_Q6_K || g.tokens > 32) return hipErrorInvalidValue;
+  // up to 16 tokens the K split inside the workgroup; 17..32 the split
+  // launch with whole-group prefetch (28.0 against 28.3 us at 24 tokens)
+  if (g.tokens <= 16) return launch_mmq_rk<TT_Q6_K, 12>(g, s);
   int ksplit = wds_q6k_slices(g);
   if (!work || work_bytes < mmq_split_bytes(g, 32, kWdBR, ksplit)) ksplit = 1;
   const int nsb = g.cols / 256;
