@@ -364,8 +364,10 @@ def bench_mmq(c: Ctx):
     [16,256], packed by the ragged quantizer, one launch) and a dense 512-token
     sequence.  Config 5: Q4_K gate [17408,5120] and Q6_K down [5120,17408] at
     T = 1, 2, 4, 8, 16, 32, 64, 512 on the GEMV and on the MMQ (with the
-    split-K workspace the Exec mirror passes), and the crossover.  Throughput:
-    tokens/s, and 2*rows*cols*T / time against the int8 MFMA peak.  `mmq_us`
+    split-K workspace the Exec mirror passes), and the crossover; weight
+    copies (with their images) rotated per launch past the Infinity Cache.
+    Throughput: tokens/s, and 2*rows*cols*T / time against the int8 MFMA
+    peak.  `mmq_us`
     is the fastest of the MMQ on the GGUF rows, from the fragment image and
     (Q6_K) from the MMQ image; `mirror_us` is what the Exec mirror launches."""
     torch, lib, ops, synth, dev, stream = c.torch, c.lib, c.ops, c.synth, c.dev, c.stream
@@ -420,12 +422,21 @@ def bench_mmq(c: Ctx):
     del w, xq, yo, seqs
 
     sweep = {}
+
+    def rotated(fn, iters):
+        return time_loop(torch, fn, iters, 3)
+
     for name, tt, rows, cols in (("q4_k_17408x5120", TQ4, 17408, 5120), ("q6_k_5120x17408", TQ6, 5120, 17408)):
-        w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
-        # the prepared MMQ weight image the Exec mirror uses for Q6_K prefill,
-        # and the fragment image it uses for 3..32 tokens
-        img = ops.mmq_image(tt, w, rows, cols) if tt == TQ6 else None
-        frag = ops.wd_image(tt, w, rows, cols)
+        # weight copies, each with the images the Exec mirror derives from it
+        # (the fragment image it reads from 2 tokens, Q6_K's MMQ image from
+        # 96), rotated per launch so that every launch streams its weight
+        # from HBM as a decode does (one copy would stay in the 256 MB
+        # Infinity Cache)
+        wh = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
+        ncopy = max(1, -(-ROTATE_BYTES // wh.nbytes))
+        ws = [torch.from_numpy(wh).to(dev) for _ in range(ncopy)]
+        frags = [ops.wd_image(tt, w, rows, cols) for w in ws]
+        imgs = [ops.mmq_image(tt, w, rows, cols) for w in ws] if tt == TQ6 else None
         rows_out = []
         cross = None
         for T in (1, 2, 4, 8, 16, 32, 64, 512):
@@ -436,32 +447,37 @@ def bench_mmq(c: Ctx):
             # the split-K workspace the Exec mirror passes (small grids split K)
             work = ops.mul_mat_work(rows, cols, T, tt, dev)
             wp, wn = (work.data_ptr(), work.numel()) if work is not None else (None, 0)
-            s_g = timed(lambda: lib.qhip_launch_mul_mat(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
-                                                        PATH_GEMV, stream), it)
-            s_t = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
-                                                             tt, PATH_MMQ, wp, wn, stream), it)
+            s_g = rotated(lambda i: lib.qhip_launch_mul_mat(ws[i % ncopy].data_ptr(), aq.data_ptr(), y.data_ptr(),
+                                                            rows, cols, T, tt, PATH_GEMV, stream), it)
+            s_t = rotated(lambda i: lib.qhip_launch_mul_mat_work(ws[i % ncopy].data_ptr(), aq.data_ptr(),
+                                                                 y.data_ptr(), rows, cols, T, tt, PATH_MMQ, wp, wn,
+                                                                 stream), it)
             pt = {"T": T, "gemv_us": round(s_g * 1e6, 2), "mmq_tile_us": round(s_t * 1e6, 2)}
             s_m = s_t
-            if img is not None:
-                s_i = timed(lambda: lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows,
-                                                                  cols, T, tt, 0, 0, wp, wn, stream), it)
+            s_i = None
+            if imgs is not None:
+                s_i = rotated(lambda i: lib.qhip_launch_mul_mat_image(imgs[i % ncopy].data_ptr(), aq.data_ptr(),
+                                                                      y.data_ptr(), rows, cols, T, tt, 0, 0, wp, wn,
+                                                                      stream), it)
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
             s_f = None
             if tt == TQ4 or T <= 32:
-                s_f = timed(lambda: lib.qhip_launch_mul_mat_wd_image(frag.data_ptr(), aq.data_ptr(), y.data_ptr(),
-                                                                     rows, cols, T, tt, wp, wn, stream), it)
+                s_f = rotated(lambda i: lib.qhip_launch_mul_mat_wd_image(frags[i % ncopy].data_ptr(), aq.data_ptr(),
+                                                                         y.data_ptr(), rows, cols, T, tt, wp, wn,
+                                                                         stream), it)
                 pt["mmq_fragment_image_us"] = round(s_f * 1e6, 2)
                 s_m = min(s_m, s_f)
             # the C ABI's automatic path (GEMV or tile MMQ by the measured
             # crossover), and what the Exec mirror's matvecBatchK launches: the
             # same, except the fragment image from 2 tokens (Q6_K up to 32)
             # and the Q6_K MMQ image from 96
-            s_a = timed(lambda: lib.qhip_launch_mul_mat_work(w.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
-                                                             tt, PATH_AUTO, wp, wn, stream), it)
+            s_a = rotated(lambda i: lib.qhip_launch_mul_mat_work(ws[i % ncopy].data_ptr(), aq.data_ptr(),
+                                                                 y.data_ptr(), rows, cols, T, tt, PATH_AUTO, wp, wn,
+                                                                 stream), it)
             pt["auto_us"] = round(s_a * 1e6, 2)
-            s_mirror = s_i if img is not None and T >= 96 else s_f if s_f is not None and T >= 2 else s_a
-            pt["mirror_path"] = ("mmq_image" if img is not None and T >= 96 else
+            s_mirror = s_i if s_i is not None and T >= 96 else s_f if s_f is not None and T >= 2 else s_a
+            pt["mirror_path"] = ("mmq_image" if s_i is not None and T >= 96 else
                                  "fragment_image" if s_f is not None and T >= 2 else "auto")
             pt["mirror_us"] = round(s_mirror * 1e6, 2)
             if s_mirror > 1.1 * min(s_g, s_m):
@@ -478,10 +494,11 @@ def bench_mmq(c: Ctx):
         # 2..8 tokens over the batch-1 GEMV
         t1 = next(p["gemv_us"] for p in rows_out if p["T"] == 1)
         ratio = max(p["mirror_us"] for p in rows_out if 2 <= p["T"] <= 8) / t1
-        sweep[name] = {"points": rows_out, "crossover_T": cross, "mirror_2_8_over_gemv_1": round(ratio, 3)}
+        sweep[name] = {"points": rows_out, "crossover_T": cross, "mirror_2_8_over_gemv_1": round(ratio, 3),
+                       "weight_copies": ncopy}
         log(f"mmq cfg5 {name}: " + ", ".join(f"T={p['T']} gemv {p['gemv_us']} / mmq {p['mmq_us']} us"
                                               for p in rows_out) + f"; crossover T={cross}")
-        del w, img, frag
+        del ws, imgs, frags
         torch.cuda.empty_cache()
     res["cfg5_sweep"] = sweep
     return res
