@@ -112,15 +112,15 @@ bool mmq_image_preferred(const GemvArgs& g) {
 
 // Batches of a large Q6_K or Q4_K weight: the Exec mirror multiplies them
 // from the weight's fragment image (the GGUF bytes once more, permuted).
-// Measured on MI355X: Q6_K [5120, 17408] 17.5 / 17.6 / 17.7 / 22.6 / 27.8 /
-// 34.1 us at 2 / 4 / 8 / 16 / 24 / 32 tokens from the image, against GEMV
-// 19.4 / 27.1 / 42.4 us at 2 / 4 / 8 and the GGUF-row MMQ 31.5 / 31.4 / 31.4 /
-// 34.2 / 36.9 / 37.7 us; Q4_K [17408, 5120] 11.0 / 11.3 / 11.4 / 13.3 / 20.0
-// / 30.3 / 137.8 us at 2 / 4 / 8 / 16 / 32 / 64 / 512 tokens, against GEMV
-// 12.5 / 18.5 / 29.5 us at 2 / 4 / 8 and the GGUF-row MMQ 16.5 / 16.7 / 16.8 /
-// 18.0 / 21.7 / 33.1 / 146.6 us.  The image from 2 tokens (at one the GEMV,
-// 10.3 / 14.9 us, is ahead); Q6_K up to its 32-token limit (the MMQ image
-// from 96).
+// Measured on MI355X with the weights streamed from HBM (rotated copies):
+// Q6_K [5120, 17408] 19.6 / 20.0 / 21.0 / 26.4 / 36.4 us at 2 / 4 / 8 / 16 /
+// 32 tokens from the image, against GEMV 18.2 / 25.3 / 33.5 / 49.0 us at 1 /
+// 2 / 4 / 8 and the GGUF-row MMQ 33.0 / 33.4 / 33.4 / 38.0 / 43.8 us; Q4_K
+// [17408, 5120] 13.0 / 13.4 / 14.2 / 17.5 / 22.6 / 35.2 / 145.9 us at 2 / 4 /
+// 8 / 16 / 32 / 64 / 512 tokens, against GEMV 11.4 / 15.0 / 21.0 / 33.1 us at
+// 1 / 2 / 4 / 8 and the GGUF-row MMQ 19.7 / 20.0 / 19.7 / 21.2 / 25.7 / 39.8 /
+// 154.0 us.  The image from 2 tokens (at one the GEMV is ahead: 12.7 / 19.5
+// us from the images); Q6_K up to its 32-token limit (the MMQ image from 96).
 bool wd_image_preferred(const GemvArgs& g) {
   if (g.tokens < 2 || (long)g.rows * g.cols < (1L << 23) || !fast_ok(g)) return false;
   if (g.ttype == TT_Q6_K) return g.tokens <= 32 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
