@@ -2045,14 +2045,18 @@ hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows,
 // launches (partials written through to the coherence point, a counter
 // round trip, the last workgroup reading every slice back) costs 3.5-4 us at
 // config 5 whatever the token count; here the sum stays in the workgroup.
-// Measured on MI355X, config 5, 1 / 8 / 16 / 24 tokens: Q4_K [17408, 5120]
-// with 4 waves 10.6 / 11.4 / 13.1 / 17.1 us (2 / 3 / 5 / 6 / 8 waves: 13.4 /
+// Measured on MI355X (one weight copy, read from the Infinity Cache), config
+// 5, 1 / 8 / 16 / 24 tokens: Q4_K [17408, 5120] with 4 waves 10.6 / 11.4 /
+// 13.1 / 17.1 us (2 / 3 / 5 / 6 / 8 waves: 13.4 /
 // 11.6 / 11.2 / 11.2 / 11.7 us at 1 token), against 14.5 / 14.7 / 15.8 / 20.0
 // for the split launches; Q6_K [5120, 17408] (160 groups) with 12 waves
 // 17.3 / 17.8 / 22.6 / 28.3 us (8 / 10 / 14 / 16 waves: 19.4 / 18.9 / 18.9 /
 // 18.8 at 1 token), against 20.9 / 21.2 / 24.0 / 27.8.  One super-block per
 // load round (CPS = 1) beats whole groups of 2-5 (Q4_K 11.6-15.4 us at 1
-// token): fewer registers, more waves resident.
+// token): fewer registers, more waves resident.  With the weights streamed
+// from HBM (rotated copies) the same choices win: Q4_K 12.6 / 14.2 us at 1 / 8
+// tokens (3 / 6 / 8 waves 13.8 / 13.3 / 13.8 at 1 token; two super-blocks per
+// round 14.7), Q6_K 19.6 / 21.0 (8 / 16 waves 22.5 / 25.9).
 template <int TT, int NG, int NW, int CPS>
 __global__ __launch_bounds__(64 * NW) void k_mmq_rk(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                      float* __restrict__ Y, int rows, int tokens, long act_bytes,
