@@ -497,11 +497,15 @@ __device__ __forceinline__ void mmq_write_tile(f32x16 (&acc)[NA][NB], float* __r
 }
 
 // ---- the kernel -------------------------------------------------------------------------
-template <int TT, int BT, int BR, int NT = 256>
+// SPLIT = false: the launch is not cut over K (ksplit == 1); without the
+// hand-off's code the kernel needs fewer registers (Q8_0 64 x 64: 156 VGPRs
+// against 171, three waves per SIMD instead of two).
+template <int TT, int BT, int BR, int NT = 256, bool SPLIT = true>
 __global__ __launch_bounds__(NT) void k_mmq(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                               float* __restrict__ Y, int rows, int tokens, long row_bytes,
                                               long act_bytes, int upr, int ntile_t, int ksplit, int cps,
                                               float* __restrict__ part, unsigned* __restrict__ cnt) {
+  if constexpr (!SPLIT) ksplit = 1;
   grid_prologue<TT>();
   constexpr bool K32 = act32(TT);
   // waves: 2 x 2 over (tokens, rows), or stacked along rows for a 32-token
@@ -2305,9 +2309,14 @@ static hipError_t launch_mmq_t(const GemvArgs& g, int ksplit, void* work, hipStr
   if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr * ntt > kSkMaxTiles)) return hipErrorInvalidValue;
   unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
   float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
-  hipLaunchKernelGGL((k_mmq<TT, BT, BR, NT>), dim3((unsigned)G), dim3(NT), 0, s, (const uint8_t*)g.w,
-                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
-                     ksplit, cps, part, cnt);
+  if (ksplit > 1)
+    hipLaunchKernelGGL((k_mmq<TT, BT, BR, NT, true>), dim3((unsigned)G), dim3(NT), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
+                       ksplit, cps, part, cnt);
+  else
+    hipLaunchKernelGGL((k_mmq<TT, BT, BR, NT, false>), dim3((unsigned)G), dim3(NT), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, upr, (int)ntt,
+                       ksplit, cps, part, cnt);
   return hipGetLastError();
 }
 
