@@ -241,10 +241,11 @@ int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_ou
                               int tokens, int ttype, int tile_tokens, int tile_rows, void *d_work,
                               long work_bytes, void *stream);
 
-/* Fragment images of Q6_K and Q4_K weights (no reference counterpart; the
+/* Fragment images of Q6_K, Q4_K and Q8_0 weights (no reference counterpart; the
  * reference's CUDA MMQ decodes the GGUF blocks in every launch,
- * mmq.cu:499-659).  The GGUF bytes permuted -- the same bytes per row and 256
- * values -- so that the weights-direct MMQ loads each matrix-core fragment as
+ * mmq.cu:499-659, and declines Q8_0 to its GEMV, mmq.cu:2250-2264).  The GGUF
+ * bytes permuted -- the same bytes per row and 256 values -- so that the
+ * weights-direct MMQ loads each matrix-core fragment as
  * one aligned, contiguous 1 KB per wave instruction (a GGUF row's blocks
  * otherwise give a wave instruction 32 rows' pieces, most of them misaligned
  * for Q6_K's 210-byte blocks).  Rows in groups of 32, the last padded with
@@ -257,13 +258,21 @@ int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_ou
  *   Q4_K, 4608-byte tiles: [0, 4096) lane L holds qs bytes 32c + 16k .. +15
  *     of row i at 1024c + 16L (c < 4); [4096, 4608) row i's 16-byte header
  *     (d, dmin, scales) at 16i.
- *   qhip_wd_image_bytes    image size, -1 unless ttype is Q6_K / Q4_K and cols % 256 == 0
+ *   Q8_0, per group r (nb = cols/32 blocks) at r * nb * 1088: nb 1024-byte
+ *     quant tiles (block b's at 1024b: lane L holds values 16k .. 16k+15 of
+ *     row i at 16L), then nb runs of the 32 rows' f16 d (block b's at
+ *     1024nb + 64b: row 8q + 4h + j at 2 (16h + 4q + j), the order of the
+ *     rows in a lane's MFMA result elements).
+ *   qhip_wd_image_bytes    image size, -1 unless ttype is Q6_K / Q4_K / Q8_0 and cols % 256 == 0
  *   qhip_launch_wd_prepare build it from GGUF bytes (d_image 16-byte aligned)
  *   qhip_launch_mul_mat_wd_image  d_out [tokens, rows] from the image (Q6_K
- *     1..32 tokens, Q4_K any count; Q8_K activations as for
+ *     1..32 tokens, Q4_K and Q8_0 any count; activations as for
  *     qhip_launch_mul_mat); d_work (nullable) as for qhip_launch_mul_mat_work,
- *     qhip_mul_mat_work_bytes covers it; the same bits as the MMQ on the GGUF
- *     rows (QHIP_PATH_MMQ) with the same workspace */
+ *     qhip_mul_mat_work_bytes covers it.  Q6_K / Q4_K: the same integers as
+ *     the MMQ on the GGUF rows (QHIP_PATH_MMQ), and the same bits where the
+ *     launches cut K alike; Q8_0: the same block integers, scaled as
+ *     (da sumi) dw per block and added in four K quarters (within 1e-6
+ *     relative of the GGUF-row MMQ), d_work unused */
 long qhip_wd_image_bytes(int ttype, int rows, int cols);
 int qhip_launch_wd_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
 int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
@@ -373,7 +382,8 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
  * so adjacent weights get adjacent images and matvecPair stays one launch),
  * the fragment image of a Q6_K or Q4_K weight with rows * cols >= 2^23
  * (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads it
- * from 2 tokens, Q6_K up to 32) and the MMQ image of a Q6_K weight
+ * from 2 tokens, Q6_K up to 32) or of a Q8_0 weight with cols <= 1024 (from
+ * 6 tokens) and the MMQ image of a Q6_K weight
  * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 96 tokens).
  * 0 = built or nothing to build; QHIP_DECLINE = not all built (images off, or
  * past the memory budget): the products then read the GGUF bytes.

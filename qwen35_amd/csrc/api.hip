@@ -121,7 +121,18 @@ bool mmq_image_preferred(const GemvArgs& g) {
 // 1 / 2 / 4 / 8 and the GGUF-row MMQ 19.7 / 20.0 / 19.7 / 21.2 / 25.7 / 39.8 /
 // 154.0 us.  The image from 2 tokens (at one the GEMV is ahead: 12.7 / 19.5
 // us from the images); Q6_K up to its 32-token limit (the MMQ image from 96).
+//
+// Q8_0 (the image MMQ from 6 tokens where K is one 1024-value super-chunk):
+// measured on MI355X, [3584, 1024] GEMV 3.59 / 4.36 / 4.84 / 7.84 / 14.02 us
+// at 4 / 6 / 8 / 16 / 32 tokens against 4.23 / 4.25 / 4.32 / 4.47 / 4.90
+// from the image (the GGUF-row MMQ 9.4 us at 16); 64 / 512 / 1673 tokens
+// 7.0 / 11.5 / 28.0 us against 9.7 / 12.6 / 30.0 on the GGUF rows.  With K
+// = 3584 ([1024, 3584]: 16 workgroups walking four super-chunks) the image
+// loses to the GEMV up to 24 tokens (13.3 against 16.9 us there), so wider
+// Q8_0 rows keep the GGUF-row paths.
 bool wd_image_preferred(const GemvArgs& g) {
+  if (g.ttype == TT_Q8_0)
+    return g.tokens >= 6 && g.cols <= 1024 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
   if (g.tokens < 2 || (long)g.rows * g.cols < (1L << 23) || !fast_ok(g)) return false;
   if (g.ttype == TT_Q6_K) return g.tokens <= 32 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
   return g.ttype == TT_Q4_K && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;

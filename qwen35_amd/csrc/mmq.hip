@@ -2019,8 +2019,253 @@ __global__ __launch_bounds__(256) void k_wd_prepare_q4k(const uint8_t* __restric
   if (k == 0) *(uint4*)(t + 4096 + 16 * i) = h;
 }
 
+// ---- Q8_0 fragment image and its MMQ ----------------------------------------------------
+// Image of a Q8_0 weight: per 32-row group, with nb = cols / 32 blocks, nb
+// 1024-byte quant tiles (block b's tile: lane L's 16 bytes at 16 L are row
+// L % 32, values 16 (L / 32)..+15, the MFMA operand fragment), then nb runs of
+// the 32 rows' f16 scales in accumulator order (position 16 h + 4 q + i holds
+// row 8 q + 4 h + i: the rows a lane with h = lane / 32 holds in its result
+// elements 4 q + i).  1088 bytes per group and block, the GGUF rows' size.
+constexpr int kQ8iBlk = 1088;
+constexpr int kQ8iRow = 1040;  // LDS bytes per staged token row: 32 blocks + 16 (rows 4 banks apart)
+
+__device__ __forceinline__ int q8i_pos(int i) { return 16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3); }
+// staging unit u (TK tokens x 16 block pairs) -> token, pair
+template <int TK>
+__device__ __forceinline__ int q8i_unit_tok(int u) { return (u & 3) + 4 * ((u >> 4) & (TK / 4 - 1)); }
+template <int TK>
+__device__ __forceinline__ int q8i_unit_pair(int u) { return ((u >> 2) & 3) + 4 * (u / (4 * TK)); }
+
+// One thread per (group, block, lane L): lane L's 16 quant bytes (2-byte
+// aligned in the 34-byte GGUF block, read bytewise); lanes L < 32 also the
+// row's scale.  Rows past the end: zeros.
+__global__ __launch_bounds__(256) void k_wd_prepare_q8(const uint8_t* __restrict__ W, uint8_t* __restrict__ IMG,
+                                                        int rows, long row_bytes, int nb, long nthreads) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= nthreads) return;
+  const int L = (int)(gid & 63), i = L & 31, k = L >> 5;
+  const long tile = gid >> 6;  // group * nb + b
+  const long grp = tile / nb;
+  const int b = (int)(tile - grp * nb);
+  const long row = grp * 32 + i;
+  uint8_t* t = IMG + grp * nb * kQ8iBlk;
+  uint32_t q[4] = {0, 0, 0, 0};
+  uint16_t d = 0;
+  if (row < rows) {
+    const uint8_t* blk = W + row * row_bytes + 34L * b;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) q[w] = ld32_bytes(blk + 2 + 16 * k + 4 * w);
+    d = (uint16_t)(blk[0] | (blk[1] << 8));
+  }
+  *(uint4*)(t + 1024L * b + 16 * L) = make_uint4(q[0], q[1], q[2], q[3]);
+  if (k == 0) *(uint16_t*)(t + 1024L * nb + 64L * b + 2 * q8i_pos(i)) = d;
+}
+
+// Q8_0 MMQ from the fragment image (cols a multiple of 256).  A workgroup of
+// eight waves owns 64 rows x 32 NG tokens; wave w takes row group w & 1 and
+// K quarter w >> 1 of each 32-block super-chunk.  Operand A is the weights,
+// loaded from the image straight into registers; operand B the activations,
+// copied from the Q8_0 rows into LDS once per workgroup (1040-byte token
+// rows, the block scales apart as f16).  So every lane holds one token and 16
+// rows: its activation scale is one value per block, the 16 weight scales are
+// read from an f32 LDS plane in accumulator order.  Per block the MFMA result
+// read as a float is 1.5 2^23 + sumi (exact, |sumi| <= 2^19) and
+//   t = fma(F, da, -1.5 2^23 da) = da sumi,   acc = fma(t, dw, acc)
+// (kernels32.c:447-464: sumi * (dw * da), here rounded as (da * sumi) * dw).
+// At the end the four K quarters' partial tiles are added through LDS in
+// quarter order, so the result does not depend on timing.
+// Occupancy: two workgroups per CU (under 80 KB of LDS each, at most 128
+// VGPRs), four waves per SIMD.
+template <int NG, bool ONE, bool FULL>
+__global__ __launch_bounds__(512, 4) void k_mmq_q8i(const uint8_t* __restrict__ IMG, const uint8_t* __restrict__ XQ,
+                                                     float* __restrict__ Y, int rows, int tokens, int nb,
+                                                     long act_bytes, int ntt) {
+  constexpr int TK = 32 * NG;  // tokens per tile
+  constexpr int AQ = TK * kQ8iRow, DAH = 4 * TK * 16, DWF = 32 * 2 * 32 * 4;
+  constexpr int PRT = 2 * 4 * TK * 36 * 4;  // partial tiles [row group][quarter][token][36]
+  constexpr int LDSB = AQ + DAH + DWF > PRT ? AQ + DAH + DWF : PRT;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[LDSB];
+  uint8_t* aq = lds;
+  uint8_t* dah = lds + AQ;  // [block / 8][token][8] f16
+  float* dwf = (float*)(lds + AQ + DAH);  // [block][row group][32] in accumulator order
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  const int rg = wv & 1, kq = wv >> 1;
+  const int G = gridDim.x;
+  int g = blockIdx.x;
+  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);
+  const int rt = g / ntt, t0 = (g - rt * ntt) * TK;
+  const int ngrp = (rows + 31) >> 5;
+  const long gbytes = (long)nb * kQ8iBlk;
+  const int grp = 2 * rt + rg;
+  const uint8_t* wimg = IMG + (long)(grp < ngrp ? grp : ngrp - 1) * gbytes;
+
+  f32x16 acc[NG];
+#pragma unroll
+  for (int a = 0; a < NG; ++a)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
+  i32x16 bias;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) bias[e] = kBiasBits;
+  asm volatile("" : "+v"(bias));
+
+  // ONE: the launch guarantees nb <= 32 (one super-chunk, so nothing but the
+  // bias is live across the staging: 64 tokens fit the register budget)
+  const int nbl = ONE ? 32 : nb;
+  for (int sc0 = 0; sc0 < nbl && sc0 < nb; sc0 += 32) {
+    const int n = nb - sc0 < 32 ? nb - sc0 : 32;  // a multiple of 8
+    const int q4 = FULL ? 8 : n >> 2, bl0 = kq * q4;  // FULL: nb % 32 == 0
+    // this wave's first two weight fragments, then the activation and scale
+    // loads of the whole workgroup
+    u32x4 wf[3];
+    const uint8_t* wq = wimg + 1024L * (sc0 + bl0) + 16 * lane;
+    wf[0] = *(const u32x4*)wq;
+    wf[1] = *(const u32x4*)(wq + 1024);
+    // activation unit u = tid + 512 i: blocks 2 p, 2 p + 1 of one token, 68
+    // bytes from a 4-byte aligned address.  Sixteen consecutive lanes take 4
+    // tokens x 4 pairs (unit_tok / unit_pair): their 16-byte LDS writes land
+    // in 16 different bank groups (token rows are 65 groups apart), and each
+    // token's 4 pairs are 272 contiguous bytes of the row.
+    uint32_t x[NG][17];
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int u = tid + 512 * i, tok = q8i_unit_tok<TK>(u), p = q8i_unit_pair<TK>(u);
+      const int tt = t0 + tok < tokens ? t0 + tok : tokens - 1;
+      const uint8_t* src = XQ + (long)tt * act_bytes + 34L * (sc0 + 2 * (2 * p < n ? p : 0));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 v = *(const u32x4*)(src + 16 * c);
+        x[i][4 * c] = v.x; x[i][4 * c + 1] = v.y; x[i][4 * c + 2] = v.z; x[i][4 * c + 3] = v.w;
+      }
+      x[i][16] = *(const uint32_t*)(src + 64);
+    }
+    // weight scales: thread tid < 256 converts 8 of one row group's block
+    u32x4 ws = {0u, 0u, 0u, 0u};
+    const int spart = tid & 3, sr = (tid >> 2) & 1, sbl = tid >> 3;
+    const int sgrp = 2 * rt + sr;
+    if (tid < 256 && sbl < n)
+      ws = *(const u32x4*)(IMG + (long)(sgrp < ngrp ? sgrp : ngrp - 1) * gbytes + 1024L * nb + 64L * (sc0 + sbl) +
+                           16 * spart);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int u = tid + 512 * i, tok = q8i_unit_tok<TK>(u), p = q8i_unit_pair<TK>(u);
+      if (2 * p < n) {
+        uint32_t q0[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q0[j] = __builtin_amdgcn_alignbyte(x[i][j + 1], x[i][j], 2);
+        uint8_t* dst = aq + tok * kQ8iRow + 64 * p;
+        st16(dst, q0[0], q0[1], q0[2], q0[3]);
+        st16(dst + 16, q0[4], q0[5], q0[6], q0[7]);
+        st16(dst + 32, x[i][9], x[i][10], x[i][11], x[i][12]);
+        st16(dst + 48, x[i][13], x[i][14], x[i][15], x[i][16]);
+        *(uint32_t*)(dah + ((p >> 2) * TK + tok) * 16 + 4 * (p & 3)) = (x[i][0] & 0xFFFFu) | (x[i][8] & 0xFFFF0000u);
+      }
+    }
+    if (tid < 256 && sbl < n) {
+      const uint32_t h[4] = {ws.x, ws.y, ws.z, ws.w};
+      float f[8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f[2 * j] = h2f(h[j] & 0xFFFFu);
+        f[2 * j + 1] = h2f(h[j] >> 16);
+      }
+      float* dst = dwf + (sbl * 2 + sr) * 32 + 8 * spart;
+      *(f32x4*)dst = f32x4{f[0], f[1], f[2], f[3]};
+      *(f32x4*)(dst + 4) = f32x4{f[4], f[5], f[6], f[7]};
+    }
+    __syncthreads();
+
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s < q4) {
+        if (s + 2 < q4) wf[(s + 2) % 3] = *(const u32x4*)(wq + 1024L * (s + 2));
+        const int bl = bl0 + s;
+        i32x16 c[NG];
+#pragma unroll
+        for (int a = 0; a < NG; ++a) {
+          const i32x4 af = *(const i32x4*)(aq + (32 * a + li) * kQ8iRow + 32 * bl + 16 * lh);
+          const u32x4 w = wf[s % 3];
+          c[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(i32x4{(int)w.x, (int)w.y, (int)w.z, (int)w.w}, af, bias, 0,
+                                                        0, 0);
+        }
+        float da[NG], nbd[NG];
+#pragma unroll
+        for (int a = 0; a < NG; ++a) {
+          da[a] = h2f(*(const uint16_t*)(dah + ((bl >> 3) * TK + 32 * a + li) * 16 + 2 * (bl & 7)));
+          nbd[a] = -kBias * da[a];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 dw = *(const f32x4*)(dwf + (bl * 2 + rg) * 32 + 16 * lh + 4 * q);
+#pragma unroll
+          for (int a = 0; a < NG; ++a)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int ce = c[a][4 * q + i];
+              const float t = __builtin_fmaf(__int_as_float(ce), da[a], nbd[a]);
+              acc[a][4 * q + i] = __builtin_fmaf(t, dw[i], acc[a][4 * q + i]);
+            }
+        }
+      }
+    }
+    __syncthreads();  // the next super-chunk (or the partial tiles) overwrites the stages
+  }
+
+  // partial tiles, then the sum over the quarters in quarter order
+  float* prt = (float*)lds;
+#pragma unroll
+  for (int a = 0; a < NG; ++a)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      *(f32x4*)(prt + ((rg * 4 + kq) * TK + 32 * a + li) * 36 + 8 * q + 4 * lh) =
+          f32x4{acc[a][4 * q], acc[a][4 * q + 1], acc[a][4 * q + 2], acc[a][4 * q + 3]};
+  __syncthreads();
+  const int orr = wv >> 2, tb = wv & 3, rq = lane & 7, tl = lane >> 3;
+#pragma unroll
+  for (int m = 0; m < NG; ++m) {
+    const int tok = 8 * NG * tb + 8 * m + tl;
+    const float* pp = prt + (orr * 4 * TK + tok) * 36 + 4 * rq;
+    f32x4 v = *(const f32x4*)pp;
+#pragma unroll
+    for (int k = 1; k < 4; ++k) v += *(const f32x4*)(pp + k * TK * 36);
+    const int row = 32 * (2 * rt + orr) + 4 * rq;
+    if (t0 + tok < tokens) {
+      float* yo = Y + (long)(t0 + tok) * rows + row;
+      if (row < rows) yo[0] = v.x;
+      if (row + 1 < rows) yo[1] = v.y;
+      if (row + 2 < rows) yo[2] = v.z;
+      if (row + 3 < rows) yo[3] = v.w;
+    }
+  }
+}
+
+static hipError_t launch_mmq_q8i(const GemvArgs& g, hipStream_t s) {
+  const int nb = g.cols / 32;
+  const long ntr = (g.rows + 63) / 64;
+  // 64-token tiles where K is one super-chunk (up to 1024 values), else 32
+  const int tk = g.tokens > 32 && nb <= 32 ? 64 : 32;
+  const long ntt = (g.tokens + tk - 1) / tk;
+  const long G = ntr * ntt;
+  if (G > 0x7FFFFFFFL || g.act_bytes != 34L * nb) return hipErrorInvalidValue;
+#define QHIP_Q8I(NG, ONE, FULL)                                                                               \
+  hipLaunchKernelGGL((k_mmq_q8i<NG, ONE, FULL>), dim3((unsigned)G), dim3(512), 0, s, (const uint8_t*)g.w,       \
+                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, nb, g.act_bytes, (int)ntt)
+  const bool full = nb % 32 == 0;
+  if (tk == 32) {
+    if (full) QHIP_Q8I(1, false, true);
+    else QHIP_Q8I(1, false, false);
+  } else {
+    if (full) QHIP_Q8I(2, true, true);
+    else QHIP_Q8I(2, true, false);
+  }
+#undef QHIP_Q8I
+  return hipGetLastError();
+}
+
 long wd_image_bytes(int ttype, int rows, int cols) {
-  if ((ttype != TT_Q6_K && ttype != TT_Q4_K) || rows < 0 || cols <= 0 || cols % 256) return -1;
+  if ((ttype != TT_Q6_K && ttype != TT_Q4_K && ttype != TT_Q8_0) || rows < 0 || cols <= 0 || cols % 256) return -1;
+  if (ttype == TT_Q8_0) return (long)((rows + 31) / 32) * (cols / 32) * kQ8iBlk;
   return (long)((rows + 31) / 32) * (cols / 256) * (ttype == TT_Q6_K ? kWdiTile : kWdiTile4);
 }
 
@@ -2028,6 +2273,13 @@ hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows,
                              hipStream_t s) {
   if (wd_image_bytes(ttype, rows, cols) < 0) return hipErrorInvalidValue;
   const int nsb = cols / 256;
+  if (ttype == TT_Q8_0) {
+    const long n8 = (long)((rows + 31) / 32) * (cols / 32) * 64;
+    if (n8 == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_wd_prepare_q8, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
+                       (uint8_t*)img, rows, row_bytes, cols / 32, n8);
+    return hipGetLastError();
+  }
   const long n = (long)((rows + 31) / 32) * nsb * 64;
   if (n == 0) return hipSuccess;
   if (ttype == TT_Q6_K)
@@ -2265,6 +2517,7 @@ static hipError_t launch_mmq_rk(const GemvArgs& g, hipStream_t s) {
 
 hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  if (g.ttype == TT_Q8_0) return launch_mmq_q8i(g, s);
   if (g.ttype == TT_Q4_K) {
     // up to 24 tokens the K split inside the workgroup; beyond, the 32- and
     // 64-token weights-direct tiles (split over workgroups on small grids)

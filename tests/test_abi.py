@@ -127,16 +127,20 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert lib.qhip_launch_mul_mat_vec_image(p, p, None, 16, 2560, 20, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 2560, 14, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 9728, 20, 0, None) == INVALID
-    # Q6_K fragment image: Q6_K only, whole super-blocks, 1..32 tokens, alignment
+    # fragment images: Q6_K, Q4_K, Q8_0; whole 256-value super-blocks; Q6_K 1..32 tokens; alignment
     assert lib.qhip_wd_image_bytes(14, 33, 512) == 2 * 2 * 6720
     assert lib.qhip_wd_image_bytes(14, 0, 512) == 0
     assert lib.qhip_wd_image_bytes(12, 33, 512) == 2 * 2 * 4608
-    assert lib.qhip_wd_image_bytes(8, 32, 512) == -1
+    assert lib.qhip_wd_image_bytes(8, 33, 512) == 2 * 16 * 1088
+    assert lib.qhip_wd_image_bytes(8, 32, 544) == -1
+    assert lib.qhip_wd_image_bytes(2, 32, 512) == -1
     assert lib.qhip_wd_image_bytes(14, 32, 300) == -1
-    assert lib.qhip_launch_wd_prepare(8, p, 32, 512, p, None) == INVALID
+    assert lib.qhip_launch_wd_prepare(2, p, 32, 512, p, None) == INVALID
+    assert lib.qhip_launch_wd_prepare(8, p, 32, 544, p, None) == INVALID
     assert lib.qhip_launch_wd_prepare(14, p, 32, 512, ctypes.c_void_p(0x1008), None) == INVALID
     assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 33, 14, None, 0, None) == INVALID
-    assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 8, 8, None, 0, None) == INVALID
+    assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 8, 2, None, 0, None) == INVALID
+    assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 544, 8, 8, None, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_wd_image(ctypes.c_void_p(0x1008), p, p, 32, 512, 8, 14, None, 0,
                                             None) == INVALID
     assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 8, 14, ctypes.c_void_p(0x1004), 4096,

@@ -254,3 +254,142 @@ def test_wd_image_k_split_in_workgroup(gpu, oracle, tt, rows, cols, tokens):
     want = oracle.matvec(tt, np.ascontiguousarray(w[idx]), x)
     assert rel_l2(got.cpu().numpy()[:, idx], want) < TOL
     assert torch.equal(got, ops.mul_mat_wd_image(tt, img, xq, rows, cols, tokens))
+
+
+# ---- Q8_0 fragment image --------------------------------------------------------
+TQ8 = po.TT_Q8_0
+
+
+def wd_image_q8_of(w, rows, cols):
+    """The documented Q8_0 fragment-image layout, from the GGUF bytes."""
+    nb = cols // 32
+    ngrp = (rows + 31) // 32
+    pad = np.zeros((ngrp * 32, nb, 34), np.uint8)
+    pad[:rows] = w.reshape(rows, nb, 34)
+    g = pad.reshape(ngrp, 32, nb, 34).transpose(0, 2, 1, 3)  # [group, block, row, 34]
+    qs = np.zeros((ngrp, nb, 1024), np.uint8)
+    for k in range(2):
+        qs[:, :, 512 * k:512 * (k + 1)] = g[:, :, :, 2 + 16 * k:18 + 16 * k].reshape(ngrp, nb, 512)
+    pos = [16 * ((i >> 2) & 1) + 4 * (i >> 3) + (i & 3) for i in range(32)]
+    dd = np.zeros((ngrp, nb, 32, 2), np.uint8)
+    dd[:, :, pos, :] = g[:, :, :, 0:2]
+    return np.concatenate([qs.reshape(ngrp, -1), dd.reshape(ngrp, -1)], axis=1).reshape(-1)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 256), (33, 512), (70, 1024), (64, 3584)])
+def test_wd_image_q8_layout(gpu, rows, cols):
+    w = synth.make_weight(TQ8, rows, cols, seed=60, tag=rows)
+    n = ops.load().qhip_wd_image_bytes(TQ8, rows, cols)
+    assert n == (rows + 31) // 32 * (cols // 32) * 1088
+    img = ops.wd_image(TQ8, to_dev(w, gpu), rows, cols).cpu().numpy()
+    assert np.array_equal(img[:n], wd_image_q8_of(w, rows, cols))
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [
+    (100, 1024, 1), (100, 1024, 6), (100, 1024, 32), (100, 1024, 33), (100, 1024, 64), (100, 1024, 65),
+    (100, 1024, 130), (33, 768, 40), (70, 256, 9), (64, 2048, 20), (96, 3584, 70), (40, 5120, 33)])
+def test_wd_image_q8_vs_oracle(gpu, oracle, rows, cols, tokens):
+    """The Q8_0 image MMQ at both token tiles, one and several 32-block
+    super-chunks, partial ones (K not a multiple of 1024) and rows off the
+    64-row tiles: within tolerance of the oracle, within 1e-6 of the MMQ on
+    the GGUF rows (the same block integers scaled as (da sumi) dw and added
+    in four K quarters), the same bits on every run."""
+    w = synth.make_weight(TQ8, rows, cols, seed=61, tag=rows)
+    x = synth.make_act(cols, tokens, seed=62, tag=tokens)
+    wd = to_dev(w, gpu)
+    img = ops.wd_image(TQ8, wd, rows, cols)
+    xq = ops.quantize_act(TQ8, to_dev(x, gpu))
+    got = ops.mul_mat_wd_image(TQ8, img, xq, rows, cols, tokens)
+    assert rel_l2(got.cpu().numpy(), oracle.matvec(TQ8, w, x)) < TOL
+    raw = ops.mul_mat(TQ8, wd, xq, rows, cols, tokens, PATH_MMQ)
+    assert rel_l2(got.cpu().numpy(), raw.cpu().numpy()) < 1e-6
+    assert torch.equal(got, ops.mul_mat_wd_image(TQ8, img, xq, rows, cols, tokens))
+
+
+@pytest.mark.parametrize("cols,tokens", [(1024, 3), (1024, 40), (1024, 100), (2048, 33), (512, 64)])
+def test_wd_image_q8_integers_exact(gpu, oracle, cols, tokens):
+    """Unit scales: the exact sums of the block integers (up to 32 blocks of
+    +-127 x +-127, so |sumi| reaches 2^19 where the MFMA's float bias trick
+    must stay exact)."""
+    rows = 96
+    w = unit_scale_weight(TQ8, rows, cols, seed=63)
+    x = unit_scale_act(cols, tokens, seed=63)
+    act = oracle.quantize_act(TQ8, x)
+    want = oracle.block_ints(TQ8, w, act, cols).astype(np.int64).sum(-1)
+    assert np.abs(want).max() < 2 ** 24
+    img = ops.wd_image(TQ8, to_dev(w, gpu), rows, cols)
+    xq = ops.quantize_act(TQ8, to_dev(x, gpu))
+    got = ops.mul_mat_wd_image(TQ8, img, xq, rows, cols, tokens).cpu().numpy()
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+def test_wd_image_q8_extreme_blocks(gpu, oracle):
+    """Every weight and activation value +-127 at unit scales: each block's
+    |sumi| can reach 32 * 127 * 127, the bias trick's limit is 2^22."""
+    rows, cols, tokens = 64, 1024, 48
+    w = unit_scale_weight(TQ8, rows, cols, seed=64).reshape(rows, -1, 34)
+    rng = np.random.default_rng(64)
+    w[:, :, 2:] = np.where(rng.random((rows, w.shape[1], 32)) < 0.5, 0x81, 0x7F).astype(np.uint8)
+    w[:8, :, 2:] = 0x7F  # rows of +127 only: against an all +-127 token, |sumi| = 32 * 127 * 127
+    w = w.reshape(rows, -1)
+    x = np.where(rng.random((tokens, cols)) < 0.5, -127.0, 127.0).astype(np.float32)
+    x[0] = 127.0
+    act = oracle.quantize_act(TQ8, x)
+    want = oracle.block_ints(TQ8, w, act, cols).astype(np.int64).sum(-1)
+    assert np.abs(want).max() == 32 * 32 * 127 * 127
+    img = ops.wd_image(TQ8, to_dev(w, gpu), rows, cols)
+    got = ops.mul_mat_wd_image(TQ8, img, ops.quantize_act(TQ8, to_dev(x, gpu)), rows, cols, tokens).cpu().numpy()
+    assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("tokens", [512, 1673])
+def test_wd_image_q8_config4(gpu, oracle, tokens):
+    """Config 4's Q8_0 [3584, 1024] at the dense 512 tokens and the ragged
+    batch's 1673 (packed by the ragged quantizer): 512 sampled rows against
+    the oracle, all rows against the GGUF-row MMQ."""
+    rows, cols = 3584, 1024
+    w = synth.make_weight(TQ8, rows, cols, seed=65, tag=TQ8)
+    wd = to_dev(w, gpu)
+    img = ops.wd_image(TQ8, wd, rows, cols)
+    if tokens == 512:
+        x = synth.make_act(cols, tokens, seed=66, tag=tokens)
+        xq = ops.quantize_act(TQ8, to_dev(x, gpu))
+    else:
+        lens = [int(v) for v in synth.ragged_lengths(8, 16, 256, seed=0)]
+        assert sum(lens) == tokens
+        seqs = [synth.make_act(cols, n, seed=67, tag=i) for i, n in enumerate(lens)]
+        x = np.concatenate(seqs)
+        xq, _, _ = ops.quantize_ragged(TQ8, [to_dev(s, gpu) for s in seqs], cols)
+    got = ops.mul_mat_wd_image(TQ8, img, xq, rows, cols, tokens)
+    idx = np.linspace(0, rows - 1, 512).astype(int)
+    want = oracle.matvec(TQ8, np.ascontiguousarray(w[idx]), x)
+    assert rel_l2(got.cpu().numpy()[:, idx], want) < TOL
+    raw = ops.mul_mat(TQ8, wd, xq, rows, cols, tokens, PATH_MMQ)
+    assert rel_l2(got.cpu().numpy(), raw.cpu().numpy()) < 1e-6
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(3584, 1024, 6), (3584, 1024, 64), (6144, 1024, 200), (256, 2048, 64)])
+def test_backend_batches_q8_from_fragment_image(gpu, oracle, backend, rows, cols, tokens):
+    """matvecBatchK of a Q8_0 weight: from its fragment image from 6 tokens
+    where K is at most 1024 (prepare_linear builds it), else the GGUF rows;
+    with images off the GGUF-row products, within 1e-6."""
+    w = synth.make_weight(TQ8, rows, cols, seed=68, tag=rows)
+    x = synth.make_act(cols, tokens, seed=68, tag=tokens)
+    lin = backend.load_linear(TQ8, rows, cols, w)
+    base = backend.mem_placed()
+    assert backend.prepare_linear(lin) == 0
+    img = (rows + 31) // 32 * (cols // 32) * 1088
+    assert (backend.mem_placed() - base >= img) == (cols <= 1024)
+    xd = to_dev(x, gpu)
+    out = torch.empty((tokens, rows), device=gpu)
+    backend.matvec_batch_k(out, lin, xd, tokens)
+    backend.sync()
+    got = out.cpu().numpy()
+    idx = np.arange(rows) if rows <= 512 else np.linspace(0, rows - 1, 512).astype(int)
+    assert rel_l2(got[:, idx], oracle.matvec(TQ8, np.ascontiguousarray(w[idx]), x)) < TOL
+    backend.set_mmq_images(False)
+    off = torch.empty((tokens, rows), device=gpu)
+    backend.matvec_batch_k(off, lin, xd, tokens)
+    backend.sync()
+    assert rel_l2(off.cpu().numpy(), got) < 1e-6
+    backend.set_mmq_images(True)
