@@ -226,15 +226,19 @@ int qhip_launch_mmq_tuned(const void *d_w, const void *d_xq, float *d_out, int r
  * integer sub-block scales are folded into the quantized values once,
  * p = sc*q (Q4_K) or sc*(q6-32) (Q6_K), split exactly into two int8 planes
  * p = 2^S*hi + lo, so the MMQ accumulates a whole super-block on the matrix
- * core without per-group integer scaling.  560 (Q4_K) / 528 (Q6_K) bytes per
- * 256 weights.
+ * core without per-group integer scaling.  Q4_K: row-major planes, 560 bytes
+ * per 256 weights.  Q6_K: the planes in MFMA fragment order per 32-row group
+ * (16,512 bytes per 32 rows and 256 values, about 516 per 256 weights).
  *   qhip_mmq_image_bytes   image size, -1 for other types or cols % 256 != 0
  *   qhip_launch_mmq_prepare  build it from GGUF bytes (d_image 16-byte aligned)
  *   qhip_launch_mul_mat_image  the product from the image: same contract and
- *     results as qhip_launch_mul_mat_vec_tile; tile 64x64 / 64x128 / 128x64
- *     tokens x rows, 0 x 0 = default; d_work (nullable) as for
- *     qhip_launch_mul_mat_work (qhip_mul_mat_work_bytes covers the image
- *     launch too) */
+ *     results as qhip_launch_mul_mat_vec_tile; Q4_K tile 64x64 / 64x128 /
+ *     128x64 tokens x rows, 0 x 0 = default; Q6_K only 0 x 0 (its kernel has
+ *     one shape: a persistent grid over 128-row tiles of 64 or 128 tokens);
+ *     d_work (nullable) as for qhip_launch_mul_mat_work
+ *     (qhip_mul_mat_work_bytes covers the image launch too); a Q6_K launch
+ *     whose tiles must be cut over K needs it and returns invalid-value
+ *     without it */
 long qhip_mmq_image_bytes(int ttype, int rows, int cols);
 int qhip_launch_mmq_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
 int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
@@ -384,7 +388,7 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
  * (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads it
  * from 2 tokens, Q6_K up to 32) or of a Q8_0 weight with cols <= 1024 (from
  * 6 tokens) and the MMQ image of a Q6_K weight
- * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 96 tokens).
+ * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 64 tokens).
  * 0 = built or nothing to build; QHIP_DECLINE = not all built (images off, or
  * past the memory budget): the products then read the GGUF bytes.
  * No reference counterpart (its CUDA kernels decode the GGUF blocks in every

@@ -97,17 +97,17 @@ static bool mmq_supported(int ttype) {
          ttype == TT_IQ4_XS || ttype == TT_Q3_K || ttype == TT_Q2_K;
 }
 
-// The Exec mirror multiplies Q6_K weights by many tokens from their MMQ image
-// (built once per weight).  Measured on MI355X, [5120, 17408]: image 32.6 us,
-// tile 42.4 us, GEMV 44.5 us at 8 tokens; 190 / 294 us (image / tile) at 512
-// -- the tile path's per-16-value integer scaling dominates it.  For Q4_K the
-// image's 3.9x larger weight bytes cost more than the scaling they save (43 /
-// 30 us at 16 tokens, 201 / 172 us at 512), so Q4_K stays on the tile path.
-// With the deterministic split-K both run for few tokens, the tile path is
-// ahead up to 64 tokens ([5120, 17408]: 40.3 / 43.0 us image at 16 tokens,
-// 45.6 / 46.4 at 64), so the image is taken from 96 tokens.
+// The Exec mirror multiplies Q6_K weights by many tokens from their plane
+// image (built once per weight).  Measured on MI355X with the weights streamed
+// from HBM, [5120, 17408]: 48.8 / 51.9 / 53.1 / 64.7 / 76.3 / 124.6 us at 64 /
+// 96 / 128 / 192 / 256 / 512 tokens, against 49.0 / 77.8 / 78.7 / 160.9 /
+// 231.3 / 293.2 for the GGUF-row MMQ (the previous, row-major Q6_K image:
+// 54.0 / 59.6 / 61.2 / 82.0 / 106.9 / 205.9).  Below 64 tokens the fragment
+// image (up to 32) and the GGUF-row MMQ.  Q4_K stays on its fragment image:
+// its MMQ image's 3.9x larger weight bytes cost more than the scaling they
+// save.
 bool mmq_image_preferred(const GemvArgs& g) {
-  return g.ttype == TT_Q6_K && g.tokens >= 96 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+  return g.ttype == TT_Q6_K && g.tokens >= 64 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
 // Batches of a large Q6_K or Q4_K weight: the Exec mirror multiplies them
@@ -464,8 +464,11 @@ int qhip_launch_mul_mat_image(const void* d_image, const void* d_xq, float* d_ou
   hipError_t e = make_args(d_image, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
   if (mmq_image_bytes(ttype, rows, cols) < 0) return (int)hipErrorInvalidValue;
-  const bool tile_ok = (tile_tokens == 0 && tile_rows == 0) || (tile_tokens == 64 && tile_rows == 64) ||
-                       (tile_tokens == 64 && tile_rows == 128) || (tile_tokens == 128 && tile_rows == 64);
+  // Q6_K's plane-image MMQ has one shape: only the default
+  const bool tile_ok = (tile_tokens == 0 && tile_rows == 0) ||
+                       (ttype != TT_Q6_K && ((tile_tokens == 64 && tile_rows == 64) ||
+                                             (tile_tokens == 64 && tile_rows == 128) ||
+                                             (tile_tokens == 128 && tile_rows == 64)));
   if (!tile_ok || ((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
   if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
   return (int)launch_mmq_image(g, tile_tokens, tile_rows, d_work, d_work ? work_bytes : 0, S(stream));

@@ -39,7 +39,7 @@ struct qhip_backend {
   // (counters zero between launches)
   uint8_t* skwork = nullptr;
   size_t skwork_cap = 0;
-  // MMQ images of Q6_K weights: the two-plane image of the prefill MMQ
+  // MMQ images of Q6_K weights: the plane image of the prefill MMQ
   // (qhip_launch_mmq_prepare, kind kImgMmq) and the fragment image of the
   // few-token MMQ (qhip_launch_wd_prepare, kind kImgFrag), built by
   // prepare_linear or by the first product that reads them outside a graph

@@ -974,28 +974,24 @@ static long mmq_split_bytes(const GemvArgs& g, int bt, int br, int slices) {
   return kSkCountBytes + 4L * slices * tiles * bt * br;
 }
 
-// ---- MMQ on a prepared weight image (Q4_K, Q6_K) -----------------------------------------
-// The K-quants' integer sub-scales are folded into the quantized values once,
-// at weight-load time: p = sc * q (Q4_K, 0..945) or p = sc * (q6 - 32) (Q6_K,
-// -4064..4096), split exactly into two int8 planes p = 2^S * hi + lo (S = 7:
-// hi 0..7, lo 0..127; S = 6: hi -64..64, lo 0..63).  A super-block then needs
-// no per-group scaling: the 32x32x32 int8 MFMAs of both planes accumulate the
-// whole super-block, and isum = (hi_sum << S) + lo_sum is the reference's
-// integer (kernels256.c:474-498 / :720-738) exactly.  Twice the MFMAs, a sixth
-// of the VALU work per output: the loop is bound by the matrix core instead of
-// the vector ALU.  The image costs 560 (Q4_K) / 528 (Q6_K) bytes per 256
-// values (3.9x / 2.5x the GGUF bytes) -- affordable next to 288 GB of HBM.
+// ---- MMQ on a prepared weight image (Q4_K; Q6_K's image is the plane image below) -----
+// The Q4_K integer sub-scales are folded into the quantized values once, at
+// weight-load time: p = sc * q (0..945), split exactly into two int8 planes
+// p = 2^7 hi + lo (hi 0..7, lo 0..127).  A super-block then needs no
+// per-group scaling: the 32x32x32 int8 MFMAs of both planes accumulate the
+// whole super-block, and isum = (hi_sum << 7) + lo_sum is the reference's
+// integer (kernels256.c:474-498) exactly.  Twice the MFMAs, a sixth of the
+// VALU work per output.  The image costs 560 bytes per 256 values (3.9x the
+// GGUF bytes).
 //
 // Image layout (two regions, both 16-byte aligned):
 //   planes  [row][super-block] 512 bytes: hi plane [0, 256), lo plane [256, 512),
 //           values in order
-//   headers [row][super-block] Q4_K 48 bytes: min of each 16-value group as
-//           f16 (min[j/2]) [0, 32), d f32 [32, 36), dmin f32 [36, 40);
-//           Q6_K 16 bytes: d f32 [0, 4)
-// Per 256 values: 560 (Q4_K) / 528 (Q6_K) bytes.
+//   headers [row][super-block] 48 bytes: min of each 16-value group as f16
+//           (min[j/2]) [0, 32), d f32 [32, 36), dmin f32 [36, 40)
 template <int TT>
-__host__ __device__ constexpr int img_hdr_bytes() { return TT == TT_Q4_K ? 48 : 16; }
-__host__ __device__ constexpr int img_shift(int tt) { return tt == TT_Q4_K ? 7 : 6; }
+__host__ __device__ constexpr int img_hdr_bytes() { return 48; }
+__host__ __device__ constexpr int img_shift(int) { return 7; }
 // one thread per (row, super-block, 16-value group)
 template <int TT>
 __global__ __launch_bounds__(256) void k_mmq_prepare(const uint8_t* __restrict__ W, uint8_t* __restrict__ IMG,
@@ -1005,11 +1001,12 @@ __global__ __launch_bounds__(256) void k_mmq_prepare(const uint8_t* __restrict__
   const int g = (int)(gid & 15);
   const long sbi = gid >> 4;  // row * nsb + sb
   const long row = sbi / nsb, sb = sbi % nsb;
-  const uint8_t* blk = W + row * row_bytes + sb * (TT == TT_Q4_K ? 144 : 210);
+  const uint8_t* blk = W + row * row_bytes + sb * 144;
   uint8_t* ib = IMG + sbi * 512;
   uint8_t* hb = IMG + nsb_total * 512 + sbi * img_hdr_bytes<TT>();
   uint32_t hi[4] = {0, 0, 0, 0}, lo[4] = {0, 0, 0, 0};
-  if constexpr (TT == TT_Q4_K) {
+  static_assert(TT == TT_Q4_K, "the Q6_K image is the plane image");
+  {
     const int sub = g >> 1;  // 32-value sub-block, src/kernels/x86/kernels256.c:105-125
     const uint8_t* s12 = blk + 4;
     int sc, m;
@@ -1043,22 +1040,6 @@ __global__ __launch_bounds__(256) void k_mmq_prepare(const uint8_t* __restrict__
       const float d = h2f((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
       const float dmin = h2f((uint32_t)blk[2] | ((uint32_t)blk[3] << 8));
       *(uint4*)(hb + 32) = make_uint4(__float_as_uint(d), __float_as_uint(dmin), 0u, 0u);
-    }
-  } else {
-    const int sc = (int)(int8_t)blk[192 + g];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e = 16 * g + i, h = e >> 7, q = (e & 127) >> 5, l = e & 31;
-      uint32_t lq = blk[64 * h + 32 * (q & 1) + l];
-      lq = q >= 2 ? (lq >> 4) : (lq & 15u);
-      const uint32_t hb = (blk[128 + 32 * h + l] >> (2 * q)) & 3u;
-      const int pv = sc * ((int)(lq | (hb << 4)) - 32);
-      hi[i >> 2] |= ((uint32_t)(pv >> 6) & 255u) << (8 * (i & 3));  // arithmetic shift: floor
-      lo[i >> 2] |= (uint32_t)(pv & 63) << (8 * (i & 3));
-    }
-    if (g == 0) {
-      const float d = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
-      *(uint4*)(hb) = make_uint4(__float_as_uint(d), 0u, 0u, 0u);
     }
   }
   *(uint4*)(ib + 16 * g) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
@@ -1158,15 +1139,11 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
       const int q = tid + 256 * i;
       if (q < BR * NH) {
         const int row = q / NH, k = q % NH;
-        if constexpr (TT == TT_Q4_K) {
-          if (k < 2) {
-            *(i32x4*)((uint8_t*)&sm.wmn[row][0] + 16 * k) = hreg[i];
-          } else {
-            sm.wd[row] = __int_as_float(hreg[i].x);
-            sm.wdmin[row] = __int_as_float(hreg[i].y);
-          }
+        if (k < 2) {
+          *(i32x4*)((uint8_t*)&sm.wmn[row][0] + 16 * k) = hreg[i];
         } else {
           sm.wd[row] = __int_as_float(hreg[i].x);
+          sm.wdmin[row] = __int_as_float(hreg[i].y);
         }
       }
     }
@@ -1210,7 +1187,7 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
       for (int q = 0; q < 4; ++q) dy[a][q] = *(const f32x4*)&sm.ady[tb0 + 32 * a + 8 * q + 4 * lh];
 #pragma unroll
     for (int b = 0; b < NB; ++b) d[b] = sm.wd[rb0 + 32 * b + li];
-    if constexpr (TT == TT_Q4_K) {
+    {
       f16x8 am[NA], bm[NB];
       float ndm[NB];
 #pragma unroll
@@ -1233,16 +1210,6 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
             acc[a][b][e] = __builtin_fmaf(dy[a][e >> 2][e & 3], inner, acc[a][b][e]);
           }
         }
-    } else {
-#pragma unroll
-      for (int a = 0; a < NA; ++a)
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) {
-            const int isum = (chi[a][b][e] << S) + clo[a][b][e];
-            acc[a][b][e] = __builtin_fmaf(d[b] * dy[a][e >> 2][e & 3], (float)isum, acc[a][b][e]);
-          }
     }
   }
 
@@ -1250,23 +1217,20 @@ __global__ __launch_bounds__(256) void k_mmq_img(const uint8_t* __restrict__ IMG
 }
 
 long mmq_image_bytes(int ttype, int rows, int cols) {
-  if ((ttype != TT_Q4_K && ttype != TT_Q6_K) || rows < 0 || cols <= 0 || cols % 256) return -1;
-  return (long)rows * (cols / 256) * (512 + (ttype == TT_Q4_K ? img_hdr_bytes<TT_Q4_K>() : img_hdr_bytes<TT_Q6_K>()));
+  if (ttype == TT_Q6_K) return bg_image_bytes_q6k(rows, cols);
+  if (ttype != TT_Q4_K || rows < 0 || cols <= 0 || cols % 256) return -1;
+  return (long)rows * (cols / 256) * (512 + img_hdr_bytes<TT_Q4_K>());
 }
 
 hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
                               hipStream_t s) {
+  if (ttype == TT_Q6_K) return launch_bg_prepare_q6k(w, row_bytes, rows, cols, img, s);
+  if (ttype != TT_Q4_K) return hipErrorInvalidValue;
   const long nsb_total = (long)rows * (cols / 256);
   if (nsb_total <= 0) return hipSuccess;
   const unsigned grid = (unsigned)((nsb_total * 16 + 255) / 256);
-  if (ttype == TT_Q4_K)
-    hipLaunchKernelGGL(k_mmq_prepare<TT_Q4_K>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img,
-                       nsb_total, row_bytes, cols / 256);
-  else if (ttype == TT_Q6_K)
-    hipLaunchKernelGGL(k_mmq_prepare<TT_Q6_K>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img,
-                       nsb_total, row_bytes, cols / 256);
-  else
-    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_mmq_prepare<TT_Q4_K>, dim3(grid), dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img,
+                     nsb_total, row_bytes, cols / 256);
   return hipGetLastError();
 }
 
@@ -1305,11 +1269,16 @@ static int mmq_image_slices(const GemvArgs& g) {
   return mmq_slices(nsb, mmq_ksplit_for(g, 64, 64, nsb, 1));
 }
 
-long mmq_image_work_bytes(const GemvArgs& g) { return mmq_split_bytes(g, 64, 64, mmq_image_slices(g)); }
+long mmq_image_work_bytes(const GemvArgs& g) {
+  if (g.ttype == TT_Q6_K) return bg_work_bytes(g, 0);
+  return mmq_split_bytes(g, 64, 64, mmq_image_slices(g));
+}
 
-// g.w is the image
+// g.w is the image; Q6_K: the plane-image MMQ, which has one shape (bt, br
+// ignored)
 hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  if (g.ttype == TT_Q6_K) return launch_mmq_bg_q6k(g, work, work_bytes, s, 0);
   int ksplit = 1;
   if (bt <= 0 || br <= 0) {
     bt = 64;
@@ -1319,7 +1288,6 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
   }
   switch (g.ttype) {
     case TT_Q4_K: return launch_mmq_img_type<TT_Q4_K>(g, bt, br, ksplit, work, s);
-    case TT_Q6_K: return launch_mmq_img_type<TT_Q6_K>(g, bt, br, ksplit, work, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -2260,6 +2228,409 @@ static hipError_t launch_mmq_q8i(const GemvArgs& g, hipStream_t s) {
     else QHIP_Q8I(2, true, false);
   }
 #undef QHIP_Q8I
+  return hipGetLastError();
+}
+
+// ---- Q6_K MMQ from the plane image (long prompts) ---------------------------------------
+// The plane image of a Q6_K weight holds p = sc (q6 - 32) for every value
+// (kernels256.c:200-212, :720-738: q6 from ql and qh, sc the 16-value
+// group's int8 scale) split exactly as p = 64 hi + lo (lo = p & 63, hi = p >> 6
+// >= -64), both planes in MFMA fragment order: per 32-row group and
+// super-block, 8 KB of hi fragments (sub-block s at 1024 s, lane L's 16 bytes
+// at 16 L: row L % 32, values 32 s + 16 (L / 32) ..+15), 8 KB of lo fragments,
+// then the 32 rows' f32 scales d -- 16,512 bytes per 32 rows and 256 values,
+// 2.5x the GGUF bytes.  Every weight load is one aligned, contiguous 1 KB.
+//
+// Tiles of 128 rows x TK = 32 NA tokens.  Within a workgroup of four waves,
+// wave w takes row group w and all TK tokens as NA 32 x 32 tiles, so each
+// plane fragment feeds NA MFMAs.  Each tile has ONE integer accumulator: the
+// eight hi-plane MFMAs of a super-block run first, the accumulator is shifted
+// left by six, then the eight lo-plane MFMAs chain onto it, so it ends as
+// isum = 64 C_hi + C_lo, the reference's per-super-block integer exactly
+// (|isum| < 2^27).  Each plane fragment's register is reloaded with the next
+// unit's fragment as soon as its MFMAs are issued, so the weights need no
+// second register set.  Activations: the tile's TK Q8_K rows of one
+// super-block are copied into LDS by global_load_lds (double buffered): the
+// quants as 256-byte token rows with the 16-byte slots XOR-swizzled by the
+// token index (every copy instruction reads 4 tokens' contiguous 256 bytes;
+// every MFMA operand read is conflict free), the f32 scales packed.
+//
+// Work distribution (the grid is persistent: two workgroups per CU).  The
+// unit of work is one tile x one super-block.  With N workgroups and ntiles
+// tiles, the first N floor(ntiles / N) tiles are whole tiles, workgroup L
+// taking tiles L, L + N, ... (so at any time the workgroups on one XCD work
+// on neighbouring tiles: the token tiles of one row tile, which share the
+// weights); the remaining tiles are cut into P slices over K, which the
+// workgroups take after their whole tiles, piece L + N r to workgroup L.  P
+// minimises the work of the busiest workgroup (at least four super-blocks a
+// slice), and the pieces are ordered (group of ntt tiles, slice, tile) so
+// that the pieces running side by side read the same weights -- with the
+// pieces of one tile at different K they would each stream the weights.  A
+// sliced tile is finished deterministically: each slice writes its partial
+// tile to the workspace, the last to arrive adds the P partials in slice
+// order and writes the outputs.
+constexpr int kBgQ6Grp = 16512;  // plane image bytes per 32-row group and super-block
+
+struct BgPlan {
+  int ntt, nsb, ntiles, nwg;
+  int dpw;       // whole tiles per workgroup
+  int sk_tiles;  // sliced tiles
+  int P;         // slices per sliced tile
+  int gw;        // sliced tiles per piece group
+};
+
+// piece p of the sliced tiles -> (sliced tile u, slice)
+__device__ __forceinline__ void bg_piece(const BgPlan& q, int p, int& u, int& slice) {
+  const int full = q.sk_tiles / q.gw, rem = q.sk_tiles - full * q.gw;
+  if (p < full * q.P * q.gw) {
+    const int g = p / (q.P * q.gw), loc = p - g * q.P * q.gw;
+    slice = loc / q.gw;
+    u = g * q.gw + loc % q.gw;
+  } else {
+    const int loc = p - full * q.P * q.gw;
+    slice = loc / rem;
+    u = full * q.gw + loc % rem;
+  }
+}
+// the inverse
+__device__ __forceinline__ int bg_piece_index(const BgPlan& q, int u, int slice) {
+  const int full = q.sk_tiles / q.gw, rem = q.sk_tiles - full * q.gw;
+  if (u < full * q.gw) return (u / q.gw) * q.P * q.gw + slice * q.gw + u % q.gw;
+  return full * q.P * q.gw + slice * rem + (u - full * q.gw);
+}
+
+// The workgroup barrier between units: s_waitcnt vmcnt(N) lgkmcnt(0), then
+// s_barrier.  Vector memory loads complete in issue order, so vmcnt(N) means
+// everything but this wave's N most recent loads has landed; __syncthreads
+// would wait for all of them (its release fence is vmcnt(0)).  The compiler
+// barriers keep LDS accesses on their side of the s_barrier.
+template <int N>
+__device__ __forceinline__ void bg_sync() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | ((N >> 4) << 14));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int NA>
+__global__ __launch_bounds__(256, 2) void k_mmq_bg_q6k(const uint8_t* __restrict__ IMG, const uint8_t* __restrict__ XQ,
+                                                        float* __restrict__ Y, int rows, int tokens, long act_bytes,
+                                                        BgPlan P, float* __restrict__ part, unsigned* __restrict__ cnt) {
+  constexpr int TK = 32 * NA, DYO = 256 * TK, STAGE = 260 * TK;
+  constexpr long PT = 128L * TK;  // floats per partial tile
+  __shared__ __attribute__((aligned(16))) uint8_t act[2][STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
+  int L = blockIdx.x;
+  if ((P.nwg & 7) == 0) L = (L & 7) * (P.nwg >> 3) + (L >> 3);  // XCD-contiguous workgroups
+  const int nsb = P.nsb, ngrp = (rows + 31) >> 5;
+  const int dp_tiles = P.dpw * P.nwg, npieces = P.sk_tiles * P.P;
+  // this workgroup's ranges: whole tiles L + N r (r < dpw), then pieces
+  // L + N (r - dpw)
+  const int nr = P.dpw + (L < npieces ? (npieces - L + P.nwg - 1) / P.nwg : 0);
+  // a unit: range r, tile, its row tile, its token tile, super-block, the
+  // range's end, its piece (-1 for a whole tile)
+  struct U {
+    int r, tile, rt, tt, sb, end, piece;
+  };
+  auto begin = [&](int r) -> U {
+    U u;
+    u.r = r;
+    if (r < P.dpw) {
+      u.tile = L + r * P.nwg;
+      u.sb = 0;
+      u.end = nsb;
+      u.piece = -1;
+    } else {
+      int t, sl;
+      u.piece = L + (r - P.dpw) * P.nwg;
+      bg_piece(P, u.piece, t, sl);
+      u.tile = dp_tiles + t;
+      u.sb = sl * nsb / P.P;
+      u.end = (sl + 1) * nsb / P.P;
+    }
+    u.rt = u.tile / P.ntt;
+    u.tt = u.tile - u.rt * P.ntt;
+    return u;
+  };
+  auto advance = [&](U u) -> U {
+    if (u.sb + 1 < u.end) {
+      ++u.sb;
+      return u;
+    }
+    return begin(u.r + 1);
+  };
+  // The copy of a unit's activations.  Quants: instruction i of wave w copies
+  // tokens 16 i + 4 w + 0..3, 16 lanes (256 contiguous bytes) each, into
+  // 256-byte LDS rows, lane q of a token taking slot q ^ (token & 15) so that
+  // 16 consecutive tokens' slot s lie in 16 different bank groups.  Scales:
+  // one f32 per lane, the first NA / 2 waves.  Tokens past the end re-read
+  // the last one.
+  const int qtok = 4 * wv + (lane >> 4);
+  const int qoff = 4 + 16 * ((lane & 15) ^ (qtok & 15));
+  auto issue_act = [&](const U& u, uint8_t* st) {
+    const int t0 = u.tt * TK, tl = tokens - 1 - t0;
+    const uint8_t* base = XQ + (long)t0 * act_bytes + 292L * u.sb;
+#pragma unroll
+    for (int i = 0; i < TK / 16; ++i) {
+      const int tk = 16 * i + qtok < tl ? 16 * i + qtok : tl;
+      __builtin_amdgcn_global_load_lds((const void*)(base + (long)tk * act_bytes + qoff),
+                                       (__attribute__((address_space(3))) void*)(st + 1024 * (4 * i + wv)), 16, 0, 0);
+    }
+    if (wv < NA / 2) {
+      const int tk = 64 * wv + lane < tl ? 64 * wv + lane : tl;
+      __builtin_amdgcn_global_load_lds((const void*)(base + (long)tk * act_bytes),
+                                       (__attribute__((address_space(3))) void*)(st + DYO + 256 * wv), 4, 0, 0);
+    }
+  };
+  // this wave's 32-row group of unit u in the image (a group past the end
+  // re-reads the last)
+  auto wgrp = [&](const U& u) -> const uint8_t* {
+    const int grp = 4 * u.rt + wv < ngrp ? 4 * u.rt + wv : ngrp - 1;
+    return IMG + ((long)grp * nsb + u.sb) * kBgQ6Grp;
+  };
+  auto afrag = [&](const uint8_t* A, int a, int s) -> i32x4 {
+    return *(const i32x4*)(A + 256 * (32 * a + li) + 16 * ((2 * s + lh) ^ (li & 15)));
+  };
+
+  f32x16 acc[NA];
+#pragma unroll
+  for (int a = 0; a < NA; ++a)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
+  i32x16 zero = {};
+  asm volatile("" : "+v"(zero));  // one register block used as every first C operand
+  // the current unit's 16 plane fragments and row scale
+  i32x4 ph[8], pq[8];
+  float dw;
+  if (nr == 0) return;  // uniform over the workgroup
+  U cu = begin(0);
+  issue_act(cu, &act[0][0]);
+  {
+    const uint8_t* b = wgrp(cu);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      ph[s] = *(const i32x4*)(b + 1024 * s + 16 * lane);
+      pq[s] = *(const i32x4*)(b + 8192 + 1024 * s + 16 * lane);
+    }
+    dw = *(const float*)(b + 16384 + 4 * li);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int k = 0;; ++k) {
+    const bool more = cu.sb + 1 < cu.end || cu.r + 1 < nr;
+    const U nu = more ? advance(cu) : cu;  // the last unit re-reads its own operands
+    const uint8_t* A = &act[k & 1][0];
+    issue_act(nu, &act[(k & 1) ^ 1][0]);
+    const uint8_t* nb = wgrp(nu);
+    i32x16 is[NA];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+        is[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag(A, a, s), ph[s], s == 0 ? zero : is[a], 0, 0, 0);
+      ph[s] = *(const i32x4*)(nb + 1024 * s + 16 * lane);
+    }
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) is[a][e] <<= 6;
+    // the lo pass reads the same LDS operands again: without this the
+    // compiler keeps the hi pass's fragments live instead
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int a = 0; a < NA; ++a) is[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(afrag(A, a, s), pq[s], is[a], 0, 0, 0);
+      pq[s] = *(const i32x4*)(nb + 8192 + 1024 * s + 16 * lane);
+    }
+    const float d = dw;
+    dw = *(const float*)(nb + 16384 + 4 * li);
+    // acc += dy * (d * isum): lane element e holds token 8 (e / 4) + 4 (lane /
+    // 32) + e % 4 of its tile
+#pragma unroll
+    for (int a = 0; a < NA; ++a)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 dy = *(const f32x4*)(A + DYO + 4 * (32 * a + 8 * q + 4 * lh));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int e = 4 * q + i;
+          acc[a][e] = __builtin_fmaf(dy[i], d * (float)is[a][e], acc[a][e]);
+        }
+      }
+    if (!more || nu.r != cu.r) {
+      // the range ends here: a whole tile, or one slice of a sliced tile
+      const int row = 128 * cu.rt + 32 * wv + li, t0 = cu.tt * TK;
+      bool direct = cu.piece < 0 || P.P == 1;
+      if (!direct) {
+        float* pp = part + (long)cu.piece * PT + (long)wv * (1024 * NA) + lane;
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sk_store(pp + (a * 16 + e) * 64, acc[a][e]);
+        const int u = cu.tile - dp_tiles;
+        unsigned* tc = cnt + u;
+        if (sk_arrive(tc, (unsigned)P.P)) {
+#pragma unroll
+          for (int a = 0; a < NA; ++a)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
+          for (int sl = 0; sl < P.P; ++sl) {
+            const float* qq = part + (long)bg_piece_index(P, u, sl) * PT + (long)wv * (1024 * NA) + lane;
+#pragma unroll
+            for (int a = 0; a < NA; ++a) {
+              float v[16];
+#pragma unroll
+              for (int e = 0; e < 16; ++e) v[e] = sk_load(qq + (a * 16 + e) * 64);
+#pragma unroll
+              for (int e = 0; e < 16; ++e) acc[a][e] += v[e];
+            }
+          }
+          sk_reset(tc);
+          direct = true;
+        }
+      }
+      if (direct) {
+#pragma unroll
+        for (int a = 0; a < NA; ++a)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) {
+            const int t = t0 + 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
+            if (row < rows && t < tokens) Y[(long)t * rows + row] = acc[a][e];
+          }
+      }
+#pragma unroll
+      for (int a = 0; a < NA; ++a)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
+    }
+    // unit k+1's activations are in LDS once this wave's copy has landed;
+    // the 17 weight loads issued after it may stay in flight
+    bg_sync<17>();
+    if (!more) break;
+    cu = nu;
+  }
+}
+
+// One thread per (32-row group, super-block, sub-block s, lane L): the 16
+// values 32 s + 16 (L / 32) .. +15 of row 32 group + L % 32 as both planes,
+// and for s = 0 the row's f32 scale.  Rows past the end: zeros.
+__global__ __launch_bounds__(256) void k_bg_prepare_q6k(const uint8_t* __restrict__ W, uint8_t* __restrict__ IMG,
+                                                         int rows, long row_bytes, int nsb, long nthreads) {
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= nthreads) return;
+  const int Lq = (int)(gid & 63), s = (int)((gid >> 6) & 7);
+  const long gs = gid >> 9;  // group * nsb + sb
+  const long grp = gs / nsb;
+  const int sb = (int)(gs - grp * nsb);
+  const long row = grp * 32 + (Lq & 31);
+  const int e0 = 32 * s + 16 * (Lq >> 5);
+  uint32_t hi[4] = {0, 0, 0, 0}, lo[4] = {0, 0, 0, 0};
+  float d = 0.0f;
+  if (row < rows) {
+    const uint8_t* blk = W + row * row_bytes + 210L * sb;
+    const int sc = (int)(int8_t)blk[192 + (e0 >> 4)];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = e0 + i, h = e >> 7, q = (e & 127) >> 5, l = e & 31;
+      uint32_t lq = blk[64 * h + 32 * (q & 1) + l];
+      lq = q >= 2 ? (lq >> 4) : (lq & 15u);
+      const uint32_t hb = (blk[128 + 32 * h + l] >> (2 * q)) & 3u;
+      const int pv = sc * ((int)(lq | (hb << 4)) - 32);
+      hi[i >> 2] |= ((uint32_t)(pv >> 6) & 255u) << (8 * (i & 3));  // arithmetic shift: floor
+      lo[i >> 2] |= (uint32_t)(pv & 63) << (8 * (i & 3));
+    }
+    d = h2f((uint32_t)blk[208] | ((uint32_t)blk[209] << 8));
+  }
+  uint8_t* b = IMG + gs * kBgQ6Grp;
+  *(uint4*)(b + 1024 * s + 16 * Lq) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+  *(uint4*)(b + 8192 + 1024 * s + 16 * Lq) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+  if (s == 0 && Lq < 32) *(float*)(b + 16384 + 4 * Lq) = d;
+}
+
+long bg_image_bytes_q6k(int rows, int cols) {
+  if (rows < 0 || cols <= 0 || cols % 256) return -1;
+  return (long)((rows + 31) / 32) * (cols / 256) * kBgQ6Grp;
+}
+
+hipError_t launch_bg_prepare_q6k(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s) {
+  if (bg_image_bytes_q6k(rows, cols) < 0) return hipErrorInvalidValue;
+  const long n = (long)((rows + 31) / 32) * (cols / 256) * 512;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_bg_prepare_q6k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (const uint8_t*)w,
+                     (uint8_t*)img, rows, row_bytes, cols / 256, n);
+  return hipGetLastError();
+}
+
+// Token tiles of the plane-image MMQ: 64 tokens up to 192, else 128.
+// Measured on MI355X, [5120, 17408]: 64.3 / 64.7 / 78.1 / 101.1 / 108.6 /
+// 144.5 us at 160 / 192 / 256 / 320 / 384 / 512 tokens with 64-token tiles,
+// 74.8 / 72.9 / 75.7 / 96.1 / 95.7 / 123.3 with 128-token tiles.
+static int bg_na(const GemvArgs& g) { return g.tokens <= 192 ? 2 : 4; }
+
+// split = false: no tile is cut over K (no workspace needed)
+static BgPlan bg_plan(const GemvArgs& g, int nwg, bool split) {
+  BgPlan p{};
+  const int tk = 32 * bg_na(g);
+  p.nsb = g.cols / 256;
+  p.ntt = (g.tokens + tk - 1) / tk;
+  p.ntiles = p.ntt * ((g.rows + 127) / 128);
+  if (nwg <= 0) {
+    const int cus = qhip_gpu_cu_count();
+    nwg = 2 * (cus > 0 ? cus : 256);  // two workgroups per CU
+  }
+  p.nwg = nwg;
+  p.dpw = p.ntiles / p.nwg;
+  p.sk_tiles = p.ntiles - p.dpw * p.nwg;
+  p.P = 1;
+  p.gw = 1;
+  if (p.sk_tiles > 0 && split && p.sk_tiles <= kSkMaxTiles) {
+    // the slice count with the least work on the busiest workgroup (ties:
+    // fewer slices), at least four super-blocks a slice; a slice costs its
+    // super-blocks plus about two for writing and adding its partial tile
+    long best = -1;
+    const int pmax = p.nsb / 4 > 1 ? p.nsb / 4 : 1;
+    for (int q = 1; q <= pmax && q <= 64; ++q) {
+      const long per = (long)p.sk_tiles * q;
+      const long m = ((per + p.nwg - 1) / p.nwg) * ((p.nsb + q - 1) / q + (q > 1 ? 2 : 0));
+      if (best < 0 || m < best) {
+        best = m;
+        p.P = q;
+      }
+    }
+    p.gw = p.ntt < p.sk_tiles ? p.ntt : p.sk_tiles;
+  }
+  if (p.dpw == 0 && (long)p.sk_tiles * p.P < p.nwg) p.nwg = p.sk_tiles * p.P;  // no workgroup without work
+  return p;
+}
+
+// Workspace of the plane-image MMQ: tile counters, then one partial tile per
+// piece (none when no tile is sliced).
+long bg_work_bytes(const GemvArgs& g, int nwg) {
+  if (g.rows <= 0 || g.tokens <= 0 || g.cols <= 0 || g.cols % 256) return 0;
+  const BgPlan p = bg_plan(g, nwg, true);
+  if (p.P <= 1) return 0;
+  return kSkCountBytes + (long)p.sk_tiles * p.P * 128L * 32 * bg_na(g) * 4;
+}
+
+// g.w: the Q6_K plane image; nwg > 0 overrides the persistent grid.  Without
+// a workspace of bg_work_bytes no tile is cut over K.
+hipError_t launch_mmq_bg_q6k(const GemvArgs& g, void* work, long work_bytes, hipStream_t s, int nwg) {
+  if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  if (g.ttype != TT_Q6_K || g.cols % 256 || g.act_bytes != 292L * (g.cols / 256) ||
+      (long)g.tokens * g.act_bytes > 0x7FFFFFFFL || (long)g.tokens * ((g.rows + 127) / 128) > 0x3FFFFFFFL)
+    return hipErrorInvalidValue;
+  const long need = bg_work_bytes(g, nwg);
+  const BgPlan p = bg_plan(g, nwg, need > 0 && work && work_bytes >= need);
+  unsigned* cnt = (unsigned*)work;
+  float* part = work ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
+  if (bg_na(g) == 2)
+    hipLaunchKernelGGL(k_mmq_bg_q6k<2>, dim3((unsigned)p.nwg), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, p, part, cnt);
+  else
+    hipLaunchKernelGGL(k_mmq_bg_q6k<4>, dim3((unsigned)p.nwg), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, p, part, cnt);
   return hipGetLastError();
 }
 

@@ -67,8 +67,15 @@ long mmq_work_bytes(const GemvArgs& g);
 long mmq_image_bytes(int ttype, int rows, int cols);
 hipError_t launch_mmq_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
                               hipStream_t s);
-// g.w = the image; bt x br tile (0 = default; splits K as launch_mmq)
+// g.w = the image; bt x br tile (0 = default; splits K as launch_mmq); Q6_K
+// (the plane image) has one shape and ignores bt, br
 hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long work_bytes, hipStream_t s);
+// Q6_K plane image and its MMQ (mmq.hip); the workspace: bg_work_bytes (0:
+// none needed), its first kSkCountBytes zero; nwg > 0 overrides the grid
+long bg_image_bytes_q6k(int rows, int cols);
+hipError_t launch_bg_prepare_q6k(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s);
+long bg_work_bytes(const GemvArgs& g, int nwg);
+hipError_t launch_mmq_bg_q6k(const GemvArgs& g, void* work, long work_bytes, hipStream_t s, int nwg);
 // Q6_K fragment image (the GGUF bytes permuted for the few-token MMQ)
 long wd_image_bytes(int ttype, int rows, int cols);
 hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,

@@ -17,7 +17,7 @@ import pytest
 import torch
 
 import pyoracle as po
-from qwen35_amd import ops, synth
+from qwen35_amd import _lib, ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -208,7 +208,7 @@ def test_backend_image_budget_and_opt_out(gpu, oracle):
     w = synth.make_weight(tt, rows, cols, seed=3, tag=tt)
     x = synth.make_act(cols, T, seed=3)
     want = oracle.matvec(tt, w, x, nthreads=THREADS)
-    img_bytes = rows * cols // 256 * 528
+    img_bytes = _lib.load().qhip_mmq_image_bytes(tt, rows, cols)  # the plane image, 2.5x the GGUF bytes
     frag_bytes = rows * cols // 256 * 210  # the few-token fragment image, built with it
     xd = to_dev(x, gpu)
     for mode in ("capped", "off", "prepared"):
@@ -276,3 +276,27 @@ def test_budget_rejects_upload(gpu):
         assert be.mem_placed() == 0
     finally:
         be.close()
+
+
+def test_q6k_plane_image_whole_and_sliced_tiles(gpu, oracle):
+    """The Q6_K plane-image MMQ on a grid with more tiles than resident
+    workgroups: whole tiles, then the remaining tiles cut over K (with the
+    workspace) or whole again (without); both within the tolerance on the
+    sampled rows (the last row tile is partly past the end), the split form
+    bit-equal on a rerun."""
+    tt, rows, cols, T = po.TT_Q6_K, 16480, 2304, 512
+    w = synth.make_weight(tt, rows, cols, seed=21, tag=tt)
+    x = synth.make_act(cols, T, seed=21)
+    idx = sample_rows(rows, 21)
+    idx = np.unique(np.concatenate([idx, np.arange(rows - 96, rows)]))
+    want = oracle.matvec(tt, np.ascontiguousarray(w[idx]), x, nthreads=THREADS)
+    wd = to_dev(w, gpu)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    img = ops.mmq_image(tt, wd, rows, cols)
+    del wd
+    work = ops.mul_mat_work(rows, cols, T, tt, gpu)
+    assert work is not None
+    a = ops.mul_mat_image(tt, img, xq, rows, cols, T, work=work)
+    check(a.cpu().numpy()[:, idx], want, "image+work")
+    assert torch.equal(a, ops.mul_mat_image(tt, img, xq, rows, cols, T, work=work))
+    check(ops.mul_mat_image(tt, img, xq, rows, cols, T).cpu().numpy()[:, idx], want, "image")

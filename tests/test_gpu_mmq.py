@@ -256,20 +256,35 @@ def _q6k_p(w, cols):
 
 @pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
 def test_mmq_image_planes(gpu, tt):
-    rows, cols = 9, 1024
+    rows, cols = 9 if tt == po.TT_Q4_K else 45, 1024
     w = synth.make_weight(tt, rows, cols, seed=12, tag=tt)
     img = ops.mmq_image(tt, to_dev(w, gpu), rows, cols).cpu().numpy()
     nsb = cols // 256
-    planes = img[:rows * nsb * 512].reshape(rows, nsb, 512)
-    S = 7 if tt == po.TT_Q4_K else 6
-    hi = planes[:, :, :256].view(np.int8).astype(np.int64)
-    lo = planes[:, :, 256:].astype(np.int64)
     p = _q4k_p(w, cols) if tt == po.TT_Q4_K else _q6k_p(w, cols)
+    if tt == po.TT_Q4_K:
+        planes = img[:rows * nsb * 512].reshape(rows, nsb, 512)
+        S = 7
+        hi = planes[:, :, :256].view(np.int8).astype(np.int64)
+        lo = planes[:, :, 256:].astype(np.int64)
+    else:
+        # per 32-row group and super-block: hi fragments [s][lane][16], lo
+        # fragments, then the 32 rows' f32 d; lane L holds row L % 32, values
+        # 32 s + 16 (L // 32) .. +15
+        S = 6
+        ngrp = -(-rows // 32)
+        g = img.reshape(ngrp, nsb, 16512)
+        fr = g[:, :, :16384].reshape(ngrp, nsb, 2, 8, 2, 32, 16)  # plane, s, L // 32, L % 32, byte
+        fr = fr.transpose(2, 0, 5, 1, 3, 4, 6).reshape(2, ngrp * 32, nsb, 256)[:, :rows]
+        hi = fr[0].view(np.int8).astype(np.int64)
+        lo = fr[1].astype(np.int64)
+        d = g[:, :, 16384:].copy().view(np.float32).transpose(0, 2, 1).reshape(ngrp * 32, nsb)
+        blk = w.reshape(rows, nsb, 210)
+        assert np.array_equal(d[:rows], blk[:, :, 208:210].copy().view(np.float16)[..., 0].astype(np.float32))
+        assert not d[rows:].any()
     assert np.array_equal(hi * (1 << S) + lo, p)
     assert lo.min() >= 0 and lo.max() < (1 << S) and hi.min() >= -128 and hi.max() <= 127
-    hdr = img[rows * nsb * 512:]
     if tt == po.TT_Q4_K:
-        hdr = hdr.reshape(rows, nsb, 48)
+        hdr = img[rows * nsb * 512:].reshape(rows, nsb, 48)
         d = hdr[:, :, 32:36].copy().view(np.float32)[..., 0]
         dmin = hdr[:, :, 36:40].copy().view(np.float32)[..., 0]
         blk = w.reshape(rows, nsb, 144)
@@ -282,14 +297,16 @@ def test_mmq_image_planes(gpu, tt):
             m = (s12[:, :, k + 4] & 63) if k < 4 else ((s12[:, :, k + 4] >> 4) | ((s12[:, :, k] >> 6) << 4))
             assert np.array_equal(mins[:, :, j], m)
     else:
-        hdr = hdr.reshape(rows, nsb, 16)
-        d = hdr[:, :, 0:4].copy().view(np.float32)[..., 0]
-        blk = w.reshape(rows, nsb, 210)
-        assert np.array_equal(d, blk[:, :, 208:210].copy().view(np.float16)[..., 0].astype(np.float32))
+        # the padding rows of the last group are zeros
+        pad = img.reshape(-1, nsb, 16512)[-1, :, :16384].reshape(nsb, 2, 8, 2, 32, 16)[:, :, :, :, rows % 32:]
+        assert not pad.any()
 
 
+# Q6_K: 64-token tiles (<= 192 tokens) and 128-token tiles, rows and tokens
+# off every tile size, grids whose tiles are cut over K
 IMG_CASES = [(po.TT_Q4_K, 150, 512, 65), (po.TT_Q4_K, 64, 2560, 16), (po.TT_Q6_K, 100, 768, 40),
-             (po.TT_Q6_K, 72, 2304, 129)]
+             (po.TT_Q6_K, 72, 2304, 129), (po.TT_Q6_K, 200, 2304, 300), (po.TT_Q6_K, 333, 4608, 70),
+             (po.TT_Q6_K, 40, 1024, 193), (po.TT_Q6_K, 129, 2560, 1)]
 
 
 @pytest.mark.parametrize("tt,rows,cols,tokens", IMG_CASES,
@@ -300,12 +317,19 @@ def test_mmq_image_matches_oracle(gpu, oracle, tt, rows, cols, tokens):
     want = oracle.matvec(tt, w, x)
     img = ops.mmq_image(tt, to_dev(w, gpu), rows, cols)
     xq = ops.quantize_act(tt, to_dev(x, gpu))
-    for bt, br in [(64, 64), (64, 128), (128, 64), (0, 0)]:
+    tiles = [(64, 64), (64, 128), (128, 64), (0, 0)] if tt == po.TT_Q4_K else [(0, 0)]
+    for bt, br in tiles:
         got = ops.mul_mat_image(tt, img, xq, rows, cols, tokens, bt, br).cpu().numpy()
         assert rel_l2(got, want) < TOL, (bt, br, rel_l2(got, want))
     work = ops.mul_mat_work(rows, cols, tokens, tt, gpu)
     got = ops.mul_mat_image(tt, img, xq, rows, cols, tokens, work=work).cpu().numpy()
     assert rel_l2(got, want) < TOL
+    if tt == po.TT_Q6_K:
+        # one shape only: an explicit tile is refused before any launch
+        L = _lib.load()
+        out = torch.empty((tokens, rows), device=gpu)
+        assert L.qhip_launch_mul_mat_image(img.data_ptr(), xq.data_ptr(), out.data_ptr(), rows, cols, tokens, tt,
+                                           64, 64, None, 0, None) == 1  # hipErrorInvalidValue
 
 
 @pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
@@ -328,7 +352,8 @@ def test_mmq_image_rejects_other_types(gpu):
     assert L.qhip_mmq_image_bytes(po.TT_Q8_0, 4, 1024) == -1
     assert L.qhip_mmq_image_bytes(po.TT_Q4_K, 4, 1000) == -1
     assert L.qhip_mmq_image_bytes(po.TT_Q4_K, 4, 1024) == 4 * 4 * 560
-    assert L.qhip_mmq_image_bytes(po.TT_Q6_K, 4, 1024) == 4 * 4 * 528
+    assert L.qhip_mmq_image_bytes(po.TT_Q6_K, 4, 1024) == 1 * 4 * 16512
+    assert L.qhip_mmq_image_bytes(po.TT_Q6_K, 33, 1024) == 2 * 4 * 16512
     w = torch.zeros(4 * 34 * 32, dtype=torch.uint8, device=gpu)
     img = torch.empty(4096, dtype=torch.uint8, device=gpu)
     assert L.qhip_launch_mmq_prepare(po.TT_Q8_0, w.data_ptr(), 4, 1024, img.data_ptr(), None) != 0
@@ -336,8 +361,9 @@ def test_mmq_image_rejects_other_types(gpu):
 
 @pytest.mark.parametrize("tt", [po.TT_Q4_K, po.TT_Q6_K])
 def test_backend_prefill_batch(gpu, oracle, tt):
-    """matvecBatchK above the crossover: the MMQ image for Q6_K, the tile MMQ
-    for Q4_K; the second call reuses the cached image."""
+    """matvecBatchK above the crossover: the MMQ image for Q6_K (the plane
+    image, from 64 tokens), the tile MMQ for Q4_K; the second call reuses the
+    cached image."""
     rows, cols, k = 130, 2560 if tt == po.TT_Q4_K else 2304, 80 if tt == po.TT_Q4_K else 130
     w = synth.make_weight(tt, rows, cols, seed=31, tag=tt)
     x = synth.make_act(cols, k, seed=31)

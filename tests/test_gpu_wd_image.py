@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import pyoracle as po
-from qwen35_amd import ops, synth
+from qwen35_amd import _lib, ops, synth
 from test_gpu_mmq import rel_l2, to_dev, unit_scale_act, unit_scale_weight
 
 pytestmark = pytest.mark.gpu
@@ -145,7 +145,9 @@ def test_backend_batches_from_fragment_image(gpu, oracle, backend, tt, tokens):
     lin = backend.load_linear(tt, rows, cols, w)
     base = backend.mem_placed()
     assert backend.prepare_linear(lin) == 0
-    img = rows * cols // 256 * (210 + 528 if tt == TQ6 else 144)  # fragment (+ Q6_K MMQ) image
+    img = rows * cols // 256 * (210 if tt == TQ6 else 144)  # the fragment image
+    if tt == TQ6:
+        img += _lib.load().qhip_mmq_image_bytes(tt, rows, cols)  # and the Q6_K plane image
     assert backend.mem_placed() - base >= img
     xd = to_dev(x, gpu)
     out = torch.empty((tokens, rows), device=gpu)
