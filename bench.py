@@ -316,7 +316,10 @@ class Cfg2:
 GEMV_CONFIGS = (("cfg1_q8_0_6144x1024", TQ8, 6144, 1024),
                 ("cfg5_q4_k_17408x5120", TQ4, 17408, 5120),
                 ("cfg5_q6_k_5120x17408", TQ6, 5120, 17408),
-                # further formats at the config-5 gate/up shape
+                # the benchmark formats Q8_0 and IQ4_NL, and the further
+                # formats, at the config-5 gate/up shape
+                ("q8_0_17408x5120", TQ8, 17408, 5120),
+                ("iq4_nl_17408x5120", TIQ, 17408, 5120),
                 ("q5_k_17408x5120", 13, 17408, 5120),
                 ("q3_k_17408x5120", 11, 17408, 5120),
                 ("q2_k_17408x5120", 10, 17408, 5120),
@@ -345,13 +348,32 @@ def bench_gemv_configs(c: Ctx):
     for name, tt, rows, cols in GEMV_CONFIGS:
         t1 = time.time()
         st, one, keep = gemv_stream(c, tt, rows, cols)
-        s = time_loop(c.torch, one, max(50, min(2000, int(2e9 // st.n))), 10)
+        iters = max(50, min(2000, int(2e9 // st.n)))
+        s = time_loop(c.torch, one, iters, 10)
         alg = gemv_bytes(rows, cols, st.n)
         extra[name] = {"gbs": round(alg / s / 1e9, 1), "hbm_frac": round(alg / s / 1e9 / HBM_PEAK_GBS, 4),
                        "avg_us": round(s * 1e6, 3), "alg_bytes": alg, "copies": st.copies,
                        "single_launch_us": round(single_latency(c.torch, one) * 1e6, 2)}
+        if c.lib.qhip_gemv_image_bytes(tt, rows, cols) > 0 and rows * cols > (1 << 23):
+            # the formats with a GEMV weight image: what the Exec mirror reads
+            # for one token (the same bytes reordered, rotated alike), on the
+            # split activation
+            imgs = [c.ops.gemv_image(tt, st.buf[k * st.stride:k * st.stride + st.n], rows, cols)
+                    for k in range(st.copies)]
+            x = c.torch.from_numpy(c.synth.make_act(cols, 1, seed=0, tag=104)).to(c.dev)
+            xa = c.ops.quantize_act_image(tt, x)
+            y = c.torch.empty(rows, device=c.dev)
+            img_one = lambda i: c.lib.qhip_launch_mul_mat_vec_image(imgs[i % len(imgs)].data_ptr(), xa.data_ptr(),
+                                                                   y.data_ptr(), rows, cols, tt, 0, c.stream)
+            si = time_loop(c.torch, img_one, iters, 10)
+            extra[name].update({"image_gbs": round(alg / si / 1e9, 1),
+                                "image_hbm_frac": round(alg / si / 1e9 / HBM_PEAK_GBS, 4),
+                                "image_avg_us": round(si * 1e6, 3)})
+            del imgs
         log(f"{name}: {extra[name]['gbs']} GB/s, {extra[name]['avg_us']} us/launch "
-            f"({st.copies} copies, {time.time() - t1:.1f}s)")
+            + (f"(GEMV image {extra[name]['image_gbs']} GB/s, {extra[name]['image_avg_us']} us) "
+               if "image_gbs" in extra[name] else "")
+            + f"({st.copies} copies, {time.time() - t1:.1f}s)")
         del st, keep
         c.torch.cuda.empty_cache()
     return extra
@@ -417,9 +439,22 @@ def bench_mmq(c: Ctx):
     res["cfg4_dense512_q8_0_3584x1024"] = {"tokens": T, "tokens_per_s": round(T / s_d, 1),
                                            "us_mmq": round(s_d * 1e6, 2), "int8_tops": tops, "int8_mfma_frac": fr,
                                            "alg_bytes": mem, "hbm_frac": round(mem / s_d / 1e9 / HBM_PEAK_GBS, 4)}
-    log(f"mmq cfg4: ragged {total} tokens {s_mm * 1e6:.1f} us "
-        f"({res['cfg4_ragged_q8_0_3584x1024']['int8_mfma_frac']:.3f} of int8 peak); dense 512 {s_d * 1e6:.1f} us")
-    del w, xq, yo, seqs
+    # what the Exec mirror launches for these (K <= 1024, from 6 tokens): the
+    # MMQ from the weight's Q8_0 fragment image, on the same packed rows
+    img8 = ops.wd_image(tt, w, rows, cols)
+    s_ri = timed(lambda: lib.qhip_launch_mul_mat_wd_image(img8.data_ptr(), xq.data_ptr(), yo.data_ptr(), rows, cols,
+                                                          total, tt, None, 0, stream), 200)
+    s_di = timed(lambda: lib.qhip_launch_mul_mat_wd_image(img8.data_ptr(), xq5.data_ptr(), y5.data_ptr(), rows, cols,
+                                                          T, tt, None, 0, stream), 200)
+    for key, sec, nt in (("cfg4_ragged_q8_0_3584x1024", s_ri, total), ("cfg4_dense512_q8_0_3584x1024", s_di, T)):
+        tops, fr = frac(rows, cols, nt, sec)
+        res[key].update({"us_mmq_fragment_image": round(sec * 1e6, 2), "fragment_image_int8_tops": tops,
+                         "fragment_image_int8_mfma_frac": fr, "mirror_path": "fragment_image",
+                         "mirror_us": round(sec * 1e6, 2)})
+    log(f"mmq cfg4: ragged {total} tokens {s_mm * 1e6:.1f} us (fragment image {s_ri * 1e6:.1f}) "
+        f"({res['cfg4_ragged_q8_0_3584x1024']['int8_mfma_frac']:.3f} of int8 peak); dense 512 {s_d * 1e6:.1f} us "
+        f"(fragment image {s_di * 1e6:.1f})")
+    del w, xq, yo, seqs, img8
 
     sweep = {}
 

@@ -283,12 +283,13 @@ int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d
                                  int tokens, int ttype, void *d_work, long work_bytes, void *stream);
 
 /* GEMV weight image (no reference counterpart; the reference's CUDA GEMV reads
- * the GGUF blocks as they are, mmvq.cu).  For the 32-value 4-bit formats
- * (IQ4_NL, Q4_0), whose 18-byte blocks leave every 16-byte piece of a row
- * misaligned: the same bytes per row (36 per 64 values), reordered so that
- * each 16-byte load of the GEMV is aligned and the lanes of a team read one
- * contiguous span -- 16 quant bytes per block in the order the team walks
- * the row, then the f16 scales, each lane's adjacent.  The order depends on
+ * the GGUF blocks as they are, mmvq.cu).  For the 32-value formats (IQ4_NL,
+ * Q4_0: 18-byte blocks; Q8_0: 34-byte blocks), whose blocks leave every
+ * 16-byte piece of a row misaligned: the same bytes per row (36 / 68 per 64
+ * values), reordered so that each 16-byte load of the GEMV is aligned and the
+ * lanes of a team read one contiguous span -- the 16-byte quant pieces of
+ * each block (one for the 4-bit formats, two for Q8_0) in the order the team
+ * walks the row, then the f16 scales, each lane's adjacent.  The order depends on
  * the row width only (the team width and pass count the library takes for
  * it); widths 1024, 1280, 2048, 2560, 3072, 3840, 4096, 5120, 6144 and 8192
  * have one.  The activation of the image GEMV is quantized

@@ -514,7 +514,7 @@ int qhip_launch_gemv_prepare(int ttype, const void* d_w, int rows, int cols, voi
   if (rows == 0) return 0;
   if (!d_w || !d_image || !aligned4(d_w) || ((uintptr_t)d_image & 15u) || d_image == d_w)
     return (int)hipErrorInvalidValue;
-  return (int)launch_gemv_image_prepare(d_w, rb, rows, cols, d_image, S(stream));
+  return (int)launch_gemv_image_prepare(d_w, rb, rows, cols, d_image, S(stream), ttype == TT_Q8_0);
 }
 
 int qhip_launch_quantize_act_image(int ttype, const float* d_x, void* d_xa, int cols, int tokens, void* stream) {

@@ -1,4 +1,4 @@
-// gemv_image.hip -- batch-1 GEMV of the 32-value 4-bit formats (IQ4_NL, Q4_0)
+// gemv_image.hip -- batch-1 GEMV of the 32-value formats (IQ4_NL, Q4_0, Q8_0)
 // from a GEMV weight image.
 //
 // Why an image.  An 18-byte block puts its 16 quant bytes at offset 2 of an
@@ -18,6 +18,11 @@
 //                                  i in the low nibble, i+16 in the high one)
 //     [32 U + 4 (j P + p)]         the f16 scales of blocks 2u (low half) and
 //                                  2u+1 (high half): a lane's P pairs adjacent
+//   Q8_0 (34-byte blocks: the quants at offset 2 of a 34-byte stride, every
+//   16-byte piece misaligned alike), 68 U bytes per row:
+//     [16 (((2p + e) 2 + h) T + j)]  quant bytes 16h..16h+15 of block 2u+e
+//                                  (the activation's slot order below)
+//     [64 U + 4 (j P + p)]         the f16 scales of blocks 2u and 2u+1
 //
 // The activation is quantized (the same Q8_0 values and scales as the
 // reference layout, quantize.hip) into the matching split layout, 72 U bytes
@@ -34,7 +39,11 @@
 
 namespace qhip {
 
-bool gemv_image_format(int ttype) { return ttype == TT_IQ4_NL || ttype == TT_Q4_0; }
+bool gemv_image_format(int ttype) { return ttype == TT_IQ4_NL || ttype == TT_Q4_0 || ttype == TT_Q8_0; }
+
+// 16-byte quant slots per 32-value block: the 4-bit formats one, Q8_0 two
+template <int TT>
+__host__ __device__ constexpr int img_qs() { return TT == TT_Q8_0 ? 2 : 1; }
 
 // Team width and passes for a row width.  Swept on MI355X over T = 8..64 and
 // one, two or four rows per team: 20-lane teams wherever U is a multiple of
@@ -56,11 +65,12 @@ bool gemv_image_width(int cols) {
   return img_geom(cols, T, P);
 }
 
-// One block's integer dot: 16 quant bytes against values 0..15 (y0) and
-// 16..31 (y1).
+// One block's integer dot (kernels32.c:342-361, :447-464): the quant slots q
+// (4-bit: one, both halves; Q8_0: two, values 0..15 and 16..31) against
+// activation values 0..15 (y0) and 16..31 (y1).
 template <int TT>
-__device__ __forceinline__ int img_block(const u32x4& q, const u32x4& y0, const u32x4& y1) {
-  const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+__device__ __forceinline__ int img_block(const u32x4 (&q)[img_qs<TT>()], const u32x4& y0, const u32x4& y1) {
+  const uint32_t qq[4] = {q[0].x, q[0].y, q[0].z, q[0].w};
   const uint32_t ya[4] = {y0.x, y0.y, y0.z, y0.w};
   const uint32_t yb[4] = {y1.x, y1.y, y1.z, y1.w};
   int s = 0;
@@ -69,9 +79,14 @@ __device__ __forceinline__ int img_block(const u32x4& q, const u32x4& y0, const 
     if constexpr (TT == TT_IQ4_NL) {
       s = dot4(iq4_lo(qq[i]), ya[i], s);
       s = dot4(iq4_hi(qq[i]), yb[i], s);
-    } else {
+    } else if constexpr (TT == TT_Q4_0) {
       s = dot4(nib_minus8(qq[i] & 0x0F0F0F0Fu), ya[i], s);
       s = dot4(nib_minus8((qq[i] >> 4) & 0x0F0F0F0Fu), yb[i], s);
+    } else {
+      const uint32_t q1[4] = {q[img_qs<TT>() - 1].x, q[img_qs<TT>() - 1].y, q[img_qs<TT>() - 1].z,
+                              q[img_qs<TT>() - 1].w};
+      s = dot4(qq[i], ya[i], s);
+      s = dot4(q1[i], yb[i], s);
     }
   }
   return s;
@@ -83,7 +98,7 @@ __device__ __forceinline__ int img_block(const u32x4& q, const u32x4& y0, const 
 template <int TT, int T, int P, int NR>
 __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XA,
                                                    float* __restrict__ Y, int rows, long row_bytes) {
-  constexpr int U = T * P, TPW = 64 / T;
+  constexpr int U = T * P, TPW = 64 / T, QS = img_qs<TT>();
   const int lane = threadIdx.x & 63;
   const int r = lane / T, j = lane - r * T;
   const long row0 = (((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW + r) * NR;
@@ -102,14 +117,16 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
 #pragma unroll
     for (int k = 0; k < NR; ++k)
 #pragma unroll
-      for (int p = 0; p < P; ++p) ws[k][p] = ld32(wr[k] + 32 * U + 4 * (j * P + p));
+      for (int p = 0; p < P; ++p) ws[k][p] = ld32(wr[k] + 32 * QS * U + 4 * (j * P + p));
 #pragma unroll
     for (int p = 0; p < P; ++p) {
-      u32x4 q[NR][2];
+      u32x4 q[NR][2][QS];
 #pragma unroll
       for (int k = 0; k < NR; ++k)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) q[k][e] = ld128(wr[k] + ((2 * p + e) * T + j) * 16);
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int h = 0; h < QS; ++h) q[k][e][h] = ld128(wr[k] + (((2 * p + e) * QS + h) * T + j) * 16);
       u32x4 y[2][2];
 #pragma unroll
       for (int e = 0; e < 2; ++e)
@@ -143,12 +160,31 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
 
 // GGUF rows -> image rows; one thread per (row, unit).
 __global__ __launch_bounds__(256) void k_gemv_img_prepare(const uint8_t* __restrict__ W, uint8_t* __restrict__ img,
-                                                           long units, int T, int P, long row_bytes) {
+                                                           long units, int T, int P, long row_bytes, int q8) {
   const long i = (long)blockIdx.x * 256 + threadIdx.x;
   if (i >= units) return;
   const int U = T * P;
   const long row = i / U;
   const int u = (int)(i - row * U), p = u / T, j = u - p * T;
+  if (q8) {
+    // Q8_0: the unit's 68 bytes (two blocks), dword aligned; block 0: d =
+    // bytes 0..1, quants 2..33; block 1: d = bytes 34..35, quants 36..67
+    const uint8_t* src = W + row * row_bytes + 68L * u;
+    uint8_t* dst = img + row * row_bytes;
+    uint32_t v[17];
+#pragma unroll
+    for (int k = 0; k < 17; ++k) v[k] = ld32(src + 4 * k);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const u32x4 qe = {funnel(v[4 * h + 1], v[4 * h], 2), funnel(v[4 * h + 2], v[4 * h + 1], 2),
+                        funnel(v[4 * h + 3], v[4 * h + 2], 2), funnel(v[4 * h + 4], v[4 * h + 3], 2)};
+      const u32x4 qo = {v[9 + 4 * h], v[10 + 4 * h], v[11 + 4 * h], v[12 + 4 * h]};
+      *(u32x4*)(dst + 16L * (((2 * p) * 2 + h) * T + j)) = qe;
+      *(u32x4*)(dst + 16L * (((2 * p + 1) * 2 + h) * T + j)) = qo;
+    }
+    *(uint32_t*)(dst + 64L * U + 4L * (j * P + p)) = (v[0] & 0xFFFFu) | (v[8] & 0xFFFF0000u);
+    return;
+  }
   const uint8_t* src = W + row * row_bytes + 36L * u;
   uint8_t* dst = img + row * row_bytes;
   uint32_t v[9];
@@ -186,13 +222,14 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_img(const float* __restri
 
 long gemv_image_act_bytes(int cols, int tokens) { return 72L * (cols / 64) * tokens; }
 
-hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s) {
+hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s,
+                                     bool q8) {
   int T, P;
   if (!img_geom(cols, T, P)) return hipErrorInvalidValue;
   const long units = (long)rows * (T * P);
   if (units <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_gemv_img_prepare, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s,
-                     (const uint8_t*)w, (uint8_t*)img, units, T, P, row_bytes);
+                     (const uint8_t*)w, (uint8_t*)img, units, T, P, row_bytes, q8 ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -258,6 +295,7 @@ hipError_t launch_gemv_image(const GemvArgs& g, int nr, hipStream_t s) {
   if (nr <= 0) nr = g.rows >= 65536 ? 2 : 1;
   if (nr > 2) return hipErrorInvalidValue;
   if (g.ttype == TT_IQ4_NL) return launch_img_tt<TT_IQ4_NL>(g, T, P, nr, s);
+  if (g.ttype == TT_Q8_0) return launch_img_tt<TT_Q8_0>(g, T, P, nr, s);
   return launch_img_tt<TT_Q4_0>(g, T, P, nr, s);
 }
 

@@ -87,7 +87,8 @@ long mmq_image_work_bytes(const GemvArgs& g);
 bool gemv_image_format(int ttype);
 bool gemv_image_width(int cols);  // a team width and pass count exist for this row width
 long gemv_image_act_bytes(int cols, int tokens);
-hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s);
+hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s,
+                                     bool q8);
 hipError_t launch_quantize_act_image(const float* x, void* out, int cols, int tokens, long x_stride, hipStream_t s);
 // g.w = the image, g.xq = one token's split activation; nr rows per team (1,
 // 2; 0 = pick)

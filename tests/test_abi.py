@@ -115,7 +115,9 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert lib.qhip_gemv_image_bytes(20, 16, 96) == -1
     assert lib.qhip_gemv_image_bytes(20, 16, 2560) == 16 * 1440
     assert lib.qhip_gemv_image_act_bytes(20, 2560, 2) == 2 * 72 * 40
-    assert lib.qhip_gemv_image_act_bytes(8, 2560, 1) == -1
+    assert lib.qhip_gemv_image_act_bytes(8, 2560, 1) == 72 * 40  # Q8_0: the same split activation
+    assert lib.qhip_gemv_image_bytes(8, 16, 2560) == 16 * 2720    # Q8_0: 68 bytes per 64 values
+    assert lib.qhip_gemv_image_act_bytes(14, 2560, 1) == -1
     assert lib.qhip_launch_gemv_prepare(12, p, 16, 2560, p, None) == INVALID
     assert lib.qhip_launch_gemv_prepare(20, p, 16, 2560, ctypes.c_void_p(0x1008), None) == INVALID
     assert lib.qhip_launch_gemv_prepare(20, p, 16, 2560, p, None) == INVALID  # in place

@@ -1,4 +1,4 @@
-"""GPU: the GEMV weight image of the 32-value 4-bit formats (IQ4_NL, Q4_0) --
+"""GPU: the GEMV weight image of the 32-value formats (IQ4_NL, Q4_0, Q8_0) --
 the image and split-activation layouts, the image GEMV against the oracle
 (every launch shape, odd row counts, exact integers at unit scales) and
 through the Exec mirror (image built and found, matvecPair over adjacent
@@ -12,7 +12,8 @@ from qwen35_amd import ops, synth
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-5
-FORMATS = [po.TT_IQ4_NL, po.TT_Q4_0]
+FORMATS = [po.TT_IQ4_NL, po.TT_Q4_0, po.TT_Q8_0]
+BLOCK = {po.TT_IQ4_NL: 18, po.TT_Q4_0: 18, po.TT_Q8_0: 34}
 
 
 def rel_l2(got, want):
@@ -30,16 +31,21 @@ def geometry(cols):
     return None
 
 
-def image_of(w, rows, cols):
-    """The documented image layout, restated on the host from the GGUF bytes."""
+def image_of(w, rows, cols, tt):
+    """The documented image layout, restated on the host from the GGUF bytes:
+    the 16-byte quant slots in the team's walking order (Q8_0: two per block,
+    the split activation's order), then the f16 scale pairs."""
     T, P = geometry(cols)
     U = T * P
-    blk = w.reshape(rows, U, 2, 18)
+    bb = BLOCK[tt]
+    qs = (bb - 2) // 16
+    blk = w.reshape(rows, U, 2, bb)
     u = np.arange(U)
     p, j = u // T, u % T
-    q = np.zeros((rows, 2 * U, 16), np.uint8)
-    q[:, 2 * p * T + j] = blk[:, :, 0, 2:]
-    q[:, (2 * p + 1) * T + j] = blk[:, :, 1, 2:]
+    q = np.zeros((rows, 2 * qs * U, 16), np.uint8)
+    for e in range(2):
+        for h in range(qs):
+            q[:, ((2 * p + e) * qs + h) * T + j] = blk[:, :, e, 2 + 16 * h:18 + 16 * h]
     sc = np.zeros((rows, U, 4), np.uint8)
     sc[:, j * P + p, 0:2] = blk[:, :, 0, 0:2]
     sc[:, j * P + p, 2:4] = blk[:, :, 1, 0:2]
@@ -51,7 +57,7 @@ def image_of(w, rows, cols):
 def test_image_layout(gpu, tt, rows, cols):
     w = synth.make_weight(tt, rows, cols, seed=3, tag=tt)
     img = ops.gemv_image(tt, torch.from_numpy(w).to(gpu), rows, cols).cpu().numpy()
-    assert np.array_equal(img[:rows * w.shape[1]].reshape(rows, -1), image_of(w, rows, cols))
+    assert np.array_equal(img[:rows * w.shape[1]].reshape(rows, -1), image_of(w, rows, cols, tt))
 
 
 @pytest.mark.parametrize("cols,tokens", [(1024, 1), (2560, 3), (5120, 2), (8192, 1)])
@@ -100,7 +106,7 @@ def test_image_gemv_integers_exact(gpu, oracle, tt):
     """Unit weight scales and integer activations of Q8_0 scale 1: every
     output is the exact sum of the row's block integers."""
     rows, cols = 96, 2560
-    w = synth.make_weight(tt, rows, cols, seed=6, tag=tt).reshape(rows, -1, 18).copy()
+    w = synth.make_weight(tt, rows, cols, seed=6, tag=tt).reshape(rows, -1, BLOCK[tt]).copy()
     w[:, :, 0:2] = np.array([1.0], np.float16).view(np.uint8)
     w = w.reshape(rows, -1)
     rng = np.random.default_rng(6)
