@@ -496,15 +496,24 @@ int qhip_launch_mul_mat_wd_image(const void* d_image, const void* d_xq, float* d
   return (int)launch_mmq_wd_image(g, d_work, d_work ? work_bytes : 0, S(stream));
 }
 
+// whether a GEMV image exists for this format and width: the 32-value
+// formats at the widths their team geometry covers, Q4_K / Q6_K at whole
+// super-blocks
+static bool gemv_image_ok(int ttype, int cols) {
+  if (gemv_kimage_format(ttype)) return cols > 0 && cols % 256 == 0;
+  return gemv_image_format(ttype) && gemv_image_width(cols);
+}
+
 long qhip_gemv_image_bytes(int ttype, int rows, int cols) {
   const long rb = weight_row_bytes(ttype, cols);
-  if (rb < 0 || rows < 0 || !gemv_image_format(ttype) || !gemv_image_width(cols)) return -1;
+  if (rb < 0 || rows < 0 || !gemv_image_ok(ttype, cols)) return -1;
   return (long)rows * rb;
 }
 
 long qhip_gemv_image_act_bytes(int ttype, int cols, int tokens) {
-  if (weight_row_bytes(ttype, cols) < 0 || !gemv_image_format(ttype) || !gemv_image_width(cols) || tokens < 0)
-    return -1;
+  if (weight_row_bytes(ttype, cols) < 0 || !gemv_image_ok(ttype, cols) || tokens < 0) return -1;
+  // Q4_K / Q6_K images read the reference Q8_K rows
+  if (gemv_kimage_format(ttype)) return act_row_bytes(ttype, cols) * tokens;
   return gemv_image_act_bytes(cols, tokens);
 }
 
@@ -514,6 +523,7 @@ int qhip_launch_gemv_prepare(int ttype, const void* d_w, int rows, int cols, voi
   if (rows == 0) return 0;
   if (!d_w || !d_image || !aligned4(d_w) || ((uintptr_t)d_image & 15u) || d_image == d_w)
     return (int)hipErrorInvalidValue;
+  if (gemv_kimage_format(ttype)) return (int)launch_kimage_prepare(ttype, d_w, rb, rows, cols, d_image, S(stream));
   return (int)launch_gemv_image_prepare(d_w, rb, rows, cols, d_image, S(stream), ttype == TT_Q8_0);
 }
 
@@ -521,6 +531,7 @@ int qhip_launch_quantize_act_image(int ttype, const float* d_x, void* d_xa, int 
   if (qhip_gemv_image_act_bytes(ttype, cols, tokens) < 0 || tokens > 65535) return (int)hipErrorInvalidValue;
   if (tokens == 0) return 0;
   if (!d_x || !d_xa || !aligned4(d_x) || ((uintptr_t)d_xa & 15u)) return (int)hipErrorInvalidValue;
+  if (gemv_kimage_format(ttype)) return qhip_launch_quantize_act(ttype, d_x, d_xa, cols, tokens, stream);
   return (int)launch_quantize_act_image(d_x, d_xa, cols, tokens, cols, S(stream));
 }
 
@@ -532,6 +543,11 @@ int qhip_launch_mul_mat_vec_image(const void* d_image, const void* d_xa, float* 
   if (rows == 0) return 0;
   if (!d_image || !d_xa || !d_out || ((uintptr_t)d_image & 15u) || ((uintptr_t)d_xa & 15u))
     return (int)hipErrorInvalidValue;
+  if (gemv_kimage_format(ttype)) {
+    GemvArgs g{ttype, d_image, d_xa, d_out, rows, cols, 1, rb, act_row_bytes(ttype, cols)};
+    g.kimg = true;
+    return (int)launch_gemv(g, 0, 0, rows_per_lane, S(stream));
+  }
   const GemvArgs g{ttype, d_image, d_xa, d_out, rows, cols, 1, rb, gemv_image_act_bytes(cols, 1)};
   return (int)launch_gemv_image(g, rows_per_lane, S(stream));
 }

@@ -351,6 +351,17 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
       }
     }
   }
+  // Q6_K at one token, quantized separately: the weight's K-quant GEMV image
+  // (the same GEMV launch as the GGUF rows, reading the image)
+  uint8_t* kimg = nullptr;
+  if (k == 1 && be->gemv_images_on) {
+    const GemvArgs gk{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
+    if (gemv_kimage_preferred(gk)) {
+      hipError_t ei;
+      kimg = gimage_for(be, wdev, ttype, rows, cols, row_bytes, &ei);
+      if (ei != hipSuccess) return report("GEMV image", ei);
+    }
+  }
   const bool hit = be->memo_on && be->memo_src == x && be->memo_cols == cols && be->memo_k == k &&
                    be->memo_fam == fam && be->act;
   if (be->memo_on) (hit ? be->memo_hits : be->memo_misses)++;
@@ -406,6 +417,12 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
     }
   }
   GemvArgs g{ttype, wdev, be->act, out, rows, cols, k, row_bytes, qhip_act_row_bytes(ttype, cols)};
+  if (kimg) {
+    GemvArgs gi = g;
+    gi.w = kimg;
+    gi.kimg = true;
+    return report("matvec", launch_gemv(gi, 0, 0, 0, be->stream));
+  }
   // the MMQ's split-K workspace for small grids, grown outside a capture
   // only (under capture a launch that does not fit runs unsplit)
   const long need = mul_mat_work_bytes(g);
@@ -517,7 +534,7 @@ int qhip_backend_prepare_linear(qhip_backend* be, const qhip_linear* w) {
   // a long prefill: whether any token count would use an image for this weight
   const GemvArgs g1{w->ttype, w->dev, w->dev, nullptr, w->rows, w->cols, 1, w->row_bytes,
                     qhip_act_row_bytes(w->ttype, w->cols)};
-  if (be->gemv_images_on && gemv_image_preferred(g1)) {
+  if (be->gemv_images_on && (gemv_image_preferred(g1) || gemv_kimage_preferred(g1))) {
     // a decode matvec: the GEMV image
     if (capturing(be->stream)) return (int)hipErrorStreamCaptureUnsupported;
     hipError_t e;

@@ -23,7 +23,7 @@
 
 namespace qhip {
 
-template <int TT, int NT, int NR>
+template <int TT, int NT, int NR, bool IMG = false>
 __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
                                                const uint8_t* __restrict__ XQ,
                                                float* __restrict__ Y, int rows, long row_bytes,
@@ -52,7 +52,7 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
     for (int u = j; u < u_end; u += team) {
       typename U::W w[NR];
 #pragma unroll
-      for (int k = 0; k < NR; ++k) w[k] = U::load_w(wrow[k], u);
+      for (int k = 0; k < NR; ++k) w[k] = load_unit<TT, IMG>(wrow[k], u, upr);
       if constexpr (NT == 1) {
         const typename U::A a = U::load_a(XQ + (long)t0 * act_bytes, u);
 #pragma unroll
@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
 // units lane + 64s, stepping 64*WV; each wave folds its lanes with the
 // shuffle tree, then the team's waves are added in wave order through LDS
 // (deterministic).
-template <int TT, int NR, int WV>
+template <int TT, int NR, int WV, bool IMG = false>
 __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
                                                   const uint8_t* __restrict__ XQ,
                                                   float* __restrict__ Y, int rows, long row_bytes,
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
   for (int u = lane + 64 * sl; u < u_end; u += 64 * WV) {
     typename U::W w[NR];
 #pragma unroll
-    for (int k = 0; k < NR; ++k) w[k] = U::load_w(wrow[k], u);
+    for (int k = 0; k < NR; ++k) w[k] = load_unit<TT, IMG>(wrow[k], u, upr);
     const typename U::A a = U::load_a(XQ, u);
 #pragma unroll
     for (int k = 0; k < NR; ++k) acc[k] += U::dot(w[k], a);
@@ -609,7 +609,15 @@ int gemv_pick_team(int rows, int cols, int target_waves) {
 // 2-token and a 1-token pass (Q4_K [17408, 5120]).
 int gemv_pick_nt(int tokens) { return tokens > 4 ? 8 : tokens > 2 ? 4 : tokens > 1 ? 2 : 1; }
 
-template <int TT, int NT, int NR>
+// the two formats with a K-quant GEMV image (g.kimg)
+template <class F>
+static hipError_t dispatch_kimg(int ttype, F&& f) {
+  if (ttype == TT_Q4_K) return f(std::integral_constant<int, TT_Q4_K>{});
+  if (ttype == TT_Q6_K) return f(std::integral_constant<int, TT_Q6_K>{});
+  return hipErrorInvalidValue;
+}
+
+template <int TT, int NT, int NR, bool IMG = false>
 static hipError_t launch_gemv_t(const GemvArgs& g, int team, hipStream_t s) {
   const int upr = g.cols / 64;
   if (team > upr) team = upr;
@@ -618,7 +626,7 @@ static hipError_t launch_gemv_t(const GemvArgs& g, int team, hipStream_t s) {
   const long teams = (g.rows + NR - 1) / NR;
   const long waves = (teams + tpw - 1) / tpw;
   const unsigned grid = (unsigned)((waves + 3) / 4);
-  hipLaunchKernelGGL((k_gemv<TT, NT, NR>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
+  hipLaunchKernelGGL((k_gemv<TT, NT, NR, IMG>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.row_bytes, g.act_bytes, upr, team,
                      g.tokens);
   return hipGetLastError();
@@ -668,10 +676,12 @@ static hipError_t launch_gemv_type(const GemvArgs& g, int team, int nt, int nr, 
 static void default_shape(const GemvArgs& g, int& team, int& nr) {
   const int upr = g.cols / 64;
   const bool nib32 = g.ttype == TT_Q4_0 || g.ttype == TT_Q4_1 || g.ttype == TT_IQ4_NL;
-  // long rows: teams of whole waves (k_gemv_mw), several rows per team
+  // long rows: teams of whole waves (k_gemv_mw), several rows per team (the
+  // Q6_K image two: [5120, 17408] 28.2 us with four against 18.1 from the
+  // GGUF rows)
   if (g.ttype == TT_Q6_K && upr >= 128) {
     team = 256;
-    nr = g.rows >= 4096 ? 4 : 2;
+    nr = g.rows >= 4096 && !g.kimg ? 4 : 2;
     return;
   }
   if (nib32 && upr >= 128) {
@@ -718,6 +728,7 @@ static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipSt
 
 hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
+  if (g.kimg && (g.tokens != 1 || !kimage_format(g.ttype) || g.cols % 256)) return hipErrorInvalidValue;
   if (team <= 0 && nr <= 0 && g.tokens == 1) {
     default_shape(g, team, nr);
   } else if (team <= 0 && nr <= 0 && nt <= 0) {
@@ -737,32 +748,43 @@ hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t 
   }
   if (team > 64) return launch_gemv_multiwave(g, nr, team / 64, s);
   if (nt <= 0) nt = gemv_pick_nt(g.tokens);
+  if (g.kimg) {
+    return dispatch_kimg(g.ttype, [&](auto tt) -> hipError_t {
+      constexpr int T = decltype(tt)::value;
+      switch (nr) {
+        case 1: return launch_gemv_t<T, 1, 1, true>(g, team, s);
+        case 2: return launch_gemv_t<T, 1, 2, true>(g, team, s);
+        case 4: return launch_gemv_t<T, 1, 4, true>(g, team, s);
+        default: return hipErrorInvalidValue;
+      }
+    });
+  }
   return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_type<decltype(tt)::value>(g, team, nt, nr, s); });
 }
 
-template <int TT, int NR, int WV>
+template <int TT, int NR, int WV, bool IMG = false>
 static hipError_t launch_gemv_mw_t(const GemvArgs& g, hipStream_t s) {
   constexpr int TPB = 4 / WV;
   const long teams = (g.rows + NR - 1) / NR;
   const unsigned grid = (unsigned)((teams + TPB - 1) / TPB);
-  hipLaunchKernelGGL((k_gemv_mw<TT, NR, WV>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
+  hipLaunchKernelGGL((k_gemv_mw<TT, NR, WV, IMG>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.row_bytes, g.cols / 64);
   return hipGetLastError();
 }
 
-template <int TT>
+template <int TT, bool IMG = false>
 static hipError_t launch_gemv_mw_type(const GemvArgs& g, int nr, int wv, hipStream_t s) {
   if (wv == 2) {
     switch (nr) {
-      case 1: return launch_gemv_mw_t<TT, 1, 2>(g, s);
-      case 2: return launch_gemv_mw_t<TT, 2, 2>(g, s);
-      case 4: return launch_gemv_mw_t<TT, 4, 2>(g, s);
+      case 1: return launch_gemv_mw_t<TT, 1, 2, IMG>(g, s);
+      case 2: return launch_gemv_mw_t<TT, 2, 2, IMG>(g, s);
+      case 4: return launch_gemv_mw_t<TT, 4, 2, IMG>(g, s);
     }
   } else if (wv == 4) {
     switch (nr) {
-      case 1: return launch_gemv_mw_t<TT, 1, 4>(g, s);
-      case 2: return launch_gemv_mw_t<TT, 2, 4>(g, s);
-      case 4: return launch_gemv_mw_t<TT, 4, 4>(g, s);
+      case 1: return launch_gemv_mw_t<TT, 1, 4, IMG>(g, s);
+      case 2: return launch_gemv_mw_t<TT, 2, 4, IMG>(g, s);
+      case 4: return launch_gemv_mw_t<TT, 4, 4, IMG>(g, s);
     }
   }
   return hipErrorInvalidValue;
@@ -771,6 +793,8 @@ static hipError_t launch_gemv_mw_type(const GemvArgs& g, int nr, int wv, hipStre
 // one token, teams of wv = 2 or 4 waves
 static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipStream_t s) {
   if (g.tokens != 1) return hipErrorInvalidValue;
+  if (g.kimg)
+    return dispatch_kimg(g.ttype, [&](auto tt) { return launch_gemv_mw_type<decltype(tt)::value, true>(g, nr, wv, s); });
   return dispatch_type(g.ttype, [&](auto tt) { return launch_gemv_mw_type<decltype(tt)::value>(g, nr, wv, s); });
 }
 
@@ -863,7 +887,7 @@ bool gemv_fused_preferred(const GemvArgs& g) {
 hipError_t launch_gemv_fused(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int wgs,
                              hipStream_t s) {
   if (g.rows <= 0) return hipSuccess;
-  if (g.tokens != 1 || !gemv_fused_fits(g.ttype, g.cols)) return hipErrorInvalidValue;
+  if (g.tokens != 1 || g.kimg || !gemv_fused_fits(g.ttype, g.cols)) return hipErrorInvalidValue;
   if (team <= 0 && nr <= 0 && wgs <= 0) {
     fused_default_shape(g, team, nr, wgs);
   } else {
@@ -935,10 +959,26 @@ bool gemv_splitk_preferred(const GemvArgs& g) {
          fused_lds_bytes(g.ttype, g.cols >= 16384 ? 2048 : 1024) <= kFusedMaxLds;
 }
 
+// The K-quant GEMV image against the GGUF rows, measured on MI355X (weights
+// rotated past the Infinity Cache, the same launch shape on both, results
+// bit-identical).  Pre-quantized GEMV: Q6_K [2560, 9728] 6.87 vs 7.62 us,
+// [19456, 2560] 12.14 vs 12.87, [17408, 5120] 20.71 vs 21.97; Q4_K [17408,
+// 5120] 11.52 vs 11.50, [19456, 2560] 8.90 vs 8.15, [12288, 4096] 8.00 vs
+// 8.13.  Read by the one-launch quantize + GEMV and its split-K form, the
+// image lost (Q4_K [19456, 2560] 9.53 vs 9.38 us, Q6_K [2560, 9728] split
+// 10.79 vs 10.20, Q4_K [5120, 17408] split 15.05 vs 14.01), so those keep
+// the GGUF rows.  The Exec mirror's batch-1 matvec therefore reads the image
+// for Q6_K where it quantizes separately (rows past the one-launch form's
+// range, widths 4096 < cols < 8192): Q6_K [17408, 5120] 23.3 vs 26.2 us.
+bool gemv_kimage_preferred(const GemvArgs& g) {
+  return g.tokens == 1 && g.ttype == TT_Q6_K && g.cols % 256 == 0 && !gemv_fused_preferred(g) &&
+         !gemv_splitk_preferred(g);
+}
+
 hipError_t launch_gemv_splitk(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int slice,
                               void* work, long work_bytes, hipStream_t s) {
   if (g.rows <= 0) return hipSuccess;
-  if (g.tokens != 1 || work == nullptr || work_bytes < gemv_splitk_work_bytes(g.rows, g.cols))
+  if (g.tokens != 1 || g.kimg || work == nullptr || work_bytes < gemv_splitk_work_bytes(g.rows, g.cols))
     return hipErrorInvalidValue;
   int dt = 0, dn = 0, ds = 0;
   splitk_default_shape(g, dt, dn, ds);

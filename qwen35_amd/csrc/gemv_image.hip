@@ -284,6 +284,70 @@ bool gemv_image_preferred(const GemvArgs& g) {
          (long)g.rows * g.cols > (1L << 23);
 }
 
+// ---- K-quant GEMV image (Q4_K, Q6_K) --------------------------------------------
+// The layout is KImg's (qhip_device.hpp): the GGUF row's bytes with each
+// unit's 16-byte pieces grouped by piece over chunks of 64 units, so that the
+// lanes of a wave, taking consecutive units, load one contiguous span per
+// instruction; the headers (Q4_K) or scales and d (Q6_K) after the pieces.
+// The GEMV, fused and split-K launchers of gemv.hip read it when g.kimg, with
+// the activation in the reference Q8_K layout.
+bool gemv_kimage_format(int ttype) { return kimage_format(ttype); }
+
+// GGUF rows -> K-quant image rows; one thread per (row, unit).  The GGUF
+// bytes are read 4-byte (Q4_K) or 2-byte (Q6_K: 210-byte super-blocks)
+// aligned; Q4_K image rows are 16-byte aligned (144 bytes per super-block),
+// Q6_K ones 2-byte aligned and written in 2-byte pieces.
+template <int TT>
+__global__ __launch_bounds__(256) void k_kimg_prepare(const uint8_t* __restrict__ W, uint8_t* __restrict__ img,
+                                                       long units, int U, long row_bytes) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= units) return;
+  const long row = i / U;
+  const int u = (int)(i - row * U), c = u >> 6, ii = u & 63, m = min(64, U - (c << 6));
+  const uint8_t* src = W + row * row_bytes;
+  uint8_t* dst = img + row * row_bytes;
+  if constexpr (TT == TT_Q4_K) {
+    const uint8_t* blk = src + 144L * (u >> 2);
+    const int q = u & 3;
+    const u32x4 a = {ld32(blk + 16 + 32 * q), ld32(blk + 20 + 32 * q), ld32(blk + 24 + 32 * q), ld32(blk + 28 + 32 * q)};
+    const u32x4 b = {ld32(blk + 32 + 32 * q), ld32(blk + 36 + 32 * q), ld32(blk + 40 + 32 * q), ld32(blk + 44 + 32 * q)};
+    *(u32x4*)(dst + 16L * (128 * c + ii)) = a;
+    *(u32x4*)(dst + 16L * (128 * c + m + ii)) = b;
+    if (q == 0) *(u32x4*)(dst + 32L * U + 16 * (u >> 2)) = u32x4{ld32(blk), ld32(blk + 4), ld32(blk + 8), ld32(blk + 12)};
+  } else {
+    const uint8_t* blk = src + 210L * (u >> 2);
+    const int h = (u >> 1) & 1, lh = u & 1;
+    auto cp16 = [](const uint8_t* from, uint8_t* to) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) ((uint16_t*)to)[k] = ((const uint16_t*)from)[k];
+    };
+    cp16(blk + 64 * h + 16 * lh, dst + 16L * (192 * c + ii));
+    cp16(blk + 64 * h + 32 + 16 * lh, dst + 16L * (192 * c + m + ii));
+    cp16(blk + 128 + 32 * h + 16 * lh, dst + 16L * (192 * c + 2 * m + ii));
+    const uint8_t* sc = blk + 192 + 8 * h + lh;  // sc[8h + lh + 2q] for q = 0..3
+    uint16_t* so = (uint16_t*)(dst + 48L * U + 4 * u);
+    so[0] = (uint16_t)(sc[0] | (sc[2] << 8));
+    so[1] = (uint16_t)(sc[4] | (sc[6] << 8));
+    if ((u & 3) == 0) *(uint16_t*)(dst + 52L * U + 2 * (u >> 2)) = *(const uint16_t*)(blk + 208);
+  }
+}
+
+hipError_t launch_kimage_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
+                                 hipStream_t s) {
+  if (!kimage_format(ttype) || cols <= 0 || cols % 256) return hipErrorInvalidValue;
+  const int U = cols / 64;
+  const long units = (long)rows * U;
+  if (units <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((units + 255) / 256));
+  if (ttype == TT_Q4_K)
+    hipLaunchKernelGGL(k_kimg_prepare<TT_Q4_K>, grid, dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img, units, U,
+                       row_bytes);
+  else
+    hipLaunchKernelGGL(k_kimg_prepare<TT_Q6_K>, grid, dim3(256), 0, s, (const uint8_t*)w, (uint8_t*)img, units, U,
+                       row_bytes);
+  return hipGetLastError();
+}
+
 // g.w = the image, g.xq = the split activation of one token.  nr: rows per
 // team, 1 or 2 (0 = two rows from 65536 rows: IQ4_NL [248320, 2560] 62.7 vs
 // 65.9 us one row; [32768, 2560] 11.4 vs 11.6 us two rows, [17408, 5120]

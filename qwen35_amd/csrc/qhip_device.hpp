@@ -695,6 +695,70 @@ struct Unit<TT_Q6_K> {
   }
 };
 
+// ---- K-quant GEMV image (batch 1) ----
+// Q4_K and Q6_K rows of a GEMV image hold the GGUF row's bytes, reordered so
+// that lanes taking consecutive units load contiguous, aligned 16-byte
+// pieces.  Units are grouped in chunks of 64 (the last chunk has m = U - 64c
+// of the row's U units); piece e of unit 64c + i sits at 16 (NP 64c + m e + i),
+// NP pieces per unit.  Q4_K (NP = 2: quant bytes 32q..32q+15 and
+// 32q+16..32q+31 of quarter q = u & 3), then the 16-byte super-block headers
+// (d, dmin, the 12 scale bytes) at 32 U + 16 sb.  Q6_K (NP = 3: the unit's
+// 16 bytes of ql at 64h + 16lh, of ql at 64h + 32 + 16lh and of qh at
+// 32h + 16lh), then each unit's four scales sc[8h + lh + 2q] at 48 U + 4u,
+// then the super-blocks' f16 d at 52 U + 2 sb.  A row keeps its GGUF byte
+// count, so row r of the image starts at r * row_bytes.
+template <int TT>
+struct KImg;
+
+template <>
+struct KImg<TT_Q4_K> {
+  static constexpr int kPieces = 2;
+  static __device__ __forceinline__ Unit<TT_Q4_K>::W load(const uint8_t* row, int u, int U) {
+    const int c = u >> 6, i = u & 63, m = min(64, U - (c << 6));
+    const uint8_t* p = row + 16L * (128 * c + i);
+    Unit<TT_Q4_K>::W w;
+    w.c = u & 3;
+    const u32x4 a = ld128(p), b = ld128(p + 16 * m);
+    const u32x4 h = ld128(row + 32L * U + 16 * (u >> 2));
+    w.hdr[0] = h.x; w.hdr[1] = h.y; w.hdr[2] = h.z; w.hdr[3] = h.w;
+    w.q[0] = a.x; w.q[1] = a.y; w.q[2] = a.z; w.q[3] = a.w;
+    w.q[4] = b.x; w.q[5] = b.y; w.q[6] = b.z; w.q[7] = b.w;
+    return w;
+  }
+};
+
+template <>
+struct KImg<TT_Q6_K> {
+  static constexpr int kPieces = 3;
+  static __device__ __forceinline__ Unit<TT_Q6_K>::W load(const uint8_t* row, int u, int U) {
+    const int c = u >> 6, i = u & 63, m = min(64, U - (c << 6));
+    const uint8_t* p = row + 16L * (192 * c + i);
+    Unit<TT_Q6_K>::W w;
+    // Q6_K rows are 210 bytes per super-block, so a row starts 2-byte aligned
+    // at worst: unaligned loads (one global_load_dwordx4 each, as in the GGUF
+    // path)
+    const u32x4_u a = *(const u32x4_u*)p, b = *(const u32x4_u*)(p + 16 * m), q = *(const u32x4_u*)(p + 32 * m);
+    const uint32_t sc = *(const u32_a2*)(row + 48L * U + 4 * u);
+    w.la[0] = a.x; w.la[1] = a.y; w.la[2] = a.z; w.la[3] = a.w;
+    w.lb[0] = b.x; w.lb[1] = b.y; w.lb[2] = b.z; w.lb[3] = b.w;
+    w.qh[0] = q.x; w.qh[1] = q.y; w.qh[2] = q.z; w.qh[3] = q.w;
+    // the dot reads bytes 0 and 2 of sc01 and sc23
+    w.sc01 = (sc & 0xFFu) | ((sc & 0xFF00u) << 8);
+    w.sc23 = ((sc >> 16) & 0xFFu) | ((sc >> 8) & 0xFF0000u);
+    w.d = *(const uint16_t*)(row + 52L * U + 2 * (u >> 2));
+    return w;
+  }
+};
+
+// a unit's weights from the GGUF row or, IMG, from the K-quant image row
+template <int TT, bool IMG>
+__device__ __forceinline__ typename Unit<TT>::W load_unit(const uint8_t* row, int u, int U) {
+  if constexpr (IMG) return KImg<TT>::load(row, u, U);
+  else return Unit<TT>::load_w(row, u);
+}
+
+constexpr bool kimage_format(int tt) { return tt == TT_Q4_K || tt == TT_Q6_K; }
+
 
 // ---- the further K-quant family (Q8_K activations, 64-value quarter units) ----
 // Every unit below covers values 64c..64c+63 of super-block u>>2 (c = u&3) in

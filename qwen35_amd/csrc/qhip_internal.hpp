@@ -14,6 +14,7 @@ struct GemvArgs {
   int rows, cols, tokens;
   long row_bytes;    // bytes of one weight row
   long act_bytes;    // bytes of one quantized activation row
+  bool kimg = false;  // w is a Q4_K / Q6_K GEMV image (one token)
 };
 
 hipError_t launch_quantize_q8_0(const float* x, void* out, long nblocks, int tokens, long x_stride,
@@ -95,5 +96,13 @@ hipError_t launch_quantize_act_image(const float* x, void* out, int cols, int to
 hipError_t launch_gemv_image(const GemvArgs& g, int nr, hipStream_t s);
 // whether quantize + image GEMV beats the GGUF-layout launches (measured rule)
 bool gemv_image_preferred(const GemvArgs& g);
+// K-quant GEMV image (Q4_K, Q6_K; KImg in qhip_device.hpp): the same bytes
+// per row, read by launch_gemv / launch_gemv_fused / launch_gemv_splitk when
+// g.kimg, with the reference Q8_K activation
+bool gemv_kimage_format(int ttype);
+hipError_t launch_kimage_prepare(int ttype, const void* w, long row_bytes, int rows, int cols, void* img,
+                                 hipStream_t s);
+// whether the Exec mirror's batch-1 matvec reads a K-quant weight's image
+bool gemv_kimage_preferred(const GemvArgs& g);
 
 }  // namespace qhip

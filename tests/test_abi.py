@@ -111,14 +111,17 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert lib.qhip_launch_quantize_mul_mat_vec_split(p, p, None, p, 16, 9728, 14, 300, 0, 0, p, need,
                                                       None) == INVALID
     # GEMV image: formats without one, widths not a multiple of 64, alignment
-    assert lib.qhip_gemv_image_bytes(12, 16, 2560) == -1
+    assert lib.qhip_gemv_image_bytes(13, 16, 2560) == -1
+    assert lib.qhip_gemv_image_bytes(12, 16, 2560) == 16 * 1440   # Q4_K: the GGUF bytes reordered
+    assert lib.qhip_gemv_image_bytes(14, 3, 2304) == 3 * 1890     # Q6_K
     assert lib.qhip_gemv_image_bytes(20, 16, 96) == -1
     assert lib.qhip_gemv_image_bytes(20, 16, 2560) == 16 * 1440
     assert lib.qhip_gemv_image_act_bytes(20, 2560, 2) == 2 * 72 * 40
     assert lib.qhip_gemv_image_act_bytes(8, 2560, 1) == 72 * 40  # Q8_0: the same split activation
     assert lib.qhip_gemv_image_bytes(8, 16, 2560) == 16 * 2720    # Q8_0: 68 bytes per 64 values
-    assert lib.qhip_gemv_image_act_bytes(14, 2560, 1) == -1
-    assert lib.qhip_launch_gemv_prepare(12, p, 16, 2560, p, None) == INVALID
+    assert lib.qhip_gemv_image_act_bytes(14, 2560, 2) == 2 * 292 * 10  # K-quants: the reference Q8_K rows
+    assert lib.qhip_gemv_image_act_bytes(13, 2560, 1) == -1
+    assert lib.qhip_launch_gemv_prepare(13, p, 16, 2560, ctypes.c_void_p(0x2000), None) == INVALID
     assert lib.qhip_launch_gemv_prepare(20, p, 16, 2560, ctypes.c_void_p(0x1008), None) == INVALID
     assert lib.qhip_launch_gemv_prepare(20, p, 16, 2560, p, None) == INVALID  # in place
     assert lib.qhip_launch_quantize_act_image(20, p, ctypes.c_void_p(0x1004), 2560, 1, None) == INVALID
@@ -127,7 +130,7 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert lib.qhip_gemv_image_bytes(20, 16, 9728) == -1    # long rows: the GGUF-layout kernels
     assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 2560, 20, 3, None) == INVALID
     assert lib.qhip_launch_mul_mat_vec_image(p, p, None, 16, 2560, 20, 0, None) == INVALID
-    assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 2560, 14, 0, None) == INVALID
+    assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 2560, 13, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_vec_image(p, p, p, 16, 9728, 20, 0, None) == INVALID
     # fragment images: Q6_K, Q4_K, Q8_0; whole 256-value super-blocks; Q6_K 1..32 tokens; alignment
     assert lib.qhip_wd_image_bytes(14, 33, 512) == 2 * 2 * 6720

@@ -210,6 +210,7 @@ def test_backend_image_budget_and_opt_out(gpu, oracle):
     want = oracle.matvec(tt, w, x, nthreads=THREADS)
     img_bytes = _lib.load().qhip_mmq_image_bytes(tt, rows, cols)  # the plane image, 2.5x the GGUF bytes
     frag_bytes = rows * cols // 256 * 210  # the few-token fragment image, built with it
+    gemv_bytes = rows * cols // 256 * 210  # and the decode matvec's GEMV image at this width
     xd = to_dev(x, gpu)
     for mode in ("capped", "off", "prepared"):
         be = ops.Backend(0)
@@ -222,7 +223,7 @@ def test_backend_image_budget_and_opt_out(gpu, oracle):
                 be.set_mmq_images(False)
             else:
                 assert be.prepare_linear(lin) == 0
-                assert be.mem_placed() == base + img_bytes + frag_bytes
+                assert be.mem_placed() == base + img_bytes + frag_bytes + gemv_bytes
             out = torch.empty((T, rows), device=gpu)
             for rep in range(2):
                 be.matvec_batch_k(out, lin, xd, T)
