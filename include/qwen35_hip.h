@@ -295,9 +295,18 @@ int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d
  * have one.  The activation of the image GEMV is quantized
  * into the matching split layout (the same Q8_0 values and scales as
  * qhip_launch_quantize_act; scales stored as f32): 72 bytes per 64 values.
+ * For Q4_K and Q6_K (any cols % 256 == 0): the same bytes per row, each
+ * 64-value unit's 16-byte pieces (Q4_K two quant pieces, Q6_K ql, ql, qh)
+ * grouped by piece over chunks of 64 units, so that lanes on consecutive
+ * units read one contiguous span per load; then the Q4_K super-block headers
+ * (16 bytes each), or the Q6_K units' four scales (4 bytes each) and the f16
+ * d of each super-block.  Its activation is the reference Q8_K row
+ * (qhip_launch_quantize_act_image = qhip_launch_quantize_act), and the image
+ * GEMV gives the same bits as qhip_launch_mul_mat_vec on the GGUF rows with
+ * the same rows per lane.
  *   qhip_gemv_image_bytes      image size (rows x GGUF row bytes); -1 for
  *                              other types or widths
- *   qhip_gemv_image_act_bytes  bytes of `tokens` split activation rows, or -1
+ *   qhip_gemv_image_act_bytes  bytes of `tokens` activation rows, or -1
  *   qhip_launch_gemv_prepare   build it from GGUF bytes (d_w 4-byte aligned,
  *                              d_image 16-byte aligned, not d_w)
  *   qhip_launch_quantize_act_image  f32 x[tokens][cols] -> split activation
@@ -382,7 +391,9 @@ int qhip_backend_wrap_linear(qhip_backend *be, int ttype, int rows, int cols, co
 void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
 /* Build what this weight's products use beyond its GGUF bytes now, at load
  * time, instead of inside the first matvec: the GEMV image of an IQ4_NL /
- * Q4_0 weight large enough for the decode matvec to read it
+ * Q4_0 / Q8_0 weight large enough for the decode matvec to read it, or of a
+ * Q6_K weight whose decode matvec quantizes separately (widths between 4096
+ * and 8192, or more than 32768 rows)
  * (qhip_launch_gemv_prepare, the GGUF bytes once more; built in load order,
  * so adjacent weights get adjacent images and matvecPair stays one launch),
  * the fragment image of a Q6_K or Q4_K weight with rows * cols >= 2^23
