@@ -524,7 +524,7 @@ int qhip_launch_gemv_prepare(int ttype, const void* d_w, int rows, int cols, voi
   if (!d_w || !d_image || !aligned4(d_w) || ((uintptr_t)d_image & 15u) || d_image == d_w)
     return (int)hipErrorInvalidValue;
   if (gemv_kimage_format(ttype)) return (int)launch_kimage_prepare(ttype, d_w, rb, rows, cols, d_image, S(stream));
-  return (int)launch_gemv_image_prepare(d_w, rb, rows, cols, d_image, S(stream), ttype == TT_Q8_0);
+  return (int)launch_gemv_image_prepare(d_w, rb, rows, cols, d_image, S(stream), ttype);
 }
 
 int qhip_launch_quantize_act_image(int ttype, const float* d_x, void* d_xa, int cols, int tokens, void* stream) {
@@ -532,7 +532,7 @@ int qhip_launch_quantize_act_image(int ttype, const float* d_x, void* d_xa, int 
   if (tokens == 0) return 0;
   if (!d_x || !d_xa || !aligned4(d_x) || ((uintptr_t)d_xa & 15u)) return (int)hipErrorInvalidValue;
   if (gemv_kimage_format(ttype)) return qhip_launch_quantize_act(ttype, d_x, d_xa, cols, tokens, stream);
-  return (int)launch_quantize_act_image(d_x, d_xa, cols, tokens, cols, S(stream));
+  return (int)launch_quantize_act_image(ttype, d_x, d_xa, cols, tokens, cols, S(stream));
 }
 
 int qhip_launch_mul_mat_vec_image(const void* d_image, const void* d_xa, float* d_out, int rows, int cols,

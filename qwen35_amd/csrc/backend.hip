@@ -223,8 +223,9 @@ static size_t act_bytes_for(int cols, int k) {
   return c / 256 * 292 * (size_t)k + 256;
 }
 
-// memo family of the split activation the GEMV image reads (the others are
-// the activation block sizes, 32 and 256)
+// memo family of the split activation the GEMV image reads: kFamSplit plus
+// its layout (gemv_image_layout; the other families are the activation
+// block sizes, 32 and 256)
 static constexpr int kFamSplit = 1 << 16;
 
 static hipError_t img_arena_alloc(qhip_backend* be, size_t bytes, uint8_t** out) {
@@ -330,8 +331,9 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
       uint8_t* img = gimage_for(be, wdev, ttype, rows, cols, row_bytes, &ei);
       if (ei != hipSuccess) return report("GEMV image", ei);
       if (img) {
+        const int sfam = kFamSplit + gemv_image_layout(ttype, cols);
         const bool hs = be->memo_on && be->memo_src == x && be->memo_cols == cols && be->memo_k == 1 &&
-                        be->memo_fam == kFamSplit && be->act;
+                        be->memo_fam == sfam && be->act;
         if (be->memo_on) (hs ? be->memo_hits : be->memo_misses)++;
         if (!hs) {
           const hipError_t ea = ensure_act(be, act_bytes_for(cols, 1));
@@ -343,7 +345,7 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
             be->memo_src = x;
             be->memo_cols = cols;
             be->memo_k = 1;
-            be->memo_fam = kFamSplit;
+            be->memo_fam = sfam;
           }
         }
         return report("matvec", (hipError_t)qhip_launch_mul_mat_vec_image(img, be->act, out, rows, cols, ttype, 0,

@@ -10,8 +10,9 @@
 // bytes per row, reordered for the kernel below: a team of T lanes walks a
 // row in P passes, lane j taking unit u = pT + j (64 values: blocks 2u and
 // 2u+1) in pass p, and every load of a pass is one aligned 16-byte piece per
-// lane with the team's lanes contiguous.  T and P depend only on the row
-// width (img_geom): U = cols / 64 = T P units per row.
+// lane with the team's lanes contiguous.  T and P depend on the row width
+// and, for Q8_0 at one width, the format (img_geom): U = cols / 64 = T P
+// units per row.
 //
 //   row, 36 U bytes (as the GGUF row):
 //     [16 ((2p + e) T + j)]        16 quant bytes of block 2u+e (byte i: value
@@ -50,9 +51,13 @@ __host__ __device__ constexpr int img_qs() { return TT == TT_Q8_0 ? 2 : 1; }
 // 20 (IQ4_NL [248320, 2560] 61.3 us, 8-lane 67.1, 10-lane 67.5; [17408,
 // 5120] 12.1 us, 10-lane 13.1), whole-wave teams at width 4096 (5.5 us,
 // 32-lane 5.8, 16-lane 6.1); 32- and 16-lane teams otherwise.
-static bool img_geom(int cols, int& T, int& P) {
+// Q8_0 (two 16-byte slots per block, twice the quant bytes per unit) takes
+// 40-lane teams of two passes at width 5120: [17408, 5120] 18.35 us against
+// 20.63 with the 20-lane geometry (IQ4_NL 14.85 against 12.19).
+static bool img_geom(int ttype, int cols, int& T, int& P) {
   if (cols <= 0 || cols % 64) return false;
   const int U = cols / 64;
+  if (ttype == TT_Q8_0 && U == 80) { T = 40; P = 2; return true; }
   if (U % 20 == 0 && U / 20 <= 4) { T = 20; P = U / 20; return true; }
   if (U % 64 == 0 && U / 64 <= 2) { T = 64; P = U / 64; return true; }
   if (U % 32 == 0 && U / 32 <= 4) { T = 32; P = U / 32; return true; }
@@ -62,7 +67,12 @@ static bool img_geom(int cols, int& T, int& P) {
 
 bool gemv_image_width(int cols) {
   int T, P;
-  return img_geom(cols, T, P);
+  return img_geom(TT_IQ4_NL, cols, T, P);
+}
+
+int gemv_image_layout(int ttype, int cols) {
+  int T, P;
+  return img_geom(ttype, cols, T, P) ? 16 * T + P : -1;
 }
 
 // One block's integer dot (kernels32.c:342-361, :447-464): the quant slots q
@@ -223,9 +233,10 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0_img(const float* __restri
 long gemv_image_act_bytes(int cols, int tokens) { return 72L * (cols / 64) * tokens; }
 
 hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s,
-                                     bool q8) {
+                                     int ttype) {
   int T, P;
-  if (!img_geom(cols, T, P)) return hipErrorInvalidValue;
+  if (!img_geom(ttype, cols, T, P)) return hipErrorInvalidValue;
+  const bool q8 = ttype == TT_Q8_0;
   const long units = (long)rows * (T * P);
   if (units <= 0) return hipSuccess;
   hipLaunchKernelGGL(k_gemv_img_prepare, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, s,
@@ -233,9 +244,10 @@ hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, in
   return hipGetLastError();
 }
 
-hipError_t launch_quantize_act_image(const float* x, void* out, int cols, int tokens, long x_stride, hipStream_t s) {
+hipError_t launch_quantize_act_image(int ttype, const float* x, void* out, int cols, int tokens, long x_stride,
+                                     hipStream_t s) {
   int T, P;
-  if (!img_geom(cols, T, P)) return hipErrorInvalidValue;
+  if (!img_geom(ttype, cols, T, P)) return hipErrorInvalidValue;
   const long nblocks = cols / 32;
   if (tokens <= 0) return hipSuccess;
   dim3 grid((unsigned)((nblocks * 32 + 255) / 256), (unsigned)tokens);
@@ -267,6 +279,9 @@ static hipError_t launch_img_tt(const GemvArgs& g, int T, int P, int nr, hipStre
   QHIP_IMG(64, 1) QHIP_IMG(64, 2)
   QHIP_IMG(32, 1) QHIP_IMG(32, 2) QHIP_IMG(32, 3) QHIP_IMG(32, 4)
   QHIP_IMG(16, 1) QHIP_IMG(16, 2) QHIP_IMG(16, 3) QHIP_IMG(16, 4)
+  if constexpr (TT == TT_Q8_0) {
+    QHIP_IMG(40, 2)
+  }
 #undef QHIP_IMG
   return hipErrorInvalidValue;
 }
@@ -355,7 +370,7 @@ hipError_t launch_kimage_prepare(int ttype, const void* w, long row_bytes, int r
 hipError_t launch_gemv_image(const GemvArgs& g, int nr, hipStream_t s) {
   if (g.rows <= 0) return hipSuccess;
   int T, P;
-  if (g.tokens != 1 || !gemv_image_format(g.ttype) || !img_geom(g.cols, T, P)) return hipErrorInvalidValue;
+  if (g.tokens != 1 || !gemv_image_format(g.ttype) || !img_geom(g.ttype, g.cols, T, P)) return hipErrorInvalidValue;
   if (nr <= 0) nr = g.rows >= 65536 ? 2 : 1;
   if (nr > 2) return hipErrorInvalidValue;
   if (g.ttype == TT_IQ4_NL) return launch_img_tt<TT_IQ4_NL>(g, T, P, nr, s);

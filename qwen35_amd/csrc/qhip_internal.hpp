@@ -87,10 +87,14 @@ long mmq_image_work_bytes(const GemvArgs& g);
 // bytes per row, quant bytes 16-byte aligned in unit order, scales apart
 bool gemv_image_format(int ttype);
 bool gemv_image_width(int cols);  // a team width and pass count exist for this row width
+// the split activation's layout for this format and width (16 T + P; -1
+// none): formats of one layout share a quantized activation
+int gemv_image_layout(int ttype, int cols);
 long gemv_image_act_bytes(int cols, int tokens);
 hipError_t launch_gemv_image_prepare(const void* w, long row_bytes, int rows, int cols, void* img, hipStream_t s,
-                                     bool q8);
-hipError_t launch_quantize_act_image(const float* x, void* out, int cols, int tokens, long x_stride, hipStream_t s);
+                                     int ttype);
+hipError_t launch_quantize_act_image(int ttype, const float* x, void* out, int cols, int tokens, long x_stride,
+                                     hipStream_t s);
 // g.w = the image, g.xq = one token's split activation; nr rows per team (1,
 // 2; 0 = pick)
 hipError_t launch_gemv_image(const GemvArgs& g, int nr, hipStream_t s);

@@ -21,10 +21,13 @@ def rel_l2(got, want):
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-# the team width and pass count the library takes for a row width: 20-lane
-# teams where the units are a multiple of 20, then whole waves, 32 and 16
-def geometry(cols):
+# the team width and pass count the library takes for a row width: Q8_0 at
+# width 5120 40-lane teams of two passes; else 20-lane teams where the units
+# are a multiple of 20, then whole waves, 32 and 16
+def geometry(cols, tt=po.TT_IQ4_NL):
     U = cols // 64
+    if tt == po.TT_Q8_0 and U == 80:
+        return 40, 2
     for T, pmax in ((20, 4), (64, 2), (32, 4), (16, 4)):
         if U % T == 0 and U // T <= pmax:
             return T, U // T
@@ -35,7 +38,7 @@ def image_of(w, rows, cols, tt):
     """The documented image layout, restated on the host from the GGUF bytes:
     the 16-byte quant slots in the team's walking order (Q8_0: two per block,
     the split activation's order), then the f16 scale pairs."""
-    T, P = geometry(cols)
+    T, P = geometry(cols, tt)
     U = T * P
     bb = BLOCK[tt]
     qs = (bb - 2) // 16
@@ -60,14 +63,15 @@ def test_image_layout(gpu, tt, rows, cols):
     assert np.array_equal(img[:rows * w.shape[1]].reshape(rows, -1), image_of(w, rows, cols, tt))
 
 
+@pytest.mark.parametrize("tt", [po.TT_IQ4_NL, po.TT_Q8_0])
 @pytest.mark.parametrize("cols,tokens", [(1024, 1), (2560, 3), (5120, 2), (8192, 1)])
-def test_split_activation_is_the_reference_quantization(gpu, cols, tokens):
+def test_split_activation_is_the_reference_quantization(gpu, tt, cols, tokens):
     x = synth.make_act(cols, tokens, seed=4)
     x[0, :32] = 0.0          # an all-zero block
     x[-1, 40] = np.float32(3e38)
-    ref = ops.quantize_act(po.TT_IQ4_NL, torch.from_numpy(x).to(gpu)).cpu().numpy().reshape(tokens, -1)
-    xa = ops.quantize_act_image(po.TT_IQ4_NL, torch.from_numpy(x).to(gpu)).cpu().numpy()
-    T, P = geometry(cols)
+    ref = ops.quantize_act(tt, torch.from_numpy(x).to(gpu)).cpu().numpy().reshape(tokens, -1)
+    xa = ops.quantize_act_image(tt, torch.from_numpy(x).to(gpu)).cpu().numpy()
+    T, P = geometry(cols, tt)
     U = T * P
     for t in range(tokens):
         a = xa[72 * U * t:72 * U * (t + 1)]
@@ -197,6 +201,31 @@ def test_backend_memo_keeps_layouts_apart(gpu, oracle, backend):
             backend.sync()
             w = wi if lin.ttype == po.TT_IQ4_NL else wq
             assert rel_l2(out.cpu().numpy(), oracle.matvec(lin.ttype, w, x)[0]) < TOL
+    backend.set_act_memo(False)
+
+
+def test_backend_memo_keeps_split_layouts_apart(gpu, oracle, backend):
+    """At width 5120 Q8_0 and IQ4_NL images read split activations of
+    different team geometries: one x through both, in both orders, with the
+    activation memo on."""
+    rows, cols = 17408, 5120
+    wi = synth.make_weight(po.TT_IQ4_NL, rows, cols, seed=11, tag=1)
+    wq = synth.make_weight(po.TT_Q8_0, rows, cols, seed=11, tag=2)
+    x = synth.make_act(cols, 1, seed=11)
+    li = backend.load_linear(po.TT_IQ4_NL, rows, cols, wi)
+    lq = backend.load_linear(po.TT_Q8_0, rows, cols, wq)
+    backend.set_act_memo(True)
+    xd = torch.from_numpy(x[0]).to(gpu)
+    want = {po.TT_IQ4_NL: oracle.matvec(po.TT_IQ4_NL, wi, x)[0], po.TT_Q8_0: oracle.matvec(po.TT_Q8_0, wq, x)[0]}
+    for order in ((li, lq), (lq, li), (lq, lq)):
+        backend.step_begin(0)
+        for lin in order:
+            out = torch.empty(rows, device=gpu)
+            backend.matvec(out, lin, xd)
+            backend.sync()
+            assert rel_l2(out.cpu().numpy(), want[lin.ttype]) < TOL
+    hits, misses = backend.act_stats()
+    assert (hits, misses) == (1, 5)  # only the repeat in one layout reuses the quantized x
     backend.set_act_memo(False)
 
 
