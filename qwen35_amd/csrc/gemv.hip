@@ -699,13 +699,23 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
     nr = g.ttype == TT_Q4_1 ? 4 : 2;
     return;
   }
+  // Q4_K at width 4096: one-wave teams of two rows ([12288, 4096] 7.56 us
+  // against 8.15 with two-wave teams of four)
+  if (g.ttype == TT_Q4_K && upr == 64 && g.rows >= 4096) {
+    team = 64;
+    nr = 2;
+    return;
+  }
   if ((g.ttype == TT_Q4_K || g.ttype == TT_Q5_K || g.ttype == TT_Q3_K) && upr >= 64) {
     team = 128;
     nr = 4;
     return;
   }
   switch (g.ttype) {
-    case TT_Q6_K: nr = g.rows >= 4096 ? 2 : 1; team = 64; break;
+    // Q6_K in 20-lane teams where the units are a multiple of 20 past 64
+    // ([17408, 5120] 20.13 us against 22.00 with 64 lanes; at 40 units the
+    // 40-lane team stays ahead, [19456, 2560] 12.89 against 14.85)
+    case TT_Q6_K: nr = g.rows >= 4096 ? 2 : 1; team = upr > 64 && upr % 20 == 0 ? 20 : 64; break;
     case TT_Q4_K: case TT_Q5_K:
       nr = g.rows >= 16384 && upr <= 40 ? 4 : 2; team = upr <= 40 ? 40 : 20; break;
     case TT_IQ4_NL: nr = 4; team = 20; break;
