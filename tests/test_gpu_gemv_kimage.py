@@ -71,10 +71,12 @@ def test_kimage_layout(gpu, tt, rows, cols):
 
 
 # (rows, cols, rows_per_lane): the default shapes (20- / 40-lane teams, 64
-# lanes, two- and four-wave teams of 2 or 4 rows) and explicit row counts
+# lanes, two- and four-wave teams of 2 or 4 rows; Q6_K 20-lane teams of two
+# rows at width 5120, Q4_K 64-lane teams of two rows at 4096) and explicit
+# row counts
 KCASES = [(300, 2560, 0), (257, 1024, 0), (129, 5120, 0), (1, 2560, 0), (250, 2560, 1), (251, 2560, 2),
           (99, 4608, 0), (64, 9728, 0), (4100, 9728, 0), (77, 17408, 0), (40, 6144, 1), (33, 3840, 2),
-          (4097, 2048, 0), (18, 2304, 0)]
+          (4097, 2048, 0), (18, 2304, 0), (4100, 5120, 0), (4097, 4096, 0)]
 
 
 @pytest.mark.gpu
