@@ -844,10 +844,14 @@ bool gemv_fused_fits(int ttype, int cols) { return fused_lds_bytes(ttype, cols) 
 // quantize the activation together, once per workgroup).  Lanes per row: the
 // candidate with the fewest wave-steps (waves x units per lane) among those
 // whose grid has at least 192 workgroups (three quarters of the CUs), ties to
-// the larger team; if none fills the GPU, the largest grid.  Swept on MI355X
+// the smaller team; if none fills the GPU, the largest grid.  Swept on MI355X
 // over Q8_0 [6144, 1024], Q4_K [9728 / 19456, 2560] and [12288, 4096], Q6_K
 // [2560, 2560] and IQ4_NL [32768, 2560]: the best shape on five, within 9% on
 // the sixth (Q4_K [19456, 2560]: 20 lanes, 8.8 us; 12 lanes 10.0 us).
+// Re-swept over 10-64 lanes, 1-2 rows and 256-1024 threads: the tie at
+// [12288, 4096] (16, 32 and 64 lanes) goes to 16 lanes (8.97 us; 32 lanes
+// 9.56, 64 lanes 10.86); at [19456, 2560] 10 lanes 9.01 against 20 lanes
+// 9.10.
 static void fused_default_shape(const GemvArgs& g, int& team, int& nr, int& wgs) {
   static const int kCand[] = {8, 10, 16, 20, 32, 40, 64};
   const long upr = g.cols / 64;
@@ -863,7 +867,7 @@ static void fused_default_shape(const GemvArgs& g, int& team, int& nr, int& wgs)
     bool take;
     if (best < 0) take = true;
     else if (full != best_full) take = full;
-    else if (full) take = w <= best_w;          // ties: the later (larger) team
+    else if (full) take = w < best_w;           // ties: the earlier (smaller) team
     else take = grid >= best_grid;
     if (take) {
       best = t;
