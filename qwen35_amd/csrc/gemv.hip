@@ -957,10 +957,21 @@ static hipError_t launch_gemv_qsk_t(const GemvArgs& g, const float* x, void* xq_
 // [2560, 9728]: eight lanes and one row per lane throughout; slices of 1024
 // values (within 0.4 us of the best on every shape), 2048 from width 16384
 // (Q4_K [5120, 17408] 14.0 vs 15.9 us).
+// Re-swept for Q6_K (1024-4096-value slices, 4-16 lanes, 1-2 rows; two
+// runs): [5120, 17408] 4096-value slices of 16 lanes 19.5 / 20.2 us against
+// 20.6 / 20.8 with 2048-value slices of 8, [4096, 12288] 2048-value slices
+// 14.1 / 14.2 against 14.6 / 14.7; [2560, 9728] and Q4_K [5120, 17408] keep
+// the rule above (10.3, 13.4 us).
 static void splitk_default_shape(const GemvArgs& g, int& team, int& nr, int& slice) {
   team = 8;
   nr = 1;
   slice = g.cols >= 16384 ? 2048 : 1024;
+  if (g.ttype == TT_Q6_K && g.cols >= 16384) {
+    slice = 4096;
+    team = 16;
+  } else if (g.ttype == TT_Q6_K && g.cols >= 12288) {
+    slice = 2048;
+  }
 }
 
 // Split-K against the separate quantize + GEMV launches, same sweep (default
