@@ -392,10 +392,25 @@ def test_iq3_fixture_pins_grid_entries(oracle, tt):
                  for r in range(len(rows)) for ib in range(8) for l in range(4)}
         assert len(signs) == 128
     else:
-        # the 11 entries no fixture row uses are held only by the ordering and
-        # level checks above (parity unpinned for those entries)
+        # the 11 entries no fixture row uses are pinned by the table fixture
+        # (test_iq3_grid_equals_reference_table)
         assert len(used) == 501
         assert sorted(set(range(512)) - used) == [32, 57, 71, 100, 104, 113, 197, 200, 207, 216, 491]
+
+
+@pytest.mark.parametrize("tt", [po.TT_IQ3_XXS, po.TT_IQ3_S])
+def test_iq3_grid_equals_reference_table(oracle, tt):
+    """Every entry of the oracle's grid (built from the product's own
+    encoding in qwen35_amd/csrc/iq_grids.h) equals the reference's table
+    (src/iq_tables.zig:322-355 iq3xxs_grid, :360-425 iq3s_grid), read as
+    numbers into tests/golden/iq3_grids.npz by tests/golden/gen_iq3_grids.py.
+    This pins the 11 IQ3_S entries no udtest fixture row uses."""
+    fix = np.load(GOLD / "iq3_grids.npz")
+    want = fix["iq3xxs_grid"] if tt == po.TT_IQ3_XXS else fix["iq3s_grid"]
+    got = oracle.iq3_grid(tt)
+    assert want.shape == got.shape
+    bad = np.flatnonzero(got != want)
+    assert bad.size == 0, [(int(i), hex(int(got[i])), hex(int(want[i]))) for i in bad[:8]]
 
 
 @pytest.mark.parametrize("tt", [po.TT_IQ3_XXS, po.TT_IQ3_S])
