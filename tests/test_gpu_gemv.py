@@ -272,10 +272,13 @@ def test_fused_declines(gpu):
 SPLIT = [(po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 37, 9728), (po.TT_Q4_K, 300, 5120), (po.TT_Q5_K, 100, 4352),
          (po.TT_Q3_K, 60, 2304), (po.TT_Q2_K, 70, 2560), (po.TT_IQ4_XS, 80, 2560), (po.TT_IQ3_XXS, 90, 2560),
          (po.TT_IQ3_S, 16, 2304), (po.TT_Q8_0, 300, 2048), (po.TT_IQ4_NL, 200, 1024), (po.TT_Q4_0, 50, 2560),
-         (po.TT_Q4_1, 70, 1536)]
+         (po.TT_Q4_1, 70, 1536), (po.TT_Q6_K, 40, 17408), (po.TT_Q6_K, 36, 12288), (po.TT_Q4_K, 44, 16384)]
 # (slice values, lanes per row, rows per lane); 0 picks.  768 leaves a short
-# last slice on most widths; 64 lanes on a 256-value slice idle most lanes.
-SPLIT_SHAPES = [(0, 0, 0), (256, 4, 1), (512, 8, 2), (768, 32, 2), (1024, 16, 4), (256, 64, 1), (2048, 64, 4)]
+# last slice on most widths; 64 lanes on a 256-value slice idle most lanes;
+# 4096 / 16 and 2048 / 16 are the Q6_K defaults from widths 16384 / 12288
+# (one slice, or a short last one, on narrower rows).
+SPLIT_SHAPES = [(0, 0, 0), (256, 4, 1), (512, 8, 2), (768, 32, 2), (1024, 16, 4), (256, 64, 1), (2048, 64, 4),
+                (4096, 16, 1), (2048, 16, 1)]
 
 
 @pytest.mark.parametrize("tt,rows,cols", SPLIT, ids=[case_id(*c) for c in SPLIT])
