@@ -105,7 +105,14 @@ int qhip_launch_dequantize_row(int ttype, const void *d_src_row, float *d_dst, i
 /* ---- matvec -----------------------------------------------------------------
  * q35_launch_mul_mat_vec (src/kernels/cuda/api.h:104-112):
  *   out[t*rows + r] = W[r] . xq[t] for t < tokens.
- * d_xq holds `tokens` rows quantized with the weight's activation family. */
+ * d_xq holds `tokens` rows quantized with the weight's activation family.
+ * These stateless launchers read the GGUF rows in every call.  The faster
+ * weight-image kernels need an image built once per weight and are reached
+ * through the Exec mirror (qhip_backend_*, which builds and keeps them) or
+ * the explicit image entry points below.  Measured on MI355X: config 5 Q6_K
+ * [5120, 17408] at 512 tokens 293.5 us here against 124.9 us from the plane
+ * image; the config-3 IQ4_NL head [248320, 2560] at one token 71.2 us against
+ * 61.6 us from the GEMV image. */
 int qhip_launch_mul_mat_vec(const void *d_w, const void *d_xq, float *d_out, int rows, int cols,
                             int tokens, int ttype, void *stream);
 /* q35_launch_mul_mat_vec_q8_0 (src/kernels/cuda/api.h:116-117). */
@@ -236,9 +243,9 @@ int qhip_launch_mmq_tuned(const void *d_w, const void *d_xq, float *d_out, int r
  *     128x64 tokens x rows, 0 x 0 = default; Q6_K only 0 x 0 (its kernel has
  *     one shape: a persistent grid over 128-row tiles of 64 or 128 tokens);
  *     d_work (nullable) as for qhip_launch_mul_mat_work
- *     (qhip_mul_mat_work_bytes covers the image launch too); a Q6_K launch
- *     whose tiles must be cut over K needs it and returns invalid-value
- *     without it */
+ *     (qhip_mul_mat_work_bytes covers the image launch too); without a
+ *     large enough d_work no Q6_K tile is cut over K (the launch runs
+ *     unsplit, with the same results) */
 long qhip_mmq_image_bytes(int ttype, int rows, int cols);
 int qhip_launch_mmq_prepare(int ttype, const void *d_w, int rows, int cols, void *d_image, void *stream);
 int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_out, int rows, int cols,
@@ -468,9 +475,58 @@ int qhip_backend_act_stats(const qhip_backend *be, unsigned long long *hits,
  * allocates nothing -- it builds no MMQ image (the tile MMQ runs instead) and
  * grows no workspace (an MMQ that would need more runs unsplit) -- but the
  * activation scratch must already be large enough, so run the step once
- * eagerly (or call alloc_scratch_k and prepare_linear) before capturing. */
+ * eagerly (or call alloc_scratch_k and prepare_linear) before capturing.
+ * Once a capture has been seen, a scratch or workspace that a later eager
+ * call outgrows is kept, not freed, until free_scratch / destroy, so a graph
+ * captured earlier never names freed memory. */
 void qhip_backend_step_begin(qhip_backend *be, unsigned pos);
 void qhip_backend_step_end(qhip_backend *be);
+
+/* ---- introspection and profiling of the backend -------------------------------
+ * describe() (src/backend.zig:494-495): a one-line account of what is in use --
+ * device, CU count, the bytes of weights, images, scratch and the budget, and
+ * which images, the memo and profiling are on.  The string belongs to the
+ * backend and stays valid until the next describe call or destroy. */
+const char *qhip_backend_describe(qhip_backend *be);
+/* Device timing of the slots (the Exec profiling slots reportProfile /
+ * profReport, src/backend.zig:500-514; the reference's per-type device table
+ * and event-timed slots, src/backend_cuda.zig:6647 reportStats, :6195
+ * slotEnter).  With profiling on, every matvec, matvec_pair, matvec_batch_k
+ * and dequant_row call records a HIP event pair on the backend's stream
+ * around its launches; the pairs are read back lazily (at most 512
+ * outstanding: the oldest half is waited for when the queue fills), so the
+ * slots still return without a host wait.  Times are summed per (slot,
+ * type, rows, cols, tokens) with the calls' algorithmic bytes (packed
+ * weights + 4 cols tokens + 4 rows tokens; dequant_row: one row + 4 cols) and
+ * int8 ops (2 rows cols tokens).  Calls made while the stream is being
+ * captured into a graph are not timed, only counted (prof_untimed).  Off by
+ * default; the binding turns it on under $QWEN35_PROF as the reference does. */
+#define QHIP_SLOT_MATVEC 0
+#define QHIP_SLOT_MATVEC_PAIR 1
+#define QHIP_SLOT_MATVEC_BATCH_K 2
+#define QHIP_SLOT_DEQUANT_ROW 3
+typedef struct qhip_prof_entry {
+  int slot;         /* QHIP_SLOT_* */
+  int ttype;
+  int rows;         /* matvec_pair: the two weights' rows together */
+  int cols;
+  int tokens;
+  long long calls;
+  double device_us; /* summed over the calls */
+  double bytes;     /* summed algorithmic bytes */
+  double ops;       /* summed int8 ops */
+} qhip_prof_entry;
+int qhip_backend_set_profiling(qhip_backend *be, int on);
+/* Waits for every recorded pair, then writes up to max_entries rows, largest
+ * device time first; returns the number of rows the table has. */
+int qhip_backend_prof_entries(qhip_backend *be, qhip_prof_entry *out, int max_entries);
+/* The same table as text (a header line, then one `HIP-PROF` line per row
+ * with calls, total and average device us, GB/s, the fraction of the 8 TB/s
+ * HBM peak and TOP/s), NUL-terminated in buf[0..len); returns the length of
+ * the whole text (snprintf semantics), -1 on a bad argument. */
+long qhip_backend_prof_report(qhip_backend *be, char *buf, long len);
+long long qhip_backend_prof_untimed(const qhip_backend *be);
+void qhip_backend_prof_reset(qhip_backend *be);
 
 #ifdef __cplusplus
 }

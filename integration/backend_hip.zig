@@ -31,6 +31,18 @@
 //! silently.  `QWEN35_HIP_MAX_DEV_MIB` caps the device memory the backend
 //! places (qhip_backend_set_mem_budget), as `QWEN35_CUDA_MAX_DEV_MIB` does
 //! (src/backend_cuda.zig:1754-1760).
+//!
+//! Introspection and profiling.  `describe` is the library's one-line account
+//! of the device, the bytes placed and the switches in use.  Under
+//! `$QWEN35_PROF` the library times every matvec slot on the device (HIP event
+//! pairs, read back lazily) and `reportProfile` / `profReport` print its
+//! per-(slot, type, shape) table -- calls, device time, GB/s, the fraction of
+//! HBM peak -- followed by the CPU backend's own table for the slots still on
+//! the CPU, as the CUDA backend prints its per-type device table
+//! (src/backend_cuda.zig:6647).  `$QWEN35_HIP_MVCHECK` cross-checks the first
+//! matvec and the first batch of each weight type against the embedded CPU
+//! backend and prints the comparison (src/backend_cuda.zig:4018-4114);
+//! `$QWEN35_HIP_MVCHECK_ONLY=<type>` restricts it to one type.
 const std = @import("std");
 const backend = @import("backend.zig");
 const gguf = @import("gguf.zig");
@@ -68,6 +80,9 @@ extern fn qhip_backend_sync(be: ?*QhipBackend) c_int;
 extern fn qhip_backend_set_mem_budget(be: ?*QhipBackend, bytes: usize) c_int;
 extern fn qhip_backend_step_begin(be: ?*QhipBackend, pos: c_uint) void;
 extern fn qhip_backend_step_end(be: ?*QhipBackend) void;
+extern fn qhip_backend_describe(be: ?*QhipBackend) [*:0]const u8;
+extern fn qhip_backend_set_profiling(be: ?*QhipBackend, on: c_int) c_int;
+extern fn qhip_backend_prof_report(be: ?*QhipBackend, buf: ?[*]u8, len: c_long) c_long;
 
 // ---- the HIP runtime (libamdhip64): pinned, device-mapped host memory ----------------
 extern fn hipHostMalloc(ptr: *?*anyopaque, size: usize, flags: c_uint) c_int;
@@ -83,6 +98,12 @@ pub const HipBackend = struct {
     resident: std.ArrayListUnmanaged(Resident) = .empty,
     /// pinned Buf regions, released by freeScratch
     pinned: std.ArrayListUnmanaged(*anyopaque) = .empty,
+    /// `$QWEN35_HIP_MVCHECK`: on, the type it is restricted to, and the weight
+    /// types already checked (one check per type and slot kind)
+    mvcheck_on: bool = false,
+    mvcheck_only: ?[]const u8 = null,
+    mvcheck_seen: [64]bool = @splat(false),
+    mvcheck_seen_k: [64]bool = @splat(false),
 
     const Resident = struct { host: [*]const u8, lin: QhipLinear };
 
@@ -95,8 +116,15 @@ pub const HipBackend = struct {
                 const mib = std.fmt.parseInt(usize, std.mem.trim(u8, v, " "), 10) catch 0;
                 if (mib != 0) _ = qhip_backend_set_mem_budget(b, mib << 20);
             }
+            if (std.posix.getenv("QWEN35_PROF") != null) _ = qhip_backend_set_profiling(b, 1);
         }
-        return .{ .alloc = alloc, .cpu = CpuBackend.init(alloc, g), .be = be };
+        return .{
+            .alloc = alloc,
+            .cpu = CpuBackend.init(alloc, g),
+            .be = be,
+            .mvcheck_on = std.posix.getenv("QWEN35_HIP_MVCHECK") != null,
+            .mvcheck_only = std.posix.getenv("QWEN35_HIP_MVCHECK_ONLY"),
+        };
     }
 
     pub fn exec(self: *HipBackend) backend.Exec {
@@ -140,6 +168,48 @@ pub const HipBackend = struct {
         if (rc != 0) return failed(what, rc, out);
         const rs = qhip_backend_sync(self.be);
         if (rs != 0) failed(what, rs, out);
+    }
+
+    /// `$QWEN35_HIP_MVCHECK`: a debug cross-check, not a computation path
+    /// (src/backend_cuda.zig:4018-4114).  The first matvec and the first
+    /// batch of each weight type run once more on the embedded CPU backend
+    /// into a temporary, and the two results are compared: relative L2 over
+    /// the output (the parity bar, 1e-5) and the count of elements more than
+    /// 2e-2 apart relative to max(|cpu|, 1e-3), the reference's per-element
+    /// test.  `out` is only read; it and `x` are host-mapped Buf regions, and
+    /// `finish` has waited for the launch.
+    fn mvCheck(self: *HipBackend, out: backend.Buf, w: backend.LinearW, x: backend.Buf, k: usize) void {
+        if (!self.mvcheck_on) return;
+        const q = switch (w) {
+            .quant => |q| q,
+            .f32 => return,
+        };
+        if (self.mvcheck_only) |only| if (!std.mem.eql(u8, only, @tagName(q.ttype))) return;
+        const ti: usize = @intCast(@intFromEnum(q.ttype));
+        const seen = if (k == 1) &self.mvcheck_seen else &self.mvcheck_seen_k;
+        if (ti >= seen.len or seen[ti]) return;
+        seen[ti] = true;
+        const n = q.rows * k;
+        const ref = self.alloc.alloc(f32, n) catch return;
+        defer self.alloc.free(ref);
+        const rbuf = backend.Buf.wrap(ref);
+        if (k == 1) CpuBackend.vtable.matvec(&self.cpu, rbuf, w, x) else CpuBackend.vtable.matvecBatchK(&self.cpu, rbuf, w, x, k);
+        var num: f64 = 0;
+        var den: f64 = 0;
+        var bad: usize = 0;
+        for (out.slice()[0..n], ref) |dv, cv| {
+            const d = @as(f64, dv) - @as(f64, cv);
+            num += d * d;
+            den += @as(f64, cv) * @as(f64, cv);
+            if (@abs(dv - cv) / @max(@abs(cv), 1e-3) > 2e-2) {
+                if (bad < 3) std.debug.print("  MVCHECK row: dev={d} cpu={d}\n", .{ dv, cv });
+                bad += 1;
+            }
+        }
+        const rel = if (den > 0) @sqrt(num / den) else @sqrt(num);
+        std.debug.print("MVCHECK[{s}] rows={d} cols={d} k={d} rel_l2={e} mismatched={d} {s}\n", .{
+            @tagName(q.ttype), q.rows, q.cols(), k, rel, bad, if (rel <= 1e-5 and bad == 0) "ok" else "FAIL",
+        });
     }
 
     // ---- slots on the GPU ---------------------------------------------------------------
@@ -195,6 +265,7 @@ pub const HipBackend = struct {
         } orelse return CpuBackend.vtable.matvec(&self.cpu, out, w, x);
         std.debug.assert(out.len >= @as(usize, @intCast(lin.rows)) and x.len >= @as(usize, @intCast(lin.cols)));
         self.finish("matvec", qhip_backend_matvec(self.be, out.ptr, lin, x.ptr), out);
+        self.mvCheck(out, w, x, 1);
     }
 
     fn vMatvecPair(ctx: *anyopaque, out: backend.Buf, a: backend.LinearW, b: backend.LinearW, x: backend.Buf) void {
@@ -219,6 +290,7 @@ pub const HipBackend = struct {
             .f32 => null,
         } orelse return CpuBackend.vtable.matvecBatchK(&self.cpu, out, w, xK, k);
         self.finish("matvecBatchK", qhip_backend_matvec_batch_k(self.be, out.ptr, lin, xK.ptr, @intCast(k)), out);
+        self.mvCheck(out, w, xK, k);
     }
 
     fn vDequantRow(ctx: *anyopaque, dst: backend.Buf, w: gguf.QuantRow, row: usize) void {
@@ -277,6 +349,37 @@ pub const HipBackend = struct {
         return if (self.be) |b| std.mem.span(qhip_backend_name(b)) else "hip (no device)";
     }
 
+    /// backend.zig:494-495: the device, the bytes placed and the switches in
+    /// use (the string is the library's, valid until the next call).
+    fn vDescribe(ctx: *anyopaque) []const u8 {
+        const self = self_(ctx);
+        return if (self.be) |b| std.mem.span(qhip_backend_describe(b)) else "hip (no device)";
+    }
+
+    /// The library's device-timed slot table, then the CPU backend's table
+    /// for the matvecs that stayed on the CPU (`.f32` weights).
+    fn printDeviceTable(self: *HipBackend) void {
+        const b = self.be orelse return;
+        const n = qhip_backend_prof_report(b, null, 0);
+        if (n <= 0) return;
+        const text = self.alloc.alloc(u8, @intCast(n + 1)) catch return;
+        defer self.alloc.free(text);
+        _ = qhip_backend_prof_report(b, text.ptr, n + 1);
+        std.debug.print("{s}", .{text[0..@intCast(n)]});
+    }
+
+    fn vReportProfile(ctx: *anyopaque) void {
+        const self = self_(ctx);
+        self.printDeviceTable();
+        CpuBackend.vtable.reportProfile(&self.cpu);
+    }
+
+    fn vProfReport(ctx: *anyopaque) void {
+        const self = self_(ctx);
+        self.printDeviceTable();
+        CpuBackend.vtable.profReport(&self.cpu);
+    }
+
     /// The CPU backend's table with the quantized-matvec slots replaced.  The
     /// `Exec` context is the embedded CPU backend, so every other slot runs as
     /// it does in a CPU run; the slots above find their HipBackend from it.
@@ -295,6 +398,9 @@ pub const HipBackend = struct {
         vt.stepBegin = dStepBegin;
         vt.stepEnd = dStepEnd;
         vt.name = vName;
+        vt.describe = vDescribe;
+        vt.reportProfile = vReportProfile;
+        vt.profReport = vProfReport;
         break :blk vt;
     };
 };

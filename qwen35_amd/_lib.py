@@ -20,6 +20,12 @@ class QhipLinear(ctypes.Structure):
                 ("row_bytes", c_long)]
 
 
+class QhipProfEntry(ctypes.Structure):
+    _fields_ = [("slot", c_int), ("ttype", c_int), ("rows", c_int), ("cols", c_int), ("tokens", c_int),
+                ("calls", ctypes.c_longlong), ("device_us", ctypes.c_double), ("bytes", ctypes.c_double),
+                ("ops", ctypes.c_double)]
+
+
 # name: (restype, argtypes)
 SIGNATURES = {
     "qhip_init": (c_int, [c_int]),
@@ -112,6 +118,12 @@ SIGNATURES = {
                                        ctypes.POINTER(ctypes.c_ulonglong)]),
     "qhip_backend_step_begin": (None, [c_void_p, ctypes.c_uint]),
     "qhip_backend_step_end": (None, [c_void_p]),
+    "qhip_backend_describe": (c_char_p, [c_void_p]),
+    "qhip_backend_set_profiling": (c_int, [c_void_p, c_int]),
+    "qhip_backend_prof_entries": (c_int, [c_void_p, ctypes.POINTER(QhipProfEntry), c_int]),
+    "qhip_backend_prof_report": (c_long, [c_void_p, ctypes.c_char_p, c_long]),
+    "qhip_backend_prof_untimed": (ctypes.c_longlong, [c_void_p]),
+    "qhip_backend_prof_reset": (None, [c_void_p]),
 }
 
 _lib = None

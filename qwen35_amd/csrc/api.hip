@@ -339,7 +339,7 @@ int qhip_launch_mul_mat(const void* d_w, const void* d_xq, float* d_out, int row
 }
 
 long qhip_mul_mat_work_bytes(int rows, int cols, int tokens, int ttype) {
-  static const uint8_t dummy[4] = {0, 0, 0, 0};  // aligned stand-ins: only the shape matters
+  alignas(16) static const uint8_t dummy[16] = {};  // 16-byte aligned stand-ins: only the shape matters
   GemvArgs g;
   if (rows <= 0 || tokens <= 0 || make_args(dummy, dummy, (float*)dummy, rows, cols, tokens, ttype, g) != hipSuccess)
     return 0;

@@ -9,10 +9,13 @@
 #include "../../include/qwen35_hip.h"
 #include "qhip_internal.hpp"
 
+#include <algorithm>
 #include <cstdio>
+#include <cstring>
 #include <map>
 #include <mutex>
 #include <new>
+#include <string>
 #include <utility>
 #include <vector>
 
@@ -39,6 +42,12 @@ struct qhip_backend {
   // (counters zero between launches)
   uint8_t* skwork = nullptr;
   size_t skwork_cap = 0;
+  // Once a launch of this backend has been captured into a graph, a scratch
+  // or workspace buffer that has to grow is not freed: the graph still names
+  // it and may be replayed.  Such buffers are kept here (and still count
+  // against the budget) until free_scratch or destroy.
+  bool graph_seen = false;
+  std::vector<std::pair<void*, size_t>> retired;
   // MMQ images of Q6_K weights: the plane image of the prefill MMQ
   // (qhip_launch_mmq_prepare, kind kImgMmq) and the fragment image of the
   // few-token MMQ (qhip_launch_wd_prepare, kind kImgFrag), built by
@@ -94,7 +103,38 @@ struct qhip_backend {
   const float* memo_src = nullptr;
   int memo_cols = 0, memo_k = 0, memo_fam = -1;
   unsigned long long memo_hits = 0, memo_misses = 0;
+  // Device timing of the slots (the Exec profiling slots, backend.zig:500-514;
+  // the reference's per-type device table, backend_cuda.zig:6647): an event
+  // pair on the backend's stream around each slot call, read back lazily, and
+  // summed per (slot, type, rows, cols, tokens).  Calls under a graph
+  // capture are counted as untimed (an event there would become a graph
+  // node).
+  struct ProfKey {
+    int slot, ttype, rows, cols, tokens;
+    bool operator<(const ProfKey& o) const {
+      if (slot != o.slot) return slot < o.slot;
+      if (ttype != o.ttype) return ttype < o.ttype;
+      if (rows != o.rows) return rows < o.rows;
+      if (cols != o.cols) return cols < o.cols;
+      return tokens < o.tokens;
+    }
+  };
+  struct ProfStat {
+    long long calls = 0;
+    double us = 0.0, bytes = 0.0, ops = 0.0;
+  };
+  struct ProfPending {
+    ProfKey key;
+    double bytes, ops;
+    hipEvent_t a, b;
+  };
+  bool prof_on = false;
+  std::map<ProfKey, ProfStat> prof;
+  std::vector<ProfPending> prof_pending;
+  std::vector<hipEvent_t> prof_events;  // created and free for reuse
+  long long prof_untimed = 0;
   char name[96] = "hip";
+  char desc[512] = "";
 };
 
 static void memo_clear(qhip_backend* be) {
@@ -139,11 +179,40 @@ static hipError_t arena_alloc(qhip_backend* be, size_t bytes, uint8_t** out) {
   return hipSuccess;
 }
 
+static bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
+// Give up a scratch buffer that is being replaced by a larger one: freed now,
+// or kept until free_scratch / destroy when a graph captured earlier may
+// still read or write it.
+static void release_buffer(qhip_backend* be, void* p, size_t bytes) {
+  if (!p) return;
+  if (be->graph_seen) {
+    be->retired.emplace_back(p, bytes);
+    return;
+  }
+  (void)hipFree(p);
+  be->placed -= bytes;
+}
+
+// The size a growing buffer takes: at least half again its old size, so a
+// sequence of growing prefills keeps few retired buffers (their total stays
+// below twice the live one); exactly `bytes` when the budget has no room for
+// more.
+static size_t grown_size(const qhip_backend* be, size_t cap, size_t bytes) {
+  const size_t g = cap + cap / 2;
+  if (g <= bytes) return bytes;
+  return over_budget(be, be->graph_seen ? g : g - cap) ? bytes : g;
+}
+
 static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
   if (be->act_cap >= bytes) return hipSuccess;
-  if (over_budget(be, bytes - be->act_cap)) return budget_error(be, "activation scratch", bytes - be->act_cap);
-  if (be->act) (void)hipFree(be->act);
-  be->placed -= be->act_cap;
+  if (over_budget(be, be->graph_seen ? bytes : bytes - be->act_cap))
+    return budget_error(be, "activation scratch", bytes - be->act_cap);
+  bytes = grown_size(be, be->act_cap, bytes);
+  release_buffer(be, be->act, be->act_cap);
   be->act = nullptr;
   be->act_cap = 0;
   memo_clear(be);
@@ -156,16 +225,12 @@ static hipError_t ensure_act(qhip_backend* be, size_t bytes) {
   return hipSuccess;
 }
 
-static bool capturing(hipStream_t s) {
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  return hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
-}
-
 static hipError_t ensure_skwork(qhip_backend* be, size_t bytes) {
   if (be->skwork_cap >= bytes) return hipSuccess;
-  if (over_budget(be, bytes - be->skwork_cap)) return budget_error(be, "split-K workspace", bytes - be->skwork_cap);
-  if (be->skwork) (void)hipFree(be->skwork);
-  be->placed -= be->skwork_cap;
+  if (over_budget(be, be->graph_seen ? bytes : bytes - be->skwork_cap))
+    return budget_error(be, "split-K workspace", bytes - be->skwork_cap);
+  bytes = grown_size(be, be->skwork_cap, bytes);
+  release_buffer(be, be->skwork, be->skwork_cap);
   be->skwork = nullptr;
   be->skwork_cap = 0;
   void* p = nullptr;
@@ -319,6 +384,7 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
                long row_bytes, const float* x, int k) {
   if (!out || !x || k < 0) return (int)hipErrorInvalidValue;
   if (k == 0 || rows == 0) return 0;
+  if (!be->graph_seen && capturing(be->stream)) be->graph_seen = true;
   // the activation family: Q8_0 rows for 32-value weight blocks, Q8_K for
   // 256-value super-blocks (backend_cpu.zig:42-50 actFamily)
   const int fam = qhip_quant_act_block_elems(ttype);
@@ -453,6 +519,92 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   return report("matvec", dispatch_mul_mat(g, QHIP_PATH_AUTO, work, work_bytes, be->stream));
 }
 
+// ---- device timing of the slots ---------------------------------------------------
+
+static constexpr size_t kProfMaxPending = 512;
+static const char* const kSlotNames[] = {"matvec", "matvecPair", "matvecBatchK", "dequantRow"};
+
+static hipEvent_t prof_event(qhip_backend* be) {
+  if (!be->prof_events.empty()) {
+    hipEvent_t e = be->prof_events.back();
+    be->prof_events.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
+
+// Read the oldest recorded pairs (waiting for them) until `keep` remain.
+static void prof_resolve(qhip_backend* be, size_t keep) {
+  const size_t n = be->prof_pending.size() > keep ? be->prof_pending.size() - keep : 0;
+  for (size_t i = 0; i < n; ++i) {
+    qhip_backend::ProfPending& p = be->prof_pending[i];
+    float ms = 0.0f;
+    if (hipEventSynchronize(p.b) == hipSuccess && hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+      qhip_backend::ProfStat& st = be->prof[p.key];
+      st.calls += 1;
+      st.us += 1e3 * (double)ms;
+      st.bytes += p.bytes;
+      st.ops += p.ops;
+    }
+    be->prof_events.push_back(p.a);
+    be->prof_events.push_back(p.b);
+  }
+  be->prof_pending.erase(be->prof_pending.begin(), be->prof_pending.begin() + (long)n);
+}
+
+// One timed slot call: start() records the opening event, finish() the
+// closing one and queues the pair with the call's algorithmic bytes
+// (weights + f32 x + f32 y) and int8 ops (2 rows cols tokens).
+struct ProfScope {
+  qhip_backend* be;
+  hipEvent_t a = nullptr;
+  ProfScope(qhip_backend* b) : be(b) {
+    if (!be->prof_on) return;
+    if (capturing(be->stream)) {
+      ++be->prof_untimed;
+      return;
+    }
+    a = prof_event(be);
+    if (a && hipEventRecord(a, be->stream) != hipSuccess) {
+      be->prof_events.push_back(a);
+      a = nullptr;
+    }
+  }
+  int finish(int rc, int slot, int ttype, int rows, int cols, int tokens, double wbytes) {
+    if (!a) return rc;
+    hipEvent_t b = rc == 0 ? prof_event(be) : nullptr;
+    if (!b || hipEventRecord(b, be->stream) != hipSuccess) {
+      be->prof_events.push_back(a);
+      if (b) be->prof_events.push_back(b);
+      return rc;
+    }
+    const double bytes = slot == 3 ? wbytes + 4.0 * cols : wbytes + 4.0 * ((double)cols + rows) * tokens;
+    const double ops = slot == 3 ? 0.0 : 2.0 * rows * (double)cols * tokens;
+    be->prof_pending.push_back({{slot, ttype, rows, cols, tokens}, bytes, ops, a, b});
+    if (be->prof_pending.size() >= kProfMaxPending) prof_resolve(be, kProfMaxPending / 2);
+    return rc;
+  }
+};
+
+static const char* type_name(int ttype) {
+  switch (ttype) {
+    case QHIP_TT_Q4_0: return "Q4_0";
+    case QHIP_TT_Q4_1: return "Q4_1";
+    case QHIP_TT_Q8_0: return "Q8_0";
+    case QHIP_TT_Q2_K: return "Q2_K";
+    case QHIP_TT_Q3_K: return "Q3_K";
+    case QHIP_TT_Q4_K: return "Q4_K";
+    case QHIP_TT_Q5_K: return "Q5_K";
+    case QHIP_TT_Q6_K: return "Q6_K";
+    case QHIP_TT_IQ3_XXS: return "IQ3_XXS";
+    case QHIP_TT_IQ4_NL: return "IQ4_NL";
+    case QHIP_TT_IQ3_S: return "IQ3_S";
+    case QHIP_TT_IQ4_XS: return "IQ4_XS";
+    default: return "?";
+  }
+}
+
 extern "C" {
 
 qhip_backend* qhip_backend_create(int device, int* err) {
@@ -473,6 +625,8 @@ void qhip_backend_destroy(qhip_backend* be) {
   if (!be) return;
   (void)hipSetDevice(be->device);
   (void)hipDeviceSynchronize();
+  prof_resolve(be, 0);
+  for (hipEvent_t e : be->prof_events) (void)hipEventDestroy(e);
   qhip_backend_free_scratch(be);
   for (auto& kv : be->images) (void)hipFree(kv.second.p);
   for (auto& c : be->arena) (void)hipFree(c.base);
@@ -606,6 +760,11 @@ void qhip_backend_free_scratch(qhip_backend* be) {
     be->placed -= b.second;
   }
   be->bufs.clear();
+  for (auto& b : be->retired) {
+    (void)hipFree(b.first);
+    be->placed -= b.second;
+  }
+  be->retired.clear();
 }
 
 int qhip_backend_alloc_buf(qhip_backend* be, size_t len, float** d_out) {
@@ -621,9 +780,13 @@ int qhip_backend_alloc_buf(qhip_backend* be, size_t len, float** d_out) {
   return 0;
 }
 
+static double weight_bytes(const qhip_linear* w) { return (double)w->rows * (double)w->row_bytes; }
+
 int qhip_backend_matvec(qhip_backend* be, float* d_out, const qhip_linear* w, const float* d_x) {
   if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
-  return run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_x, 1);
+  ProfScope ps(be);
+  const int rc = run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_x, 1);
+  return ps.finish(rc, 0, w->ttype, w->rows, w->cols, 1, weight_bytes(w));
 }
 
 int qhip_backend_matvec_pair(qhip_backend* be, float* d_out, const qhip_linear* a,
@@ -632,24 +795,120 @@ int qhip_backend_matvec_pair(qhip_backend* be, float* d_out, const qhip_linear* 
   const bool alike = a->ttype == b->ttype && a->rows == b->rows && a->cols == b->cols;
   const bool adjacent =
       alike && (const uint8_t*)a->dev + (size_t)a->rows * a->row_bytes == (const uint8_t*)b->dev;
-  if (adjacent)
-    return run(be, d_out, a->dev, a->ttype, 2 * a->rows, a->cols, a->row_bytes, d_x, 1);
-  int rc = run(be, d_out, a->dev, a->ttype, a->rows, a->cols, a->row_bytes, d_x, 1);
-  if (rc) return rc;
-  return run(be, d_out + a->rows, b->dev, b->ttype, b->rows, b->cols, b->row_bytes, d_x, 1);
+  ProfScope ps(be);
+  int rc;
+  if (adjacent) {
+    rc = run(be, d_out, a->dev, a->ttype, 2 * a->rows, a->cols, a->row_bytes, d_x, 1);
+  } else {
+    rc = run(be, d_out, a->dev, a->ttype, a->rows, a->cols, a->row_bytes, d_x, 1);
+    if (rc == 0) rc = run(be, d_out + a->rows, b->dev, b->ttype, b->rows, b->cols, b->row_bytes, d_x, 1);
+  }
+  return ps.finish(rc, 1, a->ttype, a->rows + b->rows, a->cols, 1, weight_bytes(a) + weight_bytes(b));
 }
 
 int qhip_backend_matvec_batch_k(qhip_backend* be, float* d_out, const qhip_linear* w,
                                 const float* d_xK, int k) {
   if (!be || !valid_linear(w)) return (int)hipErrorInvalidValue;
-  return run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_xK, k);
+  ProfScope ps(be);
+  const int rc = run(be, d_out, w->dev, w->ttype, w->rows, w->cols, w->row_bytes, d_xK, k);
+  return ps.finish(rc, 2, w->ttype, w->rows, w->cols, k, weight_bytes(w));
 }
 
 int qhip_backend_dequant_row(qhip_backend* be, float* d_dst, const qhip_linear* w, int row) {
   if (!be || !valid_linear(w) || !d_dst || row < 0 || row >= w->rows) return (int)hipErrorInvalidValue;
-  return report("dequantRow", (hipError_t)qhip_launch_dequantize_row(
-                                  w->ttype, (const uint8_t*)w->dev + (size_t)row * w->row_bytes, d_dst,
-                                  w->cols, be->stream));
+  ProfScope ps(be);
+  const int rc = report("dequantRow", (hipError_t)qhip_launch_dequantize_row(
+                                          w->ttype, (const uint8_t*)w->dev + (size_t)row * w->row_bytes, d_dst,
+                                          w->cols, be->stream));
+  return ps.finish(rc, 3, w->ttype, 1, w->cols, 1, (double)w->row_bytes);
+}
+
+int qhip_backend_set_profiling(qhip_backend* be, int on) {
+  if (!be) return (int)hipErrorInvalidValue;
+  be->prof_on = on != 0;
+  return 0;
+}
+
+void qhip_backend_prof_reset(qhip_backend* be) {
+  if (!be) return;
+  prof_resolve(be, 0);
+  be->prof.clear();
+  be->prof_untimed = 0;
+}
+
+// The table, largest device time first.
+static std::vector<std::pair<qhip_backend::ProfKey, qhip_backend::ProfStat>> prof_sorted(qhip_backend* be) {
+  prof_resolve(be, 0);
+  std::vector<std::pair<qhip_backend::ProfKey, qhip_backend::ProfStat>> v(be->prof.begin(), be->prof.end());
+  std::stable_sort(v.begin(), v.end(), [](const auto& x, const auto& y) { return x.second.us > y.second.us; });
+  return v;
+}
+
+int qhip_backend_prof_entries(qhip_backend* be, qhip_prof_entry* out, int max_entries) {
+  if (!be || max_entries < 0 || (max_entries > 0 && !out)) return (int)hipErrorInvalidValue;
+  const auto v = prof_sorted(be);
+  const int n = (int)v.size() < max_entries ? (int)v.size() : max_entries;
+  for (int i = 0; i < n; ++i) {
+    const auto& k = v[(size_t)i].first;
+    const auto& st = v[(size_t)i].second;
+    out[i] = qhip_prof_entry{k.slot, k.ttype, k.rows, k.cols, k.tokens, st.calls, st.us, st.bytes, st.ops};
+  }
+  return (int)v.size();
+}
+
+long long qhip_backend_prof_untimed(const qhip_backend* be) { return be ? be->prof_untimed : 0; }
+
+long qhip_backend_prof_report(qhip_backend* be, char* buf, long len) {
+  if (!be || len < 0 || (len > 0 && !buf)) return -1;
+  const auto v = prof_sorted(be);
+  std::string t;
+  char line[320];
+  double us = 0.0;
+  long long calls = 0;
+  for (const auto& e : v) {
+    us += e.second.us;
+    calls += e.second.calls;
+  }
+  snprintf(line, sizeof line, "HIP-PROF %s slots=%zu calls=%lld device_ms=%.3f untimed_under_capture=%lld\n",
+           be->name, v.size(), calls, us / 1e3, be->prof_untimed);
+  t += line;
+  for (const auto& e : v) {
+    const auto& k = e.first;
+    const auto& st = e.second;
+    const double avg = st.calls ? st.us / (double)st.calls : 0.0;
+    const double gbs = st.us > 0 ? st.bytes / (st.us * 1e3) : 0.0;
+    const double tops = st.us > 0 ? st.ops / (st.us * 1e6) : 0.0;
+    snprintf(line, sizeof line,
+             "HIP-PROF %-12s %-7s rows=%-7d cols=%-6d k=%-5d calls=%-7lld total_us=%-11.1f avg_us=%-9.2f "
+             "GB/s=%-7.0f hbm=%4.1f%% TOP/s=%.1f\n",
+             kSlotNames[k.slot], type_name(k.ttype), k.rows, k.cols, k.tokens, st.calls, st.us, avg, gbs,
+             100.0 * gbs / 8000.0, tops);
+    t += line;
+  }
+  if (len > 0) {
+    const size_t n = t.size() < (size_t)len - 1 ? t.size() : (size_t)len - 1;
+    memcpy(buf, t.data(), n);
+    buf[n] = 0;
+  }
+  return (long)t.size();
+}
+
+const char* qhip_backend_describe(qhip_backend* be) {
+  if (!be) return "";
+  size_t weights = 0, gemv_img = 0, mmq_img = 0;
+  for (const auto& c : be->arena) weights += c.used;
+  for (const auto& c : be->img_arena) gemv_img += c.used;
+  for (const auto& kv : be->images) mmq_img += kv.second.bytes;
+  const size_t scratch = be->act_cap + be->skwork_cap;
+  char budget[48] = "no cap";
+  if (be->budget) snprintf(budget, sizeof budget, "%zu MiB", be->budget >> 20);
+  snprintf(be->desc, sizeof be->desc,
+           "%s, %d CUs; weights %zu MiB, GEMV images %zu MiB, MMQ images %zu MiB, scratch %zu MiB, "
+           "placed %zu MiB (budget %s); GEMV images %s, MMQ images %s, activation memo %s, profiling %s",
+           be->name, qhip_gpu_cu_count(), weights >> 20, gemv_img >> 20, mmq_img >> 20, scratch >> 20,
+           be->placed >> 20, budget, be->gemv_images_on ? "on" : "off", be->images_on ? "on" : "off",
+           be->memo_on ? "on" : "off", be->prof_on ? "on" : "off");
+  return be->desc;
 }
 
 int qhip_backend_set_stream(qhip_backend* be, void* stream) {

@@ -2320,6 +2320,10 @@ __device__ __forceinline__ void bg_sync() {
   asm volatile("" ::: "memory");
 }
 
+// Vector loads a wave of k_mmq_bg_q6k issues after a unit's activation copy:
+// the 8 hi-plane and 8 lo-plane fragments of the next unit and its row scale.
+constexpr int kBgLoadsAfterCopy = 2 * 8 + 1;
+
 template <int NA>
 __global__ __launch_bounds__(256, 2) void k_mmq_bg_q6k(const uint8_t* __restrict__ IMG, const uint8_t* __restrict__ XQ,
                                                         float* __restrict__ Y, int rows, int tokens, long act_bytes,
@@ -2429,6 +2433,9 @@ __global__ __launch_bounds__(256, 2) void k_mmq_bg_q6k(const uint8_t* __restrict
     const U nu = more ? advance(cu) : cu;  // the last unit re-reads its own operands
     const uint8_t* A = &act[k & 1][0];
     issue_act(nu, &act[(k & 1) ^ 1][0]);
+    // no load of the next unit's weights may be issued ahead of the copy:
+    // the barrier below counts them as the last kBgLoadsAfterCopy loads
+    asm volatile("" ::: "memory");
     const uint8_t* nb = wgrp(nu);
     i32x16 is[NA];
 #pragma unroll
@@ -2513,8 +2520,9 @@ __global__ __launch_bounds__(256, 2) void k_mmq_bg_q6k(const uint8_t* __restrict
         for (int e = 0; e < 16; ++e) acc[a][e] = 0.0f;
     }
     // unit k+1's activations are in LDS once this wave's copy has landed;
-    // the 17 weight loads issued after it may stay in flight
-    bg_sync<17>();
+    // the weight loads issued after it (8 hi-plane and 8 lo-plane fragments,
+    // the row scale) may stay in flight
+    bg_sync<kBgLoadsAfterCopy>();
     if (!more) break;
     cu = nu;
   }

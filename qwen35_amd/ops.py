@@ -9,7 +9,7 @@ import ctypes
 
 import torch
 
-from ._lib import QhipLinear, check, load
+from ._lib import QhipLinear, QhipProfEntry, check, load
 
 _GEOM = {8: (32, 34), 20: (32, 18), 12: (256, 144), 14: (256, 210), 13: (256, 176), 11: (256, 110),
          10: (256, 84), 23: (256, 136), 2: (32, 18), 3: (32, 20), 18: (256, 98), 21: (256, 110)}
@@ -398,3 +398,31 @@ class Backend:
 
     def step_end(self) -> None:
         self.lib.qhip_backend_step_end(self._h)
+
+    def describe(self) -> str:
+        return self.lib.qhip_backend_describe(self._h).decode()
+
+    def set_profiling(self, on: bool) -> None:
+        check("set_profiling", self.lib.qhip_backend_set_profiling(self._h, int(bool(on))))
+
+    def prof_entries(self) -> list[dict]:
+        """The device-time table, largest total first (waits for outstanding timings)."""
+        n = self.lib.qhip_backend_prof_entries(self._h, None, 0)
+        check("prof_entries", 0 if n >= 0 else n)
+        arr = (QhipProfEntry * max(n, 1))()
+        m = self.lib.qhip_backend_prof_entries(self._h, arr, n)
+        assert m == n
+        return [{f: getattr(arr[i], f) for f, _ in QhipProfEntry._fields_} for i in range(n)]
+
+    def prof_report(self) -> str:
+        n = self.lib.qhip_backend_prof_report(self._h, None, 0)
+        assert n >= 0
+        buf = ctypes.create_string_buffer(n + 1)
+        assert self.lib.qhip_backend_prof_report(self._h, buf, n + 1) == n
+        return buf.value.decode()
+
+    def prof_untimed(self) -> int:
+        return int(self.lib.qhip_backend_prof_untimed(self._h))
+
+    def prof_reset(self) -> None:
+        self.lib.qhip_backend_prof_reset(self._h)

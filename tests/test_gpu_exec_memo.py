@@ -152,6 +152,16 @@ def test_decode_step_in_hip_graph(gpu, oracle, weights):
             step(0)
         be.set_stream(torch.cuda.current_stream())
         torch.cuda.synchronize()
+        # a prefill after the capture grows the activation scratch and the
+        # split-K workspace past what the graph was captured with; the buffers
+        # the graph names must stay valid for its replays
+        placed = be.mem_placed()
+        hk = synth.make_act(9728, 64, seed=500)
+        yk = torch.empty((64, 2560), device=gpu)
+        be.matvec_batch_k(yk, ld, torch.from_numpy(hk).to(gpu), 64)
+        torch.cuda.synchronize()
+        assert be.mem_placed() > placed
+        assert rel_l2(yk.cpu().numpy(), oracle.matvec(po.TT_Q6_K, down, hk)) < TOL
         for rep in range(4):
             x = synth.make_act(COLS, 1, seed=300 + rep)
             h = synth.make_act(9728, 1, seed=400 + rep)

@@ -19,9 +19,10 @@ HEADER = ROOT / "include" / "qwen35_hip.h"
 REF_BACKEND = Path("/root/reference/src/backend.zig")
 
 # the Exec slots of the quantized-matvec path and its support slots
-# (src/backend.zig:110-178, :470-498)
+# (src/backend.zig:110-178, :470-514)
 MATVEC_SLOTS = {"loadLinear", "freeLinear", "matvec", "matvecPair", "matvecBatchK", "dequantRow",
-                "allocScratch", "allocScratchK", "freeScratch", "allocBuf", "stepBegin", "stepEnd", "name"}
+                "allocScratch", "allocScratchK", "freeScratch", "allocBuf", "stepBegin", "stepEnd", "name",
+                "describe", "reportProfile", "profReport"}
 
 # Zig parameter / return type -> the C type it must be
 ZIG_TO_C = {"c_int": "int", "c_long": "long", "c_uint": "unsigned", "usize": "size_t", "void": "void",

@@ -79,3 +79,38 @@ def test_noalloc_rejects_shapes_beyond_its_array(gpu):
     # validation applies as in the workspace entry point: a NULL weight)
     assert L.qhip_launch_quantize_mul_mat_vec_split_noalloc(None, p, None, p, 5120, 17408, po.TT_Q6_K, 0, 0, 0,
                                                             None) == INVALID
+
+
+def test_noalloc_replays_from_a_captured_graph(gpu, oracle):
+    """The callers this entry point is for capture it: a graph holding one
+    launch, replayed with new activations copied in between replays, gives
+    on every replay the bits of the workspace entry point run eagerly on the
+    same input (the shared array's counters are zero again after each
+    replay)."""
+    tt, rows, cols = po.TT_Q6_K, 2560, 9728
+    w = synth.make_weight(tt, rows, cols, seed=4, tag=tt)
+    wd = torch.from_numpy(w).to(gpu)
+    xd = torch.zeros(cols, device=gpu)
+    out = torch.empty(rows, device=gpu)
+    xq = torch.zeros(ops.act_row_bytes(tt, cols), dtype=torch.uint8, device=gpu)
+    ops.quantize_mul_mat_vec_split_noalloc(tt, wd, xd, rows, cols, xq_out=xq, out=out)
+    torch.cuda.synchronize()
+    print(f"no-alloc split-K {po.NAMES[tt]} [{rows}x{cols}] under graph capture", flush=True)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.quantize_mul_mat_vec_split_noalloc(tt, wd, xd, rows, cols, xq_out=xq, out=out)
+    torch.cuda.synchronize()
+    work = ops.split_work(rows, cols, gpu)
+    for rep in range(3):
+        x = synth.make_act(cols, 1, seed=700 + rep)
+        xd.copy_(torch.from_numpy(x[0]))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy()
+        want = ops.quantize_mul_mat_vec_split(tt, wd, xd, rows, cols, work).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+        assert np.array_equal(xq.cpu().numpy(), oracle.quantize_act(tt, x)[0]), rep
+        assert rel_l2(got, oracle.matvec(tt, w, x)[0]) < TOL, rep
+    del g
+    torch.cuda.synchronize()
