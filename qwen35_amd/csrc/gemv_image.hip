@@ -87,8 +87,7 @@ __device__ __forceinline__ int img_block(const u32x4 (&q)[img_qs<TT>()], const u
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if constexpr (TT == TT_IQ4_NL) {
-      s = dot4(iq4_lo(qq[i]), ya[i], s);
-      s = dot4(iq4_hi(qq[i]), yb[i], s);
+      s = iq4_dot8(qq[i], ya[i], yb[i], s);
     } else if constexpr (TT == TT_Q4_0) {
       s = dot4(nib_minus8(qq[i] & 0x0F0F0F0Fu), ya[i], s);
       s = dot4(nib_minus8((qq[i] >> 4) & 0x0F0F0F0Fu), yb[i], s);
