@@ -50,7 +50,8 @@ R3, C3 = 248320, 2560        # config 3 (output head)
 PROFILE_KERNELS = ["cfg3_gemv", "cfg3_step", "cfg3_gemv_gguf", "cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv",
                    "down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused",
                    "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
-                   "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8"]
+                   "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8", "mmq_cfg4_frag",
+                   "mmq_cfg4_ragged_frag"]
 
 
 def log(*a):
@@ -671,9 +672,20 @@ def profile(c: Ctx, which: str, launches: int):
                              "mmq_cfg5_q2k": (10, 17408, 5120, 512), "mmq_cfg5_q6k_image": (TQ6, 5120, 17408, 512),
                              "mmq_cfg4": (TQ8, 3584, 1024, 512), "mmq_cfg5_q4k_frag": (TQ4, 17408, 5120, 512),
                              "mmq_cfg5_q4k_frag_t8": (TQ4, 17408, 5120, 8),
-                             "mmq_cfg5_q6k_frag_t8": (TQ6, 5120, 17408, 8)}[which]
+                             "mmq_cfg5_q6k_frag_t8": (TQ6, 5120, 17408, 8),
+                             "mmq_cfg4_frag": (TQ8, 3584, 1024, 512),
+                             "mmq_cfg4_ragged_frag": (TQ8, 3584, 1024, 0)}[which]
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
-        aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
+        if which == "mmq_cfg4_ragged_frag":
+            # the eight ragged sequences of bench_mmq, packed by the ragged quantizer
+            lens = [int(v) for v in synth.ragged_lengths(8, 16, 256, seed=0)]
+            seqs = [torch.from_numpy(synth.make_act(cols, n, seed=0, tag=300 + i)).to(dev) for i, n in enumerate(lens)]
+            aq, off_d, T = ops.quantize_ragged(tt, seqs, cols)
+            keep += seqs + [off_d]
+        elif which == "mmq_cfg4_frag":
+            aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=400)).to(dev))
+        else:
+            aq = ops.quantize_act(tt, torch.from_numpy(synth.make_act(cols, T, seed=0, tag=500 + T)).to(dev))
         y = torch.empty((T, rows), device=dev)
         # the split-K workspace the Exec mirror passes
         wk = ops.mul_mat_work(rows, cols, T, tt, dev)
@@ -686,6 +698,14 @@ def profile(c: Ctx, which: str, launches: int):
             def fn(i):
                 assert lib.qhip_launch_mul_mat_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T, tt,
                                                      0, 0, wp, wn, stream) == 0
+        elif which.startswith("mmq_cfg4_"):
+            # the Q8_0 fragment image the Exec mirror reads for K <= 1024 (no workspace)
+            img = ops.wd_image(tt, w, rows, cols)
+            keep.append(img)
+
+            def fn(i):
+                assert lib.qhip_launch_mul_mat_wd_image(img.data_ptr(), aq.data_ptr(), y.data_ptr(), rows, cols, T,
+                                                        tt, None, 0, stream) == 0
         elif "_frag" in which:
             # the fragment image the Exec mirror reads
             img = ops.wd_image(tt, w, rows, cols)

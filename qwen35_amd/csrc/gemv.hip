@@ -100,9 +100,9 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
 // matrices with few long rows (the FFN down projection): the rows' units are
 // split over the team's waves, so NR rows can share each activation load
 // without cutting the number of waves in flight.  Wave s of a team walks
-// units lane + 64s, stepping 64*WV; each wave folds its lanes with the
-// shuffle tree, then the team's waves are added in wave order through LDS
-// (deterministic).
+// units lane + 64s, stepping 64*WV; each wave folds its lanes by DPP
+// (wave_sum_to_lane63), then the team's waves are added in wave order
+// through LDS (deterministic).
 template <int TT, int NR, int WV, bool IMG = false>
 __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
                                                   const uint8_t* __restrict__ XQ,
@@ -135,10 +135,8 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
     for (int k = 0; k < NR; ++k) acc[k] += U::dot(w[k], a);
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-    for (int k = 0; k < NR; ++k) acc[k] += __shfl_down(acc[k], off, 64);
-  if (lane == 0) {
+  for (int k = 0; k < NR; ++k) acc[k] = wave_sum_to_lane63(acc[k]);
+  if (lane == 63) {
 #pragma unroll
     for (int k = 0; k < NR; ++k) part[wv][k] = acc[k];
   }

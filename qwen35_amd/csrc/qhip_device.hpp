@@ -155,6 +155,28 @@ __device__ __forceinline__ uint32_t quant_q8_K_lane(const float* v, int& gsum, f
   return packed;
 }
 
+// ---- wave reductions --------------------------------------------------------------
+// Sum of v over the 64 lanes of a wave, in lane 63, by DPP (VALU lane moves:
+// a few cycles each, against an LDS round trip per step for ds_bpermute).
+// Adjacent lanes and lane pairs within quads (quad_perm), then the mirrored
+// half-rows and rows give every lane of a 16-lane row the row's sum;
+// row_bcast:15 adds row 0's sum into row 1 and row 2's into row 3,
+// row_bcast:31 then adds rows 0 + 1 into rows 2 and 3.  The order of the
+// additions is fixed, so the result is deterministic.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_to_lane63(float v) {
+  v += dpp_f32<0xB1>(v);         // quad_perm [1, 0, 3, 2]
+  v += dpp_f32<0x4E>(v);         // quad_perm [2, 3, 0, 1]
+  v += dpp_f32<0x141>(v);        // row_half_mirror
+  v += dpp_f32<0x140>(v);        // row_mirror
+  v += dpp_f32<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+  v += dpp_f32<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // ---- IQ4_NL codebook lookup on 4 packed indices --------------------------------
 // Codebook (reference src/iq_tables.zig:429-432):
 //   -127 -104 -83 -65 -49 -35 -22 -10 1 13 25 38 53 69 89 113
