@@ -929,30 +929,34 @@ static int mmq_ksplit_for(const GemvArgs& g, int bt, int br, int nchunks, int mi
 
 // Slices for a launch of `tiles` tiles of a kernel that holds two workgroups
 // per CU (the weights-direct and image MMQs: their registers allow two waves
-// per SIMD): the smallest count of 1..4 whose grid fills its rounds of
-// resident workgroups at least 80%, else the fullest.  A grid of 1.25 rounds
-// spends a whole round at a quarter of the GPU; cutting K evens the rounds at
-// the price of the partial tiles.  Measured on MI355X (config 5, Q6_K image /
-// Q4_K weights-direct, us at 1 / 2 / 3 / 4 slices): T = 128 106 / 66 / 49 / 66
-// and 57 / 54 / 46 / 50; T = 256 121 / 115 / 92 / 101 and 92 / 84 / 78 / 84;
-// T = 384 128 / 131 / 136 / 141 and 110 / 114 / 113 / 120; T = 512 210 / 176
-// / 180 / 188 and 144 / 147 / 152 / 162; T = 1024 334 / 349 / 372 / 385 and
-// 256 / 294 / 310 / 346 -- the rule picks the best count at all but Q4_K
-// T = 512 (147 against 144 us).
+// per SIMD).  A grid of 1.25 rounds of resident workgroups spends a whole
+// round at a quarter of the GPU; cutting K evens the rounds at the price of
+// the partial tiles' traffic.  Below one round: the smallest count of 1..4
+// whose grid fills its rounds at least 80%, else the fullest.  From one to
+// two rounds: the count with the best fill less 0.06 per extra slice.  Two
+// rounds or more: unsplit.  Measured on MI355X (config 5 Q4_K
+// weights-direct, us at 1 / 2 / 3 / 4 slices): T = 128 57 / 54 / 46 / 50;
+// T = 256 92 / 84 / 78 / 84; T = 384 110 / 114 / 113 / 120; T = 512 144 /
+// 147 / 152 / 162 (two slices also tripled the launch's HBM writes); T =
+// 1024 256 / 294 / 310 / 346 -- the rule picks the fastest count at each
+// (3, 3, 1, 1, 1).
 extern "C" int qhip_gpu_cu_count(void);
 static int mmq_round_slices(long tiles, int nchunks, int min_chunks) {
   if (tiles > kSkMaxTiles) return 1;
   const int cus = qhip_gpu_cu_count();
   const long cap = 2L * (cus > 0 ? cus : 256);
+  if (tiles >= 2 * cap) return 1;
+  const double penalty = tiles >= cap ? 0.06 : 0.0;
   int best = 1;
-  double best_u = 0.0;
+  double best_s = -1.0;
   for (int ks = 1; ks <= 4; ++ks) {
     if (ks > 1 && nchunks / ks < min_chunks) break;
     const long w = tiles * ks, rounds = (w + cap - 1) / cap;
-    const double u = (double)w / (double)(rounds * cap);
-    if (u >= 0.8) return ks;
-    if (u > best_u) {
-      best_u = u;
+    const double fill = (double)w / (double)(rounds * cap);
+    if (penalty == 0.0 && fill >= 0.8) return ks;
+    const double score = fill - penalty * (ks - 1);
+    if (score > best_s) {
+      best_s = score;
       best = ks;
     }
   }

@@ -166,14 +166,16 @@ def test_split_workspace_size(lib):
 
 
 def test_mmq_split_workspace_size(lib):
-    # cfg5 at 16 tokens splits K (a few hundred row tiles); at 512 tokens the
-    # 1088 weights-direct tiles fill 2.1 rounds of 512 resident workgroups, so
-    # K is cut in two (2176 over 5 rounds: 85% full); 1024 tokens (2176 tiles)
-    # is not split; a GEMV-only or unknown type has no workspace
+    # cfg5 at 16 tokens splits K (a few hundred row tiles); at 256 tokens the
+    # 544 weights-direct tiles are cut in three (1632 over 4 rounds of 512
+    # resident workgroups: 80% full); at 512 and 1024 tokens (1088 / 2176
+    # tiles, two rounds or more) K is not split; a GEMV-only or unknown type
+    # has no workspace
     n = lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 12)
     assert n > 32768 and n % 4 == 0
     assert lib.qhip_mul_mat_work_bytes(5120, 17408, 16, 14) > 32768
-    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 32768 + 4 * 2 * 1088 * 64 * 128
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 256, 12) == 32768 + 4 * 3 * 544 * 64 * 128
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 0
     assert lib.qhip_mul_mat_work_bytes(17408, 5120, 1024, 12) == 0
     assert lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 99) == 0
     assert lib.qhip_mul_mat_work_bytes(0, 5120, 16, 12) == 0
