@@ -647,6 +647,121 @@ def cpu_baseline(c: Ctx, cfg3: Cfg3, cfg2: Cfg2 | None, budget_s: float, all_con
     return res
 
 
+# ---- the engine binding's buffers ---------------------------------------------------------
+
+class HostMapped:
+    """Pinned host memory mapped into the GPU (hipHostMalloc, mapped + coherent), as
+    integration/backend_hip.zig allocates its Buf regions; dev is the device-side
+    address from hipHostGetDevicePointer."""
+
+    def __init__(self, nbytes: int):
+        # the runtime torch and libqwen35_hip.so already share (same soname)
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+        self.hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_uint]
+        self.hip.hipHostFree.argtypes = [ctypes.c_void_p]
+        self.host = ctypes.c_void_p(0)
+        rc = self.hip.hipHostMalloc(ctypes.byref(self.host), nbytes, 0x2 | 0x40000000)
+        if rc != 0 or not self.host.value:
+            raise RuntimeError(f"hipHostMalloc({nbytes}) failed: {rc}")
+        self.dev = ctypes.c_void_p(0)
+        rc = self.hip.hipHostGetDevicePointer(ctypes.byref(self.dev), self.host, 0)
+        if rc != 0 or not self.dev.value:
+            self.hip.hipHostFree(self.host)
+            raise RuntimeError(f"hipHostGetDevicePointer failed: {rc}")
+        self.nbytes = nbytes
+
+    def numpy_f32(self, n: int):
+        import numpy as np
+        return np.ctypeslib.as_array((ctypes.c_float * n).from_address(self.host.value))
+
+    def free(self):
+        if self.host.value:
+            self.hip.hipHostFree(self.host)
+            self.host = ctypes.c_void_p(0)
+
+
+def bench_binding(c: Ctx, c3: Cfg3, with_prefill: bool, iters: int = 200):
+    """The matvec slot as integration/backend_hip.zig calls it: x and out in
+    host-mapped Buf regions (the CPU slots around it read and write them), and
+    a host wait after the launch.  Against the same slot on device buffers
+    with the same wait, and with neither (the headline step).  Wall clock per
+    slot call; host-side rates, never the headline value."""
+    torch, lib = c.torch, c.lib
+
+    def wall(fn, n):
+        for _ in range(10):
+            fn()
+        t = time.perf_counter()
+        for _ in range(n):
+            fn()
+        return (time.perf_counter() - t) / n
+
+    xh, yh = HostMapped(4 * C3), HostMapped(4 * R3)
+    try:
+        xh.numpy_f32(C3)[:] = c3.x[0]
+        lin = c3._lin
+
+        def slot(out_p, x_p):
+            def f():
+                assert lib.qhip_backend_matvec(c3.be._h, out_p, lin, x_p) == 0
+                assert lib.qhip_backend_sync(c3.be._h) == 0
+            return f
+
+        dev_s = wall(slot(c3._p[0], c3._p[1]), iters)
+        host_s = wall(slot(yh.dev, xh.dev), iters)
+        want = c3.y.cpu().numpy()
+        got = yh.numpy_f32(R3)
+        same = bool((got == want).all())
+        res = {"cfg3_slot_us_device_bufs_with_wait": round(dev_s * 1e6, 2),
+               "cfg3_slot_us_host_mapped_with_wait": round(host_s * 1e6, 2),
+               "cfg3_host_mapped_gb_s": round(c3.alg / host_s / 1e9, 1),
+               "host_mapped_output_equals_device_output": same,
+               "note": "x (10 KB) is read and y (0.99 MB) written through the PCIe mapping; each slot waits "
+                       "for its launch, as the binding's slots do"}
+        log(f"binding: cfg3 slot {dev_s * 1e6:.1f} us on device buffers, {host_s * 1e6:.1f} us on host-mapped "
+            f"x/out (both with the per-slot wait); outputs equal: {same}")
+    finally:
+        xh.free()
+        yh.free()
+    if not with_prefill:
+        return res
+    # a config-5 prefill slot: matvecBatchK of 512 tokens on the Q4_K gate
+    # weight, 10.5 MB of x read and 35.7 MB of out written through the mapping
+    T, rows, cols = 512, 17408, 5120
+    be = c.ops.Backend(0)
+    xh, yh = HostMapped(4 * T * cols), HostMapped(4 * T * rows)
+    try:
+        lin = be.load_linear(TQ4, rows, cols, c.synth.make_weight(TQ4, rows, cols, seed=0, tag=TQ4))
+        be.prepare_linear(lin)
+        x = c.synth.make_act(cols, T, seed=0, tag=500 + T)
+        xh.numpy_f32(T * cols)[:] = x.reshape(-1)
+        xd = torch.from_numpy(x).to(c.dev)
+        yd = torch.empty((T, rows), device=c.dev)
+        lp = ctypes.byref(lin)
+
+        def bslot(out_p, x_p):
+            def f():
+                assert lib.qhip_backend_matvec_batch_k(be._h, out_p, lp, x_p, T) == 0
+                assert lib.qhip_backend_sync(be._h) == 0
+            return f
+
+        bd = wall(bslot(ctypes.c_void_p(yd.data_ptr()), ctypes.c_void_p(xd.data_ptr())), 30)
+        bh = wall(bslot(yh.dev, xh.dev), 30)
+        same = bool((yh.numpy_f32(T * rows) == yd.cpu().numpy().reshape(-1)).all())
+        res.update({"cfg5_q4k_t512_batch_us_device_bufs_with_wait": round(bd * 1e6, 2),
+                    "cfg5_q4k_t512_batch_us_host_mapped_with_wait": round(bh * 1e6, 2),
+                    "cfg5_host_mapped_output_equals_device_output": same})
+        log(f"binding: cfg5 Q4_K matvecBatchK 512 tokens {bd * 1e6:.1f} us on device buffers, {bh * 1e6:.1f} us on "
+            f"host-mapped x/out; outputs equal: {same}")
+        be.free_linear(lin)
+    finally:
+        be.close()
+        xh.free()
+        yh.free()
+    return res
+
+
 # ---- profiling entry: one kernel only ---------------------------------------------------
 
 def profile(c: Ctx, which: str, launches: int):
@@ -785,6 +900,7 @@ def main() -> int:
         f"GGUF-layout GEMV {gg_sec * 1e6:.2f} us")
     latency = {"cfg3_step_single_us": round(single_latency(torch, c3.step) * 1e6, 2),
                "cfg3_gemv_single_launch_us": round(single_latency(torch, c3.gemv) * 1e6, 2)}
+    binding = bench_binding(c, c3, not args.no_extra)
 
     cfg2 = extra = mmq = None
     c2 = None
@@ -813,6 +929,7 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "latency": latency,
+        "binding": binding,
         "cfg2_step": cfg2,
         "configs": extra,
         "mmq": mmq,
