@@ -103,7 +103,8 @@ __device__ __forceinline__ int img_block(const u32x4 (&q)[img_qs<TT>()], const u
 
 // A team of T lanes owns NR consecutive rows (64 / T teams per wave).  The
 // passes are unrolled, so the compiler issues a pass's loads ahead of the
-// previous pass's arithmetic.
+// previous pass's arithmetic.  The activation is read from an LDS copy made
+// once per workgroup.
 template <int TT, int T, int P, int NR>
 __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XA,
                                                    float* __restrict__ Y, int rows, long row_bytes) {
@@ -115,13 +116,21 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
   float acc[NR];
 #pragma unroll
   for (int k = 0; k < NR; ++k) acc[k] = 0.0f;
+  // the split activation (72 U bytes) once per workgroup into LDS: its
+  // 16-byte pieces are read by every team of the workgroup, so through the
+  // texture path they cost as much as the weights (IQ4_NL [248320, 2560]
+  // 58.5 against 59.1 us, [32768, 2560] 11.0 against 11.4; Q8_0 [17408,
+  // 5120] 17.2 against 18.4; the same bits)
+  __shared__ __attribute__((aligned(16))) uint8_t xs[72 * U];
+  for (int i = threadIdx.x; i < 72 * U / 16; i += 256) *(u32x4*)(xs + 16 * i) = ld128(XA + 16 * i);
+  __syncthreads();
   if (active) {
     const uint8_t* wr[NR];
 #pragma unroll
     for (int k = 0; k < NR; ++k) wr[k] = W + (row0 + k < rows ? row0 + k : rows - 1) * row_bytes;
     float2 ad[P];
 #pragma unroll
-    for (int p = 0; p < P; ++p) ad[p] = *(const float2*)(XA + 64 * U + 8 * (j * P + p));
+    for (int p = 0; p < P; ++p) ad[p] = *(const float2*)(xs + 64 * U + 8 * (j * P + p));
     uint32_t ws[NR][P];
 #pragma unroll
     for (int k = 0; k < NR; ++k)
@@ -140,7 +149,7 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
 #pragma unroll
       for (int e = 0; e < 2; ++e)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) y[e][h] = ld128(XA + (((2 * p + e) * 2 + h) * T + j) * 16);
+        for (int h = 0; h < 2; ++h) y[e][h] = *(const u32x4*)(xs + (((2 * p + e) * 2 + h) * T + j) * 16);
 #pragma unroll
       for (int k = 0; k < NR; ++k) {
         const int s0 = img_block<TT>(q[k][0], y[0][0], y[0][1]);
