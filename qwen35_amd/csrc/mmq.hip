@@ -1306,15 +1306,20 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
 // two sub-blocks (low / high nibbles), scaled by the split sub-block scale as
 // in k_mmq.  The workgroup's BT = 32 NA tokens of Q8_K activation are copied
 // into LDS by global_load_lds (DMA, no registers), double-buffered: chunk c+1
-// (one super-block) lands while chunk c is multiplied.  LDS token row: qs[256]
-// | bsums[16] | d, 304 bytes, so 16-byte fragment reads of 32 consecutive
-// tokens fall 12 banks apart (conflict-free).  K may be cut into ksplit slices
-// of cps super-blocks (small grids: few tokens), the partial tiles added in
-// slice order by the tile's last workgroup (mmq_write_tile).  Measured on
-// MI355X, config 5 Q4_K [17408, 5120]: T = 512 146-150 us against 184 us for
-// the 64 x 64 tile kernel in the same harness, T = 128 56 against 62 us;
-// with the split, T = 8 / 16 / 32 / 64 20.3 / 20.8 / 21.6 / 32.3 us against
-// 24.1 / 24.1 / 24.2 / 32.5 for the tile kernel's split launch.
+// (one super-block) lands while chunk c is multiplied; the weights run two
+// super-blocks ahead in two register sets.  The two stages are two LDS
+// variables: the compiler's wait insertion then knows that the copy into one
+// does not alias the reads of the other, where with one array it made every
+// read wait for the copy just issued (vmcnt(0) at the top of each
+// super-block).  LDS token row: qs[256] | bsums[16] | d, 304 bytes, so
+// 16-byte fragment reads of 32 consecutive tokens fall 12 banks apart
+// (conflict-free).  K may be cut into ksplit slices of cps super-blocks
+// (small grids: few tokens), the partial tiles added in slice order by the
+// tile's last workgroup (mmq_write_tile).  Measured on MI355X, config 5 Q4_K
+// [17408, 5120] from the fragment image, weights rotated over two copies:
+// T = 32 / 64 / 128 / 256 / 512 / 1024 23.6 / 36.0 / 48.6 / 79.7 / 125.5 /
+// 223.4 us, against 35.2 / 41.4 / 53.2 / 85.5 / 133.2 / 237.9 with one LDS
+// array and one register set (the same bits).
 constexpr int kWdRow = 304, kWdPieces = 19, kWdBR = 128;
 
 // Q4_K fragment image: the GGUF bytes permuted, the same 144 bytes per row and
@@ -1338,6 +1343,23 @@ __device__ __forceinline__ T wd_pinned(T v) {
 }
 #define wd_pin(x) ((x) = wd_pinned(x))
 
+// Vector loads issue_w makes per wave (the row header and four qs pieces).
+constexpr int kWdLoads = 5;
+
+// The workgroup barrier between super-blocks: s_waitcnt vmcnt(N) lgkmcnt(0),
+// then s_barrier.  Vector memory loads (the global_load_lds copies among
+// them) complete in issue order, so vmcnt(N) means everything but this
+// wave's N most recent loads has landed.  The compiler barriers keep memory
+// accesses on their side of the s_barrier.
+template <int N>
+__device__ __forceinline__ void wd_sync() {
+  static_assert(N >= 0 && N < 16, "vmcnt low bits");
+  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4));
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
   return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
 }
@@ -1348,7 +1370,11 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
                                                      long act_bytes, int nsb, int ntile_t, int ksplit, int cps,
                                                      float* __restrict__ part, unsigned* __restrict__ cnt) {
   constexpr int BT = 32 * NA, STAGE = BT * kWdRow, NDMA = (BT * kWdPieces + 255) / 256;
-  __shared__ __attribute__((aligned(16))) uint8_t act[2][STAGE];
+  // two stages as two variables: the copy into one and the reads of the
+  // other are then known not to alias, and the reads need not wait for the
+  // copy in flight (with one array the compiler waits for every copy)
+  __shared__ __attribute__((aligned(16))) uint8_t act0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint8_t act1[STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
   const int G = gridDim.x;
   int g = blockIdx.x;
@@ -1417,29 +1443,40 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
   const i32x16 zero = {};
   const f32x16 fz = {};
 
-  issue_act(sb0, &act[0][0]);
-  issue_w(sb0, wh, wq);
-  wd_pin(wh);
-#pragma unroll
-  for (int c = 0; c < 4; ++c) wd_pin(wq[c]);
+  // Two register sets of weights, each reloaded for super-block sb + 2 as
+  // soon as super-block sb has consumed it: the weight loads run two
+  // super-blocks ahead without register copies.
+  u32x4 whA, wqA[4], whB, wqB[4];
+  issue_act(sb0, act0);
+  issue_w(sb0, whA, wqA);
+  if (sb0 + 1 < sb1) issue_w(sb0 + 1, whB, wqB);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   // one super-block: compute from A while super-block sb + 1 lands in nxt
-  for (int sb = sb0; sb < sb1; ++sb) {
-    const int cur = (sb - sb0) & 1;
-    const uint8_t* A = &act[cur][0];
-    uint8_t* nxt = &act[cur ^ 1][0];
-    u32x4 nh, nq[4];
-    if (sb + 1 < sb1) {
-      issue_act(sb + 1, nxt);
-      issue_w(sb + 1, nh, nq);
-    }
+  auto step = [&](int sb, u32x4& wh, u32x4 (&wq)[4], const uint8_t* A, uint8_t* nxt) {
+    // the copies and loads ahead are issued unconditionally (the last
+    // super-block again past the end), so that the wait counts below hold on
+    // every path
+    issue_act(sb + 1 < sb1 ? sb + 1 : sb, nxt);
+    // the weight loads below stay behind the copy: the barrier at the end
+    // counts them as this wave's last kWdLoads loads
+    asm volatile("" ::: "memory");
+    const int sbw = sb + 2 < sb1 ? sb + 2 : sb1 - 1;
     __builtin_amdgcn_iglp_opt(0);
     // 6-bit scales and mins of this lane's row (kernels256.c:105-125)
     const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
     const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
     const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
     const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
+    float d = h2f(wh.x), ndm = -h2f(wh.x >> 16);
+    // each register is reloaded after its last use (the values taken from it
+    // are made complete first, and the loads cannot move above the compiler
+    // barrier), so that the load can target the register it replaces: a
+    // loop-carried copy would wait for the load
+    uint32_t scl = sc_lo, mnl = mn_lo, sch = sc_hi, mnh = mn_hi;
+    asm volatile("" : "+v"(scl), "+v"(mnl), "+v"(sch), "+v"(mnh), "+v"(d), "+v"(ndm) : : "memory");
+    const uint8_t* nb = IMG ? wrow + (long)kWdiTile4 * sbw : wrow + 144L * sbw;
+    wh = *(const u32x4*)(IMG ? nb + 4096 + 16 * li : nb);
     i32x16 chi[NA], clo[NA];
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
@@ -1448,13 +1485,21 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint32_t q0 = wq[c].x, q1 = wq[c].y, q2 = wq[c].z, q3 = wq[c].w;
+      uint32_t nib[2][4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t v = w == 0 ? wq[c].x : w == 1 ? wq[c].y : w == 2 ? wq[c].z : wq[c].w;
+        nib[0][w] = v & 0x0F0F0F0Fu;
+        nib[1][w] = (v >> 4) & 0x0F0F0F0Fu;
+      }
+      asm volatile("" : "+v"(nib[0][0]), "+v"(nib[0][1]), "+v"(nib[0][2]), "+v"(nib[0][3]), "+v"(nib[1][0]),
+                   "+v"(nib[1][1]), "+v"(nib[1][2]), "+v"(nib[1][3]) : : "memory");
+      wq[c] = *(const u32x4*)(IMG ? nb + 1024 * c + 16 * lane : nb + 16 + 32 * c + 16 * lh);
 #pragma unroll
       for (int hi = 0; hi < 2; ++hi) {
         const int s = 2 * c + hi;
-        const uint32_t n0 = (hi ? q0 >> 4 : q0) & 0x0F0F0F0Fu, n1 = (hi ? q1 >> 4 : q1) & 0x0F0F0F0Fu;
-        const uint32_t n2 = (hi ? q2 >> 4 : q2) & 0x0F0F0F0Fu, n3 = (hi ? q3 >> 4 : q3) & 0x0F0F0F0Fu;
-        const uint32_t sc = ((s < 4 ? sc_lo : sc_hi) >> (8 * (s & 3))) & 63u;
+        const uint32_t n0 = nib[hi][0], n1 = nib[hi][1], n2 = nib[hi][2], n3 = nib[hi][3];
+        const uint32_t sc = ((s < 4 ? scl : sch) >> (8 * (s & 3))) & 63u;
         const u16x2 mh = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
         const u16x2 ml = {(uint16_t)(sc & 7u), (uint16_t)(sc & 7u)};
         const i32x4 bh = {(int)pk_mul_u16(n0, mh), (int)pk_mul_u16(n1, mh), (int)pk_mul_u16(n2, mh),
@@ -1470,7 +1515,7 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
       }
     }
     // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
-    const uint32_t mn = lh ? mn_hi : mn_lo;
+    const uint32_t mn = lh ? mnh : mnl;
     f16x8 bm;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -1478,7 +1523,6 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
       bm[2 * k] = m;
       bm[2 * k + 1] = m;
     }
-    const float d = h2f(wh.x), ndm = -h2f(wh.x >> 16);
 #pragma unroll
     for (int a = 0; a < NA; ++a) {
       const i16x8 bs = *(const i16x8*)(A + (32 * a + li) * kWdRow + 256 + 16 * lh);
@@ -1499,14 +1543,17 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
         acc[a][0][e] = __builtin_fmaf(dy, inner, acc[a][0][e]);
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
-    __syncthreads();
-    if (sb + 1 < sb1) {
-      wh = nh;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) wq[c] = nq[c];
-    }
+    // super-block sb + 1: its copy and (issued a step earlier) its weights
+    // have landed; super-block sb + 2's weights may stay in flight
+    wd_sync<kWdLoads>();
+  };
+  int sb = sb0;
+  for (; sb + 1 < sb1; sb += 2) {
+    step(sb, whA, wqA, act0, act1);
+    step(sb + 1, whB, wqB, act1, act0);
   }
+  if (sb < sb1) step(sb, whA, wqA, act0, act1);
+  __builtin_amdgcn_s_waitcnt(0);  // nothing in flight past the loop
   mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, g, ksplit, ks, part, cnt);
 }
 
