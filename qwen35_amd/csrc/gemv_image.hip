@@ -113,6 +113,12 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
   const int r = lane / T, j = lane - r * T;
   const long row0 = (((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW + r) * NR;
   const bool active = r < TPW && row0 < rows;
+  // 4-bit types at two rows per team load before the barrier on every lane
+  // (below); the lanes past the wave's teams then address its last team's
+  // rows (their loads repeat pieces of the same instruction: no extra
+  // traffic)
+  constexpr bool EARLY = QS == 1 && NR == 2;
+  const long rowa = !EARLY || r < TPW ? row0 : row0 - (long)(r - TPW + 1) * NR;
   float acc[NR];
 #pragma unroll
   for (int k = 0; k < NR; ++k) acc[k] = 0.0f;
@@ -122,29 +128,58 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
   // 58.5 against 59.1 us, [32768, 2560] 11.0 against 11.4; Q8_0 [17408,
   // 5120] 17.2 against 18.4; the same bits)
   __shared__ __attribute__((aligned(16))) uint8_t xs[72 * U];
-  for (int i = threadIdx.x; i < 72 * U / 16; i += 256) *(u32x4*)(xs + 16 * i) = ld128(XA + 16 * i);
-  __syncthreads();
-  if (active) {
-    const uint8_t* wr[NR];
+  // EARLY: every weight load of the lane is issued before the activation
+  // copy (unconditionally: a lane past the teams or the rows reads a valid
+  // row and discards it), so that all of a wave's pieces are in flight at
+  // once from the start (IQ4_NL [248320, 2560] 58.4 against 58.8-59.6 us,
+  // [32768, 2560] 10.9 against 11.3, the same bits).  One row per team
+  // ([17408, 5120]: 11.85 against 11.72 us) and Q8_0, with twice the pieces
+  // ([17408, 5120]: 18.5 against 17.2 us), load pass by pass after the
+  // barrier.
+  const uint8_t* wr[NR];
 #pragma unroll
-    for (int k = 0; k < NR; ++k) wr[k] = W + (row0 + k < rows ? row0 + k : rows - 1) * row_bytes;
-    float2 ad[P];
-#pragma unroll
-    for (int p = 0; p < P; ++p) ad[p] = *(const float2*)(xs + 64 * U + 8 * (j * P + p));
-    uint32_t ws[NR][P];
+  for (int k = 0; k < NR; ++k) wr[k] = W + (rowa + k < rows ? rowa + k : rows - 1) * row_bytes;
+  uint32_t ws[NR][P];
+  u32x4 qa[EARLY ? P : 1][NR][2][QS];
+  auto load_ws = [&]() {
 #pragma unroll
     for (int k = 0; k < NR; ++k)
 #pragma unroll
       for (int p = 0; p < P; ++p) ws[k][p] = ld32(wr[k] + 32 * QS * U + 4 * (j * P + p));
+  };
+  auto load_pass = [&](int p, u32x4 (&q)[NR][2][QS]) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int h = 0; h < QS; ++h) q[k][e][h] = ld128(wr[k] + (((2 * p + e) * QS + h) * T + j) * 16);
+  };
+  if constexpr (EARLY) {
+    load_ws();
+#pragma unroll
+    for (int p = 0; p < P; ++p) load_pass(p, qa[p]);
+  }
+  for (int i = threadIdx.x; i < 72 * U / 16; i += 256) *(u32x4*)(xs + 16 * i) = ld128(XA + 16 * i);
+  __syncthreads();
+  if (active) {
+    if constexpr (!EARLY) load_ws();
+    float2 ad[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) ad[p] = *(const float2*)(xs + 64 * U + 8 * (j * P + p));
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       u32x4 q[NR][2][QS];
+      if constexpr (EARLY) {
 #pragma unroll
-      for (int k = 0; k < NR; ++k)
+        for (int k = 0; k < NR; ++k)
 #pragma unroll
-        for (int e = 0; e < 2; ++e)
+          for (int e = 0; e < 2; ++e)
 #pragma unroll
-          for (int h = 0; h < QS; ++h) q[k][e][h] = ld128(wr[k] + (((2 * p + e) * QS + h) * T + j) * 16);
+            for (int h = 0; h < QS; ++h) q[k][e][h] = qa[p][k][e][h];
+      } else {
+        load_pass(p, q);
+      }
       u32x4 y[2][2];
 #pragma unroll
       for (int e = 0; e < 2; ++e)

@@ -2269,8 +2269,13 @@ __global__ __launch_bounds__(512, 4) void k_mmq_q8i(const uint8_t* __restrict__ 
 static hipError_t launch_mmq_q8i(const GemvArgs& g, hipStream_t s) {
   const int nb = g.cols / 32;
   const long ntr = (g.rows + 63) / 64;
-  // 64-token tiles where K is one super-chunk (up to 1024 values), else 32
-  const int tk = g.tokens > 32 && nb <= 32 ? 64 : 32;
+  // 64-token tiles where K is one super-chunk (up to 1024 values) and they
+  // still give at least 1.75 workgroups per CU, else 32.  Measured on
+  // MI355X, [3584, 1024]: 64 / 96 / 128 / 256 tokens 5.0 / 5.1 / 5.2 / 7.1 us
+  // with 32-token tiles against 7.0 / 7.1 / 7.1 / 7.7 with 64; 512 tokens
+  // (448 tiles of 64) 11.5 against 12.3; [6144, 1024] x 200 9.9 against 11.1
+  const int cus = qhip_gpu_cu_count() > 0 ? qhip_gpu_cu_count() : 256;
+  const int tk = g.tokens > 32 && nb <= 32 && ntr * ((g.tokens + 63) / 64) * 4 >= 7L * cus ? 64 : 32;
   const long ntt = (g.tokens + tk - 1) / tk;
   const long G = ntr * ntt;
   if (G > 0x7FFFFFFFL || g.act_bytes != 34L * nb) return hipErrorInvalidValue;
