@@ -577,6 +577,12 @@ int qhip_launch_quantize_ragged(int ttype, const float* const* d_src, const int*
   if (ab < 0 || nseq < 0 || total_tokens < 0 || total_tokens > 65535) return (int)hipErrorInvalidValue;
   if (total_tokens == 0) return 0;
   if (nseq == 0 || !d_src || !d_offsets || !d_xq_packed) return (int)hipErrorInvalidValue;
+  // Q8_0: the wide form for large batches when the output allows (rows of
+  // any 4-byte alignment)
+  if (act_elems(ttype) == 32 && quantize_wide_preferred((long)(cols / 32) * total_tokens) &&
+      ((uintptr_t)d_xq_packed & 1u) == 0 && (ab & 1) == 0)
+    return (int)launch_quantize_wide(true, nullptr, d_src, d_offsets, nseq, d_xq_packed, cols / 32, total_tokens,
+                                     cols, ab, S(stream));
   if (act_elems(ttype) == 32) {
     const long nb = cols / 32;
     dim3 grid((unsigned)((nb * 32 + 255) / 256), (unsigned)total_tokens);

@@ -21,6 +21,16 @@ hipError_t launch_quantize_q8_0(const float* x, void* out, long nblocks, int tok
                                 long out_stride, hipStream_t s);
 hipError_t launch_quantize_q8_K(const float* x, void* out, long nblocks, int tokens, long x_stride,
                                 long out_stride, hipStream_t s);
+// The wide quantizers (16-byte aligned f32 rows, x_stride a multiple of 4;
+// Q8_0 output 2-byte aligned, Q8_K 4-byte): q8_0 selects the format.  With
+// src (ragged) token t of the launch is packed token t: row src[i] + (t -
+// off[i]) x_stride of its sequence i.
+hipError_t launch_quantize_wide(bool q8_0, const float* x, const float* const* src, const int* off, int nseq,
+                                void* out, long nblocks, int tokens, long x_stride, long out_stride,
+                                hipStream_t s);
+// whether the wide forms beat the one-block-per-lane-group ones at this many
+// blocks (measured rule)
+bool quantize_wide_preferred(long blocks);
 
 // Waves a GEMV launch aims for (8 per CU on 256 CUs) when choosing lanes per row.
 constexpr int kGemvTargetWaves = 2048;

@@ -55,6 +55,45 @@ def test_quantize_act_bit_exact(gpu, oracle, tt, kind):
     assert np.array_equal(got, want)
 
 
+def misaligned(x, gpu):
+    """A device copy of x whose data pointer is 4 bytes past a 16-byte boundary."""
+    buf = torch.empty(x.size + 4, dtype=torch.float32, device=gpu)
+    assert buf.data_ptr() % 16 == 0
+    view = buf[1:1 + x.size].view(x.shape)
+    view.copy_(torch.from_numpy(np.ascontiguousarray(x)))
+    assert view.data_ptr() % 16 == 4
+    return view
+
+
+@pytest.mark.parametrize("tt,k,cols", [(po.TT_Q8_0, 1, 256), (po.TT_Q8_0, 33, 1024), (po.TT_Q8_0, 1025, 1024),
+                                       (po.TT_Q4_K, 3, 768), (po.TT_Q4_K, 7, 2560), (po.TT_Q4_K, 129, 65536)])
+def test_quantize_wide_and_narrow_forms(gpu, oracle, tt, k, cols):
+    """From 32768 blocks the wide quantizers run (16-byte rows, blocks
+    numbered over tokens; here with a last workgroup only partly filled),
+    below it and on rows off a 16-byte boundary the narrow ones: all give
+    the oracle's bytes."""
+    x = QUANT_INPUTS["wide"](np.random.default_rng(k + cols), k, cols)
+    x[0, 1] = np.nan
+    want = oracle.quantize_act(tt, x)
+    assert np.array_equal(ops.quantize_act(tt, to_dev(x, gpu)).cpu().numpy(), want)
+    assert np.array_equal(ops.quantize_act(tt, misaligned(x, gpu)).cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("tt,cols,lens", [(po.TT_Q8_0, 1024, [300, 1, 512, 230]), (po.TT_Q8_0, 512, [5, 1, 9, 3]),
+                                          (po.TT_Q4_K, 512, [5, 1, 9, 3])])
+def test_quantize_ragged_rows_at_any_alignment(gpu, oracle, tt, cols, lens):
+    """The ragged packer reads each sequence's rows as they lie: 16-byte
+    aligned sequences and one 4 bytes off, packed in one launch (the first
+    case, 33376 Q8_0 blocks, in the wide form)."""
+    rng = np.random.default_rng(5)
+    seqs = [rng.standard_normal((n, cols)).astype(np.float32) for n in lens]
+    dseqs = [to_dev(s, gpu) for s in seqs]
+    dseqs[2] = misaligned(seqs[2], gpu)
+    xq, _, total = ops.quantize_ragged(tt, dseqs, cols)
+    want = oracle.quantize_act(tt, np.concatenate(seqs))
+    assert np.array_equal(xq[:total].cpu().numpy(), want)
+
+
 def test_quantize_header_quirk(gpu, oracle):
     # scale rounding out of the f16 subnormal range -> 0x0380 (kernels32.c:96)
     x = np.random.default_rng(1).uniform(-1, 1, 64).astype(np.float32) * np.float32(0.0077)
