@@ -447,11 +447,29 @@ def bench_mmq(c: Ctx):
                                                           total, tt, None, 0, stream), 200)
     s_di = timed(lambda: lib.qhip_launch_mul_mat_wd_image(img8.data_ptr(), xq5.data_ptr(), y5.data_ptr(), rows, cols,
                                                           T, tt, None, 0, stream), 200)
-    for key, sec, nt in (("cfg4_ragged_q8_0_3584x1024", s_ri, total), ("cfg4_dense512_q8_0_3584x1024", s_di, T)):
+    # and end to end: the f32 activations quantized (the ragged batch packed)
+    # then the fragment-image MMQ
+    def ragged_mirror_step():
+        assert lib.qhip_launch_quantize_ragged(tt, ptrs.data_ptr(), off_d.data_ptr(), len(lens), total, cols,
+                                               xq.data_ptr(), stream) == 0
+        assert lib.qhip_launch_mul_mat_wd_image(img8.data_ptr(), xq.data_ptr(), yo.data_ptr(), rows, cols, total,
+                                                tt, None, 0, stream) == 0
+
+    def dense_mirror_step():
+        assert lib.qhip_launch_quantize_act(tt, xd.data_ptr(), xq5.data_ptr(), cols, T, stream) == 0
+        assert lib.qhip_launch_mul_mat_wd_image(img8.data_ptr(), xq5.data_ptr(), y5.data_ptr(), rows, cols, T, tt,
+                                                None, 0, stream) == 0
+
+    s_rs = timed(ragged_mirror_step, 200)
+    s_ds = timed(dense_mirror_step, 200)
+    for key, sec, nt, step in (("cfg4_ragged_q8_0_3584x1024", s_ri, total, s_rs),
+                               ("cfg4_dense512_q8_0_3584x1024", s_di, T, s_ds)):
         tops, fr = frac(rows, cols, nt, sec)
         res[key].update({"us_mmq_fragment_image": round(sec * 1e6, 2), "fragment_image_int8_tops": tops,
                          "fragment_image_int8_mfma_frac": fr, "mirror_path": "fragment_image",
-                         "mirror_us": round(sec * 1e6, 2)})
+                         "mirror_us": round(sec * 1e6, 2),
+                         "us_quantize_and_mirror_mmq": round(step * 1e6, 2),
+                         "mirror_tokens_per_s": round(nt / step, 1)})
     log(f"mmq cfg4: ragged {total} tokens {s_mm * 1e6:.1f} us (fragment image {s_ri * 1e6:.1f}) "
         f"({res['cfg4_ragged_q8_0_3584x1024']['int8_mfma_frac']:.3f} of int8 peak); dense 512 {s_d * 1e6:.1f} us "
         f"(fragment image {s_di * 1e6:.1f})")
