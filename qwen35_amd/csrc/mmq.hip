@@ -2557,6 +2557,37 @@ __device__ __forceinline__ void bg_sync() {
   asm volatile("" ::: "memory");
 }
 
+// global_load_lds through inline assembly: the instruction the builtin emits
+// (M0 = the wave's LDS destination; lane l's 16 / 4 bytes land at M0 + 16 l /
+// 4 l), but invisible to the compiler's wait insertion, which otherwise makes
+// every later LDS read of the same array wait for all copies in flight
+// (vmcnt(0)) -- including the copy into the other stage just issued.  The
+// caller orders the copies itself: each is issued before the loads that its
+// later s_waitcnt vmcnt(N) leaves in flight (vector memory loads complete in
+// issue order), and a barrier follows that wait.  The compiler's own vmcnt
+// waits stay sufficient with these extra loads in the queue: it counts fewer
+// newer loads than there are, so it waits longer, never shorter.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+// (M0 is saved and restored around the copy: the compiler keeps it reserved.)
+__device__ __forceinline__ void lds_copy16(const void* src, const void* lds_dst) {
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(keep)
+      : "v"(src), "s"(lds_addr(lds_dst))
+      : "memory");
+}
+__device__ __forceinline__ void lds_copy4(const void* src, const void* lds_dst) {
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(keep)
+      : "v"(src), "s"(lds_addr(lds_dst))
+      : "memory");
+}
+
 // Vector loads a wave of k_mmq_bg_q6k issues after a unit's activation copy:
 // the 8 hi-plane and 8 lo-plane fragments of the next unit and its row scale.
 constexpr int kBgLoadsAfterCopy = 2 * 8 + 1;
@@ -2622,13 +2653,17 @@ __global__ __launch_bounds__(256, 2) void k_mmq_bg_q6k(const uint8_t* __restrict
 #pragma unroll
     for (int i = 0; i < TK / 16; ++i) {
       const int tk = 16 * i + qtok < tl ? 16 * i + qtok : tl;
-      __builtin_amdgcn_global_load_lds((const void*)(base + (long)tk * act_bytes + qoff),
-                                       (__attribute__((address_space(3))) void*)(st + 1024 * (4 * i + wv)), 16, 0, 0);
+      const uint8_t* src = base + (long)tk * act_bytes + qoff;
+      uint8_t* dst = st + 1024 * (4 * i + wv);
+      if constexpr (NA == 4) lds_copy16(src, dst);
+      else __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
     }
     if (wv < NA / 2) {
       const int tk = 64 * wv + lane < tl ? 64 * wv + lane : tl;
-      __builtin_amdgcn_global_load_lds((const void*)(base + (long)tk * act_bytes),
-                                       (__attribute__((address_space(3))) void*)(st + DYO + 256 * wv), 4, 0, 0);
+      const uint8_t* src = base + (long)tk * act_bytes;
+      uint8_t* dst = st + DYO + 256 * wv;
+      if constexpr (NA == 4) lds_copy4(src, dst);
+      else __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 4, 0, 0);
     }
   };
   // this wave's 32-row group of unit u in the image (a group past the end
