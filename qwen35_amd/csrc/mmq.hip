@@ -1299,6 +1299,37 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
   }
 }
 
+// global_load_lds through inline assembly: the instruction the builtin emits
+// (M0 = the wave's LDS destination; lane l's 16 / 4 bytes land at M0 + 16 l /
+// 4 l), but invisible to the compiler's wait insertion, which otherwise makes
+// every later LDS read of the same array wait for all copies in flight
+// (vmcnt(0)) -- including the copy into the other stage just issued.  The
+// caller orders the copies itself: each is issued before the loads that its
+// later s_waitcnt vmcnt(N) leaves in flight (vector memory loads complete in
+// issue order), and a barrier follows that wait.  The compiler's own vmcnt
+// waits stay sufficient with these extra loads in the queue: it counts fewer
+// newer loads than there are, so it waits longer, never shorter.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+// (M0 is saved and restored around the copy: the compiler keeps it reserved.)
+__device__ __forceinline__ void lds_copy16(const void* src, const void* lds_dst) {
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(keep)
+      : "v"(src), "s"(lds_addr(lds_dst))
+      : "memory");
+}
+__device__ __forceinline__ void lds_copy4(const void* src, const void* lds_dst) {
+  uint32_t keep;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+      : "=&s"(keep)
+      : "v"(src), "s"(lds_addr(lds_dst))
+      : "memory");
+}
+
 // ---- weights-direct MMQ (Q4_K, 32 or 64 tokens x 128 rows) -----------------------------------
 // Each wave owns 32 weight rows and reads their Q4_K bytes from global memory
 // straight into MFMA B fragments, with no LDS image of the weights: lane l
@@ -1311,6 +1342,10 @@ hipError_t launch_mmq_image(const GemvArgs& g, int bt, int br, void* work, long 
 // consecutive tokens fall 12 banks apart (conflict-free).  K may be cut into
 // ksplit slices of cps super-blocks (small grids: few tokens), the partial
 // tiles added in slice order by the tile's last workgroup (mmq_write_tile).
+// The copies are issued as inline assembly (lds_copy16), so the super-block's
+// LDS reads do not wait for the copy into the other stage (config 5 Q4_K from
+// the fragment image with the mirror's K split, T = 32 / 64 / 128: 18.6 /
+// 28.4 / 40.8 us against 19.4 / 29.8 / 43.3 with the builtin's copies).
 // Long slices run k_mmq_wdr_q4k instead (below).  Measured on MI355X, config
 // 5 Q4_K [17408, 5120]: T = 512 146-150 us (before the fragment image)
 // against 184 us for the 64 x 64 tile kernel in the same harness, T = 128 56
@@ -1410,9 +1445,7 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
-        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
-                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
-                                         16, 0, 0);
+        lds_copy16(XQ + goff[i] + 292L * sb, buf + 1024 * (4 * i + wv));
     }
   };
   u32x4 wh, wq[4];
@@ -2555,37 +2588,6 @@ __device__ __forceinline__ void bg_sync() {
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// global_load_lds through inline assembly: the instruction the builtin emits
-// (M0 = the wave's LDS destination; lane l's 16 / 4 bytes land at M0 + 16 l /
-// 4 l), but invisible to the compiler's wait insertion, which otherwise makes
-// every later LDS read of the same array wait for all copies in flight
-// (vmcnt(0)) -- including the copy into the other stage just issued.  The
-// caller orders the copies itself: each is issued before the loads that its
-// later s_waitcnt vmcnt(N) leaves in flight (vector memory loads complete in
-// issue order), and a barrier follows that wait.  The compiler's own vmcnt
-// waits stay sufficient with these extra loads in the queue: it counts fewer
-// newer loads than there are, so it waits longer, never shorter.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
-}
-// (M0 is saved and restored around the copy: the compiler keeps it reserved.)
-__device__ __forceinline__ void lds_copy16(const void* src, const void* lds_dst) {
-  uint32_t keep;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-      : "=&s"(keep)
-      : "v"(src), "s"(lds_addr(lds_dst))
-      : "memory");
-}
-__device__ __forceinline__ void lds_copy4(const void* src, const void* lds_dst) {
-  uint32_t keep;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-      : "=&s"(keep)
-      : "v"(src), "s"(lds_addr(lds_dst))
-      : "memory");
 }
 
 // Vector loads a wave of k_mmq_bg_q6k issues after a unit's activation copy:
