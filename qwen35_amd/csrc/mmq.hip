@@ -1861,9 +1861,7 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q4k(const uint8_t* __restrict__
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
-        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
-                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
-                                         16, 0, 0);
+        lds_copy16(XQ + goff[i] + 292L * sb, buf + 1024 * (4 * i + wv));
     }
   };
   u32x4 wh, wq[4];
@@ -2076,9 +2074,7 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q6k(const uint8_t* __restrict__
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       if (4 * i + wv < (NPC + 63) / 64 && gst[i] == 0)
-        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
-                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
-                                         16, 0, 0);
+        lds_copy16(XQ + goff[i] + 292L * sb, buf + 1024 * (4 * i + wv));
     }
   };
   auto issue_w = [&](int sb, Q6Regs<false>& q) {
