@@ -1344,9 +1344,10 @@ __device__ __forceinline__ void lds_copy4(const void* src, const void* lds_dst) 
 // tiles added in slice order by the tile's last workgroup (mmq_write_tile).
 // The copies are issued as inline assembly (lds_copy16), so the super-block's
 // LDS reads do not wait for the copy into the other stage (config 5 Q4_K from
-// the fragment image with the mirror's K split, T = 32 / 64 / 128: 18.6 /
-// 28.4 / 40.8 us against 19.4 / 29.8 / 43.3 with the builtin's copies).
-// Long slices run k_mmq_wdr_q4k instead (below).  Measured on MI355X, config
+// the fragment image, two weight copies rotated: unsplit T = 64 / 512 33.6 /
+// 127.3 us against 41.2 / 136.3 with the builtin's copies; with the mirror's
+// K split T = 32 / 64 / 128 18.6 / 28.4 / 40.8 against 19.4 / 29.8 / 43.3).
+// Measured on MI355X, config
 // 5 Q4_K [17408, 5120]: T = 512 146-150 us (before the fragment image)
 // against 184 us for the 64 x 64 tile kernel in the same harness, T = 128 56
 // against 62 us; with the split, T = 8 / 16 / 32 / 64 20.3 / 20.8 / 21.6 /
@@ -1374,25 +1375,6 @@ __device__ __forceinline__ T wd_pinned(T v) {
   return v;
 }
 #define wd_pin(x) ((x) = wd_pinned(x))
-
-// Vector loads issue_w makes per wave (the row header and four qs pieces).
-constexpr int kWdLoads = 5;
-// Super-blocks per K slice from which the launcher runs k_mmq_wdr_q4k.
-constexpr int kWdRingMin = 8;
-
-// The workgroup barrier between super-blocks: s_waitcnt vmcnt(N) lgkmcnt(0),
-// then s_barrier.  Vector memory loads (the global_load_lds copies among
-// them) complete in issue order, so vmcnt(N) means everything but this
-// wave's N most recent loads has landed.  The compiler barriers keep memory
-// accesses on their side of the s_barrier.
-template <int N>
-__device__ __forceinline__ void wd_sync() {
-  static_assert(N >= 0 && N < 16, "vmcnt low bits");
-  __builtin_amdgcn_s_waitcnt(N | (0x7 << 4));
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
   return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
@@ -1561,213 +1543,6 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
       for (int c = 0; c < 4; ++c) wq[c] = nq[c];
     }
   }
-  mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, g, ksplit, ks, part, cnt);
-}
-
-// The long-slice form of k_mmq_wd_q4k (the same tiles, products and bits):
-// the weights run two super-blocks ahead in two register sets, each register
-// reloaded right after its last use (so no loop-carried copy has to wait for
-// a load), and the two activation stages are two LDS variables, so the
-// compiler's wait insertion knows that the copy into one does not alias the
-// reads of the other (with one array it made the first read of every
-// super-block wait for the copy just issued, vmcnt(0)).  The copies and loads
-// ahead are unconditional (past the slice they repeat its last super-block),
-// which short slices pay for: the launcher uses it from 8 super-blocks per
-// slice.  Measured on MI355X, config 5 Q4_K [17408, 5120] from the fragment
-// image, two weight copies rotated: T = 512 125.5-128.4 us against 133.2-135.4
-// for the one-array form, T = 128 42.9 against 43.4 (unsplit launches, the
-// same bits); with K slices of 3-5 super-blocks (T = 32 / 64) 20.7 / 31.8
-// against 19.6 / 30.3.
-template <int NA, bool IMG>
-__global__ __launch_bounds__(256) void k_mmq_wdr_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
-                                                     float* __restrict__ Y, int rows, int tokens, long row_bytes,
-                                                     long act_bytes, int nsb, int ntile_t, int ksplit, int cps,
-                                                     float* __restrict__ part, unsigned* __restrict__ cnt) {
-  constexpr int BT = 32 * NA, STAGE = BT * kWdRow, NDMA = (BT * kWdPieces + 255) / 256;
-  // two stages as two variables: the copy into one and the reads of the
-  // other are then known not to alias, and the reads need not wait for the
-  // copy in flight (with one array the compiler waits for every copy)
-  __shared__ __attribute__((aligned(16))) uint8_t act0[STAGE];
-  __shared__ __attribute__((aligned(16))) uint8_t act1[STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
-  const int G = gridDim.x;
-  int g = blockIdx.x;
-  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
-  // tiles ordered (row tile, K slice, token tile): the workgroups side by side
-  // read the same weights at the same K (Q4_K config 5 at 256 / 512 tokens
-  // 72.9 / 130.4 us against 77.5 / 133.6 slice-minor)
-  const int per = ksplit * ntile_t, rt = g / per, ks = (g - rt * per) / ntile_t;
-  const int tt = g - rt * per - ks * ntile_t;
-  g = rt * ntile_t + tt;
-  const int r0 = rt * kWdBR, t0 = tt * BT;
-  const uint8_t* wrow;
-  if constexpr (IMG) {
-    // this wave's group of 32 rows (a group past the end re-reads the last)
-    const int ngrp = (rows + 31) >> 5, grp = (r0 >> 5) + wv;
-    wrow = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile4;
-  } else {
-    const int row = r0 + 32 * wv + li;
-    wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
-  }
-  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
-
-  // DMA piece p = 64*(4i + wave) + lane of the stage: token p/19, 16-byte
-  // slot p%19 (16 qs slots, two bsum slots, one slot holding d); tokens past
-  // the end re-read the last one
-  long goff[NDMA];
-  bool gon[NDMA];
-#pragma unroll
-  for (int i = 0; i < NDMA; ++i) {
-    const int p = 64 * (4 * i + wv) + lane;
-    gon[i] = p < BT * kWdPieces;
-    const int tp = p / kWdPieces, j = p - tp * kWdPieces;
-    int tok = t0 + tp;
-    tok = tok < tokens ? tok : tokens - 1;
-    goff[i] = (long)tok * act_bytes + (j < 16 ? 4 + 16 * j : j == 16 ? 260 : j == 17 ? 276 : 0);
-  }
-  auto issue_act = [&](int sb, uint8_t* buf) {
-#pragma unroll
-    for (int i = 0; i < NDMA; ++i) {
-      if (4 * i + wv < (BT * kWdPieces + 63) / 64 && gon[i])
-        __builtin_amdgcn_global_load_lds((const void*)(XQ + goff[i] + 292L * sb),
-                                         (__attribute__((address_space(3))) void*)(buf + 1024 * (4 * i + wv)),
-                                         16, 0, 0);
-    }
-  };
-  u32x4 wh, wq[4];
-  auto issue_w = [&](int sb, u32x4& h, u32x4 (&q)[4]) {
-    if constexpr (IMG) {
-      const uint8_t* b = wrow + (long)kWdiTile4 * sb;
-      h = *(const u32x4*)(b + 4096 + 16 * li);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 1024 * c + 16 * lane);
-    } else {
-      const uint8_t* b = wrow + 144L * sb;
-      h = *(const u32x4*)b;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) q[c] = *(const u32x4*)(b + 16 + 32 * c + 16 * lh);
-    }
-  };
-
-  f32x16 acc[NA][1];
-#pragma unroll
-  for (int a = 0; a < NA; ++a)
-#pragma unroll
-    for (int e = 0; e < 16; ++e) acc[a][0][e] = 0.0f;
-  const i32x16 zero = {};
-  const f32x16 fz = {};
-
-  // Two register sets of weights, each reloaded for super-block sb + 2 as
-  // soon as super-block sb has consumed it: the weight loads run two
-  // super-blocks ahead without register copies.
-  u32x4 whA, wqA[4], whB, wqB[4];
-  issue_act(sb0, act0);
-  issue_w(sb0, whA, wqA);
-  if (sb0 + 1 < sb1) issue_w(sb0 + 1, whB, wqB);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  // one super-block: compute from A while super-block sb + 1 lands in nxt
-  auto step = [&](int sb, u32x4& wh, u32x4 (&wq)[4], const uint8_t* A, uint8_t* nxt) {
-    // the copies and loads ahead are issued unconditionally (the last
-    // super-block again past the end), so that the wait counts below hold on
-    // every path
-    issue_act(sb + 1 < sb1 ? sb + 1 : sb, nxt);
-    // the weight loads below stay behind the copy: the barrier at the end
-    // counts them as this wave's last kWdLoads loads
-    asm volatile("" ::: "memory");
-    const int sbw = sb + 2 < sb1 ? sb + 2 : sb1 - 1;
-    __builtin_amdgcn_iglp_opt(0);
-    // 6-bit scales and mins of this lane's row (kernels256.c:105-125)
-    const uint32_t S0 = wh.y, S1 = wh.z, S2 = wh.w;
-    const uint32_t sc_lo = S0 & 0x3F3F3F3Fu, mn_lo = S1 & 0x3F3F3F3Fu;
-    const uint32_t sc_hi = (S2 & 0x0F0F0F0Fu) | ((S0 >> 2) & 0x30303030u);
-    const uint32_t mn_hi = ((S2 >> 4) & 0x0F0F0F0Fu) | ((S1 >> 2) & 0x30303030u);
-    float d = h2f(wh.x), ndm = -h2f(wh.x >> 16);
-    // each register is reloaded after its last use (the values taken from it
-    // are made complete first, and the loads cannot move above the compiler
-    // barrier), so that the load can target the register it replaces: a
-    // loop-carried copy would wait for the load
-    uint32_t scl = sc_lo, mnl = mn_lo, sch = sc_hi, mnh = mn_hi;
-    asm volatile("" : "+v"(scl), "+v"(mnl), "+v"(sch), "+v"(mnh), "+v"(d), "+v"(ndm) : : "memory");
-    const uint8_t* nb = IMG ? wrow + (long)kWdiTile4 * sbw : wrow + 144L * sbw;
-    wh = *(const u32x4*)(IMG ? nb + 4096 + 16 * li : nb);
-    i32x16 chi[NA], clo[NA];
-#pragma unroll
-    for (int a = 0; a < NA; ++a) {
-      chi[a] = zero;
-      clo[a] = zero;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint32_t nib[2][4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t v = w == 0 ? wq[c].x : w == 1 ? wq[c].y : w == 2 ? wq[c].z : wq[c].w;
-        nib[0][w] = v & 0x0F0F0F0Fu;
-        nib[1][w] = (v >> 4) & 0x0F0F0F0Fu;
-      }
-      asm volatile("" : "+v"(nib[0][0]), "+v"(nib[0][1]), "+v"(nib[0][2]), "+v"(nib[0][3]), "+v"(nib[1][0]),
-                   "+v"(nib[1][1]), "+v"(nib[1][2]), "+v"(nib[1][3]) : : "memory");
-      wq[c] = *(const u32x4*)(IMG ? nb + 1024 * c + 16 * lane : nb + 16 + 32 * c + 16 * lh);
-#pragma unroll
-      for (int hi = 0; hi < 2; ++hi) {
-        const int s = 2 * c + hi;
-        const uint32_t n0 = nib[hi][0], n1 = nib[hi][1], n2 = nib[hi][2], n3 = nib[hi][3];
-        const uint32_t sc = ((s < 4 ? scl : sch) >> (8 * (s & 3))) & 63u;
-        const u16x2 mh = {(uint16_t)(sc >> 3), (uint16_t)(sc >> 3)};
-        const u16x2 ml = {(uint16_t)(sc & 7u), (uint16_t)(sc & 7u)};
-        const i32x4 bh = {(int)pk_mul_u16(n0, mh), (int)pk_mul_u16(n1, mh), (int)pk_mul_u16(n2, mh),
-                          (int)pk_mul_u16(n3, mh)};
-        const i32x4 bl = {(int)pk_mul_u16(n0, ml), (int)pk_mul_u16(n1, ml), (int)pk_mul_u16(n2, ml),
-                          (int)pk_mul_u16(n3, ml)};
-#pragma unroll
-        for (int a = 0; a < NA; ++a) {
-          const i32x4 af = *(const i32x4*)(A + (32 * a + li) * kWdRow + 32 * s + 16 * lh);
-          chi[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bh, chi[a], 0, 0, 0);
-          clo[a] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bl, clo[a], 0, 0, 0);
-        }
-      }
-    }
-    // mins: summs[t][r] = sum_j bsum[t][j] * min[r][j/2], exact in the f16 MFMA
-    const uint32_t mn = lh ? mnh : mnl;
-    f16x8 bm;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const _Float16 m = (_Float16)(float)((mn >> (8 * k)) & 255u);
-      bm[2 * k] = m;
-      bm[2 * k + 1] = m;
-    }
-#pragma unroll
-    for (int a = 0; a < NA; ++a) {
-      const i16x8 bs = *(const i16x8*)(A + (32 * a + li) * kWdRow + 256 + 16 * lh);
-      f16x8 am;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const short v = bs[k];
-        am[k] = (_Float16)v;
-      }
-      const f32x16 cm = __builtin_amdgcn_mfma_f32_32x32x16_f16(am, bm, fz, 0, 0, 0);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int t = 32 * a + 8 * (e >> 2) + 4 * lh + (e & 3);
-        const float dy = *(const float*)(A + t * kWdRow + 288);
-        const int ci = chi[a][e], cl = clo[a][e];  // (scalar copies: see k_mmq)
-        const int isum = 8 * ci + cl;
-        const float inner = __builtin_fmaf(d, (float)isum, ndm * cm[e]);
-        acc[a][0][e] = __builtin_fmaf(dy, inner, acc[a][0][e]);
-      }
-    }
-    // super-block sb + 1: its copy and (issued a step earlier) its weights
-    // have landed; super-block sb + 2's weights may stay in flight
-    wd_sync<kWdLoads>();
-  };
-  int sb = sb0;
-  for (; sb + 1 < sb1; sb += 2) {
-    step(sb, whA, wqA, act0, act1);
-    step(sb + 1, whB, wqB, act1, act0);
-  }
-  if (sb < sb1) step(sb, whA, wqA, act0, act1);
-  __builtin_amdgcn_s_waitcnt(0);  // nothing in flight past the loop
   mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, g, ksplit, ks, part, cnt);
 }
 
@@ -3115,20 +2890,14 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipSt
       return hipGetLastError();
     }
   }
-  // long slices: the two-deep weight ring (k_mmq_wdr_q4k)
-#define QHIP_WD(K, NA)                                                                                      \
-  hipLaunchKernelGGL((K<NA, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,                  \
-                     (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt, \
-                     ksplit, cps, part, cnt)
-  const bool ring = cps >= kWdRingMin;
-  if (bt == 32) {
-    if (ring) QHIP_WD(k_mmq_wdr_q4k, 1);
-    else QHIP_WD(k_mmq_wd_q4k, 1);
-  } else {
-    if (ring) QHIP_WD(k_mmq_wdr_q4k, 2);
-    else QHIP_WD(k_mmq_wd_q4k, 2);
-  }
-#undef QHIP_WD
+  if (bt == 32)
+    hipLaunchKernelGGL((k_mmq_wd_q4k<1, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
+                       ksplit, cps, part, cnt);
+  else
+    hipLaunchKernelGGL((k_mmq_wd_q4k<2, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
+                       (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
+                       ksplit, cps, part, cnt);
   return hipGetLastError();
 }
 
