@@ -1380,23 +1380,60 @@ __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t v, u16x2 m) {
   return __builtin_bit_cast(uint32_t, (u16x2)(__builtin_bit_cast(u16x2, v) * m));
 }
 
+// Grid of a weights-direct launch: workgroups [0, nwhole) take whole tiles
+// 0 .. nwhole - 1 (all of K); the rest take the remaining tiles cut into
+// ksplit slices of cps super-blocks.  nwhole = 0 splits every tile; ksplit = 1
+// splits none.  The sliced tiles come last in the grid, so they fill the
+// final, partial round of resident workgroups instead of leaving it to a few.
+// Within each part, block b's tile is XCD-contiguous (b % 8 is the XCD the
+// block is dispatched to), and the slices are ordered (group of ntile_t
+// tiles, slice, tile): the workgroups side by side read the same weights at
+// the same K (Q4_K config 5 at 256 / 512 tokens 72.9 / 130.4 us against
+// 77.5 / 133.6 slice-minor, every tile split).  Sets the tile, its slice and
+// the slice count of this workgroup, and the index of its partial tiles among
+// the sliced ones.
+struct WdTile {
+  int tile, ks, ksplit, su;
+};
+__device__ __forceinline__ WdTile wd_tile(int ntile_t, int nwhole, int ksplit) {
+  const int G = gridDim.x, b = blockIdx.x;
+  WdTile r;
+  if (b < nwhole || ksplit <= 1) {
+    const int n = ksplit <= 1 ? G : nwhole;
+    r.tile = (n & 7) == 0 ? (b & 7) * (n >> 3) + (b >> 3) : b;
+    r.ks = 0;
+    r.ksplit = 1;
+    r.su = 0;
+    return r;
+  }
+  const int np = G - nwhole, nsplit = np / ksplit;
+  int p = b - nwhole;
+  if ((np & 7) == 0) p = (p & 7) * (np >> 3) + (p >> 3);
+  const int gw = ntile_t < nsplit ? ntile_t : nsplit, full = nsplit / gw, rem = nsplit - full * gw;
+  if (p < full * ksplit * gw) {
+    const int grp = p / (ksplit * gw), loc = p - grp * ksplit * gw;
+    r.ks = loc / gw;
+    r.su = grp * gw + (loc - r.ks * gw);
+  } else {
+    const int loc = p - full * ksplit * gw;
+    r.ks = loc / rem;
+    r.su = full * gw + (loc - r.ks * rem);
+  }
+  r.tile = nwhole + r.su;
+  r.ksplit = ksplit;
+  return r;
+}
+
 template <int NA, bool IMG>
 __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                      float* __restrict__ Y, int rows, int tokens, long row_bytes,
-                                                     long act_bytes, int nsb, int ntile_t, int ksplit, int cps,
-                                                     float* __restrict__ part, unsigned* __restrict__ cnt) {
+                                                     long act_bytes, int nsb, int ntile_t, int nwhole, int ksplit,
+                                                     int cps, float* __restrict__ part, unsigned* __restrict__ cnt) {
   constexpr int BT = 32 * NA, STAGE = BT * kWdRow, NDMA = (BT * kWdPieces + 255) / 256;
   __shared__ __attribute__((aligned(16))) uint8_t act[2][STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, li = lane & 31, lh = lane >> 5;
-  const int G = gridDim.x;
-  int g = blockIdx.x;
-  if ((G & 7) == 0) g = (g & 7) * (G >> 3) + (g >> 3);  // XCD-contiguous tiles, as k_mmq
-  // tiles ordered (row tile, K slice, token tile): the workgroups side by side
-  // read the same weights at the same K (Q4_K config 5 at 256 / 512 tokens
-  // 72.9 / 130.4 us against 77.5 / 133.6 slice-minor)
-  const int per = ksplit * ntile_t, rt = g / per, ks = (g - rt * per) / ntile_t;
-  const int tt = g - rt * per - ks * ntile_t;
-  g = rt * ntile_t + tt;
+  const WdTile wt = wd_tile(ntile_t, nwhole, ksplit);
+  const int rt = wt.tile / ntile_t, tt = wt.tile - rt * ntile_t, ks = wt.ks;
   const int r0 = rt * kWdBR, t0 = tt * BT;
   const uint8_t* wrow;
   if constexpr (IMG) {
@@ -1407,7 +1444,8 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
     const int row = r0 + 32 * wv + li;
     wrow = W + (long)(row < rows ? row : rows - 1) * row_bytes;
   }
-  const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
+  const int sb0 = wt.ksplit > 1 ? ks * cps : 0;
+  const int sb1 = wt.ksplit > 1 && sb0 + cps < nsb ? sb0 + cps : nsb;
 
   // DMA piece p = 64*(4i + wave) + lane of the stage: token p/19, 16-byte
   // slot p%19 (16 qs slots, two bsum slots, one slot holding d); tokens past
@@ -1535,6 +1573,10 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
         acc[a][0][e] = __builtin_fmaf(dy, inner, acc[a][0][e]);
       }
     }
+    // the whole super-block's products and epilogue stay above the wait:
+    // otherwise the scheduler may sink half of them below it, so the loads
+    // for sb + 1 get only the first half to land in
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(0);  // chunk sb+1: DMA and weight registers
     __syncthreads();
     if (sb + 1 < sb1) {
@@ -1543,7 +1585,7 @@ __global__ __launch_bounds__(256) void k_mmq_wd_q4k(const uint8_t* __restrict__ 
       for (int c = 0; c < 4; ++c) wq[c] = nq[c];
     }
   }
-  mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+  mmq_write_tile<NA, 1, 4>(acc, Y, rows, tokens, r0, t0, 32 * wv, 0, wt.su, wt.ksplit, ks, part, cnt);
 }
 
 // Few tokens (T <= 8 NG, NG < 4; one 32-token tile): the same staging, one
@@ -2854,25 +2896,68 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_rk(const uint8_t* __restrict__ 
 // spend half its MFMA and epilogue work on padding), else 64.
 static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
 
-// Slices of a weights-direct launch: with one token tile, K split when the
-// grid has fewer than two workgroups per CU, aiming at four, at least two
-// super-blocks per slice (a split aiming at eight workgroups per CU, or one
-// super-block per slice, is slower: the partial tiles' traffic grows with the
-// slices); with several, the round-filling count (mmq_round_slices).
-static int wd_slices(const GemvArgs& g) {
+// Grid plan of a weights-direct launch (wd_tile): the first nwhole tiles
+// whole, the rest cut into ksplit slices.
+struct WdPlan {
+  int ksplit;
+  long nwhole;
+};
+
+// With one token tile, every tile is cut when the grid has fewer than two
+// workgroups per CU, aiming at four, at least two super-blocks per slice (a
+// split aiming at eight workgroups per CU, or one super-block per slice, is
+// slower: the partial tiles' traffic grows with the slices).  With several
+// token tiles and less than one round of resident workgroups (two per CU),
+// every tile is cut by the round-filling count (mmq_round_slices).  From one
+// round on, the whole rounds stay whole and only the tiles of the last,
+// partial round are cut, into the slice count that minimises that round's
+// cost in units of one whole tile: (rounds of slices) x (super-blocks per
+// slice) / nsb, plus 0.13 per round of slices for their partial tiles'
+// stores and loads; a partial round left whole costs 0.6 + 0.4 x its fill (a
+// workgroup alone on its CU runs faster than two).
+static WdPlan wd_plan(const GemvArgs& g) {
   const int nsb = g.cols / 256;
-  const long ntt = (g.tokens + wd_bt(g) - 1) / wd_bt(g);
-  if (ntt >= 2) return mmq_slices(nsb, mmq_round_slices(ntt * ((g.rows + kWdBR - 1) / kWdBR), nsb, 2));
-  return mmq_slices(nsb, mmq_ksplit_for(g, wd_bt(g), kWdBR, nsb, 2));
+  const long ntt = (g.tokens + wd_bt(g) - 1) / wd_bt(g), tiles = ntt * ((g.rows + kWdBR - 1) / kWdBR);
+  if (ntt < 2) return WdPlan{mmq_slices(nsb, mmq_ksplit_for(g, wd_bt(g), kWdBR, nsb, 2)), 0};
+  const int cus = qhip_gpu_cu_count();
+  const long cap = 2L * (cus > 0 ? cus : 256);
+  if (tiles < cap) return WdPlan{mmq_slices(nsb, mmq_round_slices(tiles, nsb, 2)), 0};
+  const long rem = tiles % cap;
+  WdPlan best{1, tiles};
+  if (rem == 0 || rem > kSkMaxTiles) return best;
+  double best_c = 0.6 + 0.4 * (double)rem / (double)cap;
+  for (int cps = nsb / 2; cps >= 2; --cps) {
+    const int sl = (nsb + cps - 1) / cps;
+    if (sl < 2) continue;
+    const long pieces = rem * sl, rounds = (pieces + cap - 1) / cap;
+    const double c = (double)rounds * cps / nsb + 0.13 * (double)pieces / (double)cap;
+    if (c < best_c - 1e-9) {
+      best_c = c;
+      best = WdPlan{sl, tiles - rem};
+    }
+  }
+  return best;
+}
+
+static long wd_work_bytes(const GemvArgs& g, const WdPlan& p) {
+  if (p.ksplit <= 1) return 0;
+  const long tiles = ((g.tokens + wd_bt(g) - 1) / wd_bt(g)) * ((g.rows + kWdBR - 1) / kWdBR);
+  return kSkCountBytes + 4L * p.ksplit * (tiles - p.nwhole) * wd_bt(g) * kWdBR;
 }
 
 template <bool IMG>
-static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
+static hipError_t launch_mmq_wd(const GemvArgs& g, WdPlan plan, void* work, hipStream_t s) {
   const int bt = wd_bt(g), nsb = g.cols / 256;
-  const long ntt = (g.tokens + bt - 1) / bt, ntr = (g.rows + kWdBR - 1) / kWdBR;
+  const long ntt = (g.tokens + bt - 1) / bt, ntr = (g.rows + kWdBR - 1) / kWdBR, tiles = ntt * ntr;
+  if (plan.ksplit <= 1) plan = WdPlan{1, tiles};
+  const int ksplit = plan.ksplit;
+  if (plan.nwhole < 0 || plan.nwhole > tiles) return hipErrorInvalidValue;
   const int cps = (nsb + ksplit - 1) / ksplit;
-  const long G = ntt * ntr * ksplit;
-  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntt * ntr > kSkMaxTiles)) return hipErrorInvalidValue;
+  const long nsplit = ksplit > 1 ? tiles - plan.nwhole : 0;
+  const long G = ksplit > 1 ? plan.nwhole + nsplit * ksplit : tiles;
+  if (G > 0x7FFFFFFFL || nsplit > kSkMaxTiles || (ksplit > 1 && (nsb + cps - 1) / cps != ksplit))
+    return hipErrorInvalidValue;
+  const int nwhole = (int)plan.nwhole;
   unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
   float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
   if constexpr (!IMG) {
@@ -2893,11 +2978,11 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, int ksplit, void* work, hipSt
   if (bt == 32)
     hipLaunchKernelGGL((k_mmq_wd_q4k<1, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
-                       ksplit, cps, part, cnt);
+                       nwhole, ksplit, cps, part, cnt);
   else
     hipLaunchKernelGGL((k_mmq_wd_q4k<2, IMG>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.row_bytes, g.act_bytes, nsb, (int)ntt,
-                       ksplit, cps, part, cnt);
+                       nwhole, ksplit, cps, part, cnt);
   return hipGetLastError();
 }
 
@@ -2953,9 +3038,9 @@ hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, h
     // up to 24 tokens the K split inside the workgroup; beyond, the 32- and
     // 64-token weights-direct tiles (split over workgroups on small grids)
     if (g.tokens <= 24) return launch_mmq_rk<TT_Q4_K, 4>(g, s);
-    int ksplit = wd_slices(g);
-    if (!work || work_bytes < mmq_split_bytes(g, wd_bt(g), kWdBR, ksplit)) ksplit = 1;
-    return launch_mmq_wd<true>(g, ksplit, work, s);
+    WdPlan plan = wd_plan(g);
+    if (!work || work_bytes < wd_work_bytes(g, plan)) plan = WdPlan{1, 0};
+    return launch_mmq_wd<true>(g, plan, work, s);
   }
   if (g.ttype != TT_Q6_K || g.tokens > 32) return hipErrorInvalidValue;
   // up to 16 tokens the K split inside the workgroup; 17..32 the split
@@ -3009,7 +3094,7 @@ static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit,
   // Q4_K's 64 x 128 tile is the weights-direct kernel (never split when
   // asked for explicitly)
   if constexpr (TT == TT_Q4_K)
-    if (bt == 64 && br == 128) return launch_mmq_wd<false>(g, ksplit, work, s);
+    if (bt == 64 && br == 128) return launch_mmq_wd<false>(g, WdPlan{ksplit, 0}, work, s);
   if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, work, s);
   if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, work, s);
   if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, work, s);
@@ -3042,7 +3127,6 @@ static void mmq_default_tile(const GemvArgs& g, int& bt, int& br) {
 
 // Slices of the default tile launch.
 static int mmq_default_slices(const GemvArgs& g, int bt, int br) {
-  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return wd_slices(g);
   if (wds_q6k(g)) return wds_q6k_slices(g);
   const int nchunks = (g.cols / 64 + 3) / 4;
   return mmq_slices(nchunks, mmq_ksplit_for(g, bt, br, nchunks, 2));
@@ -3051,7 +3135,7 @@ static int mmq_default_slices(const GemvArgs& g, int bt, int br) {
 long mmq_work_bytes(const GemvArgs& g) {
   int bt = 0, br = 0;
   mmq_default_tile(g, bt, br);
-  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return mmq_split_bytes(g, wd_bt(g), kWdBR, wd_slices(g));
+  if (g.ttype == TT_Q4_K && bt == 64 && br == 128) return wd_work_bytes(g, wd_plan(g));
   return mmq_split_bytes(g, bt, br, mmq_default_slices(g, bt, br));
 }
 
@@ -3060,9 +3144,13 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, void* work, long work_b
   int ksplit = 1;
   if (bt <= 0 || br <= 0) {
     mmq_default_tile(g, bt, br);
+    if (g.ttype == TT_Q4_K && bt == 64 && br == 128) {  // the weights-direct kernel
+      WdPlan plan = wd_plan(g);
+      if (!work || work_bytes < wd_work_bytes(g, plan)) plan = WdPlan{1, 0};
+      return launch_mmq_wd<false>(g, plan, work, s);
+    }
     ksplit = mmq_default_slices(g, bt, br);
-    const bool wd = g.ttype == TT_Q4_K && bt == 64 && br == 128;
-    if (!work || work_bytes < mmq_split_bytes(g, wd ? wd_bt(g) : bt, br, ksplit)) ksplit = 1;
+    if (!work || work_bytes < mmq_split_bytes(g, bt, br, ksplit)) ksplit = 1;
     if (wds_q6k(g)) return launch_mmq_wds_q6k(g, ksplit, work, s);
   }
   switch (g.ttype) {

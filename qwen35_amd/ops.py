@@ -203,7 +203,7 @@ def mul_mat_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, co
 
 
 def wd_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
-    """The fragment image of a Q6_K weight (the GGUF bytes permuted for the few-token MMQ)."""
+    """The fragment image of a Q4_K / Q6_K / Q8_0 weight (the GGUF bytes permuted for the MMQ)."""
     n = load().qhip_wd_image_bytes(ttype, rows, cols)
     if n < 0:
         raise ValueError(f"no fragment image for type {ttype} at cols={cols}")
@@ -214,7 +214,7 @@ def wd_image(ttype: int, w: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
 
 def mul_mat_wd_image(ttype: int, img: torch.Tensor, xq: torch.Tensor, rows: int, cols: int, tokens: int,
                      work: torch.Tensor | None = None) -> torch.Tensor:
-    """out [tokens, rows] from the fragment image (1..32 tokens)."""
+    """out [tokens, rows] from the fragment image (Q6_K: 1..32 tokens; Q4_K, Q8_0: any)."""
     out = torch.empty((tokens, rows), dtype=torch.float32, device=img.device)
     check("mul_mat_wd_image", load().qhip_launch_mul_mat_wd_image(
         _p(img), _p(xq), _p(out), rows, cols, tokens, ttype,

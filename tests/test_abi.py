@@ -166,17 +166,18 @@ def test_split_workspace_size(lib):
 
 
 def test_mmq_split_workspace_size(lib):
-    # cfg5 at 16 tokens splits K (a few hundred row tiles); at 256 tokens the
-    # 544 weights-direct tiles are cut in three (1632 over 4 rounds of 512
-    # resident workgroups: 80% full); at 512 and 1024 tokens (1088 / 2176
-    # tiles, two rounds or more) K is not split; a GEMV-only or unknown type
-    # has no workspace
+    # cfg5 at 16 tokens splits K (a few hundred row tiles).  From one round of
+    # resident weights-direct tiles (512 workgroups), the whole rounds stay
+    # whole and only the last, partial round's tiles are cut over K (20
+    # super-blocks): 256 tokens, 544 tiles, the last 32 in 10 slices; 512
+    # tokens, 1088 tiles, the last 64 in 7; 1024 tokens, 2176 tiles, the last
+    # 128 in 4.  A GEMV-only or unknown type has no workspace
     n = lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 12)
     assert n > 32768 and n % 4 == 0
     assert lib.qhip_mul_mat_work_bytes(5120, 17408, 16, 14) > 32768
-    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 256, 12) == 32768 + 4 * 3 * 544 * 64 * 128
-    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 0
-    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 1024, 12) == 0
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 256, 12) == 32768 + 4 * 10 * 32 * 64 * 128
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 512, 12) == 32768 + 4 * 7 * 64 * 64 * 128
+    assert lib.qhip_mul_mat_work_bytes(17408, 5120, 1024, 12) == 32768 + 4 * 4 * 128 * 64 * 128
     assert lib.qhip_mul_mat_work_bytes(17408, 5120, 16, 99) == 0
     assert lib.qhip_mul_mat_work_bytes(0, 5120, 16, 12) == 0
     p = ctypes.c_void_p(0x1000)

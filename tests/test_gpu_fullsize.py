@@ -301,3 +301,36 @@ def test_q6k_plane_image_whole_and_sliced_tiles(gpu, oracle):
     check(a.cpu().numpy()[:, idx], want, "image+work")
     assert torch.equal(a, ops.mul_mat_image(tt, img, xq, rows, cols, T, work=work))
     check(ops.mul_mat_image(tt, img, xq, rows, cols, T).cpu().numpy()[:, idx], want, "image")
+
+
+@pytest.mark.parametrize("rows,cols", [(17408, 5120), (16480, 2304)], ids=["17408x5120", "16480x2304"])
+def test_q4k_weights_direct_whole_and_sliced_tiles(gpu, oracle, rows, cols):
+    """The Q4_K weights-direct MMQ at 512 tokens, more tiles than resident
+    workgroups: the whole rounds of tiles run over all of K and only the
+    tiles of the last, partial round are cut into K slices (with the
+    workspace; without it every tile is whole).  From the GGUF rows and from
+    the fragment image: within the tolerance on the sampled rows plus the
+    last two row tiles (the sliced ones; at 16480 rows the last is partly
+    past the end), bit-equal on a rerun, and within the tolerance of the
+    unsplit launch over the whole output."""
+    tt, T = po.TT_Q4_K, 512
+    print(f"Q4_K weights-direct whole+sliced [{rows}x{cols}] T={T}", flush=True)
+    w = synth.make_weight(tt, rows, cols, seed=31, tag=tt)
+    x = synth.make_act(cols, T, seed=31)
+    idx = sample_rows(rows, 31)
+    idx = np.unique(np.concatenate([idx, np.arange(rows - 192, rows)]))
+    want = oracle.matvec(tt, np.ascontiguousarray(w[idx]), x, nthreads=THREADS)
+    wd = to_dev(w, gpu)
+    xq = ops.quantize_act(tt, to_dev(x, gpu))
+    work = ops.mul_mat_work(rows, cols, T, tt, gpu)
+    assert work is not None  # the last round is sliced
+    a = ops.mul_mat_split(tt, wd, xq, rows, cols, T, work, PATH_MMQ)
+    check(a.cpu().numpy()[:, idx], want, "gguf+work")
+    assert torch.equal(a, ops.mul_mat_split(tt, wd, xq, rows, cols, T, work, PATH_MMQ))
+    whole = ops.mul_mat(tt, wd, xq, rows, cols, T, PATH_MMQ)
+    assert rel_l2(a.cpu().numpy(), whole.cpu().numpy()) < TOL
+    img = ops.wd_image(tt, wd, rows, cols)
+    b = ops.mul_mat_wd_image(tt, img, xq, rows, cols, T, work)
+    check(b.cpu().numpy()[:, idx], want, "image+work")
+    assert torch.equal(b, ops.mul_mat_wd_image(tt, img, xq, rows, cols, T, work))
+    check(ops.mul_mat_wd_image(tt, img, xq, rows, cols, T).cpu().numpy()[:, idx], want, "image")
