@@ -2896,6 +2896,32 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_rk(const uint8_t* __restrict__ 
 // spend half its MFMA and epilogue work on padding), else 64.
 static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
 
+// K slices for a launch of one token tile (the few-token weights-direct and
+// Q6_K kernels): the most slices that keep the grid within one round of
+// resident workgroups (two per CU) with at least four super-blocks in every
+// slice.  Longer slices keep each workgroup's copy pipeline in its steady
+// state longer, and a second, partial round costs a whole slice time.
+// Measured on MI355X, us at the slice counts tried against the earlier rule
+// (aim at four workgroups per CU, two super-blocks per slice): Q4_K [17408,
+// 5120] T = 32 / 48 / 64 3 slices 20.7 / 27.4 / 27.7 against 7 slices 22.5
+// / 34.6 / 35.1 (4: 22.3 / 32.2 / 32.8, 2: 24.2 / 31.0 / 31.1); [9728,
+// 2560] T = 32 / 64 3 slices 11.1 / 14.6 against 12.8 / 17.5; [12288,
+// 4096] 4 slices 14.7 / 19.6 against 17.2 / 25.5; [4096, 12288] 8 slices
+// 15.5 / 21.3 against 23.2 / 34.1; [19456, 2560] T = 64 3 slices 21.5
+// against 25.6 (unsplit 20.2); Q6_K [5120, 17408] T = 20 / 32 12 slices
+// 28.2 / 30.9 against 23 slices 31.9 / 37.4 (14: 31.9 / 40.1, 8: 34.6 /
+// 38.1); [2560, 9728] 10 slices 16.3 / 18.3 against 19 slices 17.1 / 19.1.
+static int wd_one_round_slices(long tiles, int nsb) {
+  const int cus = qhip_gpu_cu_count();
+  const long cap = 2L * (cus > 0 ? cus : 256);
+  int best = 1;
+  for (int s = 2; s <= nsb; ++s) {
+    if (tiles * s > cap || (nsb + s - 1) / s < 4) break;
+    best = s;
+  }
+  return mmq_slices(nsb, best);
+}
+
 // Grid plan of a weights-direct launch (wd_tile): the first nwhole tiles
 // whole, the rest cut into ksplit slices.
 struct WdPlan {
@@ -2903,10 +2929,8 @@ struct WdPlan {
   long nwhole;
 };
 
-// With one token tile, every tile is cut when the grid has fewer than two
-// workgroups per CU, aiming at four, at least two super-blocks per slice (a
-// split aiming at eight workgroups per CU, or one super-block per slice, is
-// slower: the partial tiles' traffic grows with the slices).  With several
+// With one token tile, every tile is cut into the one-round slice count
+// (wd_one_round_slices).  With several
 // token tiles and less than one round of resident workgroups (two per CU),
 // every tile is cut by the round-filling count (mmq_round_slices).  From one
 // round on, the whole rounds stay whole and only the tiles of the last,
@@ -2918,7 +2942,7 @@ struct WdPlan {
 static WdPlan wd_plan(const GemvArgs& g) {
   const int nsb = g.cols / 256;
   const long ntt = (g.tokens + wd_bt(g) - 1) / wd_bt(g), tiles = ntt * ((g.rows + kWdBR - 1) / kWdBR);
-  if (ntt < 2) return WdPlan{mmq_slices(nsb, mmq_ksplit_for(g, wd_bt(g), kWdBR, nsb, 2)), 0};
+  if (ntt < 2) return WdPlan{wd_one_round_slices(tiles, nsb), 0};
   const int cus = qhip_gpu_cu_count();
   const long cap = 2L * (cus > 0 ? cus : 256);
   if (tiles < cap) return WdPlan{mmq_slices(nsb, mmq_round_slices(tiles, nsb, 2)), 0};
@@ -2991,8 +3015,7 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, WdPlan plan, void* work, hipS
 static bool wds_q6k(const GemvArgs& g) { return g.ttype == TT_Q6_K && g.tokens <= 24; }
 
 static int wds_q6k_slices(const GemvArgs& g) {
-  const int nsb = g.cols / 256;
-  return mmq_slices(nsb, mmq_ksplit_for(g, 32, kWdBR, nsb, 2));
+  return wd_one_round_slices((g.rows + kWdBR - 1) / kWdBR, g.cols / 256);
 }
 
 static hipError_t launch_mmq_wds_q6k(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
