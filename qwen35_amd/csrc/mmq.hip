@@ -2897,29 +2897,39 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_rk(const uint8_t* __restrict__ 
 static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
 
 // K slices for a launch of one token tile (the few-token weights-direct and
-// Q6_K kernels): the most slices that keep the grid within one round of
-// resident workgroups (two per CU) with at least four super-blocks in every
-// slice.  Longer slices keep each workgroup's copy pipeline in its steady
-// state longer, and a second, partial round costs a whole slice time.
-// Measured on MI355X, us at the slice counts tried against the earlier rule
-// (aim at four workgroups per CU, two super-blocks per slice): Q4_K [17408,
-// 5120] T = 32 / 48 / 64 3 slices 20.7 / 27.4 / 27.7 against 7 slices 22.5
-// / 34.6 / 35.1 (4: 22.3 / 32.2 / 32.8, 2: 24.2 / 31.0 / 31.1); [9728,
-// 2560] T = 32 / 64 3 slices 11.1 / 14.6 against 12.8 / 17.5; [12288,
-// 4096] 4 slices 14.7 / 19.6 against 17.2 / 25.5; [4096, 12288] 8 slices
-// 15.5 / 21.3 against 23.2 / 34.1; [19456, 2560] T = 64 3 slices 21.5
-// against 25.6 (unsplit 20.2); Q6_K [5120, 17408] T = 20 / 32 12 slices
-// 28.2 / 30.9 against 23 slices 31.9 / 37.4 (14: 31.9 / 40.1, 8: 34.6 /
-// 38.1); [2560, 9728] 10 slices 16.3 / 18.3 against 19 slices 17.1 / 19.1.
-static int wd_one_round_slices(long tiles, int nsb) {
-  const int cus = qhip_gpu_cu_count();
-  const long cap = 2L * (cus > 0 ? cus : 256);
+// Q6_K kernels).  A workgroup's time is about its super-blocks times the time
+// of one, and a super-block takes `share` times as long where two workgroups
+// share a CU as where one runs alone (Q4_K about 1.6, Q6_K about 1.2); so the
+// count minimises (super-blocks per slice) x (share if the grid has more
+// workgroups than CUs, else 1), within one round of resident workgroups (two
+// per CU) and with at
+// least four super-blocks per slice (shorter slices never reach the copy
+// pipeline's steady state), fewer slices on a tie.  Measured on MI355X, us
+// (slices) against the earlier rule (aim at four workgroups per CU, two
+// super-blocks per slice): Q4_K [17408, 5120] T = 32 / 48 / 64 20.7 / 27.4
+// / 27.7 (3) against 22.5 / 34.6 / 35.1 (7) (2: 24.2 / 31.0 / 31.1, 4: 22.3
+// / 32.2 / 32.8); [9728, 2560] T = 32 / 64 11.1 / 14.6 (3) against 12.8 /
+// 17.5; [12288, 4096] 14.7 / 19.6 (4) against 17.2 / 25.5; [4096, 12288]
+// 15.6 / 20.9 (8) against 23.2 / 34.1 (12: 16.7 / 23.9); [19456, 2560] T =
+// 64 21.5 (3) against 25.6 (unsplit 20.2); Q6_K [5120, 17408] T = 20 / 32
+// 28.2 / 30.9 (12) against 31.9 / 37.4 (23) (14: 31.9 / 40.1, 8: 34.6 /
+// 38.1); [2560, 9728] 16.3 / 18.3 (10) against 17.1 / 19.1 (19); [4096,
+// 12288] T = 24 / 32 21.3 / 23.1 (12) against 22.4 / 27.5 (24) (8: 23.9 /
+// 25.8).
+static int wd_one_round_slices(long tiles, int nsb, double share) {
+  const int cus0 = qhip_gpu_cu_count(), cus = cus0 > 0 ? cus0 : 256;
   int best = 1;
+  double best_c = (double)nsb * (tiles > cus ? share : 1.0);
   for (int s = 2; s <= nsb; ++s) {
-    if (tiles * s > cap || (nsb + s - 1) / s < 4) break;
-    best = s;
+    const int cps = (nsb + s - 1) / s, sl = (nsb + cps - 1) / cps;
+    if (tiles * sl > 2L * cus || cps < 4) break;
+    const double c = (double)cps * (tiles * sl > cus ? share : 1.0);
+    if (c < best_c - 1e-9) {
+      best_c = c;
+      best = sl;
+    }
   }
-  return mmq_slices(nsb, best);
+  return best;
 }
 
 // Grid plan of a weights-direct launch (wd_tile): the first nwhole tiles
@@ -2942,7 +2952,7 @@ struct WdPlan {
 static WdPlan wd_plan(const GemvArgs& g) {
   const int nsb = g.cols / 256;
   const long ntt = (g.tokens + wd_bt(g) - 1) / wd_bt(g), tiles = ntt * ((g.rows + kWdBR - 1) / kWdBR);
-  if (ntt < 2) return WdPlan{wd_one_round_slices(tiles, nsb), 0};
+  if (ntt < 2) return WdPlan{wd_one_round_slices(tiles, nsb, 1.6), 0};
   const int cus = qhip_gpu_cu_count();
   const long cap = 2L * (cus > 0 ? cus : 256);
   if (tiles < cap) return WdPlan{mmq_slices(nsb, mmq_round_slices(tiles, nsb, 2)), 0};
@@ -3015,7 +3025,7 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, WdPlan plan, void* work, hipS
 static bool wds_q6k(const GemvArgs& g) { return g.ttype == TT_Q6_K && g.tokens <= 24; }
 
 static int wds_q6k_slices(const GemvArgs& g) {
-  return wd_one_round_slices((g.rows + kWdBR - 1) / kWdBR, g.cols / 256);
+  return wd_one_round_slices((g.rows + kWdBR - 1) / kWdBR, g.cols / 256, 1.2);
 }
 
 static hipError_t launch_mmq_wds_q6k(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
