@@ -2893,8 +2893,16 @@ __global__ __launch_bounds__(64 * NW) void k_mmq_rk(const uint8_t* __restrict__ 
 }
 
 // Tokens per weights-direct tile: 32 up to 32 tokens (a 64-token tile would
-// spend half its MFMA and epilogue work on padding), else 64.
-static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 ? 32 : 64; }
+// spend half its MFMA and epilogue work on padding) and from 65 to 96 (two
+// 64-token tiles would pad up to 63 tokens; three 32-token ones pad at most
+// 31), else 64.  Measured on MI355X, Q4_K from the image, weights from HBM,
+// 65 / 80 / 96 tokens: [17408, 5120] 39.4 / 39.3 / 39.5 us against 45.0 /
+// 45.3 / 45.8; [9728, 2560] 80 / 96 15.2 / 15.0 against 18.9 / 18.3;
+// [12288, 4096] and [4096, 12288] at 96 26.7 / 27.6 against 29.0 / 28.7.
+// 33 to 64 tokens keep one 64-token tile ([17408, 5120] 48 / 64 26.9 / 27.8
+// us against 28.6 / 29.7 in two 32-token tiles), and 97 to 128 two
+// ([9728, 2560] 128: 18.5 against 19.2).
+static int wd_bt(const GemvArgs& g) { return g.tokens <= 32 || (g.tokens > 64 && g.tokens <= 96) ? 32 : 64; }
 
 // K slices for a launch of one token tile (the few-token weights-direct and
 // Q6_K kernels).  A workgroup's time is about its super-blocks times the time
@@ -2980,8 +2988,8 @@ static long wd_work_bytes(const GemvArgs& g, const WdPlan& p) {
 }
 
 template <bool IMG>
-static hipError_t launch_mmq_wd(const GemvArgs& g, WdPlan plan, void* work, hipStream_t s) {
-  const int bt = wd_bt(g), nsb = g.cols / 256;
+static hipError_t launch_mmq_wd(const GemvArgs& g, WdPlan plan, void* work, hipStream_t s, int bt) {
+  const int nsb = g.cols / 256;
   const long ntt = (g.tokens + bt - 1) / bt, ntr = (g.rows + kWdBR - 1) / kWdBR, tiles = ntt * ntr;
   if (plan.ksplit <= 1) plan = WdPlan{1, tiles};
   const int ksplit = plan.ksplit;
@@ -3073,7 +3081,7 @@ hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, h
     if (g.tokens <= 24) return launch_mmq_rk<TT_Q4_K, 4>(g, s);
     WdPlan plan = wd_plan(g);
     if (!work || work_bytes < wd_work_bytes(g, plan)) plan = WdPlan{1, 0};
-    return launch_mmq_wd<true>(g, plan, work, s);
+    return launch_mmq_wd<true>(g, plan, work, s, wd_bt(g));
   }
   if (g.ttype != TT_Q6_K || g.tokens > 32) return hipErrorInvalidValue;
   // up to 16 tokens the K split inside the workgroup; 17..32 the split
@@ -3127,7 +3135,8 @@ static hipError_t launch_mmq_type(const GemvArgs& g, int bt, int br, int ksplit,
   // Q4_K's 64 x 128 tile is the weights-direct kernel (never split when
   // asked for explicitly)
   if constexpr (TT == TT_Q4_K)
-    if (bt == 64 && br == 128) return launch_mmq_wd<false>(g, WdPlan{ksplit, 0}, work, s);
+    if (bt == 64 && br == 128)
+      return launch_mmq_wd<false>(g, WdPlan{ksplit, 0}, work, s, g.tokens <= 32 ? 32 : 64);
   if (bt == 32 && br == 128) return launch_mmq_t<TT, 32, 128>(g, ksplit, work, s);
   if (bt == 32 && br == 64) return launch_mmq_t<TT, 32, 64, 128>(g, ksplit, work, s);
   if (bt == 64 && br == 64) return launch_mmq_t<TT, 64, 64>(g, ksplit, work, s);
@@ -3180,7 +3189,7 @@ hipError_t launch_mmq(const GemvArgs& g, int bt, int br, void* work, long work_b
     if (g.ttype == TT_Q4_K && bt == 64 && br == 128) {  // the weights-direct kernel
       WdPlan plan = wd_plan(g);
       if (!work || work_bytes < wd_work_bytes(g, plan)) plan = WdPlan{1, 0};
-      return launch_mmq_wd<false>(g, plan, work, s);
+      return launch_mmq_wd<false>(g, plan, work, s, wd_bt(g));
     }
     ksplit = mmq_default_slices(g, bt, br);
     if (!work || work_bytes < mmq_split_bytes(g, bt, br, ksplit)) ksplit = 1;

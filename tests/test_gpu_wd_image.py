@@ -204,7 +204,7 @@ def q4(gpu):
     return rows, cols, w, wd, ops.wd_image(TQ4, wd, rows, cols)
 
 
-@pytest.mark.parametrize("tokens", [1, 2, 8, 9, 24, 25, 32, 33, 64, 65, 130, 257])
+@pytest.mark.parametrize("tokens", [1, 2, 8, 9, 24, 25, 32, 33, 64, 65, 96, 97, 130, 257])
 def test_wd_image_q4k_vs_oracle(gpu, oracle, q4, tokens):
     """Every Q4_K launch from the image: above 24 tokens the same bits as from
     the GGUF rows (same slices, same order); up to 24 the K split inside the
