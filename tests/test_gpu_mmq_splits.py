@@ -1,7 +1,8 @@
 """GPU: the default MMQ launches that pick their own kernel and K split --
 the weights-direct Q4_K kernel (its few-token variant up to 24 tokens,
-32-token tiles up to 32, 64-token tiles beyond; K split over workgroups on
-small grids and to fill whole rounds with several token tiles), the
+32-token tiles up to 32 and from 65 to 96, 64-token tiles otherwise; K split
+over workgroups on small grids and to fill whole rounds with several token
+tiles), the
 few-token weights-direct Q6_K kernel (up to 24 tokens) and the Q6_K image --
 against the oracle at token counts either side of every switch with
 row counts that are no multiple of a tile; exact block integers at unit
@@ -19,7 +20,7 @@ pytestmark = pytest.mark.gpu
 TOL = 1e-5
 PATH_MMQ = 2
 
-Q4K_T = [1, 2, 3, 5, 8, 9, 16, 17, 24, 25, 31, 32, 33, 63, 64, 65, 96, 128, 130]
+Q4K_T = [1, 2, 3, 5, 8, 9, 16, 17, 24, 25, 31, 32, 33, 63, 64, 65, 96, 97, 128, 130]
 
 
 @pytest.fixture(scope="module")
