@@ -48,7 +48,7 @@ H2, F2 = 2560, 9728          # config 2 (4B-class FFN)
 R3, C3 = 248320, 2560        # config 3 (output head)
 
 PROFILE_KERNELS = ["cfg3_gemv", "cfg3_step", "cfg3_gemv_gguf", "cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv",
-                   "down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused",
+                   "down", "gate_up", "fused_gate_up", "split_down", "mirror_down", "step", "step_unfused",
                    "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
                    "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8", "mmq_cfg4_frag",
                    "mmq_cfg4_ragged_frag"]
@@ -292,16 +292,19 @@ class Cfg2:
             return {"alg_bytes": alg, "avg_us": round(s * 1e6, 3), "gbs": round(alg / s / 1e9, 1),
                     "hbm_frac": round(alg / s / 1e9 / HBM_PEAK_GBS, 4)}
 
-        res = {"workload": "matvecPair Q4_K gate/up [9728,2560]x2 from f32 x[2560] + matvec Q6_K down "
-                           "[2560,9728] from f32 h[9728] through the Exec mirror",
+        res = {"workload": "matvecPair Q4_K gate/up [9728,2560]x2 from f32 x[2560] (one fused quantize + GEMV "
+                           "launch) + matvec Q6_K down [2560,9728] from f32 h[9728] (quantize, then the GEMV from "
+                           "the weight's K-quant image) through the Exec mirror",
                "step_alg_bytes": self.step_bytes, "us_per_step": round(sec * 1e6, 3),
                "gbs": round(self.step_bytes / sec / 1e9, 1),
                "hbm_frac": round(self.step_bytes / sec / 1e9 / HBM_PEAK_GBS, 4),
                "us_per_step_separate_quantize_launches": round(sec_unfused * 1e6, 2),
                "weight_copies_rotated": self.copies,
                "kernels": {"fused_q4_k_gate_up_19456x2560": entry(gu_alg, time_loop(torch, self.fused_gate_up, n_k, 20)),
-                           "split_q6_k_down_2560x9728": entry(d_alg, time_loop(torch, self.split_down, n_k, 20))},
+                           # the mirror's down matvec: quantize h, then the GEMV from the K-quant image
+                           "mirror_q6_k_down_2560x9728": entry(d_alg, time_loop(torch, self.down, n_k, 20))},
                "kernels_off_step": {
+                   "split_q6_k_down_2560x9728": entry(d_alg, time_loop(torch, self.split_down, n_k, 20)),
                    "gemv_q4_k_gate_up_19456x2560_prequantized": entry(gu_alg, time_loop(torch, self.gemv_gate_up, n_k, 20)),
                    "gemv_q6_k_down_2560x9728_prequantized": entry(d_alg, time_loop(torch, self.gemv_down, n_k, 20)),
                    "quantize_q8_k_9728": entry(4 * F2 + self.c.lib.qhip_act_row_bytes(TQ6, F2),
@@ -795,11 +798,12 @@ def profile(c: Ctx, which: str, launches: int):
                           "cfg5_q6k_gemv": (TQ6, 5120, 17408)}[which]
         st, fn, k = gemv_stream(c, tt, rows, cols)
         keep += [st, k]
-    elif which in ("down", "gate_up", "fused_gate_up", "split_down", "step", "step_unfused"):
+    elif which in ("down", "gate_up", "fused_gate_up", "split_down", "mirror_down", "step", "step_unfused"):
         c2 = Cfg2(c)
         keep.append(c2)
         fn = {"down": c2.gemv_down, "gate_up": c2.gemv_gate_up, "fused_gate_up": c2.fused_gate_up,
-              "split_down": c2.split_down, "step": c2.step, "step_unfused": c2.step_unfused}[which]
+              "split_down": c2.split_down, "mirror_down": c2.down, "step": c2.step,
+              "step_unfused": c2.step_unfused}[which]
     else:
         tt, rows, cols, T = {"mmq_cfg5_q4k": (TQ4, 17408, 5120, 512), "mmq_cfg5_q3k": (11, 17408, 5120, 512),
                              "mmq_cfg5_q2k": (10, 17408, 5120, 512), "mmq_cfg5_q6k_image": (TQ6, 5120, 17408, 512),

@@ -420,7 +420,8 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
     }
   }
   // Q6_K at one token, quantized separately: the weight's K-quant GEMV image
-  // (the same GEMV launch as the GGUF rows, reading the image)
+  // (the same GEMV launch as the GGUF rows, reading the image), in place of
+  // the one-launch split-K form
   uint8_t* kimg = nullptr;
   if (k == 1 && be->gemv_images_on) {
     const GemvArgs gk{ttype, wdev, x, out, rows, cols, 1, row_bytes, qhip_act_row_bytes(ttype, cols)};
@@ -433,7 +434,7 @@ static int run(qhip_backend* be, float* out, const void* wdev, int ttype, int ro
   const bool hit = be->memo_on && be->memo_src == x && be->memo_cols == cols && be->memo_k == k &&
                    be->memo_fam == fam && be->act;
   if (be->memo_on) (hit ? be->memo_hits : be->memo_misses)++;
-  if (!hit && k == 1) {
+  if (!hit && k == 1 && !kimg) {
     // one launch, the activation quantized inside the GEMV, where that is
     // faster than a separate quantize launch (widths up to 4096 whole; long
     // rows split over K); with the memo on, the launch also leaves the

@@ -131,6 +131,13 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
 #pragma unroll
     for (int k = 0; k < NR; ++k) w[k] = load_unit<TT, IMG>(wrow[k], u, upr);
     const typename U::A a = U::load_a(XQ, u);
+    // every load of the unit is issued before the first dot: left to itself
+    // the scheduler sinks some of them between the dots to save registers,
+    // and each such load then costs the wave a memory round trip of its own
+    // (Q6_K [5120, 17408] from the K-quant image, two rows per four-wave
+    // team: 16.7 us against 22.7; [2560, 9728] 6.05 against 6.61; Q4_K
+    // [17408, 5120] from the GGUF rows 11.3 against 11.8)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < NR; ++k) acc[k] += U::dot(w[k], a);
   }
@@ -990,12 +997,15 @@ bool gemv_splitk_preferred(const GemvArgs& g) {
 // 8.13.  Read by the one-launch quantize + GEMV and its split-K form, the
 // image lost (Q4_K [19456, 2560] 9.53 vs 9.38 us, Q6_K [2560, 9728] split
 // 10.79 vs 10.20, Q4_K [5120, 17408] split 15.05 vs 14.01), so those keep
-// the GGUF rows.  The Exec mirror's batch-1 matvec therefore reads the image
-// for Q6_K where it quantizes separately (rows past the one-launch form's
-// range, widths 4096 < cols < 8192): Q6_K [17408, 5120] 23.3 vs 26.2 us.
+// the GGUF rows.  The Exec mirror's batch-1 matvec reads the image for Q6_K
+// wherever the whole-row one-launch form is not preferred, quantizing
+// separately: Q6_K [17408, 5120] 23.3 vs 26.2 us; and, once k_gemv_mw issued
+// every load of a unit before its dots (image GEMV [2560, 9728] 6.05 us,
+// [5120, 17408] 16.5), also instead of the split-K form: the config-2 decode
+// step (its Q6_K down projection [2560, 9728]) 17.8 against 19.2 us,
+// [5120, 17408] 18.4 against 18.3.
 bool gemv_kimage_preferred(const GemvArgs& g) {
-  return g.tokens == 1 && g.ttype == TT_Q6_K && g.cols % 256 == 0 && !gemv_fused_preferred(g) &&
-         !gemv_splitk_preferred(g);
+  return g.tokens == 1 && g.ttype == TT_Q6_K && g.cols % 256 == 0 && !gemv_fused_preferred(g);
 }
 
 hipError_t launch_gemv_splitk(const GemvArgs& g, const float* x, void* xq_out, int team, int nr, int slice,

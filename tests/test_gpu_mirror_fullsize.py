@@ -4,9 +4,9 @@ decode step runs:
 
 * config 3, IQ4_NL [248320, 2560]: the split quantize + GEMV-image launch
   (`k_gemv_img`, image built by prepare_linear), 10,347 workgroups;
-* config 5 Q6_K [5120, 17408] (down projection): the one-launch split-K
-  quantize + GEMV with 4096-value slices of 16 lanes;
-* Q6_K [4096, 12288]: the same launch with 2048-value slices;
+* config 5 Q6_K [5120, 17408] (down projection) and Q6_K [4096, 12288]: the
+  quantize launch, then the multi-wave GEMV (two rows per four-wave team)
+  from the weight's K-quant image, built by prepare_linear;
 * config 5 Q4_K [17408, 5120]: quantize + the multi-wave GEMV.
 
 Bar: the float outputs within 1e-5 relative L2 of the oracle on 512 sampled
@@ -88,16 +88,18 @@ def explicit_route(tt, wd, xd, rows, cols, gpu):
         img = ops.gemv_image(tt, wd, rows, cols)
         return ops.mul_mat_vec_image(tt, img, ops.quantize_act_image(tt, xd[None, :]), rows, cols)
     if tt == po.TT_Q6_K:
-        slice_values, lanes = (4096, 16) if cols >= 16384 else (2048, 8)
-        work = ops.split_work(rows, cols, gpu)
-        return ops.quantize_mul_mat_vec_split(tt, wd, xd, rows, cols, work, slice_values, lanes, 1)
+        # the K-quant image holds the GGUF bytes reordered; its GEMV gives the
+        # bits of the GGUF-row launch of the same shape (two rows per
+        # four-wave team)
+        xq = ops.quantize_act(tt, xd[None, :])
+        return ops.gemv_tuned(tt, wd, xq, rows, cols, 1, 256, 1, 2)[0]
     xq = ops.quantize_act(tt, xd[None, :])
     return ops.mul_mat(tt, wd, xq, rows, cols, 1, 1)[0]
 
 
 ROUTES = [("cfg3-iq4_nl-image", po.TT_IQ4_NL, 248320, 2560),
-          ("cfg5-q6_k-splitk-4096", po.TT_Q6_K, 5120, 17408),
-          ("q6_k-splitk-2048", po.TT_Q6_K, 4096, 12288),
+          ("cfg5-q6_k-kimage", po.TT_Q6_K, 5120, 17408),
+          ("q6_k-kimage-12288", po.TT_Q6_K, 4096, 12288),
           ("cfg5-q4_k-gemv", po.TT_Q4_K, 17408, 5120)]
 
 
