@@ -55,10 +55,15 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
       for (int k = 0; k < NR; ++k) w[k] = load_unit<TT, IMG>(wrow[k], u, upr);
       if constexpr (NT == 1) {
         const typename U::A a = U::load_a(XQ + (long)t0 * act_bytes, u);
-        // Q8_0: the unit's loads before its dots, as in k_gemv_mw ([17408,
-        // 5120] 23.4 against 31.9 us); the other formats keep the compiler's
-        // order (IQ4_NL [17408, 5120] 15.3 against 19.2 with the barrier)
-        if constexpr (TT == TT_Q8_0) __builtin_amdgcn_sched_barrier(0);
+        // the unit's loads before its dots, as in k_gemv_mw, for the formats
+        // it helps (Q8_0 [17408, 5120] 23.4 against 31.9 us; Q6_K image
+        // [19456, 2560] 64 lanes x 2 rows 10.3 against 12.1, [17408, 5120]
+        // 20 x 2 16.9 against 19.1; Q4_K [19456, 2560] 40 x 4 8.1 against
+        // 8.3; IQ3_XXS 12.1-12.9 against 13.2); the others keep the
+        // compiler's order (IQ4_NL [17408, 5120] 15.3 against 19.2 with it;
+        // Q2_K, IQ4_XS, IQ3_S 1-2% slower)
+        if constexpr (TT == TT_Q8_0 || TT == TT_Q4_K || TT == TT_Q6_K || TT == TT_IQ3_XXS)
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < NR; ++k) acc[0][k] += U::dot(w[k], a);
       } else {
