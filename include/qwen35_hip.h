@@ -399,8 +399,8 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
 /* Build what this weight's products use beyond its GGUF bytes now, at load
  * time, instead of inside the first matvec: the GEMV image of an IQ4_NL /
  * Q4_0 / Q8_0 weight large enough for the decode matvec to read it, or of a
- * Q6_K weight whose decode matvec quantizes separately (widths between 4096
- * and 8192, or more than 32768 rows)
+ * Q6_K weight whose decode matvec quantizes separately (widths above 4096, or
+ * more than 32768 rows)
  * (qhip_launch_gemv_prepare, the GGUF bytes once more; built in load order,
  * so adjacent weights get adjacent images and matvecPair stays one launch),
  * the fragment image of a Q6_K or Q4_K weight with rows * cols >= 2^23
