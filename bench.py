@@ -48,6 +48,7 @@ H2, F2 = 2560, 9728          # config 2 (4B-class FFN)
 R3, C3 = 248320, 2560        # config 3 (output head)
 
 PROFILE_KERNELS = ["cfg3_gemv", "cfg3_step", "cfg3_gemv_gguf", "cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv",
+                   "cfg5_q6k_kimage",
                    "down", "gate_up", "fused_gate_up", "split_down", "mirror_down", "step", "step_unfused",
                    "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
                    "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8", "mmq_cfg4_frag",
@@ -395,7 +396,8 @@ def bench_mmq(c: Ctx):
     Throughput: tokens/s, and 2*rows*cols*T / time against the int8 MFMA
     peak.  `mmq_us`
     is the fastest of the MMQ on the GGUF rows, from the fragment image and
-    (Q6_K) from the MMQ image; `mirror_us` is what the Exec mirror launches."""
+    (Q6_K) from the MMQ image; `mirror_us` is what the Exec mirror launches
+    (Q6_K at one token: the GEMV from the K-quant image)."""
     torch, lib, ops, synth, dev, stream = c.torch, c.lib, c.ops, c.synth, c.dev, c.stream
     res = {}
 
@@ -494,6 +496,7 @@ def bench_mmq(c: Ctx):
         ws = [torch.from_numpy(wh).to(dev) for _ in range(ncopy)]
         frags = [ops.wd_image(tt, w, rows, cols) for w in ws]
         imgs = [ops.mmq_image(tt, w, rows, cols) for w in ws] if tt == TQ6 else None
+        kimgs = [ops.gemv_image(tt, w, rows, cols) for w in ws] if tt == TQ6 else None
         rows_out = []
         cross = None
         for T in (1, 2, 4, 8, 16, 32, 64, 512):
@@ -533,9 +536,18 @@ def bench_mmq(c: Ctx):
                                                                  y.data_ptr(), rows, cols, T, tt, PATH_AUTO, wp, wn,
                                                                  stream), it)
             pt["auto_us"] = round(s_a * 1e6, 2)
-            s_mirror = s_i if s_i is not None and T >= 64 else s_f if s_f is not None and T >= 2 else s_a
+            s_k = None
+            if kimgs is not None and T == 1:
+                # the GEMV from the K-quant image (the activation in the same
+                # Q8_K rows)
+                s_k = rotated(lambda i: lib.qhip_launch_mul_mat_vec_image(kimgs[i % ncopy].data_ptr(), aq.data_ptr(),
+                                                                          y.data_ptr(), rows, cols, tt, 0, stream), it)
+                pt["gemv_kimage_us"] = round(s_k * 1e6, 2)
+            s_mirror = (s_i if s_i is not None and T >= 64 else s_f if s_f is not None and T >= 2 else
+                        s_k if s_k is not None else s_a)
             pt["mirror_path"] = ("mmq_image" if s_i is not None and T >= 64 else
-                                 "fragment_image" if s_f is not None and T >= 2 else "auto")
+                                 "fragment_image" if s_f is not None and T >= 2 else
+                                 "gemv_kimage" if s_k is not None else "auto")
             pt["mirror_us"] = round(s_mirror * 1e6, 2)
             if s_mirror > 1.1 * min(s_g, s_m):
                 pt["mirror_warning"] = "the Exec mirror's choice is more than 10% slower than the fastest path"
@@ -548,14 +560,16 @@ def bench_mmq(c: Ctx):
             if cross is None and s_m < s_g:
                 cross = T
         # small batches against one token: what the Exec mirror launches at
-        # 2..8 tokens over the batch-1 GEMV
+        # 2..8 tokens over the batch-1 GEMV on the GGUF rows, and over what
+        # it launches for one token
         t1 = next(p["gemv_us"] for p in rows_out if p["T"] == 1)
-        ratio = max(p["mirror_us"] for p in rows_out if 2 <= p["T"] <= 8) / t1
-        sweep[name] = {"points": rows_out, "crossover_T": cross, "mirror_2_8_over_gemv_1": round(ratio, 3),
-                       "weight_copies": ncopy}
+        m1 = next(p["mirror_us"] for p in rows_out if p["T"] == 1)
+        worst = max(p["mirror_us"] for p in rows_out if 2 <= p["T"] <= 8)
+        sweep[name] = {"points": rows_out, "crossover_T": cross, "mirror_2_8_over_gemv_1": round(worst / t1, 3),
+                       "mirror_2_8_over_mirror_1": round(worst / m1, 3), "weight_copies": ncopy}
         log(f"mmq cfg5 {name}: " + ", ".join(f"T={p['T']} gemv {p['gemv_us']} / mmq {p['mmq_us']} us"
                                               for p in rows_out) + f"; crossover T={cross}")
-        del ws, imgs, frags
+        del ws, imgs, frags, kimgs
         torch.cuda.empty_cache()
     res["cfg5_sweep"] = sweep
     return res
@@ -793,11 +807,22 @@ def profile(c: Ctx, which: str, launches: int):
         c3 = Cfg3(c)
         keep.append(c3)
         fn = {"cfg3_gemv": c3.gemv, "cfg3_step": c3.step, "cfg3_gemv_gguf": c3.gemv_gguf}[which]
-    elif which in ("cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv"):
+    elif which in ("cfg1_gemv", "cfg5_q4k_gemv", "cfg5_q6k_gemv", "cfg5_q6k_kimage"):
         tt, rows, cols = {"cfg1_gemv": (TQ8, 6144, 1024), "cfg5_q4k_gemv": (TQ4, 17408, 5120),
-                          "cfg5_q6k_gemv": (TQ6, 5120, 17408)}[which]
+                          "cfg5_q6k_gemv": (TQ6, 5120, 17408), "cfg5_q6k_kimage": (TQ6, 5120, 17408)}[which]
         st, fn, k = gemv_stream(c, tt, rows, cols)
         keep += [st, k]
+        if which == "cfg5_q6k_kimage":
+            # the K-quant image of every rotated copy (what the Exec mirror
+            # reads for one token), on the same pre-quantized activation
+            imgs = [ops.gemv_image(tt, st.buf[j * st.stride:j * st.stride + st.n], rows, cols)
+                    for j in range(st.copies)]
+            aq, yo = k
+            keep.append(imgs)
+
+            def fn(i):
+                assert lib.qhip_launch_mul_mat_vec_image(imgs[i % len(imgs)].data_ptr(), aq.data_ptr(),
+                                                         yo.data_ptr(), rows, cols, tt, 0, stream) == 0
     elif which in ("down", "gate_up", "fused_gate_up", "split_down", "mirror_down", "step", "step_unfused"):
         c2 = Cfg2(c)
         keep.append(c2)

@@ -310,7 +310,10 @@ int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d
  * d of each super-block.  Its activation is the reference Q8_K row
  * (qhip_launch_quantize_act_image = qhip_launch_quantize_act), and the image
  * GEMV gives the same bits as qhip_launch_mul_mat_vec on the GGUF rows with
- * the same rows per lane.
+ * the same rows per lane -- except the Q6_K image's default launch from 4096
+ * rows at widths of 64a + b units with a = 1 (b <= 32), 3 or 4, whose
+ * balanced teams sum a row's units in another order (within 1e-6 relative
+ * L2 of the GGUF-row launch; config 5's [5120, 17408] 15.4 us against 18.4).
  *   qhip_gemv_image_bytes      image size (rows x GGUF row bytes); -1 for
  *                              other types or widths
  *   qhip_gemv_image_act_bytes  bytes of `tokens` activation rows, or -1

@@ -165,6 +165,84 @@ __global__ __launch_bounds__(256) void k_gemv_mw(const uint8_t* __restrict__ W,
   }
 }
 
+// Balanced teams of WV whole waves (1, 2 or 4) owning NR rows of 64a + b
+// units (1 <= a <= A WV, NR b <= 64 WV), one token, every load of a lane
+// issued before its first dot.  Wave s takes the whole rounds r = s, s + WV,
+// ... (unit lane + 64 r of each of the NR rows, one activation unit shared by
+// them); the NR b tail pairs (row, unit) of the team go one per lane, pair
+// t = WV lane + s to row t / b, unit 64 a + t % b, with an activation unit of
+// its own.  k_gemv_mw gives the tail units to the first b lanes, which then
+// make a second round trip for the NR rows while the rest of the team idles.
+// The partials fold as in k_gemv_mw (deterministic).
+template <int TT, int NR, int WV, int A, bool IMG = false>
+__global__ __launch_bounds__(256) void k_gemv_bal(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
+                                                   float* __restrict__ Y, int rows, long row_bytes, int upr) {
+  using U = Unit<TT>;
+  constexpr int TPB = 4 / WV;  // teams per workgroup
+  __shared__ float part[4][NR];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int tm = wv / WV, sl = wv % WV;
+  const long row0 = ((long)blockIdx.x * TPB + tm) * NR;
+  const bool active = row0 < rows;
+  const int a = upr >> 6, b = upr & 63;
+  const int t = lane * WV + sl;
+  const bool tail = active && t < NR * b;
+  const int tk = tail ? t / b : 0;
+  float acc[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) acc[k] = 0.0f;
+  if (active) {
+    const uint8_t* wrow[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) wrow[k] = W + (row0 + k < rows ? row0 + k : rows - 1) * row_bytes;
+    typename U::W w[A][NR];
+    typename U::A x[A];
+#pragma unroll
+    for (int i = 0; i < A; ++i) {
+      if (sl + WV * i < a) {
+        const int u = lane + 64 * (sl + WV * i);
+#pragma unroll
+        for (int k = 0; k < NR; ++k) w[i][k] = load_unit<TT, IMG>(wrow[k], u, upr);
+        x[i] = U::load_a(XQ, u);
+      }
+    }
+    typename U::W wt;
+    typename U::A xt;
+    if (tail) {
+      const int u = 64 * a + (t - tk * b);
+      wt = load_unit<TT, IMG>(W + (row0 + tk < rows ? row0 + tk : rows - 1) * row_bytes, u, upr);
+      xt = U::load_a(XQ, u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < A; ++i) {
+      if (sl + WV * i < a) {
+#pragma unroll
+        for (int k = 0; k < NR; ++k) acc[k] += U::dot(w[i][k], x[i]);
+      }
+    }
+    if (tail) {
+      const float v = U::dot(wt, xt);
+#pragma unroll
+      for (int k = 0; k < NR; ++k)
+        if (k == tk) acc[k] += v;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < NR; ++k) acc[k] = wave_sum_to_lane63(acc[k]);
+  if (lane == 63) {
+#pragma unroll
+    for (int k = 0; k < NR; ++k) part[wv][k] = acc[k];
+  }
+  __syncthreads();
+  if (sl == 0 && lane < NR && active && row0 + lane < rows) {
+    float v = part[tm * WV][lane];
+#pragma unroll
+    for (int q = 1; q < WV; ++q) v += part[tm * WV + q][lane];
+    Y[row0 + lane] = v;
+  }
+}
+
 // ---- quantize + GEMV in one launch (batch 1) ---------------------------------------
 // Every workgroup quantizes the f32 activation itself, bit-exactly as the
 // standalone quantizers do, into an LDS image split into planes (ActSplit:
@@ -750,10 +828,57 @@ static void default_shape(const GemvArgs& g, int& team, int& nr) {
 
 static hipError_t launch_gemv_multiwave(const GemvArgs& g, int nr, int wv, hipStream_t s);
 
+// Balanced teams (k_gemv_bal) for one-token Q6_K matvecs from the K-quant
+// image with rows of 64a + b units, 1 <= a <= 4, and >= 4096 rows: one wave
+// of two rows where a = 1, four waves of two (a = 3) or four (a = 4) rows
+// otherwise.  Measured on MI355X against the default team shapes, weights
+// rotated: [5120, 17408] 15.4-15.9 us against 17.4-17.9, [12288, 6144] 12.7
+// against 14.9-15.4, [17408, 5120] 15.0 against 17.2, [4096, 12288] 9.2-9.3
+// against 9.7-9.8.  Fewer rows keep the default shapes ([2560, 9728] 7.3
+// against 6.1: half the waves in flight), and so do the GGUF rows, whose
+// misaligned 210-byte super-blocks lose with every load at once ([5120,
+// 17408] 21.0 against 19.0 us, [4096, 12288] 12.2 against 11.1).
+static bool bal_shape(const GemvArgs& g, int& nr, int& wv) {
+  if (!g.kimg || g.ttype != TT_Q6_K || g.tokens != 1 || g.rows < 4096 || g.cols % 256) return false;
+  const int upr = g.cols / 64, a = upr / 64, b = upr % 64;
+  if (a == 1) {
+    nr = 2;
+    wv = 1;
+  } else if (a == 3 || a == 4) {
+    nr = a == 4 ? 4 : 2;
+    wv = 4;
+  } else {
+    return false;
+  }
+  return nr * b <= 64 * wv;
+}
+
+template <int TT, int NR, int WV, bool IMG>
+static hipError_t launch_gemv_bal_t(const GemvArgs& g, hipStream_t s) {
+  constexpr int TPB = 4 / WV;
+  const int upr = g.cols / 64;
+  if (upr / 64 < 1 || upr / 64 > WV || NR * (upr % 64) > 64 * WV) return hipErrorInvalidValue;
+  const long teams = (g.rows + NR - 1) / NR;
+  const unsigned grid = (unsigned)((teams + TPB - 1) / TPB);
+  hipLaunchKernelGGL((k_gemv_bal<TT, NR, WV, 1, IMG>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
+                     (const uint8_t*)g.xq, g.out, g.rows, g.row_bytes, upr);
+  return hipGetLastError();
+}
+
+static hipError_t launch_gemv_bal(const GemvArgs& g, int nr, int wv, hipStream_t s) {
+  if (g.ttype != TT_Q6_K || !g.kimg) return hipErrorInvalidValue;
+  if (wv == 1 && nr == 2) return launch_gemv_bal_t<TT_Q6_K, 2, 1, true>(g, s);
+  if (wv == 4 && nr == 2) return launch_gemv_bal_t<TT_Q6_K, 2, 4, true>(g, s);
+  if (wv == 4 && nr == 4) return launch_gemv_bal_t<TT_Q6_K, 4, 4, true>(g, s);
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(const GemvArgs& g, int team, int nt, int nr, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   if (g.kimg && (g.tokens != 1 || !kimage_format(g.ttype) || g.cols % 256)) return hipErrorInvalidValue;
   if (team <= 0 && nr <= 0 && g.tokens == 1) {
+    int bwv = 0;
+    if (bal_shape(g, nr, bwv)) return launch_gemv_bal(g, nr, bwv, s);
     default_shape(g, team, nr);
   } else if (team <= 0 && nr <= 0 && nt <= 0) {
     // several tokens: each weight unit is decoded once (Prep<TT>) and

@@ -1,7 +1,9 @@
 """GPU: the K-quant GEMV image (Q4_K, Q6_K) -- its layout restated on the
 host from the GGUF bytes, the image GEMV against the oracle and bit for bit
 against the GGUF-layout GEMV of the same launch shape (every default shape:
-team-of-lanes, whole-wave teams, several rows per team), and through the Exec
+team-of-lanes, whole-wave teams, several rows per team; the balanced teams
+that only the Q6_K image takes at >= 4096 rows sum in another order), and
+through the Exec
 mirror, which reads a Q6_K weight's image where it quantizes separately:
 bit-identical with images off, matvecPair over adjacent images, and no image
 for the routes that keep the GGUF rows."""
@@ -72,11 +74,22 @@ def test_kimage_layout(gpu, tt, rows, cols):
 
 # (rows, cols, rows_per_lane): the default shapes (20- / 40-lane teams, 64
 # lanes, two- and four-wave teams of 2 or 4 rows; Q6_K 20-lane teams of two
-# rows at width 5120, Q4_K 64-lane teams of two rows at 4096) and explicit
-# row counts
+# rows at width 5120, Q4_K 64-lane teams of two rows at 4096; the Q6_K
+# image's balanced teams from 4096 rows: one wave of two rows at widths 5120
+# and 6144, four waves of two rows at 12288 and of four at 17408, with a last
+# team short of rows) and explicit row counts
 KCASES = [(300, 2560, 0), (257, 1024, 0), (129, 5120, 0), (1, 2560, 0), (250, 2560, 1), (251, 2560, 2),
           (99, 4608, 0), (64, 9728, 0), (4100, 9728, 0), (77, 17408, 0), (40, 6144, 1), (33, 3840, 2),
-          (4097, 2048, 0), (18, 2304, 0), (4100, 5120, 0), (4097, 4096, 0)]
+          (4097, 2048, 0), (18, 2304, 0), (4100, 5120, 0), (4097, 4096, 0), (4099, 6144, 0),
+          (4097, 12288, 0), (4099, 17408, 0)]
+
+
+def balanced(tt, rows, cols, nr):
+    """Default-shape Q6_K image launches from 4096 rows of 64a + b units take
+    the balanced teams (their own summation order): a = 1 with b <= 32, a = 3,
+    a = 4 with b <= 64."""
+    a, b = divmod(cols // 64, 64)
+    return tt == po.TT_Q6_K and nr == 0 and rows >= 4096 and ((a == 1 and b <= 32) or a in (3, 4))
 
 
 @pytest.mark.gpu
@@ -92,10 +105,14 @@ def test_kimage_gemv_vs_oracle_and_gguf(gpu, oracle, tt, rows, cols, nr):
     assert torch.equal(xa[:xq.numel()], xq.reshape(-1))  # the reference Q8_K rows
     out = ops.mul_mat_vec_image(tt, img, xa, rows, cols, nr).cpu().numpy()
     assert rel_l2(out, oracle.matvec(tt, w, x)[0]) < TOL
-    # the GGUF-layout GEMV of the same shape: same units, same order
+    # the GGUF-layout GEMV of the same shape: same units, same order (the
+    # balanced teams: the same block integers, summed in another order)
     if (rows * w.shape[1]) % 4 == 0:
         raw = ops.gemv_tuned(tt, wd, xq, rows, cols, 1, 0, 0, rows_per_lane=nr).cpu().numpy().reshape(-1)
-        assert np.array_equal(out, raw)
+        if balanced(tt, rows, cols, nr):
+            assert rel_l2(out, raw) < 1e-6
+        else:
+            assert np.array_equal(out, raw)
 
 
 @pytest.mark.gpu
@@ -129,7 +146,7 @@ def backend(gpu):
 # one-launch form's (up to 4096; long rows included, in place of the split-K
 # form), and rows past the one-launch form's 32768
 MIRROR = [(po.TT_Q6_K, 1500, 5120), (po.TT_Q6_K, 700, 6144), (po.TT_Q6_K, 40000, 1024),
-          (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 1000, 17408)]
+          (po.TT_Q6_K, 2560, 9728), (po.TT_Q6_K, 1000, 17408), (po.TT_Q6_K, 4100, 6144)]
 # routes that keep the GGUF rows: the one-launch form, Q4_K
 NO_IMAGE = [(po.TT_Q6_K, 700, 4096), (po.TT_Q4_K, 1500, 5120), (po.TT_Q4_K, 9728, 2560)]
 
@@ -152,13 +169,14 @@ def test_backend_matvec_reads_kimage(gpu, oracle, backend, tt, rows, cols):
     # images off: the GGUF rows -- through the same launch (the same bits)
     # where the mirror would quantize separately anyway, through the split-K
     # one-launch form (the same block integers, summed in another order) on
-    # rows of 8192 values and more
+    # rows of 8192 values and more, and in another order too where the image
+    # takes the balanced teams
     backend.set_gemv_images(False)
     out2 = torch.empty(rows, device=gpu)
     backend.matvec(out2, lin, xd)
     backend.sync()
     backend.set_gemv_images(True)
-    if cols >= 8192:
+    if cols >= 8192 or balanced(tt, rows, cols, 0):
         assert rel_l2(out2.cpu().numpy(), got) < 1e-6
     else:
         assert np.array_equal(out2.cpu().numpy(), got)

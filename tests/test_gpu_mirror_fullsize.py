@@ -5,8 +5,9 @@ decode step runs:
 * config 3, IQ4_NL [248320, 2560]: the split quantize + GEMV-image launch
   (`k_gemv_img`, image built by prepare_linear), 10,347 workgroups;
 * config 5 Q6_K [5120, 17408] (down projection) and Q6_K [4096, 12288]: the
-  quantize launch, then the multi-wave GEMV (two rows per four-wave team)
-  from the weight's K-quant image, built by prepare_linear;
+  quantize launch, then the balanced GEMV (`k_gemv_bal`: four-wave teams of
+  four rows at 17408 values, of two rows at 12288, every load of a lane at
+  once) from the weight's K-quant image, built by prepare_linear;
 * config 5 Q4_K [17408, 5120]: quantize + the multi-wave GEMV.
 
 Bar: the float outputs within 1e-5 relative L2 of the oracle on 512 sampled
@@ -88,11 +89,10 @@ def explicit_route(tt, wd, xd, rows, cols, gpu):
         img = ops.gemv_image(tt, wd, rows, cols)
         return ops.mul_mat_vec_image(tt, img, ops.quantize_act_image(tt, xd[None, :]), rows, cols)
     if tt == po.TT_Q6_K:
-        # the K-quant image holds the GGUF bytes reordered; its GEMV gives the
-        # bits of the GGUF-row launch of the same shape (two rows per
-        # four-wave team)
-        xq = ops.quantize_act(tt, xd[None, :])
-        return ops.gemv_tuned(tt, wd, xq, rows, cols, 1, 256, 1, 2)[0]
+        # the K-quant image GEMV at its default launch shape (the balanced
+        # teams at these widths)
+        img = ops.gemv_image(tt, wd, rows, cols)
+        return ops.mul_mat_vec_image(tt, img, ops.quantize_act_image(tt, xd[None, :]), rows, cols)
     xq = ops.quantize_act(tt, xd[None, :])
     return ops.mul_mat(tt, wd, xq, rows, cols, 1, 1)[0]
 
