@@ -76,12 +76,14 @@ def test_kimage_layout(gpu, tt, rows, cols):
 # lanes, two- and four-wave teams of 2 or 4 rows; Q6_K 20-lane teams of two
 # rows at width 5120, Q4_K 64-lane teams of two rows at 4096; the Q6_K
 # image's balanced teams from 4096 rows: one wave of two rows at widths 5120
-# and 6144, four waves of two rows at 12288 and of four at 17408, with a last
-# team short of rows) and explicit row counts
+# and 6144, four waves of two rows at 12288 and 13312 and of four at 17408
+# and 20224 (a tail of 60 units per row: 240 of the team's 256 lanes), with a
+# last team short of rows; width 7936, whose 60-unit tail does not fit one
+# wave of two rows, keeps the default) and explicit row counts
 KCASES = [(300, 2560, 0), (257, 1024, 0), (129, 5120, 0), (1, 2560, 0), (250, 2560, 1), (251, 2560, 2),
           (99, 4608, 0), (64, 9728, 0), (4100, 9728, 0), (77, 17408, 0), (40, 6144, 1), (33, 3840, 2),
           (4097, 2048, 0), (18, 2304, 0), (4100, 5120, 0), (4097, 4096, 0), (4099, 6144, 0),
-          (4097, 12288, 0), (4099, 17408, 0)]
+          (4097, 12288, 0), (4099, 17408, 0), (4097, 13312, 0), (4096, 20224, 0), (4097, 7936, 0)]
 
 
 def balanced(tt, rows, cols, nr):
