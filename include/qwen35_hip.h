@@ -298,7 +298,8 @@ int qhip_launch_mul_mat_wd_image(const void *d_image, const void *d_xq, float *d
  * each block (one for the 4-bit formats, two for Q8_0) in the order the team
  * walks the row, then the f16 scales, each lane's adjacent.  The order depends on
  * the row width (the team width and pass count the library takes for it;
- * Q8_0 at width 5120 takes its own, 40 lanes and two passes); widths 1024, 1280, 2048, 2560, 3072, 3840, 4096, 5120, 6144 and 8192
+ * at width 5120 Q8_0 40 lanes and two passes, IQ4_NL 16 lanes and five);
+ * widths 1024, 1280, 2048, 2560, 3072, 3840, 4096, 5120, 6144 and 8192
  * have one.  The activation of the image GEMV is quantized
  * into the matching split layout (the same Q8_0 values and scales as
  * qhip_launch_quantize_act; scales stored as f32): 72 bytes per 64 values.

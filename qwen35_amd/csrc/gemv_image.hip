@@ -48,16 +48,20 @@ __host__ __device__ constexpr int img_qs() { return TT == TT_Q8_0 ? 2 : 1; }
 
 // Team width and passes for a row width.  Swept on MI355X over T = 8..64 and
 // one, two or four rows per team: 20-lane teams wherever U is a multiple of
-// 20 (IQ4_NL [248320, 2560] 61.3 us, 8-lane 67.1, 10-lane 67.5; [17408,
-// 5120] 12.1 us, 10-lane 13.1), whole-wave teams at width 4096 (5.5 us,
-// 32-lane 5.8, 16-lane 6.1); 32- and 16-lane teams otherwise.
-// Q8_0 (two 16-byte slots per block, twice the quant bytes per unit) takes
-// 40-lane teams of two passes at width 5120: [17408, 5120] 18.35 us against
-// 20.63 with the 20-lane geometry (IQ4_NL 14.85 against 12.19).
+// 20 (IQ4_NL [248320, 2560] 61.3 us, 8-lane 67.1, 10-lane 67.5), whole-wave
+// teams at width 4096 (5.5 us, 32-lane 5.8, 16-lane 6.1); 32- and 16-lane
+// teams otherwise.  At width 5120 IQ4_NL takes 16-lane teams of five passes,
+// every lane of the wave busy ([17408, 5120] 11.93 us against 12.58 with 20
+// lanes x 4 passes, 13.4 with 40 x 2, in a standalone harness; 12.07-12.38
+// against 12.48-12.55 through the C ABI), while Q4_0, whose decode is
+// lighter, keeps 20 lanes (11.5-11.7 against 11.7-12.0 with 16); Q8_0 (two
+// 16-byte slots per block, twice the quant bytes per unit) takes 40-lane
+// teams of two passes: 17.8 us against 18.9 with 20 lanes and 19.6 with 16.
 static bool img_geom(int ttype, int cols, int& T, int& P) {
   if (cols <= 0 || cols % 64) return false;
   const int U = cols / 64;
   if (ttype == TT_Q8_0 && U == 80) { T = 40; P = 2; return true; }
+  if (ttype == TT_IQ4_NL && U == 80) { T = 16; P = 5; return true; }
   if (U % 20 == 0 && U / 20 <= 4) { T = 20; P = U / 20; return true; }
   if (U % 64 == 0 && U / 64 <= 2) { T = 64; P = U / 64; return true; }
   if (U % 32 == 0 && U / 32 <= 4) { T = 32; P = U / 32; return true; }
@@ -133,9 +137,10 @@ __global__ __launch_bounds__(256) void k_gemv_img(const uint8_t* __restrict__ W,
   // row and discards it), so that all of a wave's pieces are in flight at
   // once from the start (IQ4_NL [248320, 2560] 58.4 against 58.8-59.6 us,
   // [32768, 2560] 10.9 against 11.3, the same bits).  One row per team
-  // ([17408, 5120]: 11.85 against 11.72 us) and Q8_0, with twice the pieces
-  // ([17408, 5120]: 18.5 against 17.2 us), load pass by pass after the
-  // barrier.
+  // ([17408, 5120] 16 x 5: 11.9 against 12.9 us) and Q8_0, with twice the
+  // pieces, load pass by pass after the barrier (Q8_0 in 40-lane teams:
+  // 17.1 against 17.6-17.7 us at [17408, 5120] all loads first, but 5.9
+  // against 5.75 at [4096, 5120]).
   const uint8_t* wr[NR];
 #pragma unroll
   for (int k = 0; k < NR; ++k) wr[k] = W + (rowa + k < rows ? rowa + k : rows - 1) * row_bytes;
@@ -321,7 +326,7 @@ static hipError_t launch_img_tt(const GemvArgs& g, int T, int P, int nr, hipStre
   QHIP_IMG(20, 1) QHIP_IMG(20, 2) QHIP_IMG(20, 3) QHIP_IMG(20, 4)
   QHIP_IMG(64, 1) QHIP_IMG(64, 2)
   QHIP_IMG(32, 1) QHIP_IMG(32, 2) QHIP_IMG(32, 3) QHIP_IMG(32, 4)
-  QHIP_IMG(16, 1) QHIP_IMG(16, 2) QHIP_IMG(16, 3) QHIP_IMG(16, 4)
+  QHIP_IMG(16, 1) QHIP_IMG(16, 2) QHIP_IMG(16, 3) QHIP_IMG(16, 4) QHIP_IMG(16, 5)
   if constexpr (TT == TT_Q8_0) {
     QHIP_IMG(40, 2)
   }

@@ -21,13 +21,14 @@ def rel_l2(got, want):
     return float(np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30))
 
 
-# the team width and pass count the library takes for a row width: Q8_0 at
-# width 5120 40-lane teams of two passes; else 20-lane teams where the units
-# are a multiple of 20, then whole waves, 32 and 16
+# the team width and pass count the library takes for a row width: at
+# width 5120 Q8_0 40-lane teams of two passes, IQ4_NL 16-lane teams of five;
+# else 20-lane teams where the units are a multiple of 20, then whole waves,
+# 32 and 16
 def geometry(cols, tt=po.TT_IQ4_NL):
     U = cols // 64
-    if tt == po.TT_Q8_0 and U == 80:
-        return 40, 2
+    if U == 80 and tt in (po.TT_Q8_0, po.TT_IQ4_NL):
+        return (40, 2) if tt == po.TT_Q8_0 else (16, 5)
     for T, pmax in ((20, 4), (64, 2), (32, 4), (16, 4)):
         if U % T == 0 and U // T <= pmax:
             return T, U // T
