@@ -23,8 +23,8 @@
 
 namespace qhip {
 
-template <int TT, int NT, int NR, bool IMG = false>
-__global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
+template <int TT, int NT, int NR, bool IMG = false, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB) void k_gemv(const uint8_t* __restrict__ W,
                                                const uint8_t* __restrict__ XQ,
                                                float* __restrict__ Y, int rows, long row_bytes,
                                                long act_bytes, int upr, int team, int tokens) {
@@ -34,7 +34,7 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t* __restrict__ W,
   const int tpw = 64 / team;                       // teams per wave
   const int r = lane / team, j = lane - r * team;  // team index, lane in team
   // team r owns NR consecutive rows
-  const long row0 = (((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * tpw + r) * NR;
+  const long row0 = (((long)blockIdx.x * WPB + (threadIdx.x >> 6)) * tpw + r) * NR;
   const bool active = r < tpw && row0 < rows;
   const uint8_t* wrow[NR];
 #pragma unroll
@@ -709,6 +709,18 @@ static hipError_t dispatch_kimg(int ttype, F&& f) {
   return hipErrorInvalidValue;
 }
 
+// One-token grids of fewer than 2048 waves run one wave per workgroup
+// rather than four.  Measured on MI355X against four-wave workgroups (GGUF
+// rows, pre-quantized, weights rotated): config 1's Q8_0 [6144, 1024] (1536
+// waves) 3.84 against 4.30 us, Q8_0 [2048, 2048] (1024) 3.89 against 4.12,
+// Q4_K [2560, 2560] (1280) 3.84 against 4.02, Q2_K [9728, 2560] (1622) 5.30
+// against 5.41, IQ4_NL [6144, 1024] 3.49 against 3.55; from 2048 waves the
+// four-wave workgroups stay ahead (Q4_K [4096, 2560] 4.21 against 4.32,
+// Q6_K [4096, 4096] 5.88 against 5.95, Q8_0 [4096, 4096] at 4096 waves 6.10
+// against 6.25).  IQ3_XXS / IQ3_S keep four waves: each workgroup first
+// copies the format's grid into LDS ([4096, 2560] 5.17 against 5.40).
+static constexpr long kGemvOneWaveBelow = 2048;
+
 template <int TT, int NT, int NR, bool IMG = false>
 static hipError_t launch_gemv_t(const GemvArgs& g, int team, hipStream_t s) {
   const int upr = g.cols / 64;
@@ -717,6 +729,13 @@ static hipError_t launch_gemv_t(const GemvArgs& g, int team, hipStream_t s) {
   const int tpw = 64 / team;
   const long teams = (g.rows + NR - 1) / NR;
   const long waves = (teams + tpw - 1) / tpw;
+  if constexpr (NT == 1 && !iq3(TT)) {
+    if (waves < kGemvOneWaveBelow) {
+      hipLaunchKernelGGL((k_gemv<TT, NT, NR, IMG, 1>), dim3((unsigned)waves), dim3(64), 0, s, (const uint8_t*)g.w,
+                         (const uint8_t*)g.xq, g.out, g.rows, g.row_bytes, g.act_bytes, upr, team, g.tokens);
+      return hipGetLastError();
+    }
+  }
   const unsigned grid = (unsigned)((waves + 3) / 4);
   hipLaunchKernelGGL((k_gemv<TT, NT, NR, IMG>), dim3(grid), dim3(256), 0, s, (const uint8_t*)g.w,
                      (const uint8_t*)g.xq, g.out, g.rows, g.row_bytes, g.act_bytes, upr, team,
