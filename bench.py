@@ -488,7 +488,7 @@ def bench_mmq(c: Ctx):
     for name, tt, rows, cols in (("q4_k_17408x5120", TQ4, 17408, 5120), ("q6_k_5120x17408", TQ6, 5120, 17408)):
         # weight copies, each with the images the Exec mirror derives from it
         # (the fragment image it reads from 2 tokens, Q6_K's MMQ image from
-        # 64), rotated per launch so that every launch streams its weight
+        # 65), rotated per launch so that every launch streams its weight
         # from HBM as a decode does (one copy would stay in the 256 MB
         # Infinity Cache)
         wh = synth.make_weight(tt, rows, cols, seed=0, tag=tt)
@@ -522,7 +522,7 @@ def bench_mmq(c: Ctx):
                 pt["mmq_image_us"] = round(s_i * 1e6, 2)
                 s_m = min(s_t, s_i)
             s_f = None
-            if tt == TQ4 or T <= 32:
+            if tt == TQ4 or T <= 64:
                 s_f = rotated(lambda i: lib.qhip_launch_mul_mat_wd_image(frags[i % ncopy].data_ptr(), aq.data_ptr(),
                                                                          y.data_ptr(), rows, cols, T, tt, wp, wn,
                                                                          stream), it)
@@ -530,8 +530,8 @@ def bench_mmq(c: Ctx):
                 s_m = min(s_m, s_f)
             # the C ABI's automatic path (GEMV or tile MMQ by the measured
             # crossover), and what the Exec mirror's matvecBatchK launches: the
-            # same, except the fragment image from 2 tokens (Q6_K up to 32)
-            # and the Q6_K MMQ image from 64
+            # same, except the fragment image from 2 tokens (Q6_K up to 64)
+            # and the Q6_K MMQ image from 65
             s_a = rotated(lambda i: lib.qhip_launch_mul_mat_work(ws[i % ncopy].data_ptr(), aq.data_ptr(),
                                                                  y.data_ptr(), rows, cols, T, tt, PATH_AUTO, wp, wn,
                                                                  stream), it)
@@ -543,9 +543,9 @@ def bench_mmq(c: Ctx):
                 s_k = rotated(lambda i: lib.qhip_launch_mul_mat_vec_image(kimgs[i % ncopy].data_ptr(), aq.data_ptr(),
                                                                           y.data_ptr(), rows, cols, tt, 0, stream), it)
                 pt["gemv_kimage_us"] = round(s_k * 1e6, 2)
-            s_mirror = (s_i if s_i is not None and T >= 64 else s_f if s_f is not None and T >= 2 else
+            s_mirror = (s_i if s_i is not None and T > 64 else s_f if s_f is not None and T >= 2 else
                         s_k if s_k is not None else s_a)
-            pt["mirror_path"] = ("mmq_image" if s_i is not None and T >= 64 else
+            pt["mirror_path"] = ("mmq_image" if s_i is not None and T > 64 else
                                  "fragment_image" if s_f is not None and T >= 2 else
                                  "gemv_kimage" if s_k is not None else "auto")
             pt["mirror_us"] = round(s_mirror * 1e6, 2)

@@ -277,7 +277,7 @@ int qhip_launch_mul_mat_image(const void *d_image, const void *d_xq, float *d_ou
  *   qhip_wd_image_bytes    image size, -1 unless ttype is Q6_K / Q4_K / Q8_0 and cols % 256 == 0
  *   qhip_launch_wd_prepare build it from GGUF bytes (d_image 16-byte aligned)
  *   qhip_launch_mul_mat_wd_image  d_out [tokens, rows] from the image (Q6_K
- *     1..32 tokens, Q4_K and Q8_0 any count; activations as for
+ *     1..64 tokens, Q4_K and Q8_0 any count; activations as for
  *     qhip_launch_mul_mat); d_work (nullable) as for qhip_launch_mul_mat_work,
  *     qhip_mul_mat_work_bytes covers it.  Q6_K / Q4_K: the same integers as
  *     the MMQ on the GGUF rows (QHIP_PATH_MMQ), and the same bits where the
@@ -409,9 +409,9 @@ void qhip_backend_free_linear(qhip_backend *be, qhip_linear *w);
  * so adjacent weights get adjacent images and matvecPair stays one launch),
  * the fragment image of a Q6_K or Q4_K weight with rows * cols >= 2^23
  * (qhip_launch_wd_prepare, the GGUF bytes once more; matvec_batch_k reads it
- * from 2 tokens, Q6_K up to 32) or of a Q8_0 weight with cols <= 1024 (from
+ * from 2 tokens, Q6_K up to 64) or of a Q8_0 weight with cols <= 1024 (from
  * 6 tokens) and the MMQ image of a Q6_K weight
- * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 64 tokens).
+ * (qhip_launch_mmq_prepare, 2.5x the GGUF bytes; from 65 tokens).
  * 0 = built or nothing to build; QHIP_DECLINE = not all built (images off, or
  * past the memory budget): the products then read the GGUF bytes.
  * No reference counterpart (its CUDA kernels decode the GGUF blocks in every

@@ -102,12 +102,11 @@ static bool mmq_supported(int ttype) {
 // from HBM, [5120, 17408]: 48.8 / 51.9 / 53.1 / 64.7 / 76.3 / 124.6 us at 64 /
 // 96 / 128 / 192 / 256 / 512 tokens, against 49.0 / 77.8 / 78.7 / 160.9 /
 // 231.3 / 293.2 for the GGUF-row MMQ (the previous, row-major Q6_K image:
-// 54.0 / 59.6 / 61.2 / 82.0 / 106.9 / 205.9).  Below 64 tokens the fragment
-// image (up to 32) and the GGUF-row MMQ.  Q4_K stays on its fragment image:
-// its MMQ image's 3.9x larger weight bytes cost more than the scaling they
-// save.
+// 54.0 / 59.6 / 61.2 / 82.0 / 106.9 / 205.9).  Up to 64 tokens the fragment
+// image (46.9 us at 64).  Q4_K stays on its fragment image: its MMQ image's
+// 3.9x larger weight bytes cost more than the scaling they save.
 bool mmq_image_preferred(const GemvArgs& g) {
-  return g.ttype == TT_Q6_K && g.tokens >= 64 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
+  return g.ttype == TT_Q6_K && g.tokens > 64 && mmq_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
 }
 
 // Batches of a large Q6_K or Q4_K weight: the Exec mirror multiplies them
@@ -120,7 +119,10 @@ bool mmq_image_preferred(const GemvArgs& g) {
 // 8 / 16 / 32 / 64 / 512 tokens, against GEMV 11.4 / 15.0 / 21.0 / 33.1 us at
 // 1 / 2 / 4 / 8 and the GGUF-row MMQ 19.7 / 20.0 / 19.7 / 21.2 / 25.7 / 39.8 /
 // 154.0 us.  The image from 2 tokens (at one the GEMV is ahead: 12.7 / 19.5
-// us from the images); Q6_K up to its 32-token limit (the MMQ image from 96).
+// us from the images); Q6_K up to its 64-token limit (two 32-token tiles side
+// by side from 33: 46.8 / 46.9 us at 48 / 64 tokens against 49.4 / 49.1 from
+// the plane image and about 50 from the GGUF-row MMQ), the plane image
+// beyond.
 //
 // Q8_0 (the image MMQ from 6 tokens where K is one 1024-value super-chunk):
 // measured on MI355X, [3584, 1024] GEMV 3.59 / 4.36 / 4.84 / 7.84 / 14.02 us
@@ -134,7 +136,7 @@ bool wd_image_preferred(const GemvArgs& g) {
   if (g.ttype == TT_Q8_0)
     return g.tokens >= 6 && g.cols <= 1024 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0 && fast_ok(g);
   if (g.tokens < 2 || (long)g.rows * g.cols < (1L << 23) || !fast_ok(g)) return false;
-  if (g.ttype == TT_Q6_K) return g.tokens <= 32 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
+  if (g.ttype == TT_Q6_K) return g.tokens <= 64 && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
   return g.ttype == TT_Q4_K && wd_image_bytes(g.ttype, g.rows, g.cols) > 0;
 }
 
@@ -163,6 +165,10 @@ long mul_mat_work_bytes(const GemvArgs& g) {
   long n = mmq_work_bytes(g);
   if (mmq_image_bytes(g.ttype, g.rows, g.cols) > 0) {
     const long m = mmq_image_work_bytes(g);
+    if (m > n) n = m;
+  }
+  if (wd_image_bytes(g.ttype, g.rows, g.cols) > 0) {
+    const long m = wd_image_work_bytes(g);
     if (m > n) n = m;
   }
   return n;
@@ -489,7 +495,7 @@ int qhip_launch_mul_mat_wd_image(const void* d_image, const void* d_xq, float* d
   GemvArgs g;
   hipError_t e = make_args(d_image, d_xq, d_out, rows, cols, tokens, ttype, g);
   if (e != hipSuccess) return (int)e;
-  if (wd_image_bytes(ttype, rows, cols) < 0 || (ttype == TT_Q6_K && tokens > 32)) return (int)hipErrorInvalidValue;
+  if (wd_image_bytes(ttype, rows, cols) < 0 || (ttype == TT_Q6_K && tokens > 64)) return (int)hipErrorInvalidValue;
   if (((uintptr_t)d_image & 15u) || !aligned4(d_xq)) return (int)hipErrorInvalidValue;
   if (work_bytes < 0 || (d_work && ((uintptr_t)d_work & 15u))) return (int)hipErrorInvalidValue;
   if (rows == 0 || tokens == 0) return 0;

@@ -1931,13 +1931,19 @@ __global__ __launch_bounds__(256) void k_mmq_wds_q6k(const uint8_t* __restrict__
   mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
 }
 
-// The fragment image, T <= 8 NG: the workgroup's K slice in groups of CPS
-// super-blocks, each group's weight loads (8 per lane and super-block, every
-// wave instruction one aligned 1 KB) and activation DMA all issued before any
-// of it is used.  Measured on MI355X, config 5 Q6_K [5120, 17408], 1 / 8 / 16
-// / 24 tokens: 21.1 / 21.4 / 24.1 / 28.0 us with CPS = 2, against 22.1 / 22.2
+// The fragment image, T <= 8 NG per token tile (blockIdx.y; 33..64 tokens
+// two tiles of 32): the workgroup's K slice in groups of CPS super-blocks,
+// each group's weight loads (8 per lane and super-block, every wave
+// instruction one aligned 1 KB) and activation DMA all issued before any of
+// it is used.  Measured on MI355X, config 5 Q6_K [5120, 17408], 1 / 8 / 16 /
+// 24 tokens: 21.1 / 21.4 / 24.1 / 28.0 us with CPS = 2, against 22.1 / 22.2
 // / 24.4 / 28.2 double-buffered one super-block at a time and 22.5 / 22.7 /
-// 25.9 / 30.4 with CPS = 3 (more registers, fewer resident workgroups).
+// 25.9 / 30.4 with CPS = 3 (more registers, fewer resident workgroups).  The
+// two token tiles of a row tile run side by side and share its weight reads
+// in L2: 40 / 48 / 64 tokens 47.7 / 46.8 / 46.9 us with the K split planned
+// over both tiles' workgroups (54 us with one tile's split), against 49.0 /
+// 49.4 / 49.1 from the plane image; [2560, 9728] 21.1 / 21.4 at 48 / 64
+// against 21.8 / 21.9.
 template <int NG, int CPS>
 __global__ __launch_bounds__(256) void k_mmq_wdp_q6k(const uint8_t* __restrict__ W, const uint8_t* __restrict__ XQ,
                                                       float* __restrict__ Y, int rows, int tokens, long act_bytes,
@@ -1958,6 +1964,12 @@ __global__ __launch_bounds__(256) void k_mmq_wdp_q6k(const uint8_t* __restrict__
   const uint8_t* wbase = W + (long)(grp < ngrp ? grp : ngrp - 1) * nsb * kWdiTile;
   const int sb0 = ks * cps, sb1 = sb0 + cps < nsb ? sb0 + cps : nsb;
   const int arow = li < TR ? li : 0;
+  // token tile blockIdx.y (T > 32: NG = 4): its tokens' activation rows and
+  // outputs; its row tiles' split-K hand-offs follow those of tile y - 1
+  XQ += (long)blockIdx.y * TR * act_bytes;
+  Y += (long)blockIdx.y * TR * rows;
+  tokens = tokens - (int)blockIdx.y * TR < TR ? tokens - (int)blockIdx.y * TR : TR;
+  const int tile = g + (int)blockIdx.y * (G / ksplit);
 
   long goff[NDMA];
   int gst[NDMA];
@@ -1997,7 +2009,7 @@ __global__ __launch_bounds__(256) void k_mmq_wdp_q6k(const uint8_t* __restrict__
       }
     __syncthreads();  // the next group's DMA overwrites the stages
   }
-  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, g, ksplit, ks, part, cnt);
+  mmq_write_tile<1, 1, 4, NE>(acc, Y, rows, tokens, r0, 0, 32 * wv, 0, tile, ksplit, ks, part, cnt);
 }
 
 // One thread per (tile, lane L) of the Q6_K fragment image: lane L's 96 quant
@@ -3032,8 +3044,11 @@ static hipError_t launch_mmq_wd(const GemvArgs& g, WdPlan plan, void* work, hipS
 // kernel (one 32-token tile, 128 rows per workgroup, K split like the Q4_K one).
 static bool wds_q6k(const GemvArgs& g) { return g.ttype == TT_Q6_K && g.tokens <= 24; }
 
+// the tiles of every 32-token tile count: the fragment image's launch runs
+// them side by side (blockIdx.y)
 static int wds_q6k_slices(const GemvArgs& g) {
-  return wd_one_round_slices((g.rows + kWdBR - 1) / kWdBR, g.cols / 256, 1.2);
+  const long ntt = (g.tokens + 31) / 32;
+  return wd_one_round_slices(ntt * ((g.rows + kWdBR - 1) / kWdBR), g.cols / 256, 1.2);
 }
 
 static hipError_t launch_mmq_wds_q6k(const GemvArgs& g, int ksplit, void* work, hipStream_t s) {
@@ -3072,6 +3087,12 @@ static hipError_t launch_mmq_rk(const GemvArgs& g, hipStream_t s) {
   return hipGetLastError();
 }
 
+long wd_image_work_bytes(const GemvArgs& g) {
+  if (g.ttype == TT_Q4_K) return g.tokens <= 24 ? 0 : wd_work_bytes(g, wd_plan(g));
+  if (g.ttype == TT_Q6_K && g.tokens > 16 && g.tokens <= 64) return mmq_split_bytes(g, 32, kWdBR, wds_q6k_slices(g));
+  return 0;
+}
+
 hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s) {
   if (g.rows <= 0 || g.tokens <= 0) return hipSuccess;
   if (g.ttype == TT_Q8_0) return launch_mmq_q8i(g, s);
@@ -3083,23 +3104,24 @@ hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, h
     if (!work || work_bytes < wd_work_bytes(g, plan)) plan = WdPlan{1, 0};
     return launch_mmq_wd<true>(g, plan, work, s, wd_bt(g));
   }
-  if (g.ttype != TT_Q6_K || g.tokens > 32) return hipErrorInvalidValue;
+  if (g.ttype != TT_Q6_K || g.tokens > 64) return hipErrorInvalidValue;
   // up to 16 tokens the K split inside the workgroup; 17..32 the split
   // launch with whole-group prefetch (28.0 against 28.3 us at 24 tokens)
   if (g.tokens <= 16) return launch_mmq_rk<TT_Q6_K, 12>(g, s);
+  const int ntt = (g.tokens + 31) / 32;
   int ksplit = wds_q6k_slices(g);
   if (!work || work_bytes < mmq_split_bytes(g, 32, kWdBR, ksplit)) ksplit = 1;
   const int nsb = g.cols / 256;
   const long ntr = (g.rows + kWdBR - 1) / kWdBR;
   const int cps = (nsb + ksplit - 1) / ksplit;
   const long G = ntr * ksplit;
-  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr > kSkMaxTiles)) return hipErrorInvalidValue;
+  if (G > 0x7FFFFFFFL || (ksplit > 1 && ntr * ntt > kSkMaxTiles)) return hipErrorInvalidValue;
   unsigned* cnt = ksplit > 1 ? (unsigned*)work : nullptr;
   float* part = ksplit > 1 ? (float*)((uint8_t*)work + kSkCountBytes) : nullptr;
-  const int ng = (g.tokens + 7) / 8;
+  const int ng = ntt > 1 ? 4 : (g.tokens + 7) / 8;
 #define QHIP_WDP(N)                                                                                           \
   if (ng == N)                                                                                                \
-    hipLaunchKernelGGL((k_mmq_wdp_q6k<N, 2>), dim3((unsigned)G), dim3(256), 0, s, (const uint8_t*)g.w,         \
+    hipLaunchKernelGGL((k_mmq_wdp_q6k<N, 2>), dim3((unsigned)G, (unsigned)ntt), dim3(256), 0, s, (const uint8_t*)g.w, \
                        (const uint8_t*)g.xq, g.out, g.rows, g.tokens, g.act_bytes, nsb, ksplit, cps, part, cnt);
   QHIP_WDP(1) QHIP_WDP(2) QHIP_WDP(3) QHIP_WDP(4)
 #undef QHIP_WDP

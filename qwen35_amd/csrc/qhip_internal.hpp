@@ -93,6 +93,8 @@ hipError_t launch_wd_prepare(int ttype, const void* w, long row_bytes, int rows,
                              hipStream_t s);
 hipError_t launch_mmq_wd_image(const GemvArgs& g, void* work, long work_bytes, hipStream_t s);
 long mmq_image_work_bytes(const GemvArgs& g);
+// the split-K workspace launch_mmq_wd_image takes (fragment image; 0 = none)
+long wd_image_work_bytes(const GemvArgs& g);
 // GEMV weight image of the 32-value 4-bit formats (gemv_image.hip): the same
 // bytes per row, quant bytes 16-byte aligned in unit order, scales apart
 bool gemv_image_format(int ttype);

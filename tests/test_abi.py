@@ -143,7 +143,7 @@ def test_invalid_arguments_rejected_before_launch(lib):
     assert lib.qhip_launch_wd_prepare(2, p, 32, 512, p, None) == INVALID
     assert lib.qhip_launch_wd_prepare(8, p, 32, 544, p, None) == INVALID
     assert lib.qhip_launch_wd_prepare(14, p, 32, 512, ctypes.c_void_p(0x1008), None) == INVALID
-    assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 33, 14, None, 0, None) == INVALID
+    assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 65, 14, None, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 512, 8, 2, None, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_wd_image(p, p, p, 32, 544, 8, 8, None, 0, None) == INVALID
     assert lib.qhip_launch_mul_mat_wd_image(ctypes.c_void_p(0x1008), p, p, 32, 512, 8, 14, None, 0,

@@ -58,7 +58,7 @@ def q6(gpu):
     return rows, cols, w, wd, ops.wd_image(TQ6, wd, rows, cols)
 
 
-@pytest.mark.parametrize("tokens", [1, 2, 3, 7, 8, 9, 16, 17, 24, 25, 31, 32])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 7, 8, 9, 16, 17, 24, 25, 31, 32, 33, 40, 63, 64])
 def test_wd_image_mmq_vs_oracle(gpu, oracle, q6, tokens):
     rows, cols, w, wd, img = q6
     x = synth.make_act(cols, tokens, seed=42, tag=tokens)
@@ -81,7 +81,7 @@ def test_wd_image_mmq_vs_oracle(gpu, oracle, q6, tokens):
             assert rel_l2(got.cpu().numpy(), raw.cpu().numpy()) < 1e-6
 
 
-@pytest.mark.parametrize("tokens", [1, 6, 8, 19, 32])
+@pytest.mark.parametrize("tokens", [1, 6, 8, 19, 32, 45, 64])
 def test_wd_image_integers_exact(gpu, oracle, tokens):
     rows, cols = 96, 1024
     w = unit_scale_weight(TQ6, rows, cols, seed=43)
@@ -111,7 +111,8 @@ def test_wd_image_extreme_values(gpu, oracle):
     assert rel_l2(got.cpu().numpy(), oracle.matvec(TQ6, w, x)) < TOL
 
 
-@pytest.mark.parametrize("rows,cols,tokens", [(5120, 17408, 8), (4096, 4096, 24), (130, 256, 1)])
+@pytest.mark.parametrize("rows,cols,tokens", [(5120, 17408, 8), (4096, 4096, 24), (130, 256, 1), (5120, 17408, 64),
+                                              (2560, 9728, 48)])
 def test_wd_image_model_shapes(gpu, oracle, rows, cols, tokens):
     """The config-5 down projection and other widths, through the split."""
     w = synth.make_weight(TQ6, rows, cols, seed=45, tag=rows)
@@ -133,12 +134,13 @@ def backend(gpu):
 
 
 @pytest.mark.parametrize("tt,tokens", [(TQ6, 2), (TQ6, 3), (TQ6, 5), (TQ6, 8), (TQ6, 24), (TQ6, 32), (TQ6, 33),
+                                       (TQ6, 64), (TQ6, 65),
                                        (po.TT_Q4_K, 2), (po.TT_Q4_K, 3), (po.TT_Q4_K, 8), (po.TT_Q4_K, 40),
                                        (po.TT_Q4_K, 130)])
 def test_backend_batches_from_fragment_image(gpu, oracle, backend, tt, tokens):
     """matvecBatchK of a large Q6_K / Q4_K weight: the fragment image from 2
-    tokens (Q6_K up to 32), built by prepare_linear; with images off the
-    GGUF-row products, the same block integers."""
+    tokens (Q6_K up to 64, then its plane image), built by prepare_linear;
+    with images off the GGUF-row products, the same block integers."""
     rows, cols = 2048, 4608
     w = synth.make_weight(tt, rows, cols, seed=46, tag=tt)
     x = synth.make_act(cols, tokens, seed=46, tag=tokens)
