@@ -51,7 +51,8 @@ PROFILE_KERNELS = ["cfg3_gemv", "cfg3_step", "cfg3_gemv_gguf", "cfg1_gemv", "cfg
                    "cfg5_q6k_kimage",
                    "down", "gate_up", "fused_gate_up", "split_down", "mirror_down", "step", "step_unfused",
                    "mmq_cfg4", "mmq_cfg5_q4k", "mmq_cfg5_q6k_image", "mmq_cfg5_q3k", "mmq_cfg5_q2k",
-                   "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8", "mmq_cfg4_frag",
+                   "mmq_cfg5_q4k_frag", "mmq_cfg5_q4k_frag_t8", "mmq_cfg5_q6k_frag_t8", "mmq_cfg5_q6k_frag_t64",
+                   "mmq_cfg4_frag",
                    "mmq_cfg4_ragged_frag"]
 
 
@@ -835,6 +836,7 @@ def profile(c: Ctx, which: str, launches: int):
                              "mmq_cfg4": (TQ8, 3584, 1024, 512), "mmq_cfg5_q4k_frag": (TQ4, 17408, 5120, 512),
                              "mmq_cfg5_q4k_frag_t8": (TQ4, 17408, 5120, 8),
                              "mmq_cfg5_q6k_frag_t8": (TQ6, 5120, 17408, 8),
+                             "mmq_cfg5_q6k_frag_t64": (TQ6, 5120, 17408, 64),
                              "mmq_cfg4_frag": (TQ8, 3584, 1024, 512),
                              "mmq_cfg4_ragged_frag": (TQ8, 3584, 1024, 0)}[which]
         w = torch.from_numpy(synth.make_weight(tt, rows, cols, seed=0, tag=tt)).to(dev)
